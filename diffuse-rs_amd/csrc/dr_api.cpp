@@ -1,0 +1,712 @@
+// dr_api.cpp -- the C ABI declared in include/dr_attn.h.
+//
+// Host-side bookkeeping only: argument validation with the reference's
+// contract, device buffers, row metadata upload, launch planning.  All
+// arithmetic on the attention path runs in the HIP kernels of attn_fwd.hip
+// and kv_cache.hip; there is no CPU fallback.  If no GPU is visible every
+// compute entry point fails with DR_ERR_NO_DEVICE.
+#include "dr_attn.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "dr_internal.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? DR_ERR_OOM : DR_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+#define DR_HIP(expr)                                    \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+    } while (0)
+
+#define DR_CHECK(expr)                 \
+    do {                               \
+        int rc_ = (expr);              \
+        if (rc_ != DR_OK) return rc_;  \
+    } while (0)
+
+// Largest sequence position / window the kernels accept (int32 arithmetic
+// on |qpos - kpos|).  The reference caps sequences at 32768 (model.rs:403-407).
+constexpr size_t MAX_POS = (size_t)1 << 30;
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+
+int ensure(DevBuf& b, size_t bytes) {
+    if (bytes <= b.cap) return DR_OK;
+    if (b.p) {
+        hipError_t e = hipFree(b.p);  // implicitly waits for work using it
+        b.p = nullptr;
+        b.cap = 0;
+        if (e != hipSuccess) return hip_fail(e, "hipFree");
+    }
+    size_t nb = std::max(bytes, (size_t)4096);
+    DR_HIP(hipMalloc(&b.p, nb));
+    b.cap = nb;
+    return DR_OK;
+}
+
+void release(DevBuf& b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+}
+
+int hd_tile_for(size_t hd) { return hd <= 64 ? 64 : (hd <= 128 ? 128 : 256); }
+
+size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+}  // namespace
+
+struct dr_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipStream_t own = nullptr;
+    int n_cu = 0;
+    int force_split = 0;
+    dr::LaunchPlan last{};
+    bool has_last = false;
+    DevBuf part;                         // key-split partials
+    DevBuf q, k, v, kc, vtc, meta, out;  // dr_attention() staging
+};
+
+struct dr_pass {
+    dr_ctx* ctx = nullptr;
+    int* d_pos = nullptr;
+    size_t n = 0;
+    size_t cap = 0;
+    size_t max_pos = 0;
+};
+
+struct dr_step_cache {
+    struct Slot {
+        std::vector<int32_t> prev_seq, last_changed;
+        bool initialized = false;
+        size_t vicinity = 0;
+    };
+    dr_ctx* ctx = nullptr;
+    size_t n_total = 0, cap = 0, n_layer = 0, n_batch = 0;
+    std::vector<int> hkv, hd, hd_tile;
+    std::vector<uint16_t*> k, vt;  // [layer * n_batch + batch]
+    std::vector<Slot> slot;
+};
+
+namespace {
+
+int use_device(const dr_ctx* ctx) {
+    DR_HIP(hipSetDevice(ctx->device));
+    return DR_OK;
+}
+
+int upload_pass(dr_pass* p, const size_t* active, size_t n) {
+    if (n > 0 && !active) return fail(DR_ERR_INVALID, "pass: active is NULL with n_active=%zu", n);
+    std::vector<int32_t> h(n);
+    size_t mx = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (active[i] >= MAX_POS)
+            return fail(DR_ERR_INVALID, "pass: position %zu exceeds %zu", active[i], MAX_POS);
+        if (i > 0 && active[i] <= active[i - 1])
+            return fail(DR_ERR_INVALID, "pass: positions must be strictly ascending (index %zu)", i);
+        h[i] = (int32_t)active[i];
+        mx = std::max(mx, active[i]);
+    }
+    DR_CHECK(use_device(p->ctx));
+    if (n > p->cap) {
+        if (p->d_pos) {
+            hipError_t e = hipFree(p->d_pos);
+            p->d_pos = nullptr;
+            p->cap = 0;
+            if (e != hipSuccess) return hip_fail(e, "hipFree");
+        }
+        DR_HIP(hipMalloc(&p->d_pos, n * sizeof(int32_t)));
+        p->cap = n;
+    }
+    if (n > 0) {
+        DR_HIP(hipMemcpyAsync(p->d_pos, h.data(), n * sizeof(int32_t), hipMemcpyHostToDevice,
+                              p->ctx->stream));
+        DR_HIP(hipStreamSynchronize(p->ctx->stream));
+    }
+    p->n = n;
+    p->max_pos = mx;
+    return DR_OK;
+}
+
+std::mutex g_default_mu;
+dr_ctx* g_default_ctx = nullptr;
+
+}  // namespace
+
+extern "C" {
+
+const char* dr_last_error(void) { return g_err.c_str(); }
+
+const char* dr_version(void) { return "0.1.0"; }
+
+int dr_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int dr_ctx_create(int device, dr_ctx** out) {
+    if (!out) return fail(DR_ERR_INVALID, "dr_ctx_create: out is NULL");
+    *out = nullptr;
+    const int n = dr_device_count();
+    if (n <= 0) return fail(DR_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= n)
+        return fail(DR_ERR_INVALID, "device %d out of range (%d visible)", device, n);
+    DR_HIP(hipSetDevice(device));
+    dr_ctx* c = new dr_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    c->stream = c->own;
+    e = hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return hip_fail(e, "hipDeviceGetAttribute");
+    }
+    *out = c;
+    return DR_OK;
+}
+
+int dr_ctx_set_stream(dr_ctx* ctx, void* stream) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_stream: ctx is NULL");
+    ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own;
+    return DR_OK;
+}
+
+void* dr_ctx_stream(dr_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+int dr_ctx_synchronize(dr_ctx* ctx) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_synchronize: ctx is NULL");
+    DR_CHECK(use_device(ctx));
+    DR_HIP(hipStreamSynchronize(ctx->stream));
+    return DR_OK;
+}
+
+void dr_ctx_destroy(dr_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (DevBuf* b : {&ctx->part, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc, &ctx->meta,
+                      &ctx->out})
+        release(*b);
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
+    if (!ctx || !info) return fail(DR_ERR_INVALID, "dr_ctx_last_launch: NULL argument");
+    if (!ctx->has_last) return fail(DR_ERR_INVALID, "no attention launched on this context yet");
+    info->n_split = ctx->last.n_split;
+    info->n_workgroups = ctx->last.n_workgroups;
+    info->waves_per_wg = ctx->last.waves;
+    info->block_n = ctx->last.block_n;
+    info->head_dim_tile = ctx->last.hd_tile;
+    return DR_OK;
+}
+
+int dr_ctx_set_split(dr_ctx* ctx, int n_split) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_split: ctx is NULL");
+    if (n_split < 0 || n_split > 64) return fail(DR_ERR_INVALID, "n_split %d not in 0..64", n_split);
+    ctx->force_split = n_split;
+    return DR_OK;
+}
+
+// ---------------------------------------------------------------- passes
+
+int dr_pass_create(dr_ctx* ctx, const size_t* active, size_t n_active, dr_pass** out) {
+    if (!ctx || !out) return fail(DR_ERR_INVALID, "dr_pass_create: NULL argument");
+    *out = nullptr;
+    dr_pass* p = new dr_pass();
+    p->ctx = ctx;
+    int rc = upload_pass(p, active, n_active);
+    if (rc != DR_OK) {
+        dr_pass_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return DR_OK;
+}
+
+int dr_pass_set(dr_pass* pass, const size_t* active, size_t n_active) {
+    if (!pass) return fail(DR_ERR_INVALID, "dr_pass_set: pass is NULL");
+    return upload_pass(pass, active, n_active);
+}
+
+size_t dr_pass_len(const dr_pass* pass) { return pass ? pass->n : 0; }
+
+void dr_pass_destroy(dr_pass* pass) {
+    if (!pass) return;
+    if (pass->d_pos) {
+        (void)hipSetDevice(pass->ctx->device);
+        (void)hipStreamSynchronize(pass->ctx->stream);
+        (void)hipFree(pass->d_pos);
+    }
+    delete pass;
+}
+
+// ---------------------------------------------------------------- cache
+
+int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n_head_kv,
+                    const size_t* head_dim, size_t n_batch, dr_step_cache** out) {
+    if (!ctx || !out) return fail(DR_ERR_INVALID, "dr_cache_create: NULL argument");
+    *out = nullptr;
+    if (n_layer > 0 && (!n_head_kv || !head_dim))
+        return fail(DR_ERR_INVALID, "dr_cache_create: per-layer arrays are NULL");
+    if (n_batch < 1 || n_batch > (size_t)dr::MAX_BATCH)
+        return fail(DR_ERR_INVALID, "n_batch %zu not in 1..%d", n_batch, dr::MAX_BATCH);
+    if (n_total >= MAX_POS) return fail(DR_ERR_INVALID, "n_total %zu too large", n_total);
+    for (size_t l = 0; l < n_layer; ++l) {
+        if (n_head_kv[l] < 1 || n_head_kv[l] > 4096)
+            return fail(DR_ERR_INVALID, "layer %zu: n_head_kv %zu invalid", l, n_head_kv[l]);
+        if (head_dim[l] < 1) return fail(DR_ERR_INVALID, "layer %zu: head_dim is 0", l);
+        if (head_dim[l] > 256)
+            return fail(DR_ERR_UNSUPPORTED, "layer %zu: head_dim %zu > 256 not built", l,
+                        head_dim[l]);
+    }
+    DR_CHECK(use_device(ctx));
+    dr_step_cache* c = new dr_step_cache();
+    c->ctx = ctx;
+    c->n_total = n_total;
+    c->cap = round_up(std::max(n_total, (size_t)1), dr::KEY_ALIGN);
+    c->n_layer = n_layer;
+    c->n_batch = n_batch;
+    c->k.assign(n_layer * n_batch, nullptr);
+    c->vt.assign(n_layer * n_batch, nullptr);
+    c->slot.resize(n_batch);
+    for (auto& s : c->slot) {
+        s.prev_seq.assign(n_total, -1);
+        s.last_changed.assign(n_total, -1);
+    }
+    for (size_t l = 0; l < n_layer; ++l) {
+        c->hkv.push_back((int)n_head_kv[l]);
+        c->hd.push_back((int)head_dim[l]);
+        c->hd_tile.push_back(hd_tile_for(head_dim[l]));
+        const size_t bytes = (size_t)n_head_kv[l] * c->cap * c->hd_tile[l] * sizeof(uint16_t);
+        for (size_t b = 0; b < n_batch; ++b) {
+            for (uint16_t** dst : {&c->k[l * n_batch + b], &c->vt[l * n_batch + b]}) {
+                hipError_t e = hipMalloc(reinterpret_cast<void**>(dst), bytes);
+                if (e == hipSuccess) e = hipMemset(*dst, 0, bytes);
+                if (e != hipSuccess) {
+                    dr_cache_destroy(c);
+                    return hip_fail(e, "KV cache allocation");
+                }
+            }
+        }
+    }
+    *out = c;
+    return DR_OK;
+}
+
+void dr_cache_destroy(dr_step_cache* cache) {
+    if (!cache) return;
+    (void)hipSetDevice(cache->ctx->device);
+    (void)hipStreamSynchronize(cache->ctx->stream);
+    for (uint16_t* p : cache->k)
+        if (p) (void)hipFree(p);
+    for (uint16_t* p : cache->vt)
+        if (p) (void)hipFree(p);
+    delete cache;
+}
+
+static int check_slot(const dr_step_cache* c, size_t layer, size_t batch, const char* who) {
+    if (!c) return fail(DR_ERR_INVALID, "%s: cache is NULL", who);
+    if (layer >= c->n_layer) return fail(DR_ERR_INVALID, "%s: layer %zu >= %zu", who, layer, c->n_layer);
+    if (batch >= c->n_batch) return fail(DR_ERR_INVALID, "%s: batch %zu >= %zu", who, batch, c->n_batch);
+    return DR_OK;
+}
+
+int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
+                   const float* k, const float* v, const float* k_norm_w, float eps) {
+    DR_CHECK(check_slot(cache, layer, batch, "dr_cache_store"));
+    if (!pass) return fail(DR_ERR_INVALID, "dr_cache_store: pass is NULL");
+    if (pass->ctx != cache->ctx) return fail(DR_ERR_INVALID, "dr_cache_store: pass and cache use different contexts");
+    if (pass->n == 0) return DR_OK;
+    if (pass->max_pos >= cache->n_total)
+        return fail(DR_ERR_INVALID, "dr_cache_store: position %zu >= n_total %zu", pass->max_pos,
+                    cache->n_total);
+    if (!k || !v) return fail(DR_ERR_INVALID, "dr_cache_store: k/v is NULL");
+    DR_CHECK(use_device(cache->ctx));
+    dr::StoreArgs a{};
+    a.k = k;
+    a.v = v;
+    a.pos = pass->d_pos;
+    a.n = (int)pass->n;
+    a.n_head_kv = cache->hkv[layer];
+    a.hd = cache->hd[layer];
+    a.cap = (int)cache->cap;
+    a.kc = cache->k[layer * cache->n_batch + batch];
+    a.vtc = cache->vt[layer * cache->n_batch + batch];
+    a.kn_w = k_norm_w;
+    a.kn_eps = eps;
+    hipError_t e = dr::launch_store(cache->hd_tile[layer], a, cache->ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "kv_store launch");
+    return DR_OK;
+}
+
+int dr_cache_gather(dr_step_cache* cache, size_t layer, size_t batch, const size_t* positions,
+                    size_t n, float* out_k, float* out_v) {
+    DR_CHECK(check_slot(cache, layer, batch, "dr_cache_gather"));
+    if (n == 0) return DR_OK;
+    if (!positions || !out_k || !out_v) return fail(DR_ERR_INVALID, "dr_cache_gather: NULL argument");
+    std::vector<int32_t> h(n);
+    for (size_t i = 0; i < n; ++i) {
+        if (positions[i] >= cache->n_total)
+            return fail(DR_ERR_INVALID, "dr_cache_gather: position %zu >= n_total %zu",
+                        positions[i], cache->n_total);
+        h[i] = (int32_t)positions[i];
+    }
+    dr_ctx* ctx = cache->ctx;
+    DR_CHECK(use_device(ctx));
+    DR_CHECK(ensure(ctx->meta, n * sizeof(int32_t)));
+    DR_HIP(hipMemcpyAsync(ctx->meta.p, h.data(), n * sizeof(int32_t), hipMemcpyHostToDevice,
+                          ctx->stream));
+    dr::GatherArgs a{};
+    a.kc = cache->k[layer * cache->n_batch + batch];
+    a.vtc = cache->vt[layer * cache->n_batch + batch];
+    a.pos = static_cast<const int*>(ctx->meta.p);
+    a.n = (int)n;
+    a.n_head_kv = cache->hkv[layer];
+    a.hd = cache->hd[layer];
+    a.cap = (int)cache->cap;
+    a.out_k = out_k;
+    a.out_v = out_v;
+    hipError_t e = dr::launch_gather(cache->hd_tile[layer], a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "kv_gather launch");
+    // the staging vector h dies here; the copy above was from pageable memory
+    // and is complete when hipMemcpyAsync returns.
+    return DR_OK;
+}
+
+int dr_cache_update_seq(dr_step_cache* cache, size_t batch, const int32_t* seq, size_t n) {
+    if (!cache) return fail(DR_ERR_INVALID, "dr_cache_update_seq: cache is NULL");
+    if (batch >= cache->n_batch) return fail(DR_ERR_INVALID, "dr_cache_update_seq: batch %zu >= %zu", batch, cache->n_batch);
+    if (n != cache->n_total)
+        return fail(DR_ERR_INVALID, "dr_cache_update_seq: length %zu != n_total %zu", n, cache->n_total);
+    if (n > 0 && !seq) return fail(DR_ERR_INVALID, "dr_cache_update_seq: seq is NULL");
+    auto& s = cache->slot[batch];
+    std::copy(seq, seq + n, s.prev_seq.begin());
+    s.initialized = true;
+    return DR_OK;
+}
+
+int dr_split_active(const int32_t* prev_seq, int32_t* last_changed, const int32_t* seq,
+                    const uint8_t* is_masked, size_t n, size_t step, size_t vicinity,
+                    size_t* active, size_t* n_active, size_t* cached, size_t* n_cached) {
+    if (n > 0 && (!prev_seq || !last_changed || !seq || !is_masked || !active || !cached))
+        return fail(DR_ERR_INVALID, "dr_split_active: NULL array");
+    if (!n_active || !n_cached) return fail(DR_ERR_INVALID, "dr_split_active: NULL count");
+    if (step > (size_t)std::numeric_limits<int32_t>::max())
+        return fail(DR_ERR_INVALID, "dr_split_active: step too large");
+    const int32_t st = (int32_t)step;
+    // cache.rs:88-97: changed, still masked, or changed within
+    // EXTRA_ACTIVE_STEPS (= 2, cache.rs:23) steps.
+    std::vector<uint8_t> act(n, 0);
+    for (size_t i = 0; i < n; ++i) {
+        const bool changed = seq[i] != prev_seq[i];
+        if (changed) last_changed[i] = st;
+        const bool recent = last_changed[i] >= 0 && (st - last_changed[i]) <= 2;
+        act[i] = changed || is_masked[i] || recent;
+    }
+    // cache.rs:98-104: vicinity refresh around still-masked positions.
+    if (vicinity > 0) {
+        for (size_t m = 0; m < n; ++m) {
+            if (!is_masked[m]) continue;
+            const size_t lo = m > vicinity ? m - vicinity : 0;
+            const size_t hi = std::min(m + vicinity + 1, n);
+            std::fill(act.begin() + lo, act.begin() + hi, 1);
+        }
+    }
+    size_t na = 0, nc = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (act[i])
+            active[na++] = i;
+        else
+            cached[nc++] = i;
+    }
+    *n_active = na;
+    *n_cached = nc;
+    return DR_OK;
+}
+
+int dr_cache_split_active(dr_step_cache* cache, size_t batch, const int32_t* seq,
+                          const uint8_t* is_masked, size_t n, size_t step, size_t* active,
+                          size_t* n_active, size_t* cached, size_t* n_cached) {
+    if (!cache) return fail(DR_ERR_INVALID, "dr_cache_split_active: cache is NULL");
+    if (batch >= cache->n_batch) return fail(DR_ERR_INVALID, "dr_cache_split_active: batch %zu >= %zu", batch, cache->n_batch);
+    if (n > cache->n_total)
+        return fail(DR_ERR_INVALID, "dr_cache_split_active: length %zu > n_total %zu", n, cache->n_total);
+    auto& s = cache->slot[batch];
+    return dr_split_active(s.prev_seq.data(), s.last_changed.data(), seq, is_masked, n, step,
+                           s.vicinity, active, n_active, cached, n_cached);
+}
+
+int dr_cache_set_vicinity(dr_step_cache* cache, size_t batch, size_t vicinity) {
+    if (!cache || batch >= cache->n_batch) return fail(DR_ERR_INVALID, "dr_cache_set_vicinity: bad cache/batch");
+    cache->slot[batch].vicinity = vicinity;
+    return DR_OK;
+}
+
+int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
+    if (!cache || batch >= cache->n_batch) return 0;
+    return cache->slot[batch].initialized ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- attention
+
+static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int max_nk,
+                          bool masked, bool qnorm) {
+    dr::LaunchPlan p = dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk,
+                                          masked, qnorm, ctx->n_cu, ctx->force_split);
+    const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
+    if (ws > 0) {
+        DR_CHECK(ensure(ctx->part, ws));
+        a.part_o = static_cast<float*>(ctx->part.p);
+    }
+    hipError_t e = dr::launch_attention(p, a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "attention launch");
+    ctx->last = p;
+    ctx->has_last = true;
+    return DR_OK;
+}
+
+static float scale_log2(float scale) { return scale * 1.4426950408889634f; }
+
+static int opt_to_int(dr_opt_usize o) {
+    if (!o.present) return -1;
+    return (int)std::min(o.value, MAX_POS);
+}
+
+int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
+                        size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                        dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                        float q_norm_eps) {
+    DR_CHECK(check_slot(cache, layer, 0, "dr_attention_cached"));
+    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "dr_attention_cached: no items");
+    if (n_items > cache->n_batch)
+        return fail(DR_ERR_INVALID, "dr_attention_cached: %zu items > cache n_batch %zu", n_items,
+                    cache->n_batch);
+    const size_t hkv = (size_t)cache->hkv[layer];
+    const size_t hd = (size_t)cache->hd[layer];
+    if (n_head < hkv || n_head % hkv != 0)
+        return fail(DR_ERR_INVALID, "n_head %zu is not a multiple of n_head_kv %zu", n_head, hkv);
+    dr_ctx* ctx = cache->ctx;
+    dr::AttnArgs a{};
+    a.n_batch = (int)n_items;
+    a.n_head = (int)n_head;
+    a.n_head_kv = (int)hkv;
+    a.group = (int)(n_head / hkv);
+    a.hd = (int)hd;
+    a.cap = (int)cache->cap;
+    a.q_rstride = a.o_rstride = (int)(n_head * hd);
+    a.c = scale_log2(scale);
+    a.window = opt_to_int(sliding_window);
+    a.prefix = opt_to_int(causal_prefix);
+    a.qn_w = q_norm_w;
+    a.qn_eps = q_norm_eps;
+    int max_nq = 0;
+    const int tile = cache->hd_tile[layer];
+    for (size_t b = 0; b < n_items; ++b) {
+        const dr_batch_item& it = items[b];
+        if (!it.pass) return fail(DR_ERR_INVALID, "item %zu: pass is NULL", b);
+        if (it.pass->ctx != ctx) return fail(DR_ERR_INVALID, "item %zu: pass from another context", b);
+        if (it.pass->n > 0) {
+            if (it.pass->max_pos >= cache->n_total)
+                return fail(DR_ERR_INVALID, "item %zu: position %zu >= n_total %zu", b,
+                            it.pass->max_pos, cache->n_total);
+            if (!it.q || !it.out) return fail(DR_ERR_INVALID, "item %zu: q/out is NULL", b);
+            if ((int)hd == tile && (((uintptr_t)it.q | (uintptr_t)it.out) & 15))
+                return fail(DR_ERR_INVALID, "item %zu: q/out must be 16-byte aligned", b);
+        }
+        dr::AttnSlot& s = a.slot[b];
+        s.q = it.q;
+        s.out = it.out;
+        s.qpos = it.pass->d_pos;
+        s.k = cache->k[layer * cache->n_batch + b];
+        s.vt = cache->vt[layer * cache->n_batch + b];
+        s.nq = (int)it.pass->n;
+        s.nk = (int)cache->n_total;
+        max_nq = std::max(max_nq, s.nq);
+    }
+    if (max_nq == 0) return DR_OK;
+    DR_CHECK(use_device(ctx));
+    const bool masked = sliding_window.present || causal_prefix.present;
+    return launch_planned(ctx, a, (int)hd, max_nq, (int)cache->n_total, masked,
+                          q_norm_w != nullptr);
+}
+
+int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const float* k,
+                 size_t k_len, const float* v, size_t v_len, dr_attn_shape s, dr_rows qr,
+                 dr_rows kr) {
+    // Contract of attention.rs:106-109 (debug_asserts) plus the slice bounds
+    // the row kernels index (:143-152).
+    const size_t nq = s.nq, nk = s.nk, h = s.n_head, hkv = s.n_head_kv, hd = s.head_dim;
+    if (out_len != nq * h * hd)
+        return fail(DR_ERR_INVALID, "out.len() %zu != nq*n_head*head_dim %zu", out_len, nq * h * hd);
+    if (qr.pos_len != nq) return fail(DR_ERR_INVALID, "qr.pos.len() %zu != nq %zu", qr.pos_len, nq);
+    if (kr.pos_len != nk) return fail(DR_ERR_INVALID, "kr.pos.len() %zu != nk %zu", kr.pos_len, nk);
+    if (nq == 0 || h == 0 || hd == 0) return DR_OK;  // no (head, query) task writes anything
+    if (hkv == 0 || h % hkv != 0)
+        return fail(DR_ERR_INVALID, "n_head %zu is not a multiple of n_head_kv %zu", h, hkv);
+    if (hd > 256) return fail(DR_ERR_UNSUPPORTED, "head_dim %zu > 256 not built", hd);
+    if (!out || !q) return fail(DR_ERR_INVALID, "out/q is NULL");
+    if (q_len < nq * h * hd) return fail(DR_ERR_INVALID, "q.len() %zu < %zu", q_len, nq * h * hd);
+    if (nk > 0) {
+        if (!k || !v) return fail(DR_ERR_INVALID, "k/v is NULL");
+        if (k_len < nk * hkv * hd) return fail(DR_ERR_INVALID, "k.len() %zu < %zu", k_len, nk * hkv * hd);
+        if (v_len < nk * hkv * hd) return fail(DR_ERR_INVALID, "v.len() %zu < %zu", v_len, nk * hkv * hd);
+    }
+    if ((qr.pos_len && !qr.pos) || (kr.pos_len && !kr.pos) || (qr.seq_len && !qr.seq) ||
+        (kr.seq_len && !kr.seq) || (qr.prefix_len && !qr.prefix))
+        return fail(DR_ERR_INVALID, "row metadata pointer is NULL with nonzero length");
+    if (qr.prefix_len != 0 && qr.prefix_len < nq)
+        return fail(DR_ERR_INVALID, "qr.prefix.len() %zu < nq %zu", qr.prefix_len, nq);
+
+    // Row metadata as int32 (positions and ids must fit).
+    const bool masked = s.sliding_window.present || s.causal_prefix.present || qr.prefix_len > 0 ||
+                        qr.seq_len > 0 || kr.seq_len > 0;
+    bool kident = true;
+    for (size_t j = 0; j < nk; ++j) {
+        if (kr.pos[j] >= MAX_POS) return fail(DR_ERR_INVALID, "kr.pos[%zu] too large", j);
+        kident = kident && kr.pos[j] == j;
+    }
+    for (size_t i = 0; i < nq; ++i)
+        if (qr.pos[i] >= MAX_POS) return fail(DR_ERR_INVALID, "qr.pos[%zu] too large", i);
+    auto seq_ok = [](const dr_rows& r) {
+        for (size_t i = 0; i < r.seq_len; ++i)
+            if (r.seq[i] >= MAX_POS) return false;
+        return true;
+    };
+    if (!seq_ok(qr) || !seq_ok(kr)) return fail(DR_ERR_INVALID, "sequence id too large");
+    // Layout of the int32 metadata block: qpos | qseq | qprefix | kpos | kseq
+    const bool has_qseq = qr.seq_len > 0, has_kseq = kr.seq_len > 0;
+    const bool has_qpref = qr.prefix_len > 0, has_kpos = masked && !kident;
+    std::vector<int32_t> meta;
+    meta.reserve(3 * nq + 2 * nk);
+    size_t off_qpos = meta.size();
+    for (size_t i = 0; i < nq; ++i) meta.push_back((int32_t)qr.pos[i]);
+    size_t off_qseq = meta.size();
+    if (has_qseq)
+        for (size_t i = 0; i < nq; ++i) meta.push_back(i < qr.seq_len ? (int32_t)qr.seq[i] : 0);
+    size_t off_qpref = meta.size();
+    if (has_qpref)
+        for (size_t i = 0; i < nq; ++i)
+            meta.push_back((int32_t)std::min(qr.prefix[i], MAX_POS));
+    size_t off_kpos = meta.size();
+    if (has_kpos)
+        for (size_t j = 0; j < nk; ++j) meta.push_back((int32_t)kr.pos[j]);
+    size_t off_kseq = meta.size();
+    if (has_kseq)
+        for (size_t j = 0; j < nk; ++j) meta.push_back(j < kr.seq_len ? (int32_t)kr.seq[j] : 0);
+
+    std::lock_guard<std::mutex> lock(g_default_mu);
+    if (!g_default_ctx) DR_CHECK(dr_ctx_create(0, &g_default_ctx));
+    dr_ctx* ctx = g_default_ctx;
+    DR_CHECK(use_device(ctx));
+
+    if (nk == 0) {  // every row sees no key: 0 * (1/0) = NaN (attention.rs:181-185)
+        std::fill(out, out + out_len, std::numeric_limits<float>::quiet_NaN());
+        return DR_OK;
+    }
+
+    const int tile = hd_tile_for(hd);
+    const size_t cap = round_up(nk, dr::KEY_ALIGN);
+    const size_t qb = nq * h * hd * sizeof(float), kvb = nk * hkv * hd * sizeof(float);
+    const size_t cb = hkv * cap * tile * sizeof(uint16_t);
+    DR_CHECK(ensure(ctx->q, qb));
+    DR_CHECK(ensure(ctx->k, kvb));
+    DR_CHECK(ensure(ctx->v, kvb));
+    DR_CHECK(ensure(ctx->kc, cb));
+    DR_CHECK(ensure(ctx->vtc, cb));
+    DR_CHECK(ensure(ctx->out, qb));
+    DR_CHECK(ensure(ctx->meta, std::max(meta.size(), (size_t)1) * sizeof(int32_t)));
+    hipStream_t st = ctx->stream;
+    DR_HIP(hipMemcpyAsync(ctx->q.p, q, qb, hipMemcpyHostToDevice, st));
+    DR_HIP(hipMemcpyAsync(ctx->k.p, k, kvb, hipMemcpyHostToDevice, st));
+    DR_HIP(hipMemcpyAsync(ctx->v.p, v, kvb, hipMemcpyHostToDevice, st));
+    DR_HIP(hipMemcpyAsync(ctx->meta.p, meta.data(), meta.size() * sizeof(int32_t),
+                          hipMemcpyHostToDevice, st));
+    DR_HIP(hipMemsetAsync(ctx->kc.p, 0, cb, st));
+    DR_HIP(hipMemsetAsync(ctx->vtc.p, 0, cb, st));
+
+    // Pack K/V into the cache layout (key j at row j).
+    dr::StoreArgs sa{};
+    sa.k = static_cast<const float*>(ctx->k.p);
+    sa.v = static_cast<const float*>(ctx->v.p);
+    sa.pos = nullptr;
+    sa.n = (int)nk;
+    sa.n_head_kv = (int)hkv;
+    sa.hd = (int)hd;
+    sa.cap = (int)cap;
+    sa.kc = static_cast<uint16_t*>(ctx->kc.p);
+    sa.vtc = static_cast<uint16_t*>(ctx->vtc.p);
+    hipError_t e = dr::launch_store(tile, sa, st);
+    if (e != hipSuccess) return hip_fail(e, "pack launch");
+
+    const int32_t* m = static_cast<const int32_t*>(ctx->meta.p);
+    dr::AttnArgs a{};
+    a.n_batch = 1;
+    a.n_head = (int)h;
+    a.n_head_kv = (int)hkv;
+    a.group = (int)(h / hkv);
+    a.hd = (int)hd;
+    a.cap = (int)cap;
+    a.q_rstride = a.o_rstride = (int)(h * hd);
+    a.c = scale_log2(s.scale);
+    a.window = opt_to_int(s.sliding_window);
+    a.prefix = opt_to_int(s.causal_prefix);
+    dr::AttnSlot& sl = a.slot[0];
+    sl.q = ctx->q.p;
+    sl.out = static_cast<float*>(ctx->out.p);
+    sl.qpos = m + off_qpos;
+    sl.qseq = has_qseq ? m + off_qseq : nullptr;
+    sl.qprefix = has_qpref ? m + off_qpref : nullptr;
+    sl.k = static_cast<const uint16_t*>(ctx->kc.p);
+    sl.vt = static_cast<const uint16_t*>(ctx->vtc.p);
+    sl.kpos = has_kpos ? m + off_kpos : nullptr;
+    sl.kseq = has_kseq ? m + off_kseq : nullptr;
+    sl.nq = (int)nq;
+    sl.nk = (int)nk;
+    DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, masked, false));
+    DR_HIP(hipMemcpyAsync(out, ctx->out.p, qb, hipMemcpyDeviceToHost, st));
+    DR_HIP(hipStreamSynchronize(st));
+    return DR_OK;
+}
+
+}  // extern "C"

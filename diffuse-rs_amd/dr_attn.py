@@ -1,0 +1,400 @@
+"""ctypes binding of include/dr_attn.h (lib/libdr_attn.so).
+
+Python mirror of the reference's attention interface for the tests and the
+bench: ``AttnShape``/``Rows``/``attention()`` follow
+``src/model/attention.rs:10-27, 65-70, 106`` (same names, same argument
+meaning; a failed call raises ``DrError`` where the reference panics), and
+``StepCache``/``Pass`` wrap the device-resident KV cache (``cache.rs:25-115``)
+and per-pass row metadata (``PassRows``, ``attention.rs:79-85``).
+
+The library is the only compute path: if it is missing ``load()`` raises, and
+on a host without a GPU every compute call raises ``DrError`` with
+``DR_ERR_NO_DEVICE``.  Nothing here computes attention on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import re
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "lib" / "libdr_attn.so"
+HEADER_PATH = HERE.parent / "include" / "dr_attn.h"
+
+DR_OK, DR_ERR_INVALID, DR_ERR_NO_DEVICE, DR_ERR_OOM, DR_ERR_HIP, DR_ERR_UNSUPPORTED = range(6)
+STATUS_NAMES = {
+    DR_OK: "DR_OK",
+    DR_ERR_INVALID: "DR_ERR_INVALID",
+    DR_ERR_NO_DEVICE: "DR_ERR_NO_DEVICE",
+    DR_ERR_OOM: "DR_ERR_OOM",
+    DR_ERR_HIP: "DR_ERR_HIP",
+    DR_ERR_UNSUPPORTED: "DR_ERR_UNSUPPORTED",
+}
+
+c_size_p = ctypes.POINTER(ctypes.c_size_t)
+
+
+class OptUsize(ctypes.Structure):
+    _fields_ = [("value", ctypes.c_size_t), ("present", ctypes.c_uint8)]
+
+
+class CAttnShape(ctypes.Structure):
+    _fields_ = [
+        ("nq", ctypes.c_size_t),
+        ("nk", ctypes.c_size_t),
+        ("n_head", ctypes.c_size_t),
+        ("n_head_kv", ctypes.c_size_t),
+        ("head_dim", ctypes.c_size_t),
+        ("sliding_window", OptUsize),
+        ("causal_prefix", OptUsize),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class CRows(ctypes.Structure):
+    _fields_ = [
+        ("pos", c_size_p),
+        ("pos_len", ctypes.c_size_t),
+        ("seq", c_size_p),
+        ("seq_len", ctypes.c_size_t),
+        ("prefix", c_size_p),
+        ("prefix_len", ctypes.c_size_t),
+    ]
+
+
+class CBatchItem(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("out", ctypes.c_void_p), ("pass_", ctypes.c_void_p)]
+
+
+class CLaunchInfo(ctypes.Structure):
+    _fields_ = [
+        ("n_split", ctypes.c_int),
+        ("n_workgroups", ctypes.c_int),
+        ("waves_per_wg", ctypes.c_int),
+        ("block_n", ctypes.c_int),
+        ("head_dim_tile", ctypes.c_int),
+    ]
+
+
+class DrError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+        self.message = message
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+_VP = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SIGS = {
+    "dr_last_error": (ctypes.c_char_p, []),
+    "dr_version": (ctypes.c_char_p, []),
+    "dr_device_count": (_I, []),
+    "dr_attention": (_I, [_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, CAttnShape, CRows, CRows]),
+    "dr_ctx_create": (_I, [_I, ctypes.POINTER(_VP)]),
+    "dr_ctx_set_stream": (_I, [_VP, _VP]),
+    "dr_ctx_stream": (_VP, [_VP]),
+    "dr_ctx_synchronize": (_I, [_VP]),
+    "dr_ctx_destroy": (None, [_VP]),
+    "dr_ctx_last_launch": (_I, [_VP, ctypes.POINTER(CLaunchInfo)]),
+    "dr_ctx_set_split": (_I, [_VP, _I]),
+    "dr_pass_create": (_I, [_VP, c_size_p, _SZ, ctypes.POINTER(_VP)]),
+    "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
+    "dr_pass_len": (_SZ, [_VP]),
+    "dr_pass_destroy": (None, [_VP]),
+    "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
+    "dr_cache_destroy": (None, [_VP]),
+    "dr_cache_store": (_I, [_VP, _SZ, _SZ, _VP, _VP, _VP, _VP, _F]),
+    "dr_cache_gather": (_I, [_VP, _SZ, _SZ, c_size_p, _SZ, _VP, _VP]),
+    "dr_cache_update_seq": (_I, [_VP, _SZ, _VP, _SZ]),
+    "dr_cache_split_active": (_I, [_VP, _SZ, _VP, _VP, _SZ, _SZ, c_size_p, c_size_p, c_size_p, c_size_p]),
+    "dr_split_active": (_I, [_VP, _VP, _VP, _VP, _SZ, _SZ, _SZ, c_size_p, c_size_p, c_size_p, c_size_p]),
+    "dr_cache_set_vicinity": (_I, [_VP, _SZ, _SZ]),
+    "dr_cache_initialized": (_I, [_VP, _SZ]),
+    "dr_attention_cached": (_I, [_VP, _SZ, ctypes.POINTER(CBatchItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F]),
+}
+
+
+def header_functions(path: pathlib.Path = HEADER_PATH) -> list:
+    """Names of every function declared in include/dr_attn.h."""
+    text = path.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dr_[a-z0-9_]+)\s*\(", text)))
+
+
+def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    """Load the HIP library.  Raises if it has not been built: there is no
+    fallback implementation."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = pathlib.Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} not built (run `python -c 'import __graft_entry__ as g; g.build()'`)")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != DR_OK:
+        raise DrError(rc, load().dr_last_error().decode())
+
+
+def device_count() -> int:
+    return load().dr_device_count()
+
+
+def _opt(v: Optional[int]) -> OptUsize:
+    return OptUsize(0, 0) if v is None else OptUsize(int(v), 1)
+
+
+def _usize_array(xs) -> tuple:
+    a = np.ascontiguousarray(np.asarray(xs, dtype=np.uint64).reshape(-1)).astype(np.uintp, copy=False)
+    return a, (a.ctypes.data_as(c_size_p) if a.size else None), a.size
+
+
+# --------------------------------------------------------------------------
+# attention(): reference-shaped drop-in
+
+
+@dataclass
+class AttnShape:
+    """AttnShape (attention.rs:10-27)."""
+
+    nq: int
+    nk: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    sliding_window: Optional[int] = None
+    causal_prefix: Optional[int] = None
+    scale: float = 1.0
+
+    def c(self) -> CAttnShape:
+        return CAttnShape(self.nq, self.nk, self.n_head, self.n_head_kv, self.head_dim,
+                          _opt(self.sliding_window), _opt(self.causal_prefix), self.scale)
+
+
+@dataclass
+class Rows:
+    """Rows (attention.rs:65-70): per-row sequence position, optional
+    sequence id (empty = all 0) and optional per-row causal prefix (empty =
+    the shape's causal_prefix)."""
+
+    pos: Sequence[int]
+    seq: Sequence[int] = field(default_factory=tuple)
+    prefix: Sequence[int] = field(default_factory=tuple)
+
+    def c(self, keep: list) -> CRows:
+        parts = []
+        for xs in (self.pos, self.seq, self.prefix):
+            arr, ptr, n = _usize_array(xs)
+            keep.append(arr)
+            parts += [ptr, n]
+        return CRows(*parts)
+
+
+def idpos(n: int) -> Rows:
+    """Single-sequence rows at positions 0..n (tests.rs:4-11)."""
+    return Rows(pos=range(n))
+
+
+def attention(out: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray, s: AttnShape,
+              qr: Rows, kr: Rows) -> None:
+    """Drop-in for ``attention(out, q, k, v, s, qr, kr)`` (attention.rs:106):
+    float32 numpy arrays, ``out`` overwritten in place."""
+    lib = load()
+    for name, a in (("out", out), ("q", q), ("k", k), ("v", v)):
+        if a.dtype != np.float32 or not a.flags.c_contiguous:
+            raise TypeError(f"{name} must be a C-contiguous float32 array")
+    keep: list = []
+    rc = lib.dr_attention(out.ctypes.data, out.size, q.ctypes.data, q.size, k.ctypes.data,
+                          k.size, v.ctypes.data, v.size, s.c(), qr.c(keep), kr.c(keep))
+    _check(rc)
+
+
+def split_active(prev_seq: np.ndarray, last_changed: np.ndarray, seq, is_masked, step: int,
+                 vicinity: int = 0) -> tuple:
+    """Stateless StepCache::split_active (cache.rs:85-114).  ``last_changed``
+    (int32) is updated in place.  Returns (active, cached) position lists."""
+    lib = load()
+    n = len(seq)
+    seq_a = np.ascontiguousarray(seq, dtype=np.int32)
+    m_a = np.ascontiguousarray(is_masked, dtype=np.uint8)
+    prev = np.ascontiguousarray(prev_seq, dtype=np.int32)
+    assert last_changed.dtype == np.int32 and last_changed.flags.c_contiguous
+    act = np.zeros(max(n, 1), dtype=np.uintp)
+    cac = np.zeros(max(n, 1), dtype=np.uintp)
+    na, nc = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(lib.dr_split_active(prev.ctypes.data, last_changed.ctypes.data, seq_a.ctypes.data,
+                               m_a.ctypes.data, n, step, vicinity, act.ctypes.data_as(c_size_p),
+                               ctypes.byref(na), cac.ctypes.data_as(c_size_p), ctypes.byref(nc)))
+    return [int(x) for x in act[: na.value]], [int(x) for x in cac[: nc.value]]
+
+
+# --------------------------------------------------------------------------
+# device-resident path
+
+
+class Context:
+    """dr_ctx: one device and one HIP stream."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load()
+        h = ctypes.c_void_p()
+        _check(self.lib.dr_ctx_create(device, ctypes.byref(h)))
+        self.h = h
+
+    def set_stream(self, stream_ptr: int) -> None:
+        _check(self.lib.dr_ctx_set_stream(self.h, ctypes.c_void_p(stream_ptr)))
+
+    @property
+    def stream(self) -> int:
+        return self.lib.dr_ctx_stream(self.h) or 0
+
+    def synchronize(self) -> None:
+        _check(self.lib.dr_ctx_synchronize(self.h))
+
+    def set_split(self, n_split: int) -> None:
+        _check(self.lib.dr_ctx_set_split(self.h, n_split))
+
+    def last_launch(self) -> dict:
+        info = CLaunchInfo()
+        _check(self.lib.dr_ctx_last_launch(self.h, ctypes.byref(info)))
+        return {f: getattr(info, f) for f, _ in CLaunchInfo._fields_}
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.dr_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Pass:
+    """dr_pass: a forward pass's active positions, resident on the device."""
+
+    def __init__(self, ctx: Context, active: Sequence[int]):
+        self.ctx = ctx
+        arr, ptr, n = _usize_array(active)
+        h = ctypes.c_void_p()
+        _check(ctx.lib.dr_pass_create(ctx.h, ptr, n, ctypes.byref(h)))
+        self.h = h
+
+    def set(self, active: Sequence[int]) -> None:
+        arr, ptr, n = _usize_array(active)
+        _check(self.ctx.lib.dr_pass_set(self.h, ptr, n))
+
+    def __len__(self) -> int:
+        return self.ctx.lib.dr_pass_len(self.h)
+
+    def close(self) -> None:
+        if self.h:
+            self.ctx.lib.dr_pass_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _ptr(t) -> int:
+    """Device pointer of a torch tensor (or an int) -- torch is only used as
+    device-memory plumbing."""
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+class StepCache:
+    """dr_step_cache: per-layer bf16 K/V for every position, in HBM."""
+
+    def __init__(self, ctx: Context, n_total: int, n_head_kv: Sequence[int],
+                 head_dim: Sequence[int], n_batch: int = 1):
+        self.ctx = ctx
+        hkv, hkv_p, n_layer = _usize_array(n_head_kv)
+        hd, hd_p, n2 = _usize_array(head_dim)
+        assert n2 == n_layer
+        h = ctypes.c_void_p()
+        _check(ctx.lib.dr_cache_create(ctx.h, n_total, n_layer, hkv_p, hd_p, n_batch,
+                                       ctypes.byref(h)))
+        self.h = h
+        self.n_total = n_total
+        self.n_batch = n_batch
+
+    def store(self, layer: int, p: Pass, k, v, k_norm_w=None, eps: float = 1e-6, batch: int = 0):
+        _check(self.ctx.lib.dr_cache_store(self.h, layer, batch, p.h, _ptr(k), _ptr(v),
+                                           _ptr(k_norm_w) or None, eps))
+
+    def gather(self, layer: int, positions: Sequence[int], out_k, out_v, batch: int = 0):
+        arr, ptr, n = _usize_array(positions)
+        _check(self.ctx.lib.dr_cache_gather(self.h, layer, batch, ptr, n, _ptr(out_k),
+                                            _ptr(out_v)))
+
+    def update_seq(self, seq, batch: int = 0) -> None:
+        a = np.ascontiguousarray(seq, dtype=np.int32)
+        _check(self.ctx.lib.dr_cache_update_seq(self.h, batch, a.ctypes.data, a.size))
+
+    def split_active(self, seq, is_masked, step: int, batch: int = 0) -> tuple:
+        n = len(seq)
+        seq_a = np.ascontiguousarray(seq, dtype=np.int32)
+        m_a = np.ascontiguousarray(is_masked, dtype=np.uint8)
+        act = np.zeros(max(n, 1), dtype=np.uintp)
+        cac = np.zeros(max(n, 1), dtype=np.uintp)
+        na, nc = ctypes.c_size_t(), ctypes.c_size_t()
+        _check(self.ctx.lib.dr_cache_split_active(
+            self.h, batch, seq_a.ctypes.data, m_a.ctypes.data, n, step,
+            act.ctypes.data_as(c_size_p), ctypes.byref(na), cac.ctypes.data_as(c_size_p),
+            ctypes.byref(nc)))
+        return [int(x) for x in act[: na.value]], [int(x) for x in cac[: nc.value]]
+
+    def set_vicinity(self, vicinity: int, batch: int = 0) -> None:
+        _check(self.ctx.lib.dr_cache_set_vicinity(self.h, batch, vicinity))
+
+    def initialized(self, batch: int = 0) -> bool:
+        return bool(self.ctx.lib.dr_cache_initialized(self.h, batch))
+
+    def attention(self, layer: int, items: Sequence[tuple], n_head: int,
+                  sliding_window: Optional[int] = None, causal_prefix: Optional[int] = None,
+                  scale: float = 1.0, q_norm_w=None, q_norm_eps: float = 1e-6) -> None:
+        """items: sequence of (q, out, Pass) per batch slot (device tensors)."""
+        arr = (CBatchItem * len(items))()
+        for i, (q, out, p) in enumerate(items):
+            arr[i] = CBatchItem(_ptr(q), _ptr(out), p.h)
+        _check(self.ctx.lib.dr_attention_cached(
+            self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
+            scale, _ptr(q_norm_w) or None, q_norm_eps))
+
+    def close(self) -> None:
+        if self.h:
+            self.ctx.lib.dr_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,217 @@
+/*
+ * dr_attn.h -- C ABI of the MI355X (gfx950) denoise-step attention library.
+ *
+ * This is the drop-in boundary for diffuse-rs's per-denoise-step attention
+ * (agalimova/diffuse-rs v0.4.0).  Each entry point names the reference
+ * interface it replaces.  Plain pointers and sizes only: Rust binds
+ * `usize` as `size_t`, `Option<usize>` as `dr_opt_usize`, and an empty slice
+ * as (NULL, 0).
+ *
+ * Status codes: every fallible entry point returns DR_OK (0) or a nonzero
+ * dr_status; dr_last_error() gives a message for the calling thread.  The
+ * reference's attention() is infallible and panics on bad input; a Rust shim
+ * maps a nonzero status to panic!().
+ *
+ * Threading: a dr_ctx owns one HIP stream and is not thread-safe (mirrors the
+ * reference's single-threaded `&mut Model` discipline, server.rs:350-351).
+ * dr_attention() uses one process-wide context, serialised internally.
+ */
+#ifndef DR_ATTN_H
+#define DR_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    DR_OK = 0,
+    DR_ERR_INVALID = 1,     /* bad shape, length or argument */
+    DR_ERR_NO_DEVICE = 2,   /* no HIP device visible */
+    DR_ERR_OOM = 3,         /* device allocation failed */
+    DR_ERR_HIP = 4,         /* a HIP runtime call failed */
+    DR_ERR_UNSUPPORTED = 5  /* valid for the reference, not built here (e.g. head_dim > 256) */
+} dr_status;
+
+/* Option<usize>: present == 0 means None. */
+typedef struct {
+    size_t value;
+    uint8_t present;
+} dr_opt_usize;
+
+/* AttnShape -- src/model/attention.rs:10-27. */
+typedef struct {
+    size_t nq;
+    size_t nk;
+    size_t n_head;
+    size_t n_head_kv;
+    size_t head_dim;
+    dr_opt_usize sliding_window; /* key visible iff |qpos - kpos| < window */
+    dr_opt_usize causal_prefix;  /* queries with qpos < prefix see kpos <= qpos */
+    float scale;
+} dr_attn_shape;
+
+/* Rows -- src/model/attention.rs:65-70.  pos has one entry per row; seq and
+ * prefix may be empty ((NULL, 0)): empty seq = every row in sequence 0
+ * (:74-76), empty prefix = the shape's causal_prefix (:151). */
+typedef struct {
+    const size_t* pos;
+    size_t pos_len;
+    const size_t* seq;
+    size_t seq_len;
+    const size_t* prefix;
+    size_t prefix_len;
+} dr_rows;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* dr_last_error(void);
+
+/* Library and ABI version, "MAJOR.MINOR.PATCH". */
+const char* dr_version(void);
+
+/* Number of visible HIP devices (0 on a host without a GPU; never fails). */
+int dr_device_count(void);
+
+/*
+ * Literal drop-in for
+ *   pub(crate) fn attention(out: &mut [f32], q: &[f32], k: &[f32], v: &[f32],
+ *                           s: AttnShape, qr: Rows, kr: Rows)
+ * at src/model/attention.rs:106 (caller: src/model/forward.rs:343).
+ *
+ * Host pointers, synchronous: uploads q/k/v and row metadata, runs the fused
+ * bf16-MFMA kernel on device 0, downloads out.  Layouts as the reference:
+ * q [nq][n_head][head_dim], k and v [nk][n_head_kv][head_dim], out
+ * [nq][n_head * head_dim], all f32 row-major; out is fully overwritten.
+ * Lengths are checked as the reference's debug_asserts (:107-109) and
+ * slicing would; a query that sees no key yields NaN, as the reference's
+ * 0 * (1/0) does (:181-185).
+ */
+int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const float* k,
+                 size_t k_len, const float* v, size_t v_len, dr_attn_shape s, dr_rows qr,
+                 dr_rows kr);
+
+/* ------------------------------------------------------------------------- *
+ * Device-resident path: a context (device + stream), the inter-step KV cache
+ * kept in HBM as bf16, per-pass row metadata, and attention that reads the
+ * cache directly.  All float* below are DEVICE pointers (hipMalloc'd or torch
+ * tensors); work is enqueued on the context's stream and is asynchronous
+ * unless stated otherwise.
+ * ------------------------------------------------------------------------- */
+
+typedef struct dr_ctx dr_ctx;
+
+/* Create a context on `device` with its own (default-priority) stream. */
+int dr_ctx_create(int device, dr_ctx** out);
+/* Use the caller's hipStream_t (cast to void*) instead of the context's own. */
+int dr_ctx_set_stream(dr_ctx* ctx, void* stream);
+/* The hipStream_t the context enqueues on. */
+void* dr_ctx_stream(dr_ctx* ctx);
+int dr_ctx_synchronize(dr_ctx* ctx);
+void dr_ctx_destroy(dr_ctx* ctx);
+
+/*
+ * PassRows -- src/model/attention.rs:79-85, built once per forward pass in
+ * src/model/forward.rs:87-101: the active (recomputed) sequence positions,
+ * ascending, copied to the device once and reused by every layer's
+ * dr_cache_store and dr_attention_cached.  Queries are the active rows.
+ */
+typedef struct dr_pass dr_pass;
+int dr_pass_create(dr_ctx* ctx, const size_t* active, size_t n_active, dr_pass** out);
+/* Replace the positions (e.g. for the next denoise step); synchronous upload. */
+int dr_pass_set(dr_pass* pass, const size_t* active, size_t n_active);
+size_t dr_pass_len(const dr_pass* pass);
+void dr_pass_destroy(dr_pass* pass);
+
+/*
+ * StepCache -- src/model/cache.rs:25-115.  Per layer, per batch slot, K and V
+ * for every sequence position 0..n_total, stored as bf16 in HBM (K row-major
+ * per KV head, V transposed per KV head).  StepCache::new (:44-54) takes
+ * per-layer strides n_head_kv * head_dim (forward.rs:267); here the two
+ * factors are given separately.  n_batch > 1 holds several independent
+ * streams (e.g. the conditional and unconditional CFG streams, each of which
+ * has its own StepCache in sampler.rs:432-434) so one launch serves both.
+ * Storage is zero-initialised.  vicinity starts at 0 (cache.rs:40).
+ */
+typedef struct dr_step_cache dr_step_cache;
+int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n_head_kv,
+                    const size_t* head_dim, size_t n_batch, dr_step_cache** out);
+void dr_cache_destroy(dr_step_cache* cache);
+
+/* StepCache::store (cache.rs:62-71) for the pass's active positions: row r of
+ * k/v ([n_active][n_head_kv][head_dim] f32, device) goes to position
+ * active[r].  If k_norm_w (device, head_dim f32) is non-NULL each K head is
+ * first RMS-normalised with that gain and eps (norm_heads, ops.rs:384-389, as
+ * forward.rs:300-302 does before the store). */
+int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
+                   const float* k, const float* v, const float* k_norm_w, float eps);
+
+/* StepCache::gather (cache.rs:73-82): rows at `positions` (host array) into
+ * out_k/out_v (device, f32, [n][n_head_kv][head_dim]).  Values are the bf16
+ * cache contents widened to f32. */
+int dr_cache_gather(dr_step_cache* cache, size_t layer, size_t batch, const size_t* positions,
+                    size_t n, float* out_k, float* out_v);
+
+/* StepCache::update_seq (cache.rs:56-59) for one batch slot (host data). */
+int dr_cache_update_seq(dr_step_cache* cache, size_t batch, const int32_t* seq, size_t n);
+/* StepCache::split_active (cache.rs:85-114) for one batch slot.  active and
+ * cached must each have room for n entries; both come back ascending. */
+int dr_cache_split_active(dr_step_cache* cache, size_t batch, const int32_t* seq,
+                          const uint8_t* is_masked, size_t n, size_t step, size_t* active,
+                          size_t* n_active, size_t* cached, size_t* n_cached);
+/* The same split on caller-owned state, with no device involved: prev_seq and
+ * last_changed are StepCache's arrays (cache.rs:29-31, initially all -1),
+ * length n; last_changed is updated in place. */
+int dr_split_active(const int32_t* prev_seq, int32_t* last_changed, const int32_t* seq,
+                    const uint8_t* is_masked, size_t n, size_t step, size_t vicinity,
+                    size_t* active, size_t* n_active, size_t* cached, size_t* n_cached);
+/* StepCache.vicinity (cache.rs:37-41). */
+int dr_cache_set_vicinity(dr_step_cache* cache, size_t batch, size_t vicinity);
+/* StepCache.initialized (cache.rs:33). */
+int dr_cache_initialized(const dr_step_cache* cache, size_t batch);
+
+/* One batch slot of a cached attention call. */
+typedef struct {
+    const float* q; /* device, [n_active][n_head][head_dim] f32 */
+    float* out;     /* device, [n_active][n_head * head_dim] f32, overwritten */
+    const dr_pass* pass;
+} dr_batch_item;
+
+/*
+ * Cached attention: the attention() call of attention_block
+ * (src/model/forward.rs:312-343) with the gather/concatenate of
+ * :312-317 removed.  Item b's queries (its pass's active positions) attend
+ * to cache slot b's keys at every position 0..n_total; call dr_cache_store
+ * for the active rows first, as forward.rs:318-320 does.  The reference's
+ * key order [cached | active] and this one differ only in summation order:
+ * masking is by position (attention.rs:29-35).  sliding_window,
+ * causal_prefix and scale are AttnShape's (forward.rs:327-342).  If q_norm_w
+ * (device, head_dim f32) is non-NULL each query head is RMS-normalised with
+ * it first (forward.rs:297-299).  n_items <= the cache's n_batch and <= 8.
+ */
+int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
+                        size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                        dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                        float q_norm_eps);
+
+/* Launch configuration of the last attention kernel this context enqueued
+ * (for measurement): number of key splits, workgroups and waves per
+ * workgroup, key tile size. */
+typedef struct {
+    int n_split;
+    int n_workgroups;
+    int waves_per_wg;
+    int block_n;
+    int head_dim_tile;
+} dr_launch_info;
+int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
+
+/* Override the key-split heuristic for later calls on ctx (0 = automatic). */
+int dr_ctx_set_split(dr_ctx* ctx, int n_split);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DR_ATTN_H */

@@ -1,0 +1,212 @@
+"""Shared test helpers: input generators, a float64 brute-force attention and
+the benchmark configurations.
+
+The brute force is deliberately a different algorithm from the reference's
+online softmax (attention.rs:289-331): it materialises the full visibility
+matrix and score matrix in float64 and normalises in three passes, like the
+reference's own test oracle ``softmax_row_scalar`` (ops.rs:267-280) used by
+``test_attention_matches_naive_reference`` (tests.rs:154-186).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+
+@dataclass
+class Shape:
+    """Same fields as AttnShape (attention.rs:10-27)."""
+
+    nq: int
+    nk: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    sliding_window: Optional[int] = None
+    causal_prefix: Optional[int] = None
+    scale: float = 1.0
+
+
+@dataclass
+class RowsSpec:
+    pos: Sequence[int]
+    seq: Sequence[int] = ()
+    prefix: Sequence[int] = ()
+
+
+def closed_form(n: int, mul: int, mod: int, off: float, div: float) -> np.ndarray:
+    """((x*mul % mod) - off) / div for x in 0..n -- the input family of the
+    reference's attention tests (tests.rs:80-82, 108-110, 124-128, 159-161)."""
+    x = np.arange(n, dtype=np.int64)
+    return (((x * mul) % mod).astype(np.float32) - np.float32(off)) / np.float32(div)
+
+
+def visibility(s: Shape, qr: RowsSpec, kr: RowsSpec) -> np.ndarray:
+    """[nq, nk] bool: the key/query visibility rules stated in the
+    reference's AttnShape and Rows docs (attention.rs:17-24, 29-35, 59-64)."""
+    qpos = np.asarray(qr.pos, dtype=np.int64)[:, None]
+    kpos = np.asarray(kr.pos, dtype=np.int64)[None, :]
+
+    def ids(r, n):
+        a = np.zeros(n, dtype=np.int64)
+        if len(r.seq):
+            m = min(n, len(r.seq))
+            a[:m] = np.asarray(r.seq, dtype=np.int64)[:m]
+        return a
+
+    vis = ids(qr, s.nq)[:, None] == ids(kr, s.nk)[None, :]
+    if s.sliding_window is not None:
+        vis &= np.abs(qpos - kpos) < s.sliding_window
+    if len(qr.prefix):
+        pref = np.asarray(qr.prefix, dtype=np.int64)[:, None]
+    elif s.causal_prefix is not None:
+        pref = np.full((s.nq, 1), s.causal_prefix, dtype=np.int64)
+    else:
+        pref = None
+    if pref is not None:
+        prompt_row = qpos < pref
+        vis &= ~prompt_row | (kpos <= qpos)
+    return vis
+
+
+def brute_force(q, k, v, s: Shape, qr: RowsSpec, kr: RowsSpec) -> np.ndarray:
+    """float64 three-pass attention.  Rows with no visible key are NaN."""
+    h, hkv, hd = s.n_head, s.n_head_kv, s.head_dim
+    Q = np.asarray(q, dtype=np.float64).reshape(s.nq, h, hd)
+    K = np.asarray(k, dtype=np.float64).reshape(s.nk, hkv, hd)
+    V = np.asarray(v, dtype=np.float64).reshape(s.nk, hkv, hd)
+    vis = visibility(s, qr, kr)
+    out = np.full((s.nq, h, hd), np.nan)
+    group = h // hkv
+    live = vis.any(axis=1)
+    for head in range(h):
+        g = head // group
+        sc = (Q[:, head] @ K[:, g].T) * float(np.float32(s.scale))
+        sc = np.where(vis, sc, -np.inf)
+        m = np.max(sc, axis=1, keepdims=True)
+        m = np.where(np.isfinite(m), m, 0.0)
+        p = np.where(vis, np.exp(sc - m), 0.0)
+        l = p.sum(axis=1)
+        o = (p @ V[:, g]) / np.where(l > 0, l, 1.0)[:, None]
+        out[live, head] = o[live]
+    return out.reshape(s.nq, h * hd)
+
+
+def make_input(spec: dict, n: int) -> np.ndarray:
+    """A golden-case input: explicit values or closed_form(n, *gen)."""
+    if "values" in spec:
+        a = np.asarray(spec["values"], dtype=np.float32)
+        assert a.size == n
+        return a
+    return closed_form(n, *spec["gen"])
+
+
+def materialise(c: dict):
+    """(shape, qrows, krows, q, k, v) of a case from tests/golden/cases.json."""
+    s = Shape(**c["shape"])
+    qr = RowsSpec(**c["qrows"])
+    kr = RowsSpec(**c["krows"])
+    q = make_input(c["q"], s.nq * s.n_head * s.head_dim)
+    k = make_input(c["k"], s.nk * s.n_head_kv * s.head_dim)
+    v = make_input(c["v"], s.nk * s.n_head_kv * s.head_dim)
+    return s, qr, kr, q, k, v
+
+
+def golden_cases() -> list:
+    """[(case dict, expected float64 [nq, h*hd])] from tests/golden/."""
+    import json
+    import pathlib
+
+    d = pathlib.Path(__file__).resolve().parent / "golden"
+    cases = json.loads((d / "cases.json").read_text())
+    exp = np.load(d / "expected.npz")
+    return [(c, exp[c["name"]]) for c in cases]
+
+
+def rms_norm_f64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Per-head RMSNorm in float64 over the last axis (ops.rs:106-114)."""
+    x64 = np.asarray(x, dtype=np.float64)
+    r = np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + eps)
+    return x64 / r * np.asarray(w, dtype=np.float64)
+
+
+def normal(rng: np.random.Generator, *shape) -> np.ndarray:
+    return rng.standard_normal(shape, dtype=np.float32)
+
+
+def err_stats(got: np.ndarray, want: np.ndarray) -> tuple:
+    """(max-abs, mean-abs) error over finite expected entries; NaN positions
+    must coincide."""
+    got = np.asarray(got, dtype=np.float64).reshape(-1)
+    want = np.asarray(want, dtype=np.float64).reshape(-1)
+    nan_w, nan_g = np.isnan(want), np.isnan(got)
+    assert np.array_equal(nan_w, nan_g), "NaN pattern differs"
+    d = np.abs(got[~nan_w] - want[~nan_w])
+    if d.size == 0:
+        return 0.0, 0.0
+    return float(d.max()), float(d.mean())
+
+
+# Tolerance of the bf16-MFMA path against the f32 reference (BASELINE.json
+# north_star): max-abs <= 1e-2 and mean-abs <= 1e-3.
+TOL_MAX = 1e-2
+TOL_MEAN = 1e-3
+
+
+@dataclass
+class Config:
+    """One BASELINE.json config as a cached denoise-step attention problem."""
+
+    name: str
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    n_prompt: int
+    n_canvas: int
+    batch: int = 1
+    window: Optional[int] = None
+    qk_norm: bool = False
+    scale: Optional[float] = None
+
+    @property
+    def n_total(self) -> int:
+        return self.n_prompt + self.n_canvas
+
+    @property
+    def attn_scale(self) -> float:
+        return self.scale if self.scale is not None else 1.0 / math.sqrt(self.head_dim)
+
+    def visible_keys(self) -> int:
+        """sum over canvas queries of |visible keys| (one head, one batch)."""
+        total = 0
+        for qp in range(self.n_prompt, self.n_total):
+            if self.window is None:
+                total += self.n_total
+            else:
+                lo = max(0, qp - self.window + 1)
+                hi = min(self.n_total, qp + self.window)
+                total += hi - lo
+        return total
+
+    def flops(self) -> float:
+        """4 * h * hd * sum_q |visible(q)| per batch slot (QK^T + PV)."""
+        return 4.0 * self.n_head * self.head_dim * self.visible_keys() * self.batch
+
+
+CONFIGS = {
+    # 64 prompt + 64 canvas, all 128 rows are queries (no cache)
+    "C1": Config("llada8b_128x128", 32, 32, 128, 0, 128),
+    # the headline denoise step
+    "C2": Config("llada8b_step_512c+256q", 32, 32, 128, 512, 256),
+    "C3": Config("dream7b_gqa_cfg_1024c+256q_b2", 28, 4, 128, 1024, 256, batch=2),
+    "C4": Config("lladamoe_qknorm_2048c+512q", 16, 16, 128, 2048, 512, qk_norm=True),
+    "C5S": Config("gemma_sliding_w1024_4096c+256q", 16, 8, 256, 4096, 256, window=1024),
+    "C5G": Config("gemma_global_4096c+256q", 16, 8, 256, 4096, 256),
+}
+
+
+def config_seed(cfg_id: int, step: int = 0) -> int:
+    return 0xD1FF0000 + cfg_id + 1000 * step

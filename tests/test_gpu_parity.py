@@ -1,0 +1,385 @@
+"""Parity of the HIP path (diffuse-rs_amd/lib/libdr_attn.so, through its C
+ABI) with the CPU oracle and the golden fixtures.  Needs an MI355X.
+
+Bar: max-abs <= 1e-2 and mean-abs <= 1e-3 against
+the f32 reference on identical inputs; NaN exactly where the reference
+produces NaN (a query with no visible key); bit-exact for the integer
+bookkeeping (cache positions, split lists) and for bf16-representable data
+moved through the cache.
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import dr_attn as dr
+import oracle as orc
+from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, RowsSpec, Shape, closed_form, config_seed,
+                     err_stats, golden_cases, materialise)
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    if dr.device_count() == 0 or not t.cuda.is_available():
+        pytest.skip("no GPU visible")
+    dr.load()  # raises if the library is not built: no fallback
+    return t
+
+
+class Dev:
+    """A dr context bound to a dedicated torch stream, so torch's copies and
+    the library's kernels are ordered."""
+
+    def __init__(self, torch):
+        self.t = torch
+        self.stream = torch.cuda.Stream()
+        self.ctx = dr.Context(0)
+        self.ctx.set_stream(self.stream.cuda_stream)
+
+    def put(self, a: np.ndarray):
+        with self.t.cuda.stream(self.stream):
+            return self.t.from_numpy(np.ascontiguousarray(a)).to("cuda", non_blocking=False)
+
+    def empty(self, n: int):
+        with self.t.cuda.stream(self.stream):
+            return self.t.full((n,), float("nan"), dtype=self.t.float32, device="cuda")
+
+    def get(self, x) -> np.ndarray:
+        self.stream.synchronize()
+        return x.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def dev(torch):
+    return Dev(torch)
+
+
+def oracle_run(s, qr, kr, q, k, v):
+    out = np.zeros(s.nq * s.n_head * s.head_dim, np.float32)
+    orc.attention(out, q, k, v, s, qr, kr, threads=0)
+    return out
+
+
+def check(got, want, label, tol_max=TOL_MAX, tol_mean=TOL_MEAN):
+    mx, mean = err_stats(got, want)
+    say(f"  {label}: max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert mx <= tol_max and mean <= tol_mean, (label, mx, mean)
+    return mx, mean
+
+
+# ------------------------------------------------------------- drop-in path
+
+@pytest.mark.parametrize("case,want", golden_cases(), ids=[c["name"] for c, _ in golden_cases()])
+def test_golden_dropin(torch, case, want):
+    say(f"golden {case['name']}")
+    s, qr, kr, q, k, v = materialise(case)
+    out = np.zeros(s.nq * s.n_head * s.head_dim, np.float32)
+    dr.attention(out, q, k, v, dr.AttnShape(**s.__dict__), dr.Rows(**qr.__dict__),
+                 dr.Rows(**kr.__dict__))
+    check(out, want, case["name"])
+
+
+def test_uniform_scores_exact(torch):
+    # tests.rs:104-114; every value is bf16-exact, so the answer is exact
+    out = np.zeros(2, np.float32)
+    dr.attention(out, np.array([1, 0], np.float32), np.array([1, 0, 1, 0], np.float32),
+                 np.array([0, 2, 4, 6], np.float32), dr.AttnShape(1, 2, 1, 1, 2),
+                 dr.idpos(1), dr.idpos(2))
+    assert out.tolist() == [2.0, 4.0]
+
+
+def test_gqa_equals_repeated_kv(torch):
+    # tests.rs:116-152 at a realistic head dim
+    rng = np.random.default_rng(21)
+    nq, nk, h, hkv, hd = 40, 150, 8, 2, 128
+    q = rng.standard_normal(nq * h * hd).astype(np.float32)
+    k = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+    v = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+    rep = lambda x: np.repeat(x.reshape(nk, hkv, hd), h // hkv, axis=1).reshape(-1).copy()  # noqa
+    a = np.zeros(nq * h * hd, np.float32)
+    b = np.zeros_like(a)
+    sc = 1 / math.sqrt(hd)
+    dr.attention(a, q, k, v, dr.AttnShape(nq, nk, h, hkv, hd, scale=sc), dr.idpos(nq), dr.idpos(nk))
+    dr.attention(b, q, rep(k), rep(v), dr.AttnShape(nq, nk, h, h, hd, scale=sc), dr.idpos(nq),
+                 dr.idpos(nk))
+    assert np.max(np.abs(a - b)) < 1e-5
+
+
+def test_block_diagonal_equals_separate(torch):
+    # tests.rs:70-102 at hd 128
+    rng = np.random.default_rng(22)
+    hd, na, nb = 128, 37, 70
+    n = na + nb
+    q = rng.standard_normal(n * hd).astype(np.float32)
+    k = rng.standard_normal(n * hd).astype(np.float32)
+    v = rng.standard_normal(n * hd).astype(np.float32)
+    pos = list(range(na)) + list(range(nb))
+    seq = [0] * na + [1] * nb
+    S = lambda m: dr.AttnShape(m, m, 1, 1, hd, scale=0.09)  # noqa: E731
+    bat = np.zeros(n * hd, np.float32)
+    dr.attention(bat, q, k, v, S(n), dr.Rows(pos, seq), dr.Rows(pos, seq))
+    sa = np.zeros(na * hd, np.float32)
+    sb = np.zeros(nb * hd, np.float32)
+    dr.attention(sa, q[: na * hd].copy(), k[: na * hd].copy(), v[: na * hd].copy(), S(na),
+                 dr.idpos(na), dr.idpos(na))
+    dr.attention(sb, q[na * hd:].copy(), k[na * hd:].copy(), v[na * hd:].copy(), S(nb),
+                 dr.idpos(nb), dr.idpos(nb))
+    assert np.max(np.abs(bat[: na * hd] - sa)) < 1e-5
+    assert np.max(np.abs(bat[na * hd:] - sb)) < 1e-5
+
+
+def test_c1_dropin_vs_oracle(torch):
+    # 32/32 heads, hd 128, 128 queries x 128 keys, no mask
+    say("C1 drop-in")
+    rng = np.random.default_rng(config_seed(0))
+    nq = nk = 128
+    h, hd = 32, 128
+    q = rng.standard_normal(nq * h * hd).astype(np.float32)
+    k = rng.standard_normal(nk * h * hd).astype(np.float32)
+    v = rng.standard_normal(nk * h * hd).astype(np.float32)
+    s = Shape(nq, nk, h, h, hd, scale=1 / math.sqrt(hd))
+    want = oracle_run(s, RowsSpec(list(range(nq))), RowsSpec(list(range(nk))), q, k, v)
+    got = np.zeros_like(want)
+    dr.attention(got, q, k, v, dr.AttnShape(**s.__dict__), dr.idpos(nq), dr.idpos(nk))
+    check(got, want, "C1")
+
+
+def test_dropin_random_masks_vs_oracle(torch):
+    # arbitrary key order, windows, prefixes and sequence ids at hd 64/128/256
+    rng = np.random.default_rng(23)
+    for trial, hd in enumerate((64, 128, 256, 40)):
+        h, hkv = 4, 2
+        nq, nk = 70, 200
+        kpos = rng.permutation(nk).tolist()
+        qpos = sorted(rng.choice(nk, nq, replace=False).tolist())
+        seq_k = (np.asarray(kpos) >= 150).astype(int).tolist()
+        seq_q = (np.asarray(qpos) >= 150).astype(int).tolist()
+        s = Shape(nq, nk, h, hkv, hd, sliding_window=int(rng.integers(3, 60)),
+                  causal_prefix=int(rng.integers(0, 120)), scale=1 / math.sqrt(hd))
+        qr, kr = RowsSpec(qpos, seq_q), RowsSpec(kpos, seq_k)
+        q = rng.standard_normal(nq * h * hd).astype(np.float32)
+        k = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+        v = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+        say(f"random mask trial {trial} hd {hd} window {s.sliding_window} prefix {s.causal_prefix}")
+        want = oracle_run(s, qr, kr, q, k, v)
+        got = np.zeros_like(want)
+        dr.attention(got, q, k, v, dr.AttnShape(**s.__dict__), dr.Rows(qpos, seq_q),
+                     dr.Rows(kpos, seq_k))
+        check(got, want, f"trial {trial}")
+
+
+def test_no_visible_key_is_nan(torch):
+    s = dr.AttnShape(3, 8, 1, 1, 128, sliding_window=2, scale=0.1)
+    q = np.ones(3 * 128, np.float32)
+    k = np.ones(8 * 128, np.float32)
+    v = np.ones(8 * 128, np.float32)
+    out = np.zeros(3 * 128, np.float32)
+    dr.attention(out, q, k, v, s, dr.Rows([0, 20, 7]), dr.idpos(8))
+    out = out.reshape(3, 128)
+    assert np.all(np.isnan(out[1])) and not np.any(np.isnan(out[[0, 2]]))
+    # nk == 0: every row is NaN
+    out0 = np.zeros(2 * 128, np.float32)
+    dr.attention(out0, np.ones(256, np.float32), np.zeros(0, np.float32), np.zeros(0, np.float32),
+                 dr.AttnShape(2, 0, 1, 1, 128, scale=0.1), dr.idpos(2), dr.Rows([]))
+    assert np.all(np.isnan(out0))
+
+
+# ------------------------------------------------------------- cached path
+
+def _cfg_inputs(cfg, cfg_id, step=0):
+    rng = np.random.default_rng(config_seed(cfg_id, step))
+    kvs = cfg.n_head_kv * cfg.head_dim
+    return rng, kvs
+
+
+def _cached_problem(dev, cfg, cfg_id, batch=1, step=0):
+    """Stores prompt + canvas K/V of `batch` streams and attends with the
+    canvas queries.  Returns (outputs, inputs) with inputs as numpy."""
+    rng = np.random.default_rng(config_seed(cfg_id, step))
+    kvs = cfg.n_head_kv * cfg.head_dim
+    n_tot = cfg.n_total
+    cache = dr.StepCache(dev.ctx, n_tot, [cfg.n_head_kv], [cfg.head_dim], n_batch=batch)
+    canvas = list(range(cfg.n_prompt, n_tot))
+    p_all = dr.Pass(dev.ctx, list(range(n_tot)))
+    p_can = dr.Pass(dev.ctx, canvas)
+    qn = kn = None
+    if cfg.qk_norm:
+        g = np.random.default_rng(config_seed(cfg_id) + 100)
+        qn = g.uniform(0.5, 1.5, cfg.head_dim).astype(np.float32)
+        kn = g.uniform(0.5, 1.5, cfg.head_dim).astype(np.float32)
+    ins, outs, items = [], [], []
+    for b in range(batch):
+        K = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+        V = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+        Q = rng.standard_normal((cfg.n_canvas, cfg.n_head * cfg.head_dim), dtype=np.float32)
+        cache.store(0, p_all, dev.put(K), dev.put(V), dev.put(kn) if kn is not None else None,
+                    1e-6, batch=b)
+        out = dev.empty(cfg.n_canvas * cfg.n_head * cfg.head_dim)
+        qd = dev.put(Q)
+        items.append((qd, out, p_can))
+        outs.append(out)
+        ins.append((Q, K, V))
+    cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=cfg.attn_scale,
+                    q_norm_w=dev.put(qn) if qn is not None else None, q_norm_eps=1e-6)
+    got = [dev.get(o) for o in outs]
+    return got, ins, (qn, kn), cache
+
+
+def _oracle_cfg(cfg, Q, K, V, qn=None, kn=None):
+    Q = Q.reshape(-1).copy()
+    K = K.reshape(-1).copy()
+    if qn is not None:
+        orc.norm_heads(Q, qn, 1e-6)
+        orc.norm_heads(K, kn, 1e-6)
+    s = Shape(cfg.n_canvas, cfg.n_total, cfg.n_head, cfg.n_head_kv, cfg.head_dim,
+              sliding_window=cfg.window, scale=cfg.attn_scale)
+    qr = RowsSpec(list(range(cfg.n_prompt, cfg.n_total)))
+    kr = RowsSpec(list(range(cfg.n_total)))
+    return oracle_run(s, qr, kr, Q, K, V.reshape(-1).copy())
+
+
+@pytest.mark.parametrize("cid", ["C2", "C3", "C4", "C5S", "C5G"])
+def test_config_cached_vs_oracle(dev, cid):
+    cfg = CONFIGS[cid]
+    say(f"config {cid} ({cfg.name})")
+    got, ins, (qn, kn), _ = _cached_problem(dev, cfg, list(CONFIGS).index(cid), batch=cfg.batch)
+    say(f"  launch {dev.ctx.last_launch()}")
+    for b in range(cfg.batch):
+        Q, K, V = ins[b]
+        want = _oracle_cfg(cfg, Q, K, V, qn, kn)
+        check(got[b], want, f"{cid} batch {b}")
+
+
+def test_gemma_scale_one_error(dev):
+    # Gemma's real kq_scale is 1.0 (forward.rs:338-341): with N(0,1) inputs at
+    # hd 256 the score std is 16 and the softmax is close to one-hot, so bf16
+    # rounding of Q and K moves scores by ~0.05.  Reported, bounded loosely.
+    cfg = CONFIGS["C5S"]
+    cfg1 = type(cfg)(**{**cfg.__dict__, "scale": 1.0, "n_prompt": 1024})
+    got, ins, _, _ = _cached_problem(dev, cfg1, 4)
+    Q, K, V = ins[0]
+    want = _oracle_cfg(cfg1, Q, K, V)
+    mx, mean = err_stats(got[0], want)
+    say(f"  Gemma scale 1.0 (hd 256, N(0,1)): max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert np.isfinite(mx) and mx < 1.0
+
+
+@pytest.mark.parametrize("n_split", [1, 2, 3, 5, 8])
+def test_split_count_does_not_change_result(dev, n_split):
+    cfg = CONFIGS["C2"]
+    say(f"C2 with forced n_split={n_split}")
+    dev.ctx.set_split(n_split)
+    try:
+        got, ins, _, _ = _cached_problem(dev, cfg, 1)
+        assert dev.ctx.last_launch()["n_split"] == n_split
+    finally:
+        dev.ctx.set_split(0)
+    Q, K, V = ins[0]
+    check(got[0], _oracle_cfg(cfg, Q, K, V), f"split {n_split}")
+
+
+def test_c2_sixteen_denoise_steps(dev):
+    """the prompt K/V is stored once; each of 16 steps stores fresh
+    canvas K/V and attends with fresh canvas queries (forward.rs:312-343)."""
+    cfg = CONFIGS["C2"]
+    kvs = cfg.n_head_kv * cfg.head_dim
+    rng = np.random.default_rng(config_seed(1))
+    Kp = rng.standard_normal((cfg.n_prompt, kvs), dtype=np.float32)
+    Vp = rng.standard_normal((cfg.n_prompt, kvs), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, cfg.n_total, [cfg.n_head_kv], [cfg.head_dim])
+    cache.store(0, dr.Pass(dev.ctx, range(cfg.n_prompt)), dev.put(Kp), dev.put(Vp))
+    p_can = dr.Pass(dev.ctx, range(cfg.n_prompt, cfg.n_total))
+    out = dev.empty(cfg.n_canvas * cfg.n_head * cfg.head_dim)
+    for step in range(16):
+        r = np.random.default_rng(config_seed(1, step + 1))
+        Kc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
+        Vc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
+        Q = r.standard_normal((cfg.n_canvas, cfg.n_head * cfg.head_dim), dtype=np.float32)
+        cache.store(0, p_can, dev.put(Kc), dev.put(Vc))
+        cache.attention(0, [(dev.put(Q), out, p_can)], cfg.n_head, scale=cfg.attn_scale)
+        if step in (0, 7, 15):
+            got = dev.get(out)
+            want = _oracle_cfg(cfg, Q, np.concatenate([Kp, Kc]), np.concatenate([Vp, Vc]))
+            check(got, want, f"C2 step {step}")
+
+
+def test_cache_store_gather_roundtrip(dev):
+    # tests.rs:55-68: values are bf16-exact, so the round trip is exact
+    cache = dr.StepCache(dev.ctx, 3, [1], [4])
+    k = np.arange(8, dtype=np.float32)
+    v = np.arange(100, 108, dtype=np.float32)
+    cache.store(0, dr.Pass(dev.ctx, [0, 2]), dev.put(k[[4, 5, 6, 7, 0, 1, 2, 3]].copy()),
+                dev.put(v[[4, 5, 6, 7, 0, 1, 2, 3]].copy()))
+    ok, ov = dev.empty(8), dev.empty(8)
+    cache.gather(0, [0, 2], ok, ov)
+    assert dev.get(ok).tolist() == [4, 5, 6, 7, 0, 1, 2, 3]
+    assert dev.get(ov).tolist() == [104, 105, 106, 107, 100, 101, 102, 103]
+
+
+def test_cache_gather_is_bf16_of_store(dev):
+    rng = np.random.default_rng(31)
+    n, hkv, hd = 100, 3, 96
+    cache = dr.StepCache(dev.ctx, 130, [hkv], [hd])
+    pos = sorted(rng.choice(130, n, replace=False).tolist())
+    K = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+    V = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+    cache.store(0, dr.Pass(dev.ctx, pos), dev.put(K), dev.put(V))
+    ok, ov = dev.empty(n * hkv * hd), dev.empty(n * hkv * hd)
+    cache.gather(0, pos, ok, ov)
+    t = dev.t
+    bf = lambda a: t.from_numpy(a).to(t.bfloat16).to(t.float32).numpy().reshape(-1)  # noqa: E731
+    assert np.array_equal(dev.get(ok), bf(K))
+    assert np.array_equal(dev.get(ov), bf(V))
+
+
+def test_cache_split_active_reference_case(dev):
+    # tests.rs:39-53 through the StepCache object
+    cache = dr.StepCache(dev.ctx, 4, [1], [8])
+    assert not cache.initialized()
+    cache.update_seq([10, 20, -1, -1])
+    assert cache.initialized()
+    act, cac = cache.split_active([10, 21, -1, -1], [0, 0, 1, 1], 5)
+    assert act == [1, 2, 3] and cac == [0]
+    cache.update_seq([10, 21, -1, -1])
+    act, cac = cache.split_active([10, 21, -1, -1], [0, 0, 1, 1], 8)
+    assert act == [2, 3] and cac == [0, 1]
+
+
+def test_partial_active_split_vs_dropin(dev):
+    """A denoise step with a non-trivial ActiveSplit: the cached path (keys
+    read by position from the cache) equals the reference's [cached | active]
+    concatenation through the drop-in (forward.rs:312-343)."""
+    rng = np.random.default_rng(41)
+    n_tot, h, hkv, hd = 300, 8, 4, 128
+    kvs = hkv * hd
+    K = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+    V = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, n_tot, [hkv], [hd])
+    cache.store(0, dr.Pass(dev.ctx, range(n_tot)), dev.put(K), dev.put(V))
+    active = sorted(rng.choice(n_tot, 77, replace=False).tolist())
+    cached = [p for p in range(n_tot) if p not in set(active)]
+    Ka = rng.standard_normal((len(active), kvs), dtype=np.float32)
+    Va = rng.standard_normal((len(active), kvs), dtype=np.float32)
+    Q = rng.standard_normal((len(active), h * hd), dtype=np.float32)
+    pa = dr.Pass(dev.ctx, active)
+    cache.store(0, pa, dev.put(Ka), dev.put(Va))
+    out = dev.empty(len(active) * h * hd)
+    cache.attention(0, [(dev.put(Q), out, pa)], h, sliding_window=40, scale=0.1)
+    got = dev.get(out)
+    # reference key order: gather(cached) ++ active rows (forward.rs:312-317)
+    Kf = np.concatenate([K[cached], Ka]).reshape(-1).copy()
+    Vf = np.concatenate([V[cached], Va]).reshape(-1).copy()
+    s = Shape(len(active), n_tot, h, hkv, hd, sliding_window=40, scale=0.1)
+    want = oracle_run(s, RowsSpec(active), RowsSpec(cached + active), Q.reshape(-1).copy(), Kf, Vf)
+    check(got, want, "partial split")

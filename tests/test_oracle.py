@@ -1,0 +1,317 @@
+"""Pins the CPU oracle (oracle/attn_oracle.c) before it is trusted as the
+parity checker.  CPU only.
+
+What pins what:
+  * the reference's own attention tests, same inputs and tolerances
+    (src/model/tests.rs:70-237): known answer, GQA == repeated MHA,
+    block-diagonal == separate runs, online == naive, AVX2 == scalar;
+  * a float64 three-pass brute force (tests/helpers.py) and the committed
+    golden fixtures it produced (tests/golden/);
+  * torch.nn.functional.scaled_dot_product_attention on the CPU (a library
+    routine, independent of both);
+  * invariants: key-permutation invariance, thread-count determinism;
+  * the StepCache tests (tests.rs:39-68) and closed forms for RMSNorm;
+  * negative controls: a plausible mistake (dropped window, wrong prefix,
+    wrong GQA mapping, wrong scale) must fail the same checks.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import (RowsSpec, Shape, brute_force, closed_form, golden_cases, materialise,
+                     rms_norm_f64)
+
+
+def run(s, qr, kr, q, k, v, **kw):
+    out = np.zeros(s.nq * s.n_head * s.head_dim, dtype=np.float32)
+    orc.attention(out, q, k, v, s, qr, kr, **kw)
+    return out.reshape(s.nq, s.n_head * s.head_dim)
+
+
+def idrows(n):
+    return RowsSpec(pos=list(range(n)))
+
+
+# ---------------------------------------------------------------- visible()
+
+def test_visible_known_cases():
+    # attention.rs:17-24, 29-35: different sequences never see each other.
+    assert not orc.visible(3, 3, 0, 1)
+    # symmetric band, strict: |q - k| < w
+    assert orc.visible(10, 14, 0, 0, window=5)
+    assert orc.visible(14, 10, 0, 0, window=5)
+    assert not orc.visible(10, 15, 0, 0, window=5)
+    assert not orc.visible(15, 10, 0, 0, window=5)
+    # window 0 hides everything (|d| >= 0)
+    assert not orc.visible(4, 4, 0, 0, window=0)
+    # prompt rows (qpos < prefix) are causal; canvas rows see all
+    assert orc.visible(5, 5, 0, 0, prefix=8)
+    assert not orc.visible(5, 6, 0, 0, prefix=8)
+    assert orc.visible(5, 0, 0, 0, prefix=8)
+    assert orc.visible(8, 20, 0, 0, prefix=8)
+    assert orc.visible(9, 2, 0, 0, prefix=8)
+
+
+def test_visible_matches_visibility_matrix():
+    s = Shape(nq=9, nk=12, n_head=1, n_head_kv=1, head_dim=1, sliding_window=4, causal_prefix=6)
+    qr = RowsSpec(pos=[0, 2, 5, 6, 7, 11, 3, 8, 1], seq=[0, 0, 0, 0, 1, 1, 0, 1, 0])
+    kr = RowsSpec(pos=list(range(12)), seq=[0] * 6 + [1] * 6)
+    from helpers import visibility
+    m = visibility(s, qr, kr)
+    for i in range(s.nq):
+        for j in range(s.nk):
+            assert bool(m[i, j]) == orc.visible(qr.pos[i], kr.pos[j], qr.seq[i], kr.seq[j], 4, 6)
+
+
+# --------------------------------------------- the reference's own tests
+
+@pytest.mark.parametrize("avx2", [False, True])
+def test_uniform_scores_known_answer(avx2):
+    # tests.rs:104-114
+    s = Shape(nq=1, nk=2, n_head=1, n_head_kv=1, head_dim=2)
+    q = np.array([1.0, 0.0], np.float32)
+    k = np.array([1.0, 0.0, 1.0, 0.0], np.float32)
+    v = np.array([0.0, 2.0, 4.0, 6.0], np.float32)
+    out = run(s, idrows(1), idrows(2), q, k, v, avx2=avx2).reshape(-1)
+    assert abs(out[0] - 2.0) < 1e-6 and abs(out[1] - 4.0) < 1e-6
+
+
+@pytest.mark.parametrize("avx2", [False, True])
+def test_matches_naive_reference(avx2):
+    # tests.rs:154-186 -- online softmax == three-pass softmax, 1e-5
+    s = Shape(nq=4, nk=6, n_head=2, n_head_kv=2, head_dim=8)
+    q = closed_form(4 * 2 * 8, 37, 101, 50, 25)
+    k = closed_form(6 * 2 * 8, 53, 97, 48, 24)
+    v = closed_form(6 * 2 * 8, 71, 89, 44, 44)
+    out = run(s, idrows(4), idrows(6), q, k, v, avx2=avx2)
+    want = brute_force(q, k, v, s, idrows(4), idrows(6))
+    assert np.max(np.abs(out - want)) < 1e-5
+
+
+@pytest.mark.parametrize("avx2", [False, True])
+def test_gqa_matches_repeated_kv(avx2):
+    # tests.rs:116-152
+    nq, nk, hd = 3, 5, 8
+    gqa = Shape(nq=nq, nk=nk, n_head=4, n_head_kv=2, head_dim=hd)
+    mha = Shape(nq=nq, nk=nk, n_head=4, n_head_kv=4, head_dim=hd)
+    q = closed_form(nq * 4 * hd, 37, 101, 50, 50)
+    k = closed_form(nk * 2 * hd, 53, 97, 48, 48)
+    v = closed_form(nk * 2 * hd, 71, 89, 44, 44)
+
+    def repeat(x):
+        return np.repeat(x.reshape(nk, 2, hd), 2, axis=1).reshape(-1).copy()
+
+    a = run(gqa, idrows(nq), idrows(nk), q, k, v, avx2=avx2)
+    b = run(mha, idrows(nq), idrows(nk), q, repeat(k), repeat(v), avx2=avx2)
+    assert np.max(np.abs(a - b)) < 1e-5
+
+
+@pytest.mark.parametrize("avx2", [False, True])
+def test_block_diagonal_batches(avx2):
+    # tests.rs:70-102
+    hd, na, nb = 4, 2, 3
+    s = lambda n: Shape(nq=n, nk=n, n_head=1, n_head_kv=1, head_dim=hd)  # noqa: E731
+    q = closed_form((na + nb) * hd, 37, 101, 50, 50)
+    k = q.copy()
+    v = closed_form((na + nb) * hd, 71, 89, 44, 44)
+    br = RowsSpec(pos=[0, 1, 0, 1, 2], seq=[0, 0, 1, 1, 1])
+    batched = run(s(na + nb), br, br, q, k, v, avx2=avx2).reshape(-1)
+    sep_a = run(s(na), idrows(na), idrows(na), q[: na * hd].copy(), k[: na * hd].copy(),
+                v[: na * hd].copy(), avx2=avx2).reshape(-1)
+    sep_b = run(s(nb), idrows(nb), idrows(nb), q[na * hd:].copy(), k[na * hd:].copy(),
+                v[na * hd:].copy(), avx2=avx2).reshape(-1)
+    assert np.max(np.abs(batched[: na * hd] - sep_a)) < 1e-5
+    assert np.max(np.abs(batched[na * hd:] - sep_b)) < 1e-5
+
+
+def test_avx2_matches_scalar():
+    # tests.rs:188-213, row by row
+    s = Shape(nq=3, nk=3, n_head=2, n_head_kv=2, head_dim=16)
+    n = 3 * 2 * 16
+    q, k, v = closed_form(n, 37, 101, 50, 50), closed_form(n, 53, 97, 48, 48), closed_form(n, 71, 89, 44, 44)
+    a = np.zeros(n, np.float32)
+    b = np.zeros(n, np.float32)
+    for head in range(2):
+        for i in range(3):
+            orc.attention_row("scalar", a, q, k, v, s, idrows(3), idrows(3), head, i)
+            orc.attention_row("avx2", b, q, k, v, s, idrows(3), idrows(3), head, i)
+    assert np.max(np.abs(a - b)) < 1e-5
+
+
+# ------------------------------------------------- golden fixtures
+
+@pytest.mark.parametrize("avx2", [False, True])
+@pytest.mark.parametrize("case,want", golden_cases(), ids=[c["name"] for c, _ in golden_cases()])
+def test_golden(case, want, avx2):
+    s, qr, kr, q, k, v = materialise(case)
+    got = run(s, qr, kr, q, k, v, avx2=avx2)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    tol = 1e-5 * max(1.0, float(np.max(np.abs(want[ok])))) if ok.any() else 0
+    assert np.max(np.abs(got[ok] - want[ok]), initial=0.0) <= tol
+
+
+# ------------------------------------------------- independent cross-checks
+
+def test_torch_sdpa_crosscheck():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(7)
+    h, hkv, hd, nq, nk = 8, 2, 128, 16, 96
+    s = Shape(nq=nq, nk=nk, n_head=h, n_head_kv=hkv, head_dim=hd, scale=1 / math.sqrt(hd))
+    q = rng.standard_normal(nq * h * hd).astype(np.float32)
+    k = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+    v = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+    got = run(s, RowsSpec(pos=list(range(nk - nq, nk))), idrows(nk), q, k, v)
+    Q = torch.from_numpy(q.astype(np.float64)).view(nq, h, hd).transpose(0, 1)
+    K = torch.from_numpy(k.astype(np.float64)).view(nk, hkv, hd).transpose(0, 1)
+    V = torch.from_numpy(v.astype(np.float64)).view(nk, hkv, hd).transpose(0, 1)
+    K = K.repeat_interleave(h // hkv, dim=0)
+    V = V.repeat_interleave(h // hkv, dim=0)
+    ref = torch.nn.functional.scaled_dot_product_attention(Q, K, V, scale=s.scale)
+    ref = ref.transpose(0, 1).reshape(nq, h * hd).numpy()
+    assert np.max(np.abs(got - ref)) < 1e-5
+
+
+def test_key_permutation_invariance():
+    # Masking is by position, so the [cached | active] key order of the cache
+    # (forward.rs:91-101) must not change the result beyond rounding.
+    rng = np.random.default_rng(3)
+    h, hkv, hd, nq, nk = 4, 2, 64, 6, 50
+    s = Shape(nq=nq, nk=nk, n_head=h, n_head_kv=hkv, head_dim=hd, sliding_window=9,
+              causal_prefix=20, scale=0.125)
+    q = rng.standard_normal(nq * h * hd).astype(np.float32)
+    k = rng.standard_normal((nk, hkv * hd)).astype(np.float32)
+    v = rng.standard_normal((nk, hkv * hd)).astype(np.float32)
+    qr = RowsSpec(pos=[3, 15, 19, 20, 33, 49])
+    a = run(s, qr, idrows(nk), q, k.reshape(-1), v.reshape(-1))
+    perm = rng.permutation(nk)
+    b = run(s, qr, RowsSpec(pos=[int(p) for p in perm]), q, k[perm].reshape(-1).copy(),
+            v[perm].reshape(-1).copy())
+    assert np.max(np.abs(a - b)) < 1e-5
+
+
+def test_threads_bit_identical():
+    # each (head, query) task is sequential: the pool size cannot change bits
+    rng = np.random.default_rng(5)
+    h, hd, nq, nk = 8, 128, 32, 64
+    s = Shape(nq=nq, nk=nk, n_head=h, n_head_kv=h, head_dim=hd, scale=0.1)
+    q = rng.standard_normal(nq * h * hd).astype(np.float32)
+    k = rng.standard_normal(nk * h * hd).astype(np.float32)
+    v = rng.standard_normal(nk * h * hd).astype(np.float32)
+    a = run(s, idrows(nq), idrows(nk), q, k, v, threads=1)
+    b = run(s, idrows(nq), idrows(nk), q, k, v, threads=0)
+    assert np.array_equal(a, b)
+
+
+# ------------------------------------------------- negative controls
+
+def _dense_case():
+    rng = np.random.default_rng(11)
+    h, hkv, hd, nq, nk = 4, 2, 32, 5, 40
+    q = rng.standard_normal(nq * h * hd).astype(np.float32)
+    k = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+    v = rng.standard_normal(nk * hkv * hd).astype(np.float32)
+    return h, hkv, hd, nq, nk, q, k, v
+
+
+def test_checks_catch_plausible_mistakes():
+    h, hkv, hd, nq, nk, q, k, v = _dense_case()
+    qr = RowsSpec(pos=[2, 10, 21, 30, 39])
+    good = Shape(nq=nq, nk=nk, n_head=h, n_head_kv=hkv, head_dim=hd, sliding_window=6,
+                 causal_prefix=15, scale=0.2)
+    want = brute_force(q, k, v, good, qr, idrows(nk))
+    assert np.max(np.abs(run(good, qr, idrows(nk), q, k, v) - want)) < 1e-5
+    mistakes = [
+        Shape(**{**good.__dict__, "sliding_window": None}),   # dropped window
+        Shape(**{**good.__dict__, "sliding_window": 7}),      # off-by-one band
+        Shape(**{**good.__dict__, "causal_prefix": None}),    # dropped prefix
+        Shape(**{**good.__dict__, "causal_prefix": 3}),       # wrong prefix
+        Shape(**{**good.__dict__, "scale": 0.1}),             # wrong scale
+    ]
+    for bad in mistakes:
+        assert np.max(np.abs(run(bad, qr, idrows(nk), q, k, v) - want)) > 1e-3, bad
+    # wrong GQA mapping (head % n_head_kv instead of head / group): swapping
+    # the two KV heads' data changes the answer
+    ks = k.reshape(nk, hkv, hd)[:, ::-1].reshape(-1).copy()
+    vs = v.reshape(nk, hkv, hd)[:, ::-1].reshape(-1).copy()
+    assert np.max(np.abs(run(good, qr, idrows(nk), q, ks, vs) - want)) > 1e-3
+
+
+# ------------------------------------------------- QK-norm
+
+def test_rms_norm_closed_forms():
+    w = np.linspace(0.5, 1.5, 128).astype(np.float32)
+    # all-equal vector c: rms = |c| -> x = sign(c) * w / sqrt(1 + eps/c^2)
+    for c in (3.0, -0.25):
+        x = np.full(128, c, np.float32)
+        orc.rms_norm_inplace(x, w, 1e-6)
+        want = np.sign(c) * w / math.sqrt(1 + 1e-6 / c**2)
+        assert np.max(np.abs(x - want)) < 1e-6
+    # positive rescaling invariance (eps -> 0)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(128).astype(np.float32)
+    y = (x * 37.0).astype(np.float32)
+    orc.rms_norm_inplace(x, w, 0.0)
+    orc.rms_norm_inplace(y, w, 0.0)
+    assert np.max(np.abs(x - y)) < 1e-5
+
+
+def test_norm_heads_matches_f64():
+    rng = np.random.default_rng(1)
+    hd, n = 128, 12
+    x = rng.standard_normal(n * hd).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    want = rms_norm_f64(x.reshape(n, hd), w, 1e-6).reshape(-1)
+    orc.norm_heads(x, w, 1e-6)
+    assert np.max(np.abs(x - want)) < 1e-5
+
+
+# ------------------------------------------------- StepCache
+
+def test_cache_store_gather_roundtrip():
+    # tests.rs:55-68
+    stride = 4
+    ck = np.zeros(3 * stride, np.float32)
+    cv = np.zeros(3 * stride, np.float32)
+    k = np.arange(8, dtype=np.float32)
+    v = np.arange(100, 108, dtype=np.float32)
+    orc.cache_store(ck, cv, stride, [2, 0], k, v)
+    ok = np.zeros(8, np.float32)
+    ov = np.zeros(8, np.float32)
+    orc.cache_gather(ck, cv, stride, [0, 2], ok, ov)
+    assert ok.tolist() == [4, 5, 6, 7, 0, 1, 2, 3]
+    assert ov.tolist() == [104, 105, 106, 107, 100, 101, 102, 103]
+
+
+def test_split_active_reference_case():
+    # tests.rs:39-53
+    prev = np.array([10, 20, -1, -1], np.int32)
+    last = np.full(4, -1, np.int32)
+    act, cac = orc.split_active(prev, last, [10, 21, -1, -1], [0, 0, 1, 1], 5)
+    assert act == [1, 2, 3] and cac == [0]
+    prev = np.array([10, 21, -1, -1], np.int32)
+    act, cac = orc.split_active(prev, last, [10, 21, -1, -1], [0, 0, 1, 1], 5 + 2 + 1)
+    assert act == [2, 3] and cac == [0, 1]
+
+
+def test_split_active_vicinity_and_decay():
+    n = 12
+    prev = np.full(n, 7, np.int32)
+    last = np.full(n, -1, np.int32)
+    masked = np.zeros(n, np.uint8)
+    masked[6] = 1
+    act, cac = orc.split_active(prev, last, prev, masked, 3, vicinity=2)
+    assert act == [4, 5, 6, 7, 8]
+    assert cac == [0, 1, 2, 3, 9, 10, 11]
+    # position 1 changes at step 3 and stays active through step 5 (<= 2 later)
+    seq = prev.copy()
+    seq[1] = 9
+    act, _ = orc.split_active(prev, last, seq, np.zeros(n, np.uint8), 3)
+    assert act == [1]
+    for step, expect in ((4, [1]), (5, [1]), (6, [])):
+        act, _ = orc.split_active(seq, last, seq, np.zeros(n, np.uint8), step)
+        assert act == expect, step
