@@ -1,0 +1,259 @@
+#!/usr/bin/env python3
+"""Benchmark: denoise-step attention on one MI355X (BASELINE.json metric).
+
+Workload ("C2"): LLaDA-8B shape, 32 query heads =
+32 KV heads, head_dim 128, 512 cached prompt rows + 256 canvas rows, batch 1,
+bidirectional, scale 1/sqrt(128).  The prompt K/V is stored in the bf16 KV
+cache once.  One *step* = store the step's 256 fresh canvas K/V rows into the
+cache (f32 -> bf16, by position) + attention of the 256 canvas queries over
+all 768 keys (the attention_block sequence of forward.rs:312-343).  Inputs
+(16 distinct canvas sets, f32 N(0,1), seeded) are resident in HBM before the
+timed region.
+
+value = algorithmic attention FLOPs of K steps / wall time of the K steps,
+FLOPs = 4 * h * hd * sum_q |visible keys| = 3.221 GFLOP per step (softmax,
+masking and the store excluded).  roofline = the attention kernel alone:
+the same FLOPs / its average duration measured with HIP events on the
+library's stream, against 2516.6 TFLOP/s dense bf16 MFMA.  cpu_baseline =
+the C restatement of the reference's AVX2 attention (oracle/, "port") timed on
+this host's cores on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode eager|graph]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "diffuse-rs_amd"))
+sys.path.insert(0, str(ROOT / "oracle"))
+sys.path.insert(0, str(ROOT / "tests"))
+
+METRIC = "attn TFLOP/s & % bf16 MFMA peak per denoise step, LLaDA-8B shape, 1 MI355X"
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--mode", choices=["eager", "graph"], default="graph")
+    ap.add_argument("--split", type=int, default=0, help="force key splits (0 = automatic)")
+    ap.add_argument("--cpu-reps", type=int, default=0, help="oracle reps (0 = auto ~15 s)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        return 2
+
+    import numpy as np
+    import torch
+
+    import dr_attn as dr
+    from helpers import CONFIGS, config_seed
+
+    cfg = CONFIGS["C2"]
+    h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+    n_p, n_c, n_t = cfg.n_prompt, cfg.n_canvas, cfg.n_total
+    flops = cfg.flops()
+    kvs = hkv * hd
+    n_sets = 16
+
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    ctx = dr.Context(0)
+    ctx.set_stream(stream.cuda_stream)
+    if args.split:
+        ctx.set_split(args.split)
+
+    rng = np.random.default_rng(config_seed(1))
+    Kp = rng.standard_normal((n_p, kvs), dtype=np.float32)
+    Vp = rng.standard_normal((n_p, kvs), dtype=np.float32)
+    sets = []
+    for s in range(n_sets):
+        r = np.random.default_rng(config_seed(1, s + 1))
+        sets.append((r.standard_normal((n_c, kvs), dtype=np.float32),
+                     r.standard_normal((n_c, kvs), dtype=np.float32),
+                     r.standard_normal((n_c, h * hd), dtype=np.float32)))
+    with torch.cuda.stream(stream):
+        dKp, dVp = torch.from_numpy(Kp).to(dev), torch.from_numpy(Vp).to(dev)
+        dsets = [tuple(torch.from_numpy(x).to(dev) for x in st) for st in sets]
+        out = torch.empty(n_c * h * hd, dtype=torch.float32, device=dev)
+    cache = dr.StepCache(ctx, n_t, [hkv], [hd])
+    p_prompt = dr.Pass(ctx, range(n_p))
+    p_canvas = dr.Pass(ctx, range(n_p, n_t))
+    cache.store(0, p_prompt, dKp, dVp)
+    scale = cfg.attn_scale
+
+    def step(i: int) -> None:
+        Kc, Vc, Q = dsets[i % n_sets]
+        cache.store(0, p_canvas, Kc, Vc)
+        cache.attention(0, [(Q, out, p_canvas)], h, scale=scale)
+
+    # correctness of the measured configuration (step 0 vs the oracle)
+    step(0)
+    stream.synchronize()
+    got = out.cpu().numpy()
+    import oracle as orc
+    from helpers import RowsSpec, Shape
+    Kc, Vc, Q = sets[0]
+    s = Shape(n_c, n_t, h, hkv, hd, scale=scale)
+    want = np.zeros_like(got)
+    orc.attention(want, Q.reshape(-1).copy(), np.concatenate([Kp, Kc]).reshape(-1).copy(),
+                  np.concatenate([Vp, Vc]).reshape(-1).copy(), s,
+                  RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t))))
+    err = np.abs(got.astype(np.float64) - want)
+    parity = {"max_abs": float(err.max()), "mean_abs": float(err.mean()),
+              "ok": bool(err.max() <= 1e-2 and err.mean() <= 1e-3)}
+    log(f"parity step 0: {parity}")
+    launch = ctx.last_launch()
+    log(f"launch: {launch}")
+
+    # ---- roofline: the attention call alone, HIP events on the library stream
+    n_roof = max(50, min(2000, args.steps))
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n_roof)]
+    with torch.cuda.stream(stream):
+        for i in range(20):
+            step(i)
+        for i in range(n_roof):
+            dK, dV, dQ = dsets[i % n_sets]
+            cache.store(0, p_canvas, dK, dV)
+            ev[i][0].record(stream)
+            cache.attention(0, [(dQ, out, p_canvas)], h, scale=scale)
+            ev[i][1].record(stream)
+    stream.synchronize()
+    attn_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    attn_mean_ms = sum(attn_ms) / len(attn_ms)
+    attn_med_ms = attn_ms[len(attn_ms) // 2]
+    log(f"attention call: mean {attn_mean_ms * 1e3:.2f} us, median {attn_med_ms * 1e3:.2f} us")
+
+    # ---- timed region: K whole steps
+    graph = None
+    if args.mode == "graph":
+        try:
+            steps_per_graph = n_sets
+            with torch.cuda.stream(stream):
+                for i in range(3):
+                    step(i)
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream, capture_error_mode="thread_local"):
+                for i in range(steps_per_graph):
+                    step(i)
+            stream.synchronize()
+        except Exception as e:  # graph capture unavailable: measure eagerly
+            log(f"graph capture failed ({e}); timing eagerly")
+            graph = None
+    mode = "graph" if graph is not None else "eager"
+
+    def run(n: int) -> None:
+        with torch.cuda.stream(stream):
+            if graph is not None:
+                for _ in range(n // n_sets):
+                    graph.replay()
+                for i in range(n % n_sets):
+                    step(i)
+            else:
+                for i in range(n):
+                    step(i)
+
+    run(args.warmup)
+    torch.cuda.synchronize()
+    stream.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    run(args.steps)
+    e1.record(stream)
+    stream.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    total_s = max(wall, gpu_ms / 1e3)
+    ms_per_step = total_s * 1e3 / args.steps
+    value = flops * args.steps / total_s / 1e12
+
+    # parity again after the timed region (same buffers)
+    step(0)
+    stream.synchronize()
+    err2 = np.abs(out.cpu().numpy().astype(np.float64) - want)
+    parity["max_abs_after"] = float(err2.max())
+
+    achieved = flops / (attn_mean_ms / 1e3) / 1e12
+    algo_bytes = (n_c * h * hd * 4) * 2 + 2 * n_t * kvs * 2  # Q f32 + O f32 + K,V bf16
+    roofline = {
+        "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "kernel": "attention call (attn_fwd_kernel + attn_combine_kernel when split > 1)",
+        "flops_per_launch": flops, "launch_us_mean": round(attn_mean_ms * 1e3, 3),
+        "launch_us_median": round(attn_med_ms * 1e3, 3),
+        "algorithmic_bytes_per_launch": algo_bytes,
+        "hbm_ceiling_frac": round(min(1.0, flops / algo_bytes * PEAK_HBM_GBS * 1e9 / 1e12
+                                      / PEAK_BF16_TFLOPS), 4),
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        threads = orc.max_threads()
+        out_c = np.zeros(n_c * h * hd, np.float32)
+        qr, kr = RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t)))
+        qf = Q.reshape(-1).copy()
+        kf = np.concatenate([Kp, Kc]).reshape(-1).copy()
+        vf = np.concatenate([Vp, Vc]).reshape(-1).copy()
+        t = time.perf_counter()
+        orc.attention(out_c, qf, kf, vf, s, qr, kr, threads=threads)
+        one = time.perf_counter() - t
+        reps = args.cpu_reps or max(1, min(200, int(15.0 / max(one, 1e-3))))
+        t = time.perf_counter()
+        for _ in range(reps):
+            orc.attention(out_c, qf, kf, vf, s, qr, kr, threads=threads)
+        per = (time.perf_counter() - t) / reps
+        t = time.perf_counter()
+        orc.attention(out_c, qf, kf, vf, s, qr, kr, threads=1)
+        per1 = time.perf_counter() - t
+        cpu = {"value": round(flops / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+               "kind": "port",
+               "sample": f"{reps} C2 attention calls (256 q x 768 k x 32 heads, hd 128, f32) "
+                         f"with the C restatement of attention()+attention_row_avx2 on "
+                         f"{threads} OpenMP threads; {per * 1e3:.1f} ms/call",
+               "ms_per_call": round(per * 1e3, 3),
+               "value_1thread": round(flops / per1 / 1e12, 5),
+               "ms_per_call_1thread": round(per1 * 1e3, 2)}
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "C2: LLaDA-8B denoise step, 32/32 heads, hd 128, 512 cached + "
+                               "256 canvas, batch 1 (store canvas K/V + attention)",
+                   "global_batch": 1, "seq_len": n_t, "parallelism": "none (1 GPU)",
+                   "timing": mode, "accumulate": "fp32", "q_out_dtype": "f32",
+                   "kv_cache_dtype": "bf16"},
+        "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 3),
+        "attention_call_pct_of_peak": round(100 * achieved / PEAK_BF16_TFLOPS, 3),
+        "gpu_event_ms": round(gpu_ms, 4), "wall_s": round(wall, 4),
+        "launch": launch, "parity": parity, "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -91,6 +91,8 @@ struct dr_ctx {
     hipStream_t own = nullptr;
     int n_cu = 0;
     int force_split = 0;
+    int force_rb = 0;
+    int force_kq = 0;
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials
@@ -238,6 +240,8 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
     info->waves_per_wg = ctx->last.waves;
     info->block_n = ctx->last.block_n;
     info->head_dim_tile = ctx->last.hd_tile;
+    info->row_blocks = ctx->last.rb;
+    info->key_groups = ctx->last.kq;
     return DR_OK;
 }
 
@@ -245,6 +249,16 @@ int dr_ctx_set_split(dr_ctx* ctx, int n_split) {
     if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_split: ctx is NULL");
     if (n_split < 0 || n_split > 64) return fail(DR_ERR_INVALID, "n_split %d not in 0..64", n_split);
     ctx->force_split = n_split;
+    return DR_OK;
+}
+
+int dr_ctx_set_tuning(dr_ctx* ctx, int row_blocks, int key_groups, int n_split) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_tuning: ctx is NULL");
+    if (row_blocks < 0 || row_blocks > 8 || key_groups < 0 || key_groups > 8)
+        return fail(DR_ERR_INVALID, "row_blocks/key_groups not in 0..8");
+    DR_CHECK(dr_ctx_set_split(ctx, n_split));
+    ctx->force_rb = row_blocks;
+    ctx->force_kq = key_groups;
     return DR_OK;
 }
 
@@ -491,9 +505,10 @@ int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
 // ---------------------------------------------------------------- attention
 
 static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int max_nk,
-                          bool masked, bool qnorm) {
-    dr::LaunchPlan p = dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk,
-                                          masked, qnorm, ctx->n_cu, ctx->force_split);
+                          int mask, bool qnorm) {
+    dr::LaunchPlan p =
+        dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qnorm,
+                           ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split);
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
         DR_CHECK(ensure(ctx->part, ws));
@@ -562,12 +577,14 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
         s.vt = cache->vt[layer * cache->n_batch + b];
         s.nq = (int)it.pass->n;
         s.nk = (int)cache->n_total;
+        s.qpos_sorted = 1;  // dr_pass positions are strictly ascending
         max_nq = std::max(max_nq, s.nq);
     }
     if (max_nq == 0) return DR_OK;
     DR_CHECK(use_device(ctx));
-    const bool masked = sliding_window.present || causal_prefix.present;
-    return launch_planned(ctx, a, (int)hd, max_nq, (int)cache->n_total, masked,
+    const int mask =
+        (sliding_window.present || causal_prefix.present) ? dr::MASK_POS : dr::MASK_NONE;
+    return launch_planned(ctx, a, (int)hd, max_nq, (int)cache->n_total, mask,
                           q_norm_w != nullptr);
 }
 
@@ -703,7 +720,12 @@ int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const
     sl.kseq = has_kseq ? m + off_kseq : nullptr;
     sl.nq = (int)nq;
     sl.nk = (int)nk;
-    DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, masked, false));
+    bool sorted = true;
+    for (size_t i = 1; i < nq && sorted; ++i) sorted = qr.pos[i] > qr.pos[i - 1];
+    sl.qpos_sorted = sorted ? 1 : 0;
+    const int mask = !masked ? dr::MASK_NONE
+                             : ((has_kpos || has_kseq) ? dr::MASK_KEYS : dr::MASK_POS);
+    DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, mask, false));
     DR_HIP(hipMemcpyAsync(out, ctx->out.p, qb, hipMemcpyDeviceToHost, st));
     DR_HIP(hipStreamSynchronize(st));
     return DR_OK;

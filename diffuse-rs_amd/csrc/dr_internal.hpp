@@ -28,6 +28,7 @@ struct AttnSlot {
     const int* kseq;      // [nk] or nullptr
     int nq;
     int nk;
+    int qpos_sorted;      // qpos strictly ascending (a dr_pass): key ranges from endpoints
 };
 
 struct AttnArgs {
@@ -44,17 +45,19 @@ struct AttnArgs {
     float qn_eps;
     int rowgroups;                 // workgroup row groups per (batch, kv head)
     int n_split;                   // key splits; > 1 writes partials
-    float* part_o;                 // split partial accumulators
-    float* part_ml;                // split partial (max, sum)
+    float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
+    float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
 };
 
-// Row geometry used by both the attention and the combine kernel.
+// Merge of the key-split partials (attn_combine_kernel).
 struct CombineArgs {
     AttnSlot slot[MAX_BATCH];
     int n_batch;
     int n_head_kv, group, hd;
     int o_rstride;
+    int rows_pad;                  // partial rows per (batch, kv head) = rowgroups * rb * 32
     int rowgroups;
+    int wg_per_rowgroup;
     int n_split;
     const float* part_o;
     const float* part_ml;
@@ -86,21 +89,33 @@ struct GatherArgs {
     float* out_v;
 };
 
+// Masking mode of an attention launch.
+enum MaskMode : int {
+    MASK_NONE = 0,  // every key visible (only the key tail is masked)
+    MASK_POS = 1,   // window / causal prefix / query sequence ids; key j at position j
+    MASK_KEYS = 2,  // arbitrary key positions and/or key sequence ids (per-key metadata)
+};
+
 struct LaunchPlan {
     int hd_tile;     // 64, 128 or 256
-    int block_n;     // keys per LDS tile
-    int waves;       // waves per workgroup (32 query rows each)
-    int n_split;
-    int rowgroups;
+    int block_n;     // keys per tile (one MFMA key block is 32)
+    int rb;          // row blocks (32 query rows each) per workgroup
+    int kq;          // key groups per workgroup (merged in LDS)
+    int waves;       // rb * kq
+    int stages;      // LDS pipeline depth (super-tiles of kq tiles)
+    int n_split;     // key splits across workgroups (merged by attn_combine_kernel)
+    int rowgroups;   // workgroups per (batch, kv head) and split
     int n_workgroups;
-    bool masked;
+    int mask;        // MaskMode
     bool qnorm;
 };
 
 // Chooses tile sizes and the key split for a problem on a device with n_cu
 // compute units.  force_split > 0 overrides the split heuristic.
+// force_rb / force_kq / force_split > 0 override the heuristic (tuning).
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          bool masked, bool qnorm, int n_cu, int force_split);
+                          int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
+                          int force_split);
 
 // Bytes of split workspace a plan needs (part_o + part_ml).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);

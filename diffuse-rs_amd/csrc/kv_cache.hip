@@ -12,6 +12,8 @@
 // store:  StepCache::store (cache.rs:62-71) -- f32 rows -> bf16 at their
 //         positions, optionally after per-head RMSNorm of K (norm_heads,
 //         ops.rs:384-389, applied before the store in forward.rs:300-302).
+//         One launch: workgroups [0, n_kblocks) write K rows (one wave per
+//         (row, kv head)); the rest transpose 64x64 blocks of V through LDS.
 // gather: StepCache::gather (cache.rs:73-82) -- bf16 back to f32 rows.
 #include "dr_internal.hpp"
 
@@ -20,6 +22,9 @@
 namespace dr {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ uint16_t f2bf(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
@@ -27,28 +32,36 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
     return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-constexpr int STORE_ROWS = 32;  // rows per workgroup
+constexpr int VT_ROWS = 64;  // positions per V^T block
+constexpr int VT_D = 64;     // head-dim entries per V^T block
 
-// grid (ceil(n / 32), n_head_kv); 256 threads.
 template <int HD>
-__global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
-    constexpr int EPL = HD / 64;  // K elements per lane per row
-    __shared__ uint16_t vtile[STORE_ROWS][HD + 2];
-    const int g = blockIdx.y;
-    const int r0 = blockIdx.x * STORE_ROWS;
+__global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a, int n_kblocks) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    // K: each wave normalises, converts and stores 8 rows.
-    for (int rr = 0; rr < STORE_ROWS / 4; ++rr) {
-        const int r = r0 + wave * (STORE_ROWS / 4) + rr;
-        if (r >= a.n) break;
+    if ((int)blockIdx.x < n_kblocks) {
+        // ---- K: one wave per (row, kv head); EPL consecutive values per lane
+        constexpr int EPL = HD / 64;
+        const int pair = blockIdx.x * 4 + wave;
+        if (pair >= a.n * a.n_head_kv) return;
+        const int r = pair / a.n_head_kv, g = pair % a.n_head_kv;
         const int pos = a.pos ? a.pos[r] : r;
-        const float* src = a.k + ((size_t)r * a.n_head_kv + g) * a.hd;
+        const float* src = a.k + (size_t)pair * a.hd;
         float x[EPL];
+        if (a.hd == HD) {
+            if constexpr (EPL == 4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + lane * 4);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const int d = lane * EPL + e;
-            x[e] = d < a.hd ? src[d] : 0.0f;
+                for (int e = 0; e < 4; ++e) x[e] = v[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) x[e] = src[lane * EPL + e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const int d = lane * EPL + e;
+                x[e] = d < a.hd ? src[d] : 0.0f;
+            }
         }
         if (a.kn_w) {
             // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
@@ -70,22 +83,63 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
         uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * HD + lane * EPL;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) dst[e] = f2bf(x[e]);
+        return;
     }
 
-    // V: stage 32 rows in LDS, then write them transposed.
-    for (int idx = tid; idx < STORE_ROWS * HD; idx += 256) {
-        const int rr = idx / HD, d = idx % HD;
-        const int r = r0 + rr;
-        const float x = (r < a.n && d < a.hd) ? a.v[((size_t)r * a.n_head_kv + g) * a.hd + d] : 0.0f;
-        vtile[rr][d] = f2bf(x);
+    // ---- V^T: a block of 64 rows x 64 d of one kv head, transposed via LDS
+    __shared__ uint16_t tile[VT_D][VT_ROWS + 2];
+    constexpr int NDC = HD / VT_D;
+    const int nrc = (a.n + VT_ROWS - 1) / VT_ROWS;
+    int t = blockIdx.x - n_kblocks;
+    const int rc = t % nrc;
+    t /= nrc;
+    const int dc = t % NDC;
+    const int g = t / NDC;
+    {
+        const int row = tid >> 2, d0 = (tid & 3) * 16;
+        const int r = rc * VT_ROWS + row;
+        const int dbase = dc * VT_D + d0;
+        const float* src = a.v + ((size_t)r * a.n_head_kv + g) * a.hd + dbase;
+        float x[16];
+        if (r < a.n && a.hd == HD) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * q4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[4 * q4 + e] = v[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) x[e] = (r < a.n && dbase + e < a.hd) ? src[e] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tile[d0 + e][row] = f2bf(x[e]);
     }
     __syncthreads();
-    for (int idx = tid; idx < STORE_ROWS * HD; idx += 256) {
-        const int rr = idx % STORE_ROWS, d = idx / STORE_ROWS;
-        const int r = r0 + rr;
-        if (r < a.n) {
-            const int pos = a.pos ? a.pos[r] : r;
-            a.vtc[((size_t)g * HD + d) * a.cap + pos] = vtile[rr][d];
+    {
+        const int d = tid >> 2, r0 = (tid & 3) * 16;
+        const int rfirst = rc * VT_ROWS + r0;
+        if (rfirst >= a.n) return;
+        const int nr = min(16, a.n - rfirst);
+        uint16_t* drow = a.vtc + ((size_t)g * HD + dc * VT_D + d) * a.cap;
+        const int p0 = a.pos ? a.pos[rfirst] : rfirst;
+        const bool contiguous =
+            nr == 16 && (a.pos == nullptr || a.pos[rfirst + 15] - p0 == 15) && (p0 & 7) == 0;
+        if (contiguous) {
+            u32x4 w[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    w[h][e] = (uint32_t)tile[d][r0 + 8 * h + 2 * e] |
+                              ((uint32_t)tile[d][r0 + 8 * h + 2 * e + 1] << 16);
+            *reinterpret_cast<u32x4*>(drow + p0) = w[0];
+            *reinterpret_cast<u32x4*>(drow + p0 + 8) = w[1];
+        } else {
+            for (int e = 0; e < nr; ++e) {
+                const int pos = a.pos ? a.pos[rfirst + e] : rfirst + e;
+                drow[pos] = tile[d][r0 + e];
+            }
         }
     }
 }
@@ -110,11 +164,13 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
 
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st) {
     if (a.n <= 0) return hipSuccess;
-    dim3 grid((a.n + STORE_ROWS - 1) / STORE_ROWS, a.n_head_kv);
+    const int n_kblocks = (a.n * a.n_head_kv + 3) / 4;
+    const int n_vblocks = (a.n + VT_ROWS - 1) / VT_ROWS * (hd_tile / VT_D) * a.n_head_kv;
+    dim3 grid(n_kblocks + n_vblocks);
     switch (hd_tile) {
-        case 64: hipLaunchKernelGGL(kv_store_kernel<64>, grid, dim3(256), 0, st, a); break;
-        case 128: hipLaunchKernelGGL(kv_store_kernel<128>, grid, dim3(256), 0, st, a); break;
-        case 256: hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(256), 0, st, a); break;
+        case 64: hipLaunchKernelGGL(kv_store_kernel<64>, grid, dim3(256), 0, st, a, n_kblocks); break;
+        case 128: hipLaunchKernelGGL(kv_store_kernel<128>, grid, dim3(256), 0, st, a, n_kblocks); break;
+        case 256: hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(256), 0, st, a, n_kblocks); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -78,6 +78,8 @@ class CLaunchInfo(ctypes.Structure):
         ("waves_per_wg", ctypes.c_int),
         ("block_n", ctypes.c_int),
         ("head_dim_tile", ctypes.c_int),
+        ("row_blocks", ctypes.c_int),
+        ("key_groups", ctypes.c_int),
     ]
 
 
@@ -106,6 +108,7 @@ _SIGS = {
     "dr_ctx_destroy": (None, [_VP]),
     "dr_ctx_last_launch": (_I, [_VP, ctypes.POINTER(CLaunchInfo)]),
     "dr_ctx_set_split": (_I, [_VP, _I]),
+    "dr_ctx_set_tuning": (_I, [_VP, _I, _I, _I]),
     "dr_pass_create": (_I, [_VP, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
     "dr_pass_len": (_SZ, [_VP]),
@@ -272,6 +275,9 @@ class Context:
 
     def set_split(self, n_split: int) -> None:
         _check(self.lib.dr_ctx_set_split(self.h, n_split))
+
+    def set_tuning(self, row_blocks: int = 0, key_groups: int = 0, n_split: int = 0) -> None:
+        _check(self.lib.dr_ctx_set_tuning(self.h, row_blocks, key_groups, n_split))
 
     def last_launch(self) -> dict:
         info = CLaunchInfo()

@@ -196,19 +196,26 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
                         float q_norm_eps);
 
 /* Launch configuration of the last attention kernel this context enqueued
- * (for measurement): number of key splits, workgroups and waves per
- * workgroup, key tile size. */
+ * (for measurement): key splits across workgroups, workgroups, waves per
+ * workgroup, keys per tile, head-dim tile, 32-row query blocks and key
+ * groups per workgroup. */
 typedef struct {
     int n_split;
     int n_workgroups;
     int waves_per_wg;
     int block_n;
     int head_dim_tile;
+    int row_blocks;
+    int key_groups;
 } dr_launch_info;
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 
 /* Override the key-split heuristic for later calls on ctx (0 = automatic). */
 int dr_ctx_set_split(dr_ctx* ctx, int n_split);
+/* Override the workgroup shape (32-row query blocks x key groups) and the
+ * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
+ * to the automatic one. */
+int dr_ctx_set_tuning(dr_ctx* ctx, int row_blocks, int key_groups, int n_split);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,11 @@ from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, RowsSpec, Shape, closed_form, c
 
 pytestmark = pytest.mark.gpu
 
+try:  # import at collection: the first torch import on a fresh box is slow
+    import torch as _torch  # noqa: F401
+except ImportError:  # pragma: no cover
+    _torch = None
+
 
 def say(msg: str) -> None:
     print(msg, flush=True)
@@ -117,7 +122,11 @@ def test_gqa_equals_repeated_kv(torch):
 
 
 def test_block_diagonal_equals_separate(torch):
-    # tests.rs:70-102 at hd 128
+    """tests.rs:70-102 at hd 128: sequences batched in one call (seq ids) give
+    each sequence's separate answer.  The two GPU runs use different launch
+    plans (so bf16 rounding of P differs slightly); each is held to the parity
+    bar against the oracle of the separate problems, and any cross-sequence
+    leak would be O(0.1)."""
     rng = np.random.default_rng(22)
     hd, na, nb = 128, 37, 70
     n = na + nb
@@ -129,14 +138,18 @@ def test_block_diagonal_equals_separate(torch):
     S = lambda m: dr.AttnShape(m, m, 1, 1, hd, scale=0.09)  # noqa: E731
     bat = np.zeros(n * hd, np.float32)
     dr.attention(bat, q, k, v, S(n), dr.Rows(pos, seq), dr.Rows(pos, seq))
-    sa = np.zeros(na * hd, np.float32)
-    sb = np.zeros(nb * hd, np.float32)
-    dr.attention(sa, q[: na * hd].copy(), k[: na * hd].copy(), v[: na * hd].copy(), S(na),
-                 dr.idpos(na), dr.idpos(na))
-    dr.attention(sb, q[na * hd:].copy(), k[na * hd:].copy(), v[na * hd:].copy(), S(nb),
-                 dr.idpos(nb), dr.idpos(nb))
-    assert np.max(np.abs(bat[: na * hd] - sa)) < 1e-5
-    assert np.max(np.abs(bat[na * hd:] - sb)) < 1e-5
+    parts = []
+    for lo, m in ((0, na), (na, nb)):
+        sl = slice(lo * hd, (lo + m) * hd)
+        sep = np.zeros(m * hd, np.float32)
+        dr.attention(sep, q[sl].copy(), k[sl].copy(), v[sl].copy(), S(m), dr.idpos(m),
+                     dr.idpos(m))
+        want = oracle_run(Shape(m, m, 1, 1, hd, scale=0.09), RowsSpec(list(range(m))),
+                          RowsSpec(list(range(m))), q[sl].copy(), k[sl].copy(), v[sl].copy())
+        check(sep, want, f"separate rows {lo}..{lo + m}")
+        check(bat[sl], want, f"batched rows {lo}..{lo + m}")
+        parts.append(sep)
+    assert np.max(np.abs(bat - np.concatenate(parts))) < TOL_MAX
 
 
 def test_c1_dropin_vs_oracle(torch):
@@ -196,12 +209,6 @@ def test_no_visible_key_is_nan(torch):
 
 
 # ------------------------------------------------------------- cached path
-
-def _cfg_inputs(cfg, cfg_id, step=0):
-    rng = np.random.default_rng(config_seed(cfg_id, step))
-    kvs = cfg.n_head_kv * cfg.head_dim
-    return rng, kvs
-
 
 def _cached_problem(dev, cfg, cfg_id, batch=1, step=0):
     """Stores prompt + canvas K/V of `batch` streams and attends with the
