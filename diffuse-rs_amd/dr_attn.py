@@ -140,6 +140,15 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     if _LIB is not None and path is None:
         return _LIB
     p = pathlib.Path(path) if path else LIB_PATH
+    # torch ships its own HIP runtime under the soname libamdhip64.so.7.  When
+    # this library was loaded (and bound ROCm's copy of that runtime) before
+    # torch in the same process, torch then saw no GPU; loading torch first
+    # makes both use torch's runtime, and device pointers and streams are
+    # shared between them.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not p.exists():
         raise FileNotFoundError(
             f"{p} not built (run `python -c 'import __graft_entry__ as g; g.build()'`)")

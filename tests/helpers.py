@@ -133,6 +133,26 @@ def rms_norm_f64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     return x64 / r * np.asarray(w, dtype=np.float64)
 
 
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 (ties to even), returned as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+LOG2E = 1.4426950408889634
+
+
+def as_kernel_sees(q, k, v, scale: float):
+    """The operands the bf16 path multiplies, widened back to f32: K and V as
+    stored in the bf16 cache, Q as bf16(q * scale * log2 e) / (scale * log2 e).
+    The oracle on these isolates the kernel's own arithmetic (bf16 P, f32
+    accumulation) from the input rounding."""
+    c = np.float32(np.float32(scale) * np.float32(LOG2E))
+    qb = (bf16_round(np.asarray(q, np.float32) * c).astype(np.float64) / float(c)).astype(np.float32)
+    return qb, bf16_round(k), bf16_round(v)
+
+
 def normal(rng: np.random.Generator, *shape) -> np.ndarray:
     return rng.standard_normal(shape, dtype=np.float32)
 

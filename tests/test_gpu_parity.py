@@ -17,8 +17,8 @@ import pytest
 
 import dr_attn as dr
 import oracle as orc
-from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, RowsSpec, Shape, closed_form, config_seed,
-                     err_stats, golden_cases, materialise)
+from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, RowsSpec, Shape, as_kernel_sees, closed_form,
+                     config_seed, err_stats, golden_cases, materialise)
 
 pytestmark = pytest.mark.gpu
 
@@ -36,8 +36,9 @@ def say(msg: str) -> None:
 @pytest.fixture(scope="module")
 def torch():
     import torch as t
-    if dr.device_count() == 0 or not t.cuda.is_available():
-        pytest.skip("no GPU visible")
+    if not t.cuda.is_available() or dr.device_count() == 0:
+        pytest.skip(f"no GPU visible (torch: {t.cuda.is_available()}, "
+                    f"library: {dr.device_count()})")
     dr.load()  # raises if the library is not built: no fallback
     return t
 
@@ -189,7 +190,15 @@ def test_dropin_random_masks_vs_oracle(torch):
         got = np.zeros_like(want)
         dr.attention(got, q, k, v, dr.AttnShape(**s.__dict__), dr.Rows(qpos, seq_q),
                      dr.Rows(kpos, seq_k))
-        check(got, want, f"trial {trial}")
+        # Same inputs rounded as the kernel rounds them: the standard bar.
+        want_b = oracle_run(s, qr, kr, *as_kernel_sees(q, k, v, s.scale))
+        check(got, want_b, f"trial {trial} vs oracle on bf16 operands")
+        # Raw f32 inputs.  With windows of 3..60 keys and causal prompt rows
+        # that see a single key, an output averages only a few V rows, so the
+        # bf16 rounding of V (2^-9 relative, |v| <= ~4.5 -> <= 0.009) and of
+        # the scores (a ~0.3% weight shift times a V spread of ~6) does not
+        # average out as it does over hundreds of keys: max-abs <= 3e-2.
+        check(got, want, f"trial {trial} vs oracle on f32 inputs", tol_max=3e-2)
 
 
 def test_no_visible_key_is_nan(torch):

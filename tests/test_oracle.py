@@ -315,3 +315,16 @@ def test_split_active_vicinity_and_decay():
     for step, expect in ((4, [1]), (5, [1]), (6, [])):
         act, _ = orc.split_active(seq, last, seq, np.zeros(n, np.uint8), step)
         assert act == expect, step
+
+
+def test_bf16_round_known_values():
+    """The test-side bf16 rounding used to build the kernel's operand view:
+    ties go to even, and values already in bf16 are fixed points."""
+    from helpers import bf16_round
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1.0 + 2 ** -8 + 2 ** -20, -2.5, 0.0],
+                 np.float32)
+    want = np.array([1.0, 1.0, 1.0 + 2 ** -6, 1.0 + 2 ** -7, -2.5, 0.0], np.float32)
+    assert np.array_equal(bf16_round(x), want)
+    r = bf16_round(np.random.default_rng(0).standard_normal(1000).astype(np.float32))
+    assert np.array_equal(bf16_round(r), r)
+    assert np.all(r.view(np.uint32) & 0xFFFF == 0)
