@@ -8,41 +8,50 @@
 // Work decomposition.  Query rows of one KV head are cut into "row blocks"
 // of 32 rows (GQA: the `group` query heads of a KV head are packed into the
 // row dimension, so a K/V tile is read once for all of them).  A workgroup
-// owns RB row blocks and a range of key tiles, and runs RB x KQ waves: wave
-// (rb, kq) computes row block rb against every KQ-th tile of the range.  The
-// KQ tiles of a "super-tile" sit side by side in LDS, each shared by the RB
-// waves of its key group; at the end the KQ partial softmax states of a row
-// block are merged through LDS, which also stages the output so that it is
-// written with full-row, coalesced stores.  Optionally the key range is also
-// split across workgroups (n_split > 1), merged by attn_combine_kernel.
+// owns RB row blocks and a range of 32-key tiles, and runs RB x KQ waves:
+// wave (rb, kq) computes row block rb against every KQ-th tile of the range.
+// The KQ tiles of a "super-tile" sit side by side in LDS, each shared by the
+// RB waves of its key group, so one CU pulls each K/V byte from L2 once per
+// RB*32 query rows (L2 -> CU bandwidth is ~59 B/clk per CU on MI355X; with
+// 64 rows that is what the MFMAs consume).  At the end the KQ partial
+// softmax states of a row block are merged through LDS, which also stages
+// the output for full-row, coalesced stores.  When there are too few
+// workgroups to fill the chip the key range is also split across
+// workgroups (n_split > 1): each writes its partial rows, and the last one
+// to finish (an atomic ticket per row group) merges them.
 //
 // Per wave and 32-key block:
-//   S^T[key][q] = K Q^T    via v_mfma_f32_32x32x16_bf16, A = K (LDS),
-//                          B = the wave's Q^T fragments (registers)
-//   O^T[d][q]  += V^T P^T  via the same MFMA, A = V^T (LDS),
-//                          B = P^T straight from the S^T accumulators.
+//   S^T[key][q] = K Q^T - m  via v_mfma_f32_32x32x16_bf16, A = K (LDS),
+//                            B = Q^T fragments (registers), C = -m
+//   O^T[d][q]  += V^T P^T    via the same MFMA, A = V^T (LDS),
+//                            B = P^T straight from the S^T accumulators.
 // Computing the transposed products makes each lane own one query column, so
-// the softmax row statistics are per lane (plus one exchange with lane^32),
+// the softmax row statistics are per lane (lane and lane^32 share a column),
 // and P never leaves registers.  K rows are placed in LDS in a permuted order
 // (sigma below) chosen so that lane half `hf` ends up holding keys
 // 16*hf .. 16*hf+15 of every 32-key block, which is exactly the contiguous
 // 8-key run each half must supply as the B operand of the PV product.
 //
-// The softmax works in the log2 domain: Q is multiplied by scale*log2(e)
-// before rounding to bf16, p = exp2(s - m).  The running max is only moved
-// when it grows by more than 8 (p <= 256 is exact enough in bf16/f32), which
+// Softmax, log2 domain: Q is multiplied by scale*log2(e) before rounding to
+// bf16, and the running max m enters the QK^T product as its accumulator
+// init, so p = exp2(S) needs no subtraction.  m is only moved when a score
+// exceeds it by more than 8 (p <= 256 is exact enough in bf16/f32), which
 // skips the O rescale on almost every tile; O / l does not depend on the
-// choice of m.  l sums the bf16-rounded p that the PV product uses, so the
+// choice of m.  The first visible key of a column always sets m.  l sums the
+// bf16-rounded p that the PV product multiplies (v_dot2 with (1, 1)), so the
 // weights normalise exactly.  A row with no visible key ends with l = 0 and
 // writes 0 * (1/0) = NaN, like the reference (attention.rs:181-185).
 //
 // Memory: K is [kv head][key][HD] and V is stored transposed [kv head][d][key]
 // (the KV-cache layout written by kv_cache.hip).  Tiles move HBM -> LDS with
-// gfx950's global_load_lds_dwordx4 (16 bytes per lane, no VGPR staging),
-// NS super-tiles deep.  Each lane picks the global chunk that belongs at its
-// LDS slot, so the linear DMA writes produce the permuted, XOR-swizzled tile
-// image that keeps the MFMA operand reads (16 B per lane) free of bank
-// conflicts.
+// buffer_load_dwordx4 ... lds (16 bytes per lane, no VGPR staging), NS
+// super-tiles deep; the per-lane source offsets are loop invariant and the
+// tile base travels in a scalar register.  Each lane picks the global chunk
+// that belongs at its LDS slot, so the linear DMA writes produce the
+// permuted, XOR-swizzled tile image that keeps the MFMA operand reads
+// (16 B per lane) free of bank conflicts.  Q is loaded once per workgroup
+// (coalesced f32 rows, RMS-normalised when asked, scaled, rounded to bf16)
+// into the LDS of the last pipeline stage, before that stage is first used.
 #include "dr_internal.hpp"
 
 #include <limits.h>
@@ -52,11 +61,13 @@ namespace dr {
 namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+constexpr int BN = 32;                     // keys per tile (one MFMA key block)
 constexpr float RESCALE_THRESHOLD = 8.0f;  // log2 units
 
 // 16-byte-chunk swizzle for an LDS row holding CH chunks.  Keeps 8 (32-bank
@@ -93,14 +104,19 @@ __device__ __forceinline__ bool visible(int qpos, int kpos, int qseq, int kseq, 
     return same_seq & in_band & causal_ok;
 }
 
-// 16 bytes per lane global -> LDS (global_load_lds_dwordx4): lane i of the
-// wave writes lds_base + 16*i.  Kept in a __device__ helper: used directly in
-// a kernel body, the builtin makes the host compilation pass drop the
-// kernel's launch stub.
-__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(
-        (const __attribute__((address_space(1))) void*)src,
-        (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit
+// data format, no swizzle).  Loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane i
+// reads rsrc + soff + voff and writes lds_base + 16*i.  Kept in a __device__
+// helper: used directly in a kernel body, an LDS-DMA builtin made the host
+// compilation pass drop the kernel's launch stub.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds_base, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
+                                             16, voff, soff, 0, 0);
 }
 
 template <int N>
@@ -113,6 +129,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // instructions) issued after the current one are still in flight.
 template <int NI, int NS>
 __device__ __forceinline__ void wait_tiles(int pending) {
+    if constexpr (NS >= 4) {
+        if (pending >= 2) {
+            wait_vmcnt<2 * NI>();
+            return;
+        }
+    }
     if constexpr (NS >= 3) {
         if (pending >= 1) {
             wait_vmcnt<NI>();
@@ -122,11 +144,48 @@ __device__ __forceinline__ void wait_tiles(int pending) {
     wait_vmcnt<0>();
 }
 
-template <int HD, int BN, int RB, int KQ, int NS>
+// (head in group, query index) of packed row r = hg * nq + qi.  MHA rows are
+// the queries themselves; otherwise a float reciprocal estimate (exact to +-1
+// for r < 2^24) is corrected once, instead of an integer division.
+__device__ __forceinline__ void row_split(int r, int nq, float inv_nq, int group, int& hg,
+                                          int& qi) {
+    if (group == 1) {
+        hg = 0;
+        qi = r;
+        return;
+    }
+    int h = (int)((float)r * inv_nq);
+    int q = r - h * nq;
+    if (q < 0) {
+        --h;
+        q += nq;
+    } else if (q >= nq) {
+        ++h;
+        q -= nq;
+    }
+    hg = h;
+    qi = q;
+}
+
+// Agent-coherent 16-byte store / load (cache policy sc1: written through to,
+// and read from, the level every XCD shares), for the key-split partials.
+__device__ __forceinline__ void store16_coherent(__amdgpu_buffer_rsrc_t r, int voff, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, 0, 16);
+}
+__device__ __forceinline__ f32x4 load16_coherent(__amdgpu_buffer_rsrc_t r, int voff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16));
+}
+
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
+}
+
+template <int HD, int RB, int KQ, int NS, int NP>
 struct Geometry {
-    static constexpr int NW = RB * KQ;         // waves per workgroup
-    static constexpr int NT = NW * 64;
-    static constexpr int NB = BN / 32;         // 32-key blocks per tile
+    static constexpr int NW = RB * KQ;         // compute waves per workgroup
+    static constexpr int NWT = NW + NP;        // all waves (NP: DMA-only producer waves)
+    static constexpr int NT = NWT * 64;
+    static constexpr int NDMA = NP > 0 ? NP : NW;  // waves that issue the K/V DMA
     static constexpr int NC = HD / 16;         // QK^T contraction steps
     static constexpr int ND = HD / 32;         // 32-row blocks of O^T
     static constexpr int KCH = HD / 8;         // 16-byte chunks per K row
@@ -135,34 +194,54 @@ struct Geometry {
     static constexpr int SLOT = 2 * TILE;      // K tile then V^T tile
     static constexpr int STAGE = KQ * SLOT;    // one super-tile
     static constexpr int CPT = TILE / 8;       // 16-byte chunks per tile
-    static constexpr int NLDW = STAGE / 8 / NT;  // DMA instructions per wave per super-tile
+    static constexpr int NLDW = STAGE / 8 / (NDMA * 64);  // DMA instructions per DMA wave
+                                                          // and super-tile
+    static constexpr int QROWS = RB * 32;      // query rows per workgroup
     static constexpr int ROWF = HD + 4;        // f32 row pitch of the merge area
     static constexpr size_t STAGE_BYTES = (size_t)NS * STAGE * 2;
+    // Head dims up to 128 keep Q in LDS for the whole kernel and read its
+    // fragments per tile (registers go to the pipelined PV fragments); 256
+    // holds Q in registers and stages it in the last pipeline stage.
+    static constexpr bool QL = HD <= 128;
+    static constexpr size_t Q_BYTES = QL ? (size_t)QROWS * HD * 2 : 0;
     static constexpr size_t MERGE_BYTES = ((size_t)NW * 32 * ROWF + 2 * NW * 32) * 4;
-    static constexpr size_t LDS_BYTES = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
+    static constexpr size_t LDS_BYTES =
+        STAGE_BYTES + Q_BYTES > MERGE_BYTES ? STAGE_BYTES + Q_BYTES : MERGE_BYTES;
+    static constexpr int WAVES_PER_SIMD = (NWT + 3) / 4;
     static_assert(CPT % 64 == 0, "a DMA instruction must stay inside one tile");
-    static_assert(STAGE / 8 % NT == 0, "super-tile must split evenly over the waves");
-    static_assert(NLDW < 64, "vmcnt range");
+    static_assert(STAGE / 8 % (NDMA * 64) == 0, "super-tile must split evenly over the waves");
+    static_assert(NLDW * (NS - 1) < 64, "vmcnt range");
+    static_assert(QL || QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int HD, int BN, int RB, int KQ, int NS, int MODE, bool QNORM>
-__attribute__((amdgpu_waves_per_eu((RB * KQ + 3) / 4, (RB * KQ + 3) / 4))) __global__
-__launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
-    using G = Geometry<HD, BN, RB, KQ, NS>;
-    constexpr int NW = G::NW, NT = G::NT, NB = G::NB, NC = G::NC, ND = G::ND;
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM>
+__attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD,
+                                   Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD))) __global__
+__launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
+    using G = Geometry<HD, RB, KQ, NS, NP>;
+    constexpr int NW = G::NW, NWT = G::NWT, NT = G::NT, NC = G::NC, ND = G::ND;
     constexpr int KCH = G::KCH, VCH = G::VCH, TILE = G::TILE, SLOT = G::SLOT, STAGE = G::STAGE;
-    constexpr int CPT = G::CPT, NLDW = G::NLDW, ROWF = G::ROWF;
+    constexpr int CPT = G::CPT, NLDW = G::NLDW, ROWF = G::ROWF, QROWS = G::QROWS;
 
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    __shared__ int s_red[3][NW];
+    __shared__ int s_red[3][NWT];
+    __shared__ int s_last;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, hf = lane >> 5;
-    const int rb = wave % RB, kq = wave / RB;
+    // waves [0, NW) compute (row block rb, key group kq); with NP > 0 waves
+    // [NW, NW+NP) only move K/V tiles into LDS, so no compute wave ever
+    // stalls behind a memory instruction that the memory system cannot take
+    const bool compute = wave < NW;
+    const bool dma = NP == 0 || !compute;
+    const int dwave = NP > 0 ? wave - NW : wave;  // index among the DMA waves
+    const int rb = wave % RB, kq = (wave / RB) % KQ;
 
     // Workgroup -> (batch, kv head, row group, split).  The hardware deals
     // workgroups round-robin over the 8 XCDs; remapping keeps consecutive
-    // logical ids (same KV head, neighbouring splits) on one XCD's L2.
+    // logical ids (same row group, its splits) on one XCD's L2.
     const int nwg = gridDim.x;
     const int hw = blockIdx.x;
     const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
@@ -175,40 +254,13 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
     const AttnSlot& S = a.slot[b];
 
     const int rows_total = a.group * S.nq;
-    const int wg_row0 = rg * RB * 32;
-    if (wg_row0 >= rows_total) return;  // uniform over the workgroup and all splits
+    const int wg_row0 = rg * QROWS;
+    if (wg_row0 >= rows_total) return;  // uniform over the workgroup and all its splits
     const int r = wg_row0 + rb * 32 + col;
     const bool rvalid = r < rows_total;
-    const int hg = rvalid ? r / S.nq : 0;
-    const int qi = rvalid ? r - hg * S.nq : 0;
-    const int head = g * a.group + hg;
-
-    // ---- Q loads first (their latency overlaps the key-range work and DMA)
-    float x[NC][8];
-    {
-        const float* qrow =
-            static_cast<const float*>(S.q) + (size_t)qi * a.q_rstride + (size_t)head * a.hd;
-        if (rvalid && a.hd == HD) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const f32x4* p = reinterpret_cast<const f32x4*>(qrow + 16 * c + 8 * hf);
-                const f32x4 u = p[0], w = p[1];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[c][j] = u[j];
-                    x[c][4 + j] = w[j];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int d = 16 * c + 8 * hf + j;
-                    x[c][j] = (rvalid && d < a.hd) ? qrow[d] : 0.0f;
-                }
-        }
-    }
+    const float inv_nq = __builtin_amdgcn_rcpf((float)S.nq);
+    int hg = 0, qi = 0;
+    if (rvalid) row_split(r, S.nq, inv_nq, a.group, hg, qi);
 
     // ---- masking state and the key tile range of this workgroup
     int kt_lo = 0, kt_hi = (S.nk + BN - 1) / BN;
@@ -225,7 +277,7 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
         if (S.qpos_sorted && S.qprefix == nullptr) {
             // ascending positions: the extremes sit at the ends of the
             // workgroup's query range (the whole range if it spans heads)
-            const int r1 = min(wg_row0 + RB * 32, rows_total) - 1;
+            const int r1 = min(wg_row0 + QROWS, rows_total) - 1;
             const int h0 = wg_row0 / S.nq, h1 = r1 / S.nq;
             const int lo = h0 == h1 ? wg_row0 - h0 * S.nq : 0;
             const int hi = h0 == h1 ? r1 - h0 * S.nq : S.nq - 1;
@@ -252,7 +304,7 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
             qmax = INT_MIN;
             int anyp = 0;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
+            for (int w = 0; w < NWT; ++w) {
                 qmin = min(qmin, s_red[0][w]);
                 qmax = max(qmax, s_red[1][w]);
                 anyp |= s_red[2][w];
@@ -278,123 +330,252 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
     const int t1 = kt_lo + min((split + 1) * per, ntiles);
     const int nsup = (t1 - t0 + KQ - 1) / KQ;  // super-tiles
 
-    // ---- DMA plan of this lane: instruction j fills 64 chunks of one tile
-    // slot; slot and K/V side are uniform per instruction.
-    int doff[NLDW], dslot[NLDW];
-    bool disv[NLDW];
-#pragma unroll
-    for (int j = 0; j < NLDW; ++j) {
-        const int c0 = (wave * NLDW + j) * 64;  // first stage chunk of the instruction
-        const int region = c0 / CPT;
-        dslot[j] = region >> 1;
-        disv[j] = region & 1;
-        const int idx = c0 % CPT + lane;  // chunk within the tile
-        if (!disv[j]) {
+    // ---- DMA plan: instruction j of this wave fills 64 chunks of one tile
+    // region (region 2*i is K tile i of the super-tile, 2*i+1 its V^T tile).
+    // A wave's instructions cover whole regions or part of one, so the
+    // region of instruction j is the wave's first region plus a compile-time
+    // offset; the per-lane source offset (bytes from the tile base) is loop
+    // invariant and the tile base is a scalar.
+    constexpr bool WHOLE = (NLDW * 64) % CPT == 0;
+    static_assert(WHOLE || CPT % (NLDW * 64) == 0, "DMA split");
+    const int wreg0 = (dwave * NLDW * 64) / CPT;
+    auto voff_of = [&](int j) __attribute__((always_inline)) -> int {
+        const int jreg = WHOLE ? (j * 64) / CPT : 0;
+        const int idx = (WHOLE ? (j * 64) % CPT : (dwave * NLDW * 64) % CPT + j * 64) + lane;
+        if (((wreg0 + jreg) & 1) == 0) {
             const int R = idx / KCH, pk = idx % KCH;
-            doff[j] = ((R & ~31) + sigma(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3);
-        } else {
-            const int d = idx / VCH, pv = idx % VCH;
-            doff[j] = d * a.cap + ((pv ^ swz<VCH>(d)) << 3);
+            return (((R & ~31) + sigma(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3)) * 2;
         }
+        const int d = idx / VCH, pv = idx % VCH;
+        return (d * a.cap + ((pv ^ swz<VCH>(d)) << 3)) * 2;
+    };
+    // Compute waves that also issue DMA keep the offsets in registers; DMA
+    // waves recompute them per super-tile (they have the issue slots to
+    // spare, and the compute waves' registers stay free of them).
+    int voff[NP > 0 ? 1 : NLDW];
+    if constexpr (NP == 0) {
+#pragma unroll
+        for (int j = 0; j < NLDW; ++j) voff[j] = voff_of(j);
     }
-    const uint16_t* kbase = S.k + (size_t)g * a.cap * HD;
-    const uint16_t* vbase = S.vt + (size_t)g * HD * a.cap;
+    const uint32_t plane_bytes = (uint32_t)a.cap * HD * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k + (size_t)g * a.cap * HD, plane_bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vt + (size_t)g * HD * a.cap, plane_bytes);
 
-    auto issue = [&](int u, int st) {
-        uint16_t* stage = smem + st * STAGE + wave * NLDW * 512;
+    // DMA instructions [j0, j1) of super-tile u into stage st.
+    auto issue_range = [&](int u, int st, int j0, int j1) __attribute__((always_inline)) {
+        const int cofs = WHOLE ? 0 : (dwave * NLDW * 64) % CPT;  // first chunk in the region
 #pragma unroll
         for (int j = 0; j < NLDW; ++j) {
+            if (j < j0 || j >= j1) continue;
+            const int reg = wreg0 + (WHOLE ? (j * 64) / CPT : 0);
+            const int kqr = reg >> 1;
+            uint16_t* dst = smem + (kqr * NS + st) * SLOT + (reg & 1) * TILE +
+                            ((WHOLE ? (j * 64) % CPT : cofs + j * 64) << 3);
             // slots past the range reload the last tile: in bounds, unused
-            const int t = min(t0 + u * KQ + dslot[j], t1 - 1);
-            const uint16_t* src = disv[j] ? vbase + (size_t)t * BN : kbase + (size_t)t * BN * HD;
-            dma16(src + doff[j], stage + j * 512);
+            const int t = min(t0 + u * KQ + kqr, t1 - 1);
+            const int vo = NP > 0 ? voff_of(j) : voff[NP > 0 ? 0 : j];
+            if (reg & 1)
+                dma16(rv, dst, vo, t * (BN * 2));
+            else
+                dma16(rk, dst, vo, t * (BN * HD * 2));
         }
     };
+    auto issue = [&](int u, int st) __attribute__((always_inline)) {
+        issue_range(u, st, 0, NLDW);
+    };
 
+    // ---- Q: the workgroup's rows, loaded once (coalesced f32x4 row pieces,
+    // requested before the first K/V DMA: they gate the first MFMA),
+    // RMS-normalised when asked, times scale*log2(e), rounded to bf16 and
+    // stored in the B-operand layout in stage NS-1 (first written by the DMA
+    // of super-tile NS-1, issued after the barrier at the top of the loop).
+    constexpr int LPR = HD / 4;       // lanes per row (f32x4 each)
+    constexpr int RPI = 64 / LPR;     // rows per wave instruction
+    constexpr int RPW = QROWS / NWT;  // rows per wave
+    constexpr int QIT = RPW / RPI;
+    static_assert(RPW % RPI == 0, "Q rows must split evenly over the waves");
+    const int d0 = (lane % LPR) * 4;
+    f32x4 xq[QIT];
 #pragma unroll
-    for (int i = 0; i < NS - 1; ++i)
-        if (i < nsup) issue(i, i);
+    for (int it = 0; it < QIT; ++it) {
+        const int rr = wg_row0 + wave * RPW + it * RPI + lane / LPR;
+        const bool ok = rr < rows_total;
+        int hgq = 0, qiq = 0;
+        if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
+        const float* qrow = static_cast<const float*>(S.q) + (size_t)qiq * a.q_rstride +
+                            (size_t)(g * a.group + hgq) * a.hd;
+        if (ok && a.hd == HD) {
+            xq[it] = *reinterpret_cast<const f32x4*>(qrow + d0);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xq[it][e] = (ok && d0 + e < a.hd) ? qrow[d0 + e] : 0.0f;
+        }
+    }
 
-    // ---- Q fragments (B operand of S^T = K Q^T), scale*log2e folded in
-    bf16x8 qf[NC];
-    {
+    if (dma) {
+#pragma unroll
+        for (int i = 0; i < NS - 1; ++i)
+            if (i < nsup) issue(i, i);
+    }
+
+    uint16_t* qs = smem + (G::QL ? NS * STAGE : (NS - 1) * SLOT);
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+        f32x4 x = xq[it];
         if constexpr (QNORM) {
             // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
             double ss = 0.0;
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
+            for (int e = 0; e < 4; ++e) {
+                const float sq = x[e] * x[e];
+                ss += (double)sq;
+            }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float sq = x[c][j] * x[c][j];
-                    ss += (double)sq;
-                }
-            ss += __shfl_xor(ss, 32);
+            for (int off = 1; off < LPR; off <<= 1) ss += __shfl_xor(ss, off);
             const float sc = 1.0f / (float)sqrt(ss / (double)a.hd + (double)a.qn_eps);
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int d = 16 * c + 8 * hf + j;
-                    if (d < a.hd) x[c][j] = x[c][j] * sc * a.qn_w[d];
-                }
+            for (int e = 0; e < 4; ++e)
+                if (d0 + e < a.hd) x[e] = x[e] * sc * a.qn_w[d0 + e];
         }
+        bf16x4 y;
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
+        for (int e = 0; e < 4; ++e) y[e] = (__bf16)(x[e] * a.c);
+        const int lr = wave * RPW + it * RPI + lane / LPR;  // row within the workgroup
+        const int rl = lr & 31;  // row within its row block (the swizzle key)
+        *reinterpret_cast<bf16x4*>(qs + lr * HD + (((d0 >> 3) ^ swz<KCH>(rl)) << 3) + (d0 & 7)) =
+            y;
+    }
+    __syncthreads();
+    const uint16_t* qrow_l = qs + (rb * 32 + col) * HD;
+    auto qfrag = [&](int c) __attribute__((always_inline)) {
+        return *reinterpret_cast<const bf16x8*>(qrow_l + (((2 * c + hf) ^ swz<KCH>(col)) << 3));
+    };
+    bf16x8 qf[G::QL ? 1 : NC];
+    if constexpr (!G::QL) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qf[c][j] = (__bf16)(x[c][j] * a.c);
+        for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
     }
 
     // ---- main loop over super-tiles
     f32x16 o[ND];
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
+    // -m in every slot: the QK^T accumulator init, so the scores come out
+    // relative to m.  The pipelined head-dim-128 loop has no registers to
+    // spare for it and subtracts m from the scores instead.
+    constexpr bool MINIT = !(HD == 128);
+    f32x16 mneg = f32x16{};
+    float mu = 0.0f;          // running max m (log2 units), valid once m_set
+    bool m_set = false;
+    float thr = -INFINITY;    // a score above mu + thr moves m
+    float l_lo = 0.0f, l_hi = 0.0f;
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 
-    for (int u = 0; u < nsup; ++u) {
+    // O^T += V^T P^T for one tile whose V^T fragments and P are in registers.
+    // Contraction slot 8*hf + j of MFMA hh is key 16*hf + 8*hh + j, in both
+    // operands.
+    auto pv = [&](const bf16x8 (&vf)[ND][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pf[0], o[db], 0, 0, 0);
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pf[1], o[db], 0, 0, 0);
+        }
+    };
+
+    // One super-tile.  A compute wave software-pipelines its tiles: the PV
+    // product of its previous tile (V^T fragments and P kept in registers,
+    // pend_in) is issued right after this tile's QK^T MFMAs, so the softmax
+    // of this tile overlaps those MFMAs; this tile's V^T fragments and P are
+    // left in vout/pout (returns true) for the next step.  Without DMA waves
+    // (NP == 0) the DMA of super-tile u+NS-1 is issued in four parts spread
+    // over the compute, so that no wave stalls on a burst of memory
+    // instructions in front of its MFMAs.
+    // Head dim 256 keeps its accumulators in the whole register file: there
+    // the PV product is issued in the same step (no second fragment set).
+    constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
+    constexpr bool PIPE = HD <= 128;
+    auto step = [&](int u, bool pend_in, const bf16x8 (&vin)[ND][2], const bf16x8 (&pin)[2],
+                    bf16x8 (&vout)[ND][2], bf16x8 (&pout)[2])
+        __attribute__((always_inline)) -> bool {
         const int st = u % NS;
-        wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
-        __syncthreads();  // super-tile u visible to all waves; u-1 fully consumed
-        if (u + NS - 1 < nsup) issue(u + NS - 1, (u + NS - 1) % NS);
+        if (dma) wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
+        __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
+        const int un = u + NS - 1, stn = (u + NS - 1) % NS;
+        if constexpr (NP > 0) {
+            if (!compute) {
+                if (un < nsup) issue(un, stn);
+                return false;
+            }
+        }
+        const bool pf = NP == 0 && un < nsup;
 
         const int t = t0 + u * KQ + kq;
-        if (t >= t1) continue;  // this key group has no tile in the last super-tile
-        const uint16_t* ks = smem + st * STAGE + kq * SLOT;
+        if (t >= t1) {  // this key group has no tile in the last super-tile
+            if (pf) issue(un, stn);
+            if (pend_in) pv(vin, pin);
+            return false;
+        }
+        const uint16_t* ks = smem + (kq * NS + st) * SLOT;
         const uint16_t* vs = ks + TILE;
         const int kbase_t = t * BN;
 
         // per-key metadata (arbitrary key positions / ids): loaded per tile
-        int kp[NB][16], kqs[NB][16];
+        int kp[16], kqs[16];
         if constexpr (MODE == MASK_KEYS) {
 #pragma unroll
-            for (int kb = 0; kb < NB; ++kb)
+            for (int i = 0; i < 16; ++i) {
+                const int kidx = min(kbase_t + 16 * hf + i, S.nk - 1);
+                kp[i] = S.kpos ? S.kpos[kidx] : kidx;
+                kqs[i] = S.kseq ? S.kseq[kidx] : 0;
+            }
+        }
+        if (pf) issue_range(un, stn, 0, J1);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // S^T = K Q^T - m.  The K fragments are requested in two halves, the
+        // second while the MFMAs of the first run.
+        f32x16 s = MINIT ? mneg : f32x16{};
+        {
+            constexpr int NH = NC / 2;
+            const uint16_t* krow = ks + col * HD;
+            const int sw = swz<KCH>(col);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kidx = min(kbase_t + kb * 32 + 16 * hf + i, S.nk - 1);
-                    kp[kb][i] = S.kpos ? S.kpos[kidx] : kidx;
-                    kqs[kb][i] = S.kseq ? S.kseq[kidx] : 0;
+            for (int h = 0; h < 2; ++h) {
+                bf16x8 kf[NH], qh[G::QL ? NH : 1];
+#pragma unroll
+                for (int c = 0; c < NH; ++c) {
+                    kf[c] = *reinterpret_cast<const bf16x8*>(
+                        krow + (((2 * (h * NH + c) + hf) ^ sw) << 3));
+                    if constexpr (G::QL) qh[c] = qfrag(h * NH + c);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int c = 0; c < NH; ++c)
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        kf[c], G::QL ? qh[G::QL ? c : 0] : qf[G::QL ? 0 : h * NH + c], s, 0, 0, 0);
+            }
+        }
+        if (pend_in) pv(vin, pin);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!MINIT) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] -= mu;
         }
 
-        // S^T = K Q^T.  All K fragments of a 32-key block are read before its
-        // MFMAs so the LDS latency is paid once per block, not per MFMA.
-        f32x16 sacc[NB];
+        // this tile's V^T fragments (for the next step's PV product)
 #pragma unroll
-        for (int kb = 0; kb < NB; ++kb) {
-            const int R = kb * 32 + col;
-            const uint16_t* krow = ks + R * HD;
-            const int sw = swz<KCH>(R);
-            bf16x8 kf[NC];
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                kf[c] = *reinterpret_cast<const bf16x8*>(krow + (((2 * c + hf) ^ sw) << 3));
-            sacc[kb] = f32x16{};
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[c], sacc[kb], 0, 0, 0);
+        for (int db = 0; db < ND; ++db) {
+            const int d = db * 32 + col;
+            const uint16_t* vrow = vs + d * BN;
+            const int sw = swz<VCH>(d);
+            vout[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
+            vout[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (pf) issue_range(un, stn, J1, J2);
+        __builtin_amdgcn_sched_barrier(0);
 
-        // Masking: sacc[kb][i] is the score of key t*BN + kb*32 + 16*hf + i.
+        // Masking: s[i] is the score of key t*BN + 16*hf + i.
         bool full = kbase_t + BN <= S.nk;
         if constexpr (MODE == MASK_POS) {
             const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
@@ -405,95 +586,104 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
         }
         if (!full) {
 #pragma unroll
-            for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kidx = kbase_t + kb * 32 + 16 * hf + i;
-                    bool vis = kidx < S.nk;
-                    if constexpr (MODE == MASK_POS) {
-                        vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
-                    } else if constexpr (MODE == MASK_KEYS) {
-                        vis = vis & visible(my_qpos, kp[kb][i], my_qseq, kqs[kb][i], a.window,
-                                            my_pref);
-                    }
-                    sacc[kb][i] = vis ? sacc[kb][i] : -INFINITY;
+            for (int i = 0; i < 16; ++i) {
+                const int kidx = kbase_t + 16 * hf + i;
+                bool vis = kidx < S.nk;
+                if constexpr (MODE == MASK_POS) {
+                    vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                } else if constexpr (MODE == MASK_KEYS) {
+                    vis = vis & visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
                 }
-        }
-
-        // Online softmax with a lazily moved max.
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const bool need = (m_new - m_run) > RESCALE_THRESHOLD;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-            if (need) {
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < ND; ++db) o[db] *= alpha;
-                m_run = m_new;
+                s[i] = vis ? s[i] : -INFINITY;
             }
         }
-        const float mu = (m_run == -INFINITY) ? 0.0f : m_run;
-        // p = exp2(s - m) rounded to bf16 in pairs; l sums the rounded values
+
+        // Online softmax with a lazily moved max (scores are relative to mu).
+        float mx = max3(s[0], s[1], s[2]);
+#pragma unroll
+        for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
+        mx = __builtin_fmaxf(mx, s[15]);
+        if (__builtin_amdgcn_ballot_w64(mx > thr)) {
+            // the column max over both lane halves decides, so lane and
+            // lane^32 move m together; O (including the previous tile's PV
+            // product, issued above at the old m) is rescaled
+            const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+            const bool upd = cm > thr;
+            const float delta = upd ? cm : 0.0f;
+            const float alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+            mu += delta;
+            m_set = m_set | upd;
+            thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] -= delta;
+            if constexpr (MINIT) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mneg[i] = -mu;
+            }
+            l_lo *= alpha;
+            l_hi *= alpha;
+#pragma unroll
+            for (int db = 0; db < ND; ++db) o[db] *= alpha;
+        }
+
+        // p = exp2(s) rounded to bf16 in pairs; l sums the rounded values
         // (what the PV product multiplies), so the weights normalise exactly.
-        bf16x8 pf[NB][2];
 #pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
+        for (int hh = 0; hh < 2; ++hh) {
+            u32x4 w4;
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                u32x4 w4;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p0 = __builtin_amdgcn_exp2f(sacc[kb][8 * hh + 2 * j] - mu);
-                    const float p1 = __builtin_amdgcn_exp2f(sacc[kb][8 * hh + 2 * j + 1] - mu);
-                    const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
-                    w4[j] = __builtin_bit_cast(uint32_t, pr);
-                    l_run += __uint_as_float(w4[j] << 16) + __uint_as_float(w4[j] & 0xffff0000u);
-                }
-                pf[kb][hh] = __builtin_bit_cast(bf16x8, w4);
+            for (int j = 0; j < 4; ++j) {
+                const float p0 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j]);
+                const float p1 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j + 1]);
+                const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
+                w4[j] = __builtin_bit_cast(uint32_t, pr);
+                if (hh == 0)
+                    l_lo = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_lo, false);
+                else
+                    l_hi = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_hi, false);
             }
+            pout[hh] = __builtin_bit_cast(bf16x8, w4);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (pf) issue_range(un, stn, J2, NLDW);
+        if constexpr (!PIPE) {
+            pv(vout, pout);
+            return false;
+        }
+        return true;
+    };
 
-        // O^T += V^T P^T.  Contraction slot 8*hf + j of MFMA (kb, hh) is key
-        // kb*32 + 16*hf + 8*hh + j, in both operands.
-#pragma unroll
-        for (int db = 0; db < ND; ++db) {
-            const int d = db * 32 + col;
-            const uint16_t* vrow = vs + d * BN;
-            const int sw = swz<VCH>(d);
-            bf16x8 vf[NB][2];
-#pragma unroll
-            for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-                    vf[kb][hh] = *reinterpret_cast<const bf16x8*>(
-                        vrow + (((4 * kb + 2 * hf + hh) ^ sw) << 3));
-#pragma unroll
-            for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kb][hh], pf[kb][hh], o[db],
-                                                                    0, 0, 0);
+    {
+        bf16x8 vfa[ND][2], vfb[ND][2], pfa[2], pfb[2];
+        bool pend = false;
+        int u = 0;
+        for (; u + 1 < nsup; u += 2) {
+            pend = step(u, pend, vfa, pfa, vfb, pfb);
+            pend = step(u + 1, pend, vfb, pfb, vfa, pfa);
+        }
+        if (u < nsup) {
+            pend = step(u, pend, vfa, pfa, vfb, pfb);
+            if (pend) pv(vfb, pfb);
+        } else if (pend) {
+            pv(vfa, pfa);
         }
     }
 
-    // ---- merge the KQ key groups of each row block through LDS and write
+    // ---- merge the KQ key groups of each row block through LDS
+    const float l_run = l_lo + l_hi;
     const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float m_fin = m_set ? mu : -INFINITY;
     __syncthreads();  // every wave is done with the tile stages
     float* mrows = reinterpret_cast<float*>(smem);  // [NW][32][ROWF]
     float* sm = mrows + NW * 32 * ROWF;             // [NW][32] running max
     float* sl = sm + NW * 32;                       // [NW][32] scaled sum
-    if (hf == 0) sm[wave * 32 + col] = m_run;
+    if (compute && hf == 0) sm[wave * 32 + col] = m_fin;
     __syncthreads();
-    float M = -INFINITY;
+    if (compute) {
+        float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < KQ; ++k) M = fmaxf(M, sm[(k * RB + rb) * 32 + col]);
-    const float sc = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-    {
+        for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + col]);
+        const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
         // o[db][4j + e] is O^T[d = db*32 + 8j + 4hf + e][col]
         float* myrow = mrows + (wave * 32 + col) * ROWF;
 #pragma unroll
@@ -510,13 +700,49 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
     __syncthreads();
 
     constexpr int CHUNKS = HD / 4;
-    const size_t rows_pad = (size_t)a.rowgroups * RB * 32;
+    const size_t rows_pad = (size_t)a.rowgroups * QROWS;
     const size_t bg = (size_t)b * a.n_head_kv + g;
-    for (int item = tid; item < RB * 32 * CHUNKS; item += NT) {
+    if (a.n_split == 1) {
+        for (int item = tid; item < QROWS * CHUNKS; item += NT) {
+            const int rr = item / CHUNKS, ch = item % CHUNKS;
+            const int rbi = rr >> 5, ci = rr & 31;
+            const int rglob = wg_row0 + rr;
+            if (rglob >= rows_total) continue;
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            float L = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KQ; ++k) {
+                const int wi = k * RB + rbi;
+                acc += *reinterpret_cast<const f32x4*>(mrows + (wi * 32 + ci) * ROWF + ch * 4);
+                L += sl[wi * 32 + ci];
+            }
+            const int c0 = ch * 4;
+            int hgi, qii;
+            row_split(rglob, S.nq, inv_nq, a.group, hgi, qii);
+            float* orow = S.out + (size_t)qii * a.o_rstride + (size_t)(g * a.group + hgi) * a.hd;
+            const f32x4 val = acc * __builtin_amdgcn_rcpf(L);
+            if (a.hd == HD) {
+                *reinterpret_cast<f32x4*>(orow + c0) = val;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c0 + e < a.hd) orow[c0 + e] = val[e];
+            }
+        }
+        return;
+    }
+
+    // ---- key split: publish this split's partial rows, then the last of the
+    // n_split workgroups of the row group merges all of them.  The partials
+    // are written and read with agent-coherent (sc1) accesses and each wave
+    // waits for its writes to complete before the ticket moves, so the merge
+    // needs no cache-wide writeback or invalidate and works whichever XCDs
+    // the splits ran on.
+    const size_t plane = (size_t)a.n_batch * a.n_head_kv * rows_pad;  // rows per split
+    const uint32_t plane_o_bytes = (uint32_t)(plane * HD * 4);
+    for (int item = tid; item < QROWS * CHUNKS; item += NT) {
         const int rr = item / CHUNKS, ch = item % CHUNKS;
         const int rbi = rr >> 5, ci = rr & 31;
-        const int rglob = wg_row0 + rr;
-        if (rglob >= rows_total) continue;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
         float L = 0.0f, Mrow = -INFINITY;
 #pragma unroll
@@ -524,156 +750,132 @@ __launch_bounds__(RB * KQ * 64) void attn_fwd_kernel(const AttnArgs a) {
             const int wi = k * RB + rbi;
             acc += *reinterpret_cast<const f32x4*>(mrows + (wi * 32 + ci) * ROWF + ch * 4);
             L += sl[wi * 32 + ci];
-            Mrow = fmaxf(Mrow, sm[wi * 32 + ci]);
+            Mrow = __builtin_fmaxf(Mrow, sm[wi * 32 + ci]);
         }
-        const int d0 = ch * 4;
-        if (a.n_split == 1) {
-            const int hgi = rglob / S.nq, qii = rglob - hgi * S.nq;
-            float* orow = S.out + (size_t)qii * a.o_rstride + (size_t)(g * a.group + hgi) * a.hd;
-            const f32x4 val = acc * (1.0f / L);
-            if (a.hd == HD) {
-                *reinterpret_cast<f32x4*>(orow + d0) = val;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (d0 + e < a.hd) orow[d0 + e] = val[e];
-            }
+        const size_t prow = bg * rows_pad + wg_row0 + rr;  // row within a split plane
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o + split * plane * HD, plane_o_bytes);
+        store16_coherent(ro, (int)((prow * HD + ch * 4) * 4), acc);
+        if (ch == 0) {
+            float* ml = a.part_ml + (split * plane + prow) * 2;
+            __hip_atomic_store(ml, Mrow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    wait_vmcnt<0>();  // this wave's partial rows are complete at the coherent level
+    __syncthreads();
+    if (tid == 0) {
+        int* ticket = a.tickets + bg * a.rowgroups + rg;
+        const int prev =
+            __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == a.n_split - 1;
+        if (last) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    for (int item = tid; item < QROWS * CHUNKS; item += NT) {
+        const int rr = item / CHUNKS, ch = item % CHUNKS;
+        const int rglob = wg_row0 + rr;
+        if (rglob >= rows_total) continue;
+        const size_t prow = bg * rows_pad + rglob;
+        float Mx = -INFINITY;
+        for (int sp = 0; sp < a.n_split; ++sp)
+            Mx = __builtin_fmaxf(Mx, __hip_atomic_load(a.part_ml + (sp * plane + prow) * 2,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+        for (int sp = 0; sp < a.n_split; ++sp) {
+            const float* ml = a.part_ml + (sp * plane + prow) * 2;
+            const float ms = __hip_atomic_load(ml, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float ls = __hip_atomic_load(ml + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float w = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - Mx);
+            L += w * ls;
+            const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o + sp * plane * HD, plane_o_bytes);
+            acc += w * load16_coherent(ro, (int)((prow * HD + ch * 4) * 4));
+        }
+        const int c0 = ch * 4;
+        int hgi, qii;
+        row_split(rglob, S.nq, inv_nq, a.group, hgi, qii);
+        float* orow = S.out + (size_t)qii * a.o_rstride + (size_t)(g * a.group + hgi) * a.hd;
+        const f32x4 val = acc * __builtin_amdgcn_rcpf(L);
+        if (a.hd == HD) {
+            *reinterpret_cast<f32x4*>(orow + c0) = val;
         } else {
-            const size_t prow =
-                ((size_t)split * a.n_batch * a.n_head_kv + bg) * rows_pad + rglob;
-            *reinterpret_cast<f32x4*>(a.part_o + prow * HD + d0) = acc;
-            if (ch == 0) {
-                a.part_ml[prow * 2] = Mrow;
-                a.part_ml[prow * 2 + 1] = L;
-            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c0 + e < a.hd) orow[c0 + e] = val[e];
         }
     }
 }
 
-// Merges the key-split partials: M = max m_s, L = sum l_s 2^(m_s - M),
-// O = sum O_s 2^(m_s - M) / L.  One thread per 4 consecutive output values;
-// the workgroups of a row group run on the XCD whose L2 holds its partials.
-template <int HD>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const CombineArgs a, int rows_per_rg) {
-    constexpr int CH = HD / 4;
-    const int nwg = gridDim.x;
-    const int hw = blockIdx.x;
-    const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
-    const int c_in_rg = lid % a.wg_per_rowgroup;
-    const int rgi = lid / a.wg_per_rowgroup;  // (batch, kv head, row group)
-    const int rg = rgi % a.rowgroups;
-    const int bg = rgi / a.rowgroups;
-    const int b = bg / a.n_head_kv, g = bg % a.n_head_kv;
-    const int item = c_in_rg * 256 + threadIdx.x;
-    if (item >= rows_per_rg * CH) return;
-    const int r = rg * rows_per_rg + item / CH;
-    const int chunk = item % CH;
-    const AttnSlot& S = a.slot[b];
-    if (r >= a.group * S.nq) return;
-    const int hg = r / S.nq, qi = r - hg * S.nq;
-    const int head = g * a.group + hg;
-
-    const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.rows_pad;  // rows per split
-    const size_t prow = (size_t)bg * a.rows_pad + r;
-    float M = -INFINITY;
-    for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, a.part_ml[(s * plane + prow) * 2]);
-    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    float L = 0.0f;
-    for (int s = 0; s < a.n_split; ++s) {
-        const float ms = a.part_ml[(s * plane + prow) * 2];
-        const float w = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-        L += w * a.part_ml[(s * plane + prow) * 2 + 1];
-        const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + (s * plane + prow) * HD +
-                                                        chunk * 4);
-        o += w * v;
-    }
-    const float inv = 1.0f / L;
-    float* orow = S.out + (size_t)qi * a.o_rstride + (size_t)head * a.hd;
-    const int d0 = chunk * 4;
-    if (a.hd == HD) {
-        *reinterpret_cast<f32x4*>(orow + d0) = o * inv;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (d0 + e < a.hd) orow[d0 + e] = o[e] * inv;
-    }
+// Fills n ints with zero (the split tickets; a kernel rather than a memset so
+// that it may sit in a captured graph).
+__global__ __launch_bounds__(256) void zero_ints_kernel(int* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
 }
 
-template <int HD, int BN, int RB, int KQ, int NS, int MODE, bool QNORM>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM>
 hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    constexpr size_t lds = Geometry<HD, BN, RB, KQ, NS>::LDS_BYTES;
+    constexpr size_t lds = Geometry<HD, RB, KQ, NS, NP>::LDS_BYTES;
     static bool attr_set = false;
-    auto fn = attn_fwd_kernel<HD, BN, RB, KQ, NS, MODE, QNORM>;
+    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QNORM>;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(RB * KQ * 64), lds, st, a);
+    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3((RB * KQ + NP) * 64), lds, st, a);
     return hipGetLastError();
 }
 
-template <int HD, int BN, int RB, int KQ, int NS>
+template <int HD, int RB, int KQ, int NS, int NP>
 hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     switch (p.mask) {
         case MASK_NONE:
-            return p.qnorm ? launch_fwd<HD, BN, RB, KQ, NS, MASK_NONE, true>(p, a, st)
-                           : launch_fwd<HD, BN, RB, KQ, NS, MASK_NONE, false>(p, a, st);
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false>(p, a, st);
         case MASK_POS:
-            return p.qnorm ? launch_fwd<HD, BN, RB, KQ, NS, MASK_POS, true>(p, a, st)
-                           : launch_fwd<HD, BN, RB, KQ, NS, MASK_POS, false>(p, a, st);
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false>(p, a, st);
         default:
-            return launch_fwd<HD, BN, RB, KQ, NS, MASK_KEYS, false>(p, a, st);
+            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false>(p, a, st);
     }
 }
 
-// The (RB, KQ) shapes built for each head-dim tile (all with 32-key tiles).
-// LDS per workgroup: NS super-tiles of KQ x (K + V^T) tiles.
-//   HD  64: (1,4) (2,4)  NS 3     HD 128: (1,4) (2,4) (2,2)  NS 2
-//   HD 256: (1,2) (2,2)  NS 2
-bool shape_built(int hd_tile, int rb, int kq) {
-    switch (hd_tile) {
-        case 64: return (rb == 1 || rb == 2) && kq == 4;
-        case 128: return (rb == 1 && kq == 4) || (rb == 2 && (kq == 4 || kq == 2));
-        case 256: return (rb == 1 || rb == 2) && kq == 2;
-        default: return false;
-    }
+// The workgroup shapes built for each head-dim tile: RB row blocks x KQ key
+// groups of compute waves, NP DMA-only waves, NS pipeline stages (super-tiles
+// of KQ x (K + V^T) tiles of 32 keys).
+struct Shape {
+    int hd, rb, kq, ns, np;
+};
+constexpr Shape SHAPES[] = {
+    {64, 1, 4, 3, 4}, {64, 2, 2, 4, 4}, {64, 2, 4, 3, 0},
+    {128, 1, 4, 2, 4}, {128, 2, 2, 4, 4}, {128, 2, 4, 2, 0},
+    {256, 2, 2, 2, 0}, {256, 1, 2, 2, 0},  // one wave per SIMD: 512 VGPRs
+};
+
+const Shape* find_shape(int hd_tile, int rb, int kq) {
+    for (const Shape& s : SHAPES)
+        if (s.hd == hd_tile && s.rb == rb && s.kq == kq) return &s;
+    return nullptr;
 }
 
 hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     const int key = p.hd_tile * 100 + p.rb * 10 + p.kq;
     switch (key) {
-        case 6414: return launch_modes<64, 32, 1, 4, 3>(p, a, st);
-        case 6424: return launch_modes<64, 32, 2, 4, 3>(p, a, st);
-        case 12814: return launch_modes<128, 32, 1, 4, 2>(p, a, st);
-        case 12824: return launch_modes<128, 32, 2, 4, 2>(p, a, st);
-        case 12822: return launch_modes<128, 32, 2, 2, 2>(p, a, st);
-        case 25612: return launch_modes<256, 32, 1, 2, 2>(p, a, st);
-        case 25622: return launch_modes<256, 32, 2, 2, 2>(p, a, st);
+        case 6414: return launch_modes<64, 1, 4, 3, 4>(p, a, st);
+        case 6422: return launch_modes<64, 2, 2, 4, 4>(p, a, st);
+        case 6424: return launch_modes<64, 2, 4, 3, 0>(p, a, st);
+        case 12814: return launch_modes<128, 1, 4, 2, 4>(p, a, st);
+        case 12822: return launch_modes<128, 2, 2, 4, 4>(p, a, st);
+        case 12824: return launch_modes<128, 2, 4, 2, 0>(p, a, st);
+        case 25622: return launch_modes<256, 2, 2, 2, 0>(p, a, st);
+        case 25612: return launch_modes<256, 1, 2, 2, 0>(p, a, st);
         default: return hipErrorInvalidValue;
     }
-}
-
-template <int HD>
-hipError_t launch_combine(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    CombineArgs c;
-    for (int i = 0; i < MAX_BATCH; ++i) c.slot[i] = a.slot[i];
-    c.n_batch = a.n_batch;
-    c.n_head_kv = a.n_head_kv;
-    c.group = a.group;
-    c.hd = a.hd;
-    c.o_rstride = a.o_rstride;
-    c.rows_pad = a.rowgroups * p.rb * 32;
-    c.rowgroups = a.rowgroups;
-    c.n_split = a.n_split;
-    c.part_o = a.part_o;
-    c.part_ml = a.part_ml;
-    const int rows_per_rg = p.rb * 32;
-    c.wg_per_rowgroup = (rows_per_rg * (HD / 4) + 255) / 256;
-    const int nwg = a.n_batch * a.n_head_kv * a.rowgroups * c.wg_per_rowgroup;
-    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3(nwg), dim3(256), 0, st, c, rows_per_rg);
-    return hipGetLastError();
 }
 
 }  // namespace
@@ -683,38 +885,41 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
                           int force_split) {
     LaunchPlan p;
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : 256);
-    p.block_n = 32;
+    p.block_n = BN;
     p.mask = mask;
     p.qnorm = qnorm && mask != MASK_KEYS;
     const int cus = n_cu > 0 ? n_cu : 256;
     const int row_blocks = (group * max_nq + 31) / 32;  // per (batch, kv head)
-    const int ntiles = (max_nk + p.block_n - 1) / p.block_n;
-    const int kq_full = p.hd_tile == 256 ? 2 : 4;
-    // Prefer two row blocks per workgroup (halves the K/V traffic per row)
-    // when that still gives every CU a workgroup; otherwise one.
-    int rb = (n_batch * n_head_kv * ((row_blocks + 1) / 2) >= cus) ? 2 : 1;
-    int kq = kq_full;
+    const int ntiles = (max_nk + BN - 1) / BN;
+    // Head dims up to 128: one row block of four key groups with four DMA
+    // waves (two waves per SIMD).  256: two row blocks of two key groups,
+    // one wave per SIMD (the accumulators need the whole register file).
+    int rb = 1;
+    int kq = p.hd_tile == 256 ? 2 : 4;
+    if (p.hd_tile == 256 && row_blocks >= 2) rb = 2;
     if (force_rb > 0) rb = force_rb;
     if (force_kq > 0) kq = force_kq;
-    if (!shape_built(p.hd_tile, rb, kq)) {
-        rb = 1;
-        kq = kq_full;
+    const Shape* sh = find_shape(p.hd_tile, rb, kq);
+    if (!sh) {
+        rb = p.hd_tile == 256 && row_blocks >= 2 ? 2 : 1;
+        kq = p.hd_tile == 256 ? 2 : 4;
+        sh = find_shape(p.hd_tile, rb, kq);
     }
     p.rb = rb;
     p.kq = kq;
-    p.waves = rb * kq;
-    p.stages = p.hd_tile == 64 ? 3 : 2;
+    p.waves = rb * kq + sh->np;
+    p.stages = sh->ns;
     p.rowgroups = (row_blocks + rb - 1) / rb;
     if (p.rowgroups < 1) p.rowgroups = 1;
     const int base = n_batch * n_head_kv * p.rowgroups;
     int split = 1;
     if (force_split > 0) {
         split = force_split;
-    } else if (base < cus / 2) {
-        // Too few workgroups to fill the chip: split the keys, keeping at
-        // least two super-tiles per split.
-        split = (cus + base - 1) / base;
-        const int max_split = ntiles / (2 * kq) > 1 ? ntiles / (2 * kq) : 1;
+    } else if (2 * base <= cus) {
+        // Too few workgroups to fill the chip (one workgroup per CU): split
+        // the keys, keeping at least one super-tile per split.
+        split = cus / base;
+        const int max_split = ntiles / kq > 1 ? ntiles / kq : 1;
         if (split > max_split) split = max_split;
     }
     if (split < 1) split = 1;
@@ -729,6 +934,17 @@ size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv) {
     return (size_t)p.n_split * rows * ((size_t)p.hd_tile + 2) * sizeof(float);
 }
 
+size_t split_ticket_count(const LaunchPlan& p, int n_batch, int n_head_kv) {
+    return p.n_split <= 1 ? 0 : (size_t)n_batch * n_head_kv * p.rowgroups;
+}
+
+hipError_t zero_ints(int* p, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p,
+                       (int)n);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.rowgroups = p.rowgroups;
     a.n_split = p.n_split;
@@ -736,13 +952,7 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
         const size_t rows = (size_t)a.n_batch * a.n_head_kv * p.rowgroups * p.rb * 32;
         a.part_ml = a.part_o + (size_t)p.n_split * rows * p.hd_tile;
     }
-    hipError_t e = launch_shape(p, a, st);
-    if (e != hipSuccess || p.n_split == 1) return e;
-    switch (p.hd_tile) {
-        case 64: return launch_combine<64>(p, a, st);
-        case 128: return launch_combine<128>(p, a, st);
-        default: return launch_combine<256>(p, a, st);
-    }
+    return launch_shape(p, a, st);
 }
 
 }  // namespace dr

@@ -47,20 +47,8 @@ struct AttnArgs {
     int n_split;                   // key splits; > 1 writes partials
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
-};
-
-// Merge of the key-split partials (attn_combine_kernel).
-struct CombineArgs {
-    AttnSlot slot[MAX_BATCH];
-    int n_batch;
-    int n_head_kv, group, hd;
-    int o_rstride;
-    int rows_pad;                  // partial rows per (batch, kv head) = rowgroups * rb * 32
-    int rowgroups;
-    int wg_per_rowgroup;
-    int n_split;
-    const float* part_o;
-    const float* part_ml;
+    int* tickets;                  // [batch*kv head][rowgroups] arrival counters, zero
+                                   // between launches (the last arriver resets its own)
 };
 
 struct StoreArgs {
@@ -103,7 +91,7 @@ struct LaunchPlan {
     int kq;          // key groups per workgroup (merged in LDS)
     int waves;       // rb * kq
     int stages;      // LDS pipeline depth (super-tiles of kq tiles)
-    int n_split;     // key splits across workgroups (merged by attn_combine_kernel)
+    int n_split;     // key splits across workgroups (merged by the last one to finish)
     int rowgroups;   // workgroups per (batch, kv head) and split
     int n_workgroups;
     int mask;        // MaskMode
@@ -117,8 +105,11 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
                           int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
                           int force_split);
 
-// Bytes of split workspace a plan needs (part_o + part_ml).
+// Bytes of split workspace a plan needs (part_o + part_ml), and the number
+// of int tickets (which must be zero before the first launch).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
+size_t split_ticket_count(const LaunchPlan& p, int n_batch, int n_head_kv);
+hipError_t zero_ints(int* p, size_t n, hipStream_t st);
 
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
