@@ -10,13 +10,17 @@ all 768 keys (the attention_block sequence of forward.rs:312-343).  Inputs
 (16 distinct canvas sets, f32 N(0,1), seeded) are resident in HBM before the
 timed region.
 
-value = algorithmic attention FLOPs of K steps / wall time of the K steps,
-FLOPs = 4 * h * hd * sum_q |visible keys| = 3.221 GFLOP per step (softmax,
-masking and the store excluded).  roofline = the attention kernel alone:
-the same FLOPs / its average duration measured with HIP events on the
-library's stream, against 2516.6 TFLOP/s dense bf16 MFMA.  cpu_baseline =
-the C restatement of the reference's AVX2 attention (oracle/, "port") timed on
-this host's cores on a bounded sample of the same workload.
+value = algorithmic attention FLOPs of K steps / wall time of the K steps
+(graph replays of 16 steps each), FLOPs = 4 * h * hd * sum_q |visible keys| =
+3.221 GFLOP per step (softmax, masking and the store excluded).  roofline =
+the attention kernel alone: the same FLOPs / its mean launch duration, timed
+with HIP events on the library's stream around graph replays of 16
+back-to-back attention calls, against 2516.6 TFLOP/s dense bf16 MFMA; its
+traffic is the HBM bytes per launch from the rocprofv3 FETCH_SIZE /
+WRITE_SIZE record in profiles/.  other_configs_attention_only = the same
+attention-only timing for configs[2..4].  cpu_baseline = the C restatement of
+the reference's AVX2 attention (oracle/, "port") timed on this host's cores on
+a bounded sample of the same workload; its output also checks the GPU result.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode eager|graph]
 """
@@ -60,6 +64,71 @@ def measured_traffic():
     return None, None
 
 
+def attention_only_ms(torch, stream, call, n_calls: int, reps: int):
+    """Mean duration of one call(i), i < n_calls: the calls are captured in a
+    graph, replayed `reps` times between two events on `stream`."""
+    with torch.cuda.stream(stream):
+        for i in range(n_calls):
+            call(i)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+        for i in range(n_calls):
+            call(i)
+    stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            g.replay()
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    stream.synchronize()
+    return e0.elapsed_time(e1) / (reps * n_calls), g
+
+
+def other_configs(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
+    """Attention-only TFLOP/s of the other BASELINE.json configs (synthetic
+    N(0,1) inputs, same graph-burst timing as the roofline)."""
+    res = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    for name in ("C3", "C4", "C5S", "C5G"):
+        cfg = CONFIGS[name]
+        h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+        n_t, n_c = cfg.n_total, cfg.n_canvas
+        with torch.cuda.stream(stream):
+            K = [torch.randn(n_t, hkv * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
+            V = [torch.randn(n_t, hkv * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
+            Q = [torch.randn(n_c, h * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
+            O = [torch.empty(n_c * h * hd, device="cuda") for _ in range(cfg.batch)]
+            qn = kn = None
+            if cfg.qk_norm:
+                qn = torch.rand(hd, device="cuda", generator=gen) + 0.5
+                kn = torch.rand(hd, device="cuda", generator=gen) + 0.5
+        cache = dr.StepCache(ctx, n_t, [hkv], [hd], n_batch=cfg.batch)
+        p_all = dr.Pass(ctx, range(n_t))
+        p_can = dr.Pass(ctx, range(cfg.n_prompt, n_t))
+        for b in range(cfg.batch):
+            cache.store(0, p_all, K[b], V[b], k_norm_w=kn, batch=b)
+        items = [(Q[b], O[b], p_can) for b in range(cfg.batch)]
+
+        def call(i):
+            cache.attention(0, items, h, sliding_window=cfg.window, scale=cfg.attn_scale,
+                            q_norm_w=qn)
+        ms, _ = attention_only_ms(torch, stream, call, 4, reps)
+        fl = cfg.flops()
+        res[name] = {"workload": cfg.name, "us_per_call": round(ms * 1e3, 3),
+                     "tflops": round(fl / (ms / 1e3) / 1e12, 2),
+                     "pct_of_peak": round(100 * fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                     "launch": ctx.last_launch()}
+        log(f"{name}: {res[name]}")
+        stream.synchronize()
+        del cache
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -69,6 +138,8 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=0, help="force key splits (0 = automatic)")
     ap.add_argument("--cpu-reps", type=int, default=0, help="oracle reps (0 = auto ~15 s)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the attention-only timing of the other configs")
     ap.add_argument("--calib-mib", type=int, default=0,
                     help="also run a plain streaming kernel (out = -in) over this many MiB, "
                          "three times: the calibration for rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -140,24 +211,14 @@ def main() -> int:
         log(f"calibration: 3 x neg over {args.calib_mib} MiB (reads and writes that much)")
         del src, dst
 
-    # ---- roofline: the attention call alone, HIP events on the library stream
-    n_roof = max(50, min(2000, args.steps))
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(n_roof)]
-    with torch.cuda.stream(stream):
-        for i in range(20):
-            step(i)
-        for i in range(n_roof):
-            dK, dV, dQ = dsets[i % n_sets]
-            cache.store(0, p_canvas, dK, dV)
-            ev[i][0].record(stream)
-            cache.attention(0, [(dQ, out, p_canvas)], h, scale=scale)
-            ev[i][1].record(stream)
-    stream.synchronize()
-    attn_ms = sorted(a.elapsed_time(b) for a, b in ev)
-    attn_mean_ms = sum(attn_ms) / len(attn_ms)
-    attn_med_ms = attn_ms[len(attn_ms) // 2]
-    log(f"attention call: mean {attn_mean_ms * 1e3:.2f} us, median {attn_med_ms * 1e3:.2f} us")
+    # ---- roofline: the attention call alone.  16 calls (the 16 query sets)
+    # are captured in one graph and replayed back to back between two HIP
+    # events recorded on the library's stream; the mean launch duration is
+    # the elapsed time over the number of calls.
+    attn_mean_ms, attn_graph = attention_only_ms(
+        torch, stream, lambda i: cache.attention(0, [(dsets[i][2], out, p_canvas)], h, scale=scale),
+        n_sets, max(4, min(128, args.steps // n_sets)))
+    log(f"attention call (graph bursts): mean {attn_mean_ms * 1e3:.2f} us")
 
     # ---- timed region: K whole steps
     graph = None
@@ -212,9 +273,9 @@ def main() -> int:
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
         "traffic_source": traffic_src,
-        "kernel": "attention call (attn_fwd_kernel + attn_combine_kernel when split > 1)",
+        "kernel": "attn_fwd_kernel (one launch per attention call)",
         "flops_per_launch": flops, "launch_us_mean": round(attn_mean_ms * 1e3, 3),
-        "launch_us_median": round(attn_med_ms * 1e3, 3),
+        "launch_timing": "HIP events around graph replays of 16 back-to-back calls",
         "algorithmic_bytes_per_launch": algo_bytes,
         "hbm_ceiling_frac": round(min(1.0, flops / algo_bytes * PEAK_HBM_GBS * 1e9 / 1e12
                                       / PEAK_BF16_TFLOPS), 4),
@@ -223,6 +284,10 @@ def main() -> int:
     # ---- CPU baseline: the C restatement of the reference's attention on this
     # host's cores, on the first step's inputs; its output also checks the
     # GPU result of that step (the measured configuration).
+    others = None
+    if not args.no_others:
+        others = other_configs(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
+
     cpu, parity = None, None
     if not args.no_cpu:
         import oracle as orc
@@ -277,6 +342,7 @@ def main() -> int:
         "attention_call_pct_of_peak": round(100 * achieved / PEAK_BF16_TFLOPS, 3),
         "gpu_event_ms": round(gpu_ms, 4), "wall_s": round(wall, 4),
         "launch": launch, "parity": parity, "roofline": roofline, "cpu_baseline": cpu,
+        "other_configs_attention_only": others,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -176,6 +176,12 @@ __device__ __forceinline__ f32x4 load16_coherent(__amdgpu_buffer_rsrc_t r, int v
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16));
 }
 
+// n / d for the workgroup decode: mul-high by m = ceil(2^32 / d), exact when
+// n * d < 2^32 (the host passes m = 0 where that is not guaranteed).
+__device__ __forceinline__ int udiv(int n, int d, uint32_t m) {
+    return m ? (int)__umulhi((uint32_t)n, m) : n / d;
+}
+
 __device__ __forceinline__ float max3(float a, float b, float c) {
     return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
 }
@@ -197,13 +203,13 @@ struct Geometry {
     static constexpr int NLDW = STAGE / 8 / (NDMA * 64);  // DMA instructions per DMA wave
                                                           // and super-tile
     static constexpr int QROWS = RB * 32;      // query rows per workgroup
-    static constexpr int ROWF = HD + 4;        // f32 row pitch of the merge area
     static constexpr size_t STAGE_BYTES = (size_t)NS * STAGE * 2;
     // Head dims up to 128 keep Q in LDS for the whole kernel and read its
     // fragments per tile (registers go to the pipelined PV fragments); 256
     // holds Q in registers and stages it in the last pipeline stage.
     static constexpr bool QL = HD <= 128;
     static constexpr size_t Q_BYTES = QL ? (size_t)QROWS * HD * 2 : 0;
+    static constexpr int ROWF = HD + 4;        // f32 row pitch of the merge area
     static constexpr size_t MERGE_BYTES = ((size_t)NW * 32 * ROWF + 2 * NW * 32) * 4;
     static constexpr size_t LDS_BYTES =
         STAGE_BYTES + Q_BYTES > MERGE_BYTES ? STAGE_BYTES + Q_BYTES : MERGE_BYTES;
@@ -245,13 +251,16 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     const int nwg = gridDim.x;
     const int hw = blockIdx.x;
     const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
-    const int split = lid % a.n_split;
-    int rest = lid / a.n_split;
-    const int rg = rest % a.rowgroups;
-    rest /= a.rowgroups;
-    const int g = rest % a.n_head_kv;
-    const int b = rest / a.n_head_kv;
-    const AttnSlot& S = a.slot[b];
+    const int q1 = udiv(lid, a.n_split, a.mg_split);
+    const int split = lid - q1 * a.n_split;
+    const int q2 = udiv(q1, a.rowgroups, a.mg_rowgroups);
+    const int rg = q1 - q2 * a.rowgroups;
+    const int b = udiv(q2, a.n_head_kv, a.mg_hkv);
+    const int g = q2 - b * a.n_head_kv;
+    // One batch slot (the common case) is read at a fixed argument offset,
+    // so its fields do not wait for the index arithmetic above.
+    AttnSlot S = a.slot[0];
+    if (a.n_batch > 1) S = a.slot[b];
 
     const int rows_total = a.group * S.nq;
     const int wg_row0 = rg * QROWS;
@@ -391,15 +400,17 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     // of super-tile NS-1, issued after the barrier at the top of the loop).
     constexpr int LPR = HD / 4;       // lanes per row (f32x4 each)
     constexpr int RPI = 64 / LPR;     // rows per wave instruction
-    constexpr int RPW = QROWS / NWT;  // rows per wave
-    constexpr int QIT = RPW / RPI;
-    static_assert(RPW % RPI == 0, "Q rows must split evenly over the waves");
+    constexpr int QIT = (QROWS + NWT * RPI - 1) / (NWT * RPI);  // row groups per wave
     const int d0 = (lane % LPR) * 4;
+    // workgroup row of this lane in iteration it (rows past QROWS are idle)
+    auto q_lrow = [&](int it) __attribute__((always_inline)) {
+        return (it * NWT + wave) * RPI + lane / LPR;
+    };
     f32x4 xq[QIT];
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
-        const int rr = wg_row0 + wave * RPW + it * RPI + lane / LPR;
-        const bool ok = rr < rows_total;
+        const int rr = wg_row0 + q_lrow(it);
+        const bool ok = q_lrow(it) < QROWS && rr < rows_total;
         int hgq = 0, qiq = 0;
         if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
         const float* qrow = static_cast<const float*>(S.q) + (size_t)qiq * a.q_rstride +
@@ -440,10 +451,11 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         bf16x4 y;
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = (__bf16)(x[e] * a.c);
-        const int lr = wave * RPW + it * RPI + lane / LPR;  // row within the workgroup
-        const int rl = lr & 31;  // row within its row block (the swizzle key)
-        *reinterpret_cast<bf16x4*>(qs + lr * HD + (((d0 >> 3) ^ swz<KCH>(rl)) << 3) + (d0 & 7)) =
-            y;
+        const int lr = q_lrow(it);  // row within the workgroup
+        const int rl = lr & 31;     // row within its row block (the swizzle key)
+        if (lr < QROWS)
+            *reinterpret_cast<bf16x4*>(qs + lr * HD + (((d0 >> 3) ^ swz<KCH>(rl)) << 3) +
+                                       (d0 & 7)) = y;
     }
     __syncthreads();
     const uint16_t* qrow_l = qs + (rb * 32 + col) * HD;
@@ -461,9 +473,9 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = f32x16{};
     // -m in every slot: the QK^T accumulator init, so the scores come out
-    // relative to m.  The pipelined head-dim-128 loop has no registers to
-    // spare for it and subtracts m from the scores instead.
-    constexpr bool MINIT = !(HD == 128);
+    // relative to m (the alternative, subtracting m from the scores, costs 16
+    // VALU per tile; kept as a switch for register-starved shapes).
+    constexpr bool MINIT = true;
     f32x16 mneg = f32x16{};
     float mu = 0.0f;          // running max m (log2 units), valid once m_set
     bool m_set = false;
@@ -490,10 +502,11 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     // (NP == 0) the DMA of super-tile u+NS-1 is issued in four parts spread
     // over the compute, so that no wave stalls on a burst of memory
     // instructions in front of its MFMAs.
-    // Head dim 256 keeps its accumulators in the whole register file: there
-    // the PV product is issued in the same step (no second fragment set).
+    // Software pipelining of the PV product across steps (PIPE) measured no
+    // faster than issuing it in the same step, so it is off; the code path
+    // stays for shapes with registers to spare.
     constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
-    constexpr bool PIPE = HD <= 128;
+    constexpr bool PIPE = false;
     auto step = [&](int u, bool pend_in, const bf16x8 (&vin)[ND][2], const bf16x8 (&pin)[2],
                     bf16x8 (&vout)[ND][2], bf16x8 (&pout)[2])
         __attribute__((always_inline)) -> bool {
@@ -945,6 +958,12 @@ hipError_t zero_ints(int* p, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
+// ceil(2^32 / d) when n * d < 2^32 for every n < n_max, else 0.
+static uint32_t div_magic(int d, int n_max) {
+    if (d < 2 || (uint64_t)n_max * (uint64_t)d >= ((uint64_t)1 << 32)) return 0;
+    return (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.rowgroups = p.rowgroups;
     a.n_split = p.n_split;
@@ -952,6 +971,9 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
         const size_t rows = (size_t)a.n_batch * a.n_head_kv * p.rowgroups * p.rb * 32;
         a.part_ml = a.part_o + (size_t)p.n_split * rows * p.hd_tile;
     }
+    a.mg_split = div_magic(a.n_split, p.n_workgroups);
+    a.mg_rowgroups = div_magic(a.rowgroups, p.n_workgroups);
+    a.mg_hkv = div_magic(a.n_head_kv, p.n_workgroups);
     return launch_shape(p, a, st);
 }
 

@@ -47,6 +47,7 @@ struct AttnArgs {
     int n_split;                   // key splits; > 1 writes partials
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
+    uint32_t mg_split, mg_rowgroups, mg_hkv;  // division magic for the workgroup decode
     int* tickets;                  // [batch*kv head][rowgroups] arrival counters, zero
                                    // between launches (the last arriver resets its own)
 };
