@@ -390,6 +390,9 @@ int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pa
     a.vtc = cache->vt[layer * cache->n_batch + batch];
     a.kn_w = k_norm_w;
     a.kn_eps = eps;
+    a.vec = a.hd == cache->hd_tile[layer] && (((uintptr_t)k | (uintptr_t)v) & 15) == 0;
+    a.batch = (int)batch;
+    a.n_batch = (int)cache->n_batch;
     hipError_t e = dr::launch_store(cache->hd_tile[layer], a, cache->ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "kv_store launch");
     return DR_OK;
@@ -704,6 +707,7 @@ int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const
     sa.cap = (int)cap;
     sa.kc = static_cast<uint16_t*>(ctx->kc.p);
     sa.vtc = static_cast<uint16_t*>(ctx->vtc.p);
+    sa.vec = (int)hd == tile;
     hipError_t e = dr::launch_store(tile, sa, st);
     if (e != hipSuccess) return hip_fail(e, "pack launch");
 

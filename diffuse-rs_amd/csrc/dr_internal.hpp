@@ -55,7 +55,8 @@ struct AttnArgs {
 struct StoreArgs {
     const float* k;      // [n][n_head_kv][hd] f32 rows
     const float* v;
-    const int* pos;      // [n] destination positions (device); nullptr: row r -> r
+    const int* pos;      // [n] strictly ascending destination positions (device);
+                         // nullptr: row r -> r
     int n;
     int n_head_kv;
     int hd;              // actual head_dim (<= HD tile; tail zero-filled)
@@ -64,6 +65,10 @@ struct StoreArgs {
     uint16_t* vtc;       // [n_head_kv][HD][cap] bf16 bits
     const float* kn_w;   // K-norm gain or nullptr
     float kn_eps;
+    int vec;             // rows may be read as 16-byte pieces (hd == HD tile, aligned)
+    int batch, n_batch;  // batch slot of the cache (n_batch 0 counts as 1): picks the XCDs
+    // set by launch_store: workgroup -> (kv head, head-dim chunk, row block)
+    int n_rb, per_xcd, xcd_lo, xcd_n;
 };
 
 struct GatherArgs {

@@ -12,9 +12,11 @@
 // store:  StepCache::store (cache.rs:62-71) -- f32 rows -> bf16 at their
 //         positions, optionally after per-head RMSNorm of K (norm_heads,
 //         ops.rs:384-389, applied before the store in forward.rs:300-302).
-//         One launch: workgroups [0, n_kblocks) write K rows (one wave per
-//         (row, kv head)); the rest transpose 64x64 blocks of V through LDS.
+//         One launch, one workgroup per (64-row block, 64-wide head-dim
+//         chunk, kv head): K converted in registers, V transposed through LDS.
 // gather: StepCache::gather (cache.rs:73-82) -- bf16 back to f32 rows.
+#include <algorithm>
+
 #include "dr_internal.hpp"
 
 #include <math.h>
@@ -32,115 +34,130 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
     return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-constexpr int VT_ROWS = 64;  // positions per V^T block
-constexpr int VT_D = 64;     // head-dim entries per V^T block
+constexpr int SR = 64;   // rows per store workgroup: one 128-byte line of a V^T row
+constexpr int SD = 64;   // head-dim entries per store workgroup: one 128-byte line of a K row
+constexpr int SPT = 16;  // consecutive values per thread (4 threads per row, 256 threads)
 
+// One workgroup per (64-row block, 64-wide head-dim chunk, kv head), so that
+// every 128-byte line of K and of V^T it writes is written whole by it.  All
+// loads of the block (16 K and 16 V floats per thread) are issued before any
+// store.  K: optional per-head RMSNorm, whose sum of squares covers the whole
+// row (the other chunks' values are loaded for it), then bf16 at the row's
+// position.  V: bf16 into an LDS tile transposed to [d][row]; each thread then
+// writes 16 positions of one d-row of V^T (16-byte stores when the positions
+// are contiguous and aligned).
 template <int HD>
-__global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a, int n_kblocks) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if ((int)blockIdx.x < n_kblocks) {
-        // ---- K: one wave per (row, kv head); EPL consecutive values per lane
-        constexpr int EPL = HD / 64;
-        const int pair = blockIdx.x * 4 + wave;
-        if (pair >= a.n * a.n_head_kv) return;
-        const int r = pair / a.n_head_kv, g = pair % a.n_head_kv;
-        const int pos = a.pos ? a.pos[r] : r;
-        const float* src = a.k + (size_t)pair * a.hd;
-        float x[EPL];
-        if (a.hd == HD) {
-            if constexpr (EPL == 4) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(src + lane * 4);
+__global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
+    constexpr int NDC = HD / SD;
+    constexpr int V4 = SPT / 4;
+    __shared__ __align__(16) uint16_t tile[SD][SR + 8];
+
+    // Workgroup -> (kv head g, chunk dc, row block).  The hardware deals
+    // workgroups round-robin over the 8 XCDs (XCD = blockIdx & 7); each XCD in
+    // [xcd_lo, xcd_lo + xcd_n) takes a contiguous run of per_xcd logical ids,
+    // so kv head g is written through the L2 of the XCD on which the attention
+    // launch reads it (it deals heads to XCDs in the same contiguous way).
+    const int x = blockIdx.x & 7;
+    if (x < a.xcd_lo || x >= a.xcd_lo + a.xcd_n) return;
+    const int lid = (x - a.xcd_lo) * a.per_xcd + (int)(blockIdx.x >> 3);
+    if (lid >= a.n_head_kv * NDC * a.n_rb) return;
+    const int hc = lid / a.n_rb;
+    const int g = hc / NDC, dc = hc - g * NDC;
+    const int r0 = (lid - hc * a.n_rb) * SR;
+    const int tid = threadIdx.x, rl = tid >> 2, part = tid & 3;
+    const int r = r0 + rl;
+    const bool ok = r < a.n;
+    const int d0 = dc * SD + part * SPT;  // first head-dim entry of this thread
+    const size_t row = ((size_t)(ok ? r : 0) * a.n_head_kv + g) * a.hd;
+    f32x4 xk[V4], xv[V4];
+    if (ok && a.vec) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) x[e] = v[e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) x[e] = src[lane * EPL + e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int d = lane * EPL + e;
-                x[e] = d < a.hd ? src[d] : 0.0f;
-            }
+        for (int i = 0; i < V4; ++i) {
+            xk[i] = *reinterpret_cast<const f32x4*>(a.k + row + d0 + 4 * i);
+            xv[i] = *reinterpret_cast<const f32x4*>(a.v + row + d0 + 4 * i);
         }
-        if (a.kn_w) {
-            // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
-            double ss = 0.0;
+    } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float sq = x[e] * x[e];
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = d0 + 4 * i + e;
+                const bool in = ok && d < a.hd;
+                xk[i][e] = in ? a.k[row + d] : 0.0f;
+                xv[i][e] = in ? a.v[row + d] : 0.0f;
+            }
+    }
+    const int pos = ok ? (a.pos ? a.pos[r] : r) : 0;
+
+    if (a.kn_w) {
+        // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64 over
+        // the whole row; this thread covers entries part*16 + [0,16) of every
+        // 64-wide chunk.
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sq = xk[i][e] * xk[i][e];
                 ss += (double)sq;
             }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-            const float sc = 1.0f / (float)sqrt(ss / (double)a.hd + (double)a.kn_eps);
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int d = lane * EPL + e;
-                if (d < a.hd) x[e] = x[e] * sc * a.kn_w[d];
+        for (int c = 0; c < NDC; ++c) {
+            if (c == dc) continue;
+            const int e0 = c * SD + part * SPT;
+            for (int e = 0; e < SPT; ++e) {
+                const float x = (ok && e0 + e < a.hd) ? a.k[row + e0 + e] : 0.0f;
+                const float sq = x * x;
+                ss += (double)sq;
             }
         }
-        uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * HD + lane * EPL;
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        const float sc = 1.0f / (float)sqrt(ss / (double)a.hd + (double)a.kn_eps);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) dst[e] = f2bf(x[e]);
-        return;
-    }
-
-    // ---- V^T: a block of 64 rows x 64 d of one kv head, transposed via LDS
-    __shared__ uint16_t tile[VT_D][VT_ROWS + 2];
-    constexpr int NDC = HD / VT_D;
-    const int nrc = (a.n + VT_ROWS - 1) / VT_ROWS;
-    int t = blockIdx.x - n_kblocks;
-    const int rc = t % nrc;
-    t /= nrc;
-    const int dc = t % NDC;
-    const int g = t / NDC;
-    {
-        const int row = tid >> 2, d0 = (tid & 3) * 16;
-        const int r = rc * VT_ROWS + row;
-        const int dbase = dc * VT_D + d0;
-        const float* src = a.v + ((size_t)r * a.n_head_kv + g) * a.hd + dbase;
-        float x[16];
-        if (r < a.n && a.hd == HD) {
+        for (int i = 0; i < V4; ++i)
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * q4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) x[4 * q4 + e] = v[e];
+            for (int e = 0; e < 4; ++e) {
+                const int d = d0 + 4 * i + e;
+                if (d < a.hd) xk[i][e] = xk[i][e] * sc * a.kn_w[d];
             }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) x[e] = (r < a.n && dbase + e < a.hd) ? src[e] : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) tile[d0 + e][row] = f2bf(x[e]);
     }
+    if (ok) {
+        uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * HD + d0;
+#pragma unroll
+        for (int i = 0; i < V4; i += 2) {
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                w[2 * j] = (uint32_t)f2bf(xk[i + j][0]) | ((uint32_t)f2bf(xk[i + j][1]) << 16);
+                w[2 * j + 1] = (uint32_t)f2bf(xk[i + j][2]) | ((uint32_t)f2bf(xk[i + j][3]) << 16);
+            }
+            *reinterpret_cast<u32x4*>(dst + 4 * i) = w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < V4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[part * SPT + 4 * i + e][rl] = f2bf(xv[i][e]);
     __syncthreads();
-    {
-        const int d = tid >> 2, r0 = (tid & 3) * 16;
-        const int rfirst = rc * VT_ROWS + r0;
-        if (rfirst >= a.n) return;
-        const int nr = min(16, a.n - rfirst);
-        uint16_t* drow = a.vtc + ((size_t)g * HD + dc * VT_D + d) * a.cap;
-        const int p0 = a.pos ? a.pos[rfirst] : rfirst;
-        const bool contiguous =
-            nr == 16 && (a.pos == nullptr || a.pos[rfirst + 15] - p0 == 15) && (p0 & 7) == 0;
-        if (contiguous) {
-            u32x4 w[2];
+
+    // V^T: thread -> (d-row dl, positions p0 + [0,16)).
+    const int dl = tid >> 2, p0 = (tid & 3) * SPT;
+    const int rfirst = r0 + p0;
+    if (rfirst >= a.n) return;
+    const int cnt = min(SPT, a.n - rfirst);
+    uint16_t* drow = a.vtc + ((size_t)g * HD + dc * SD + dl) * a.cap;
+    const int q0 = a.pos ? a.pos[rfirst] : rfirst;
+    // pos is strictly ascending, so equal endpoint distance means contiguous.
+    const bool contiguous = cnt == SPT && (q0 & 7) == 0 &&
+                            (a.pos == nullptr || a.pos[rfirst + SPT - 1] - q0 == SPT - 1);
+    const uint16_t* t = &tile[dl][p0];
+    if (contiguous) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    w[h][e] = (uint32_t)tile[d][r0 + 8 * h + 2 * e] |
-                              ((uint32_t)tile[d][r0 + 8 * h + 2 * e + 1] << 16);
-            *reinterpret_cast<u32x4*>(drow + p0) = w[0];
-            *reinterpret_cast<u32x4*>(drow + p0 + 8) = w[1];
-        } else {
-            for (int e = 0; e < nr; ++e) {
-                const int pos = a.pos ? a.pos[rfirst + e] : rfirst + e;
-                drow[pos] = tile[d][r0 + e];
-            }
-        }
+        for (int h = 0; h < SPT / 8; ++h)
+            *reinterpret_cast<u32x4*>(drow + q0 + 8 * h) =
+                *reinterpret_cast<const u32x4*>(t + 8 * h);
+    } else {
+        for (int e = 0; e < cnt; ++e) drow[a.pos ? a.pos[rfirst + e] : rfirst + e] = t[e];
     }
 }
 
@@ -162,16 +179,23 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
 
 }  // namespace
 
-hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st) {
-    if (a.n <= 0) return hipSuccess;
-    const int n_kblocks = (a.n * a.n_head_kv + 3) / 4;
-    const int n_vblocks = (a.n + VT_ROWS - 1) / VT_ROWS * (hd_tile / VT_D) * a.n_head_kv;
-    dim3 grid(n_kblocks + n_vblocks);
+hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
+    if (args.n <= 0) return hipSuccess;
+    if (hd_tile != 64 && hd_tile != 128 && hd_tile != 256) return hipErrorInvalidValue;
+    StoreArgs a = args;
+    // Batch slot b of nb: the attention launch puts the slot's kv heads on
+    // XCDs [8b/nb, 8(b+1)/nb).
+    const int nb = a.n_batch > 0 ? a.n_batch : 1;
+    a.xcd_lo = 8 * a.batch / nb;
+    a.xcd_n = std::max(1, 8 * (a.batch + 1) / nb - a.xcd_lo);
+    a.n_rb = (a.n + SR - 1) / SR;
+    const int work = a.n_head_kv * (hd_tile / SD) * a.n_rb;
+    a.per_xcd = (work + a.xcd_n - 1) / a.xcd_n;
+    const dim3 grid((unsigned)(8 * a.per_xcd));
     switch (hd_tile) {
-        case 64: hipLaunchKernelGGL(kv_store_kernel<64>, grid, dim3(256), 0, st, a, n_kblocks); break;
-        case 128: hipLaunchKernelGGL(kv_store_kernel<128>, grid, dim3(256), 0, st, a, n_kblocks); break;
-        case 256: hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(256), 0, st, a, n_kblocks); break;
-        default: return hipErrorInvalidValue;
+        case 64: hipLaunchKernelGGL(kv_store_kernel<64>, grid, dim3(256), 0, st, a); break;
+        case 128: hipLaunchKernelGGL(kv_store_kernel<128>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(256), 0, st, a); break;
     }
     return hipGetLastError();
 }

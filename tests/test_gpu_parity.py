@@ -359,6 +359,33 @@ def test_cache_gather_is_bf16_of_store(dev):
     assert np.array_equal(dev.get(ov), bf(V))
 
 
+@pytest.mark.parametrize("hd,n,n_tot", [(64, 70, 200), (96, 129, 150), (128, 64, 64),
+                                        (256, 33, 90)])
+def test_cache_store_k_norm_is_bf16_of_oracle(dev, hd, n, n_tot):
+    """norm_heads(k, k_norm) + cache.store (forward.rs:300-302, 318-320): the
+    gathered K equals bf16 of the oracle's rms_norm_inplace (ops.rs:106-114)
+    per (row, kv head), bit for bit; V is stored unnormalised."""
+    rng = np.random.default_rng(hd * 1000 + n)
+    hkv, eps = 3, 1e-6
+    cache = dr.StepCache(dev.ctx, n_tot, [hkv], [hd])
+    pos = sorted(rng.choice(n_tot, n, replace=False).tolist())
+    K = rng.standard_normal((n, hkv * hd), dtype=np.float32) * 3
+    V = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    cache.store(0, dr.Pass(dev.ctx, pos), dev.put(K), dev.put(V), k_norm_w=dev.put(w), eps=eps)
+    ok, ov = dev.empty(n * hkv * hd), dev.empty(n * hkv * hd)
+    cache.gather(0, pos, ok, ov)
+    Kn = K.reshape(-1).copy()
+    for o in range(0, Kn.size, hd):
+        seg = Kn[o:o + hd].copy()
+        orc.rms_norm_inplace(seg, w, eps)
+        Kn[o:o + hd] = seg
+    t = dev.t
+    bf = lambda a: t.from_numpy(a).to(t.bfloat16).to(t.float32).numpy().reshape(-1)  # noqa: E731
+    assert np.array_equal(dev.get(ok), bf(Kn))
+    assert np.array_equal(dev.get(ov), bf(V))
+
+
 def test_cache_split_active_reference_case(dev):
     # tests.rs:39-53 through the StepCache object
     cache = dr.StepCache(dev.ctx, 4, [1], [8])
