@@ -17,8 +17,8 @@
 // softmax states of a row block are merged through LDS, which also stages
 // the output for full-row, coalesced stores.  When there are too few
 // workgroups to fill the chip the key range is also split across
-// workgroups (n_split > 1): each writes its partial rows, and the last one
-// to finish (an atomic ticket per row group) merges them.
+// workgroups (n_split > 1): each writes its partial rows, and a second,
+// small kernel (split_merge_kernel) combines them.
 //
 // Per wave and 32-key block:
 //   S^T[key][q] = K Q^T - m  via v_mfma_f32_32x32x16_bf16, A = K (LDS),
@@ -167,15 +167,6 @@ __device__ __forceinline__ void row_split(int r, int nq, float inv_nq, int group
     qi = q;
 }
 
-// Agent-coherent 16-byte store / load (cache policy sc1: written through to,
-// and read from, the level every XCD shares), for the key-split partials.
-__device__ __forceinline__ void store16_coherent(__amdgpu_buffer_rsrc_t r, int voff, f32x4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, 0, 16);
-}
-__device__ __forceinline__ f32x4 load16_coherent(__amdgpu_buffer_rsrc_t r, int voff) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16));
-}
-
 // n / d for the workgroup decode: mul-high by m = ceil(2^32 / d), exact when
 // n * d < 2^32 (the host passes m = 0 where that is not guaranteed).
 __device__ __forceinline__ int udiv(int n, int d, uint32_t m) {
@@ -204,20 +195,16 @@ struct Geometry {
                                                           // and super-tile
     static constexpr int QROWS = RB * 32;      // query rows per workgroup
     static constexpr size_t STAGE_BYTES = (size_t)NS * STAGE * 2;
-    // Head dims up to 128 keep Q in LDS for the whole kernel and read its
-    // fragments per tile (registers go to the pipelined PV fragments); 256
-    // holds Q in registers and stages it in the last pipeline stage.
-    static constexpr bool QL = HD <= 128;
-    static constexpr size_t Q_BYTES = QL ? (size_t)QROWS * HD * 2 : 0;
+    // Q fragments are held in registers for the whole kernel; Q is staged
+    // once, through the first slot of the last pipeline stage.
     static constexpr int ROWF = HD + 4;        // f32 row pitch of the merge area
     static constexpr size_t MERGE_BYTES = ((size_t)NW * 32 * ROWF + 2 * NW * 32) * 4;
-    static constexpr size_t LDS_BYTES =
-        STAGE_BYTES + Q_BYTES > MERGE_BYTES ? STAGE_BYTES + Q_BYTES : MERGE_BYTES;
+    static constexpr size_t LDS_BYTES = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
     static constexpr int WAVES_PER_SIMD = (NWT + 3) / 4;
     static_assert(CPT % 64 == 0, "a DMA instruction must stay inside one tile");
     static_assert(STAGE / 8 % (NDMA * 64) == 0, "super-tile must split evenly over the waves");
     static_assert(NLDW * (NS - 1) < 64, "vmcnt range");
-    static_assert(QL || QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
+    static_assert(QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -227,13 +214,25 @@ __attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD,
 __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     using G = Geometry<HD, RB, KQ, NS, NP>;
     constexpr int NW = G::NW, NWT = G::NWT, NT = G::NT, NC = G::NC, ND = G::ND;
-    constexpr int KCH = G::KCH, VCH = G::VCH, TILE = G::TILE, SLOT = G::SLOT, STAGE = G::STAGE;
+    constexpr int KCH = G::KCH, VCH = G::VCH, TILE = G::TILE, SLOT = G::SLOT;
     constexpr int CPT = G::CPT, NLDW = G::NLDW, ROWF = G::ROWF, QROWS = G::QROWS;
 
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_red[3][NWT];
-    __shared__ int s_last;
 
+    // Every scalar of the decode and the first loads, and batch slot 0, is
+    // requested here at once (wide scalar loads, one wait) rather than by one
+    // dependent load at each first use.  The empty asm also keeps the
+    // compiler from turning "slot 0 or slot b" below into a pointer select
+    // and a second, dependent load.
+    AttnSlot S = a.slot[0];
+    asm volatile("" : "+s"(S.q), "+s"(S.out), "+s"(S.qpos), "+s"(S.qseq), "+s"(S.qprefix),
+                 "+s"(S.k), "+s"(S.vt), "+s"(S.kpos), "+s"(S.kseq), "+s"(S.nq), "+s"(S.nk),
+                 "+s"(S.qpos_sorted)
+                 : "s"(a.n_batch), "s"(a.n_head_kv), "s"(a.group), "s"(a.hd), "s"(a.cap),
+                   "s"(a.q_rstride), "s"(a.rowgroups), "s"(a.n_split), "s"(a.mg_split),
+                   "s"(a.mg_rowgroups), "s"(a.mg_hkv), "s"(a.c), "s"(a.n_wg), "s"(a.window),
+                   "s"(a.prefix));
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, hf = lane >> 5;
@@ -248,7 +247,7 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     // Workgroup -> (batch, kv head, row group, split).  The hardware deals
     // workgroups round-robin over the 8 XCDs; remapping keeps consecutive
     // logical ids (same row group, its splits) on one XCD's L2.
-    const int nwg = gridDim.x;
+    const int nwg = a.n_wg;
     const int hw = blockIdx.x;
     const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
     const int q1 = udiv(lid, a.n_split, a.mg_split);
@@ -257,9 +256,6 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     const int rg = q1 - q2 * a.rowgroups;
     const int b = udiv(q2, a.n_head_kv, a.mg_hkv);
     const int g = q2 - b * a.n_head_kv;
-    // One batch slot (the common case) is read at a fixed argument offset,
-    // so its fields do not wait for the index arithmetic above.
-    AttnSlot S = a.slot[0];
     if (a.n_batch > 1) S = a.slot[b];
 
     const int rows_total = a.group * S.nq;
@@ -429,7 +425,7 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
             if (i < nsup) issue(i, i);
     }
 
-    uint16_t* qs = smem + (G::QL ? NS * STAGE : (NS - 1) * SLOT);
+    uint16_t* qs = smem + (NS - 1) * SLOT;
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
         f32x4 x = xq[it];
@@ -462,21 +458,14 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     auto qfrag = [&](int c) __attribute__((always_inline)) {
         return *reinterpret_cast<const bf16x8*>(qrow_l + (((2 * c + hf) ^ swz<KCH>(col)) << 3));
     };
-    bf16x8 qf[G::QL ? 1 : NC];
-    if constexpr (!G::QL) {
+    bf16x8 qf[NC];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
-    }
+    for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
 
     // ---- main loop over super-tiles
     f32x16 o[ND];
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-    // -m in every slot: the QK^T accumulator init, so the scores come out
-    // relative to m (the alternative, subtracting m from the scores, costs 16
-    // VALU per tile; kept as a switch for register-starved shapes).
-    constexpr bool MINIT = true;
-    f32x16 mneg = f32x16{};
     float mu = 0.0f;          // running max m (log2 units), valid once m_set
     bool m_set = false;
     float thr = -INFINITY;    // a score above mu + thr moves m
@@ -495,21 +484,22 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     };
 
     // One super-tile.  A compute wave software-pipelines its tiles: the PV
-    // product of its previous tile (V^T fragments and P kept in registers,
-    // pend_in) is issued right after this tile's QK^T MFMAs, so the softmax
-    // of this tile overlaps those MFMAs; this tile's V^T fragments and P are
-    // left in vout/pout (returns true) for the next step.  Without DMA waves
-    // (NP == 0) the DMA of super-tile u+NS-1 is issued in four parts spread
-    // over the compute, so that no wave stalls on a burst of memory
-    // instructions in front of its MFMAs.
-    // Software pipelining of the PV product across steps (PIPE) measured no
-    // faster than issuing it in the same step, so it is off; the code path
-    // stays for shapes with registers to spare.
+    // product of its previous tile (V^T fragments vf and P pin, in registers)
+    // is issued in program order between the VALU instructions of this
+    // tile's softmax, so the matrix core and the VALU work at the same time
+    // (with one compute wave per SIMD nothing else would fill either).  This
+    // tile's P goes to pout, and its V^T fragments replace vf once those
+    // MFMAs have read them (one set of V^T registers, which leaves room for
+    // Q's); the first step multiplies zero fragments.  Without DMA waves (NP == 0)
+    // the DMA of super-tile u+NS-1 is issued in three parts spread over the
+    // compute, so that no wave stalls on a burst of memory instructions in
+    // front of its MFMAs.  Head dim 256 has no registers for a second set of
+    // V^T fragments (Q stays in registers there): its PV product is issued
+    // in the step of its tile, after the softmax (PIPE false).
+    constexpr bool PIPE = HD <= 128;
     constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
-    constexpr bool PIPE = false;
-    auto step = [&](int u, bool pend_in, const bf16x8 (&vin)[ND][2], const bf16x8 (&pin)[2],
-                    bf16x8 (&vout)[ND][2], bf16x8 (&pout)[2])
-        __attribute__((always_inline)) -> bool {
+    auto step = [&](int u, bf16x8 (&vf)[ND][2], const bf16x8 (&pin)[2], bf16x8 (&pout)[2])
+        __attribute__((always_inline)) {
         const int st = u % NS;
         if (dma) wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
         __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
@@ -517,7 +507,7 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         if constexpr (NP > 0) {
             if (!compute) {
                 if (un < nsup) issue(un, stn);
-                return false;
+                return;
             }
         }
         const bool pf = NP == 0 && un < nsup;
@@ -525,8 +515,9 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         const int t = t0 + u * KQ + kq;
         if (t >= t1) {  // this key group has no tile in the last super-tile
             if (pf) issue(un, stn);
-            if (pend_in) pv(vin, pin);
-            return false;
+            if constexpr (PIPE) pv(vf, pin);
+            pout[0] = pout[1] = bf16x8{};  // vf holds finite values: nothing is added
+            return;
         }
         const uint16_t* ks = smem + (kq * NS + st) * SLOT;
         const uint16_t* vs = ks + TILE;
@@ -545,48 +536,44 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         if (pf) issue_range(un, stn, 0, J1);
         __builtin_amdgcn_sched_barrier(0);
 
-        // S^T = K Q^T - m.  The K fragments are requested in two halves, the
-        // second while the MFMAs of the first run.
-        f32x16 s = MINIT ? mneg : f32x16{};
+        // S^T = K Q^T - m: -m enters as the accumulator init, so the scores
+        // come out relative to m.  The K fragments are requested in two
+        // halves, the second while the MFMAs of the first run.
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = -mu;
         {
             constexpr int NH = NC / 2;
             const uint16_t* krow = ks + col * HD;
             const int sw = swz<KCH>(col);
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                bf16x8 kf[NH], qh[G::QL ? NH : 1];
+                bf16x8 kf[NH];
 #pragma unroll
-                for (int c = 0; c < NH; ++c) {
+                for (int c = 0; c < NH; ++c)
                     kf[c] = *reinterpret_cast<const bf16x8*>(
                         krow + (((2 * (h * NH + c) + hf) ^ sw) << 3));
-                    if constexpr (G::QL) qh[c] = qfrag(h * NH + c);
-                }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int c = 0; c < NH; ++c)
-                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        kf[c], G::QL ? qh[G::QL ? c : 0] : qf[G::QL ? 0 : h * NH + c], s, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[h * NH + c], s, 0, 0, 0);
             }
         }
-        if (pend_in) pv(vin, pin);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (!MINIT) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] -= mu;
-        }
 
-        // this tile's V^T fragments (for the next step's PV product)
+        // this tile's V^T fragments
+        auto read_v = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int db = 0; db < ND; ++db) {
-            const int d = db * 32 + col;
-            const uint16_t* vrow = vs + d * BN;
-            const int sw = swz<VCH>(d);
-            vout[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
-            vout[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
-        }
-        __builtin_amdgcn_sched_barrier(0);
+            for (int db = 0; db < ND; ++db) {
+                const int d = db * 32 + col;
+                const uint16_t* vrow = vs + d * BN;
+                const int sw = swz<VCH>(d);
+                vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
+                vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
+            }
+        };
+        if constexpr (!PIPE) read_v();
         if (pf) issue_range(un, stn, J1, J2);
-        __builtin_amdgcn_sched_barrier(0);
 
         // Masking: s[i] is the score of key t*BN + 16*hf + i.
         bool full = kbase_t + BN <= S.nk;
@@ -616,31 +603,29 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
 #pragma unroll
         for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
         mx = __builtin_fmaxf(mx, s[15]);
-        if (__builtin_amdgcn_ballot_w64(mx > thr)) {
-            // the column max over both lane halves decides, so lane and
-            // lane^32 move m together; O (including the previous tile's PV
-            // product, issued above at the old m) is rescaled
+        // The column max over both lane halves decides, so lane and lane^32
+        // move m together.  O is rescaled after the previous tile's PV
+        // product (whose P is relative to the old m) has gone into it, and
+        // before this tile's.
+        const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+        float alpha = 1.0f;
+        if (moved) {
             const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
             const bool upd = cm > thr;
             const float delta = upd ? cm : 0.0f;
-            const float alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+            alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
             mu += delta;
             m_set = m_set | upd;
             thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[i] -= delta;
-            if constexpr (MINIT) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mneg[i] = -mu;
-            }
             l_lo *= alpha;
             l_hi *= alpha;
-#pragma unroll
-            for (int db = 0; db < ND; ++db) o[db] *= alpha;
         }
 
         // p = exp2(s) rounded to bf16 in pairs; l sums the rounded values
         // (what the PV product multiplies), so the weights normalise exactly.
+        // The previous tile's PV MFMAs are interleaved with this VALU work.
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             u32x4 w4;
@@ -657,28 +642,39 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
             }
             pout[hh] = __builtin_bit_cast(bf16x8, w4);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (pf) issue_range(un, stn, J2, NLDW);
-        if constexpr (!PIPE) {
-            pv(vout, pout);
-            return false;
+        if constexpr (PIPE) {
+            pv(vf, pin);
+#pragma unroll
+            for (int i = 0; i < 2 * ND; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
+            }
         }
-        return true;
+        __builtin_amdgcn_sched_barrier(0);
+        if (moved) {
+#pragma unroll
+            for (int db = 0; db < ND; ++db) o[db] *= alpha;
+        }
+        if constexpr (PIPE) read_v();
+        if (pf) issue_range(un, stn, J2, NLDW);
+        if constexpr (!PIPE) pv(vf, pout);
     };
 
     {
-        bf16x8 vfa[ND][2], vfb[ND][2], pfa[2], pfb[2];
-        bool pend = false;
+        bf16x8 vf[ND][2], pfa[2], pfb[2];
+#pragma unroll
+        for (int db = 0; db < ND; ++db) vf[db][0] = vf[db][1] = bf16x8{};
+        pfa[0] = pfa[1] = bf16x8{};
         int u = 0;
         for (; u + 1 < nsup; u += 2) {
-            pend = step(u, pend, vfa, pfa, vfb, pfb);
-            pend = step(u + 1, pend, vfb, pfb, vfa, pfa);
+            step(u, vf, pfa, pfb);
+            step(u + 1, vf, pfb, pfa);
         }
         if (u < nsup) {
-            pend = step(u, pend, vfa, pfa, vfb, pfb);
-            if (pend) pv(vfb, pfb);
-        } else if (pend) {
-            pv(vfa, pfa);
+            step(u, vf, pfa, pfb);
+            if (PIPE && compute) pv(vf, pfb);
+        } else if (PIPE && compute) {
+            pv(vf, pfa);
         }
     }
 
@@ -745,14 +741,14 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         return;
     }
 
-    // ---- key split: publish this split's partial rows, then the last of the
-    // n_split workgroups of the row group merges all of them.  The partials
-    // are written and read with agent-coherent (sc1) accesses and each wave
-    // waits for its writes to complete before the ticket moves, so the merge
-    // needs no cache-wide writeback or invalidate and works whichever XCDs
-    // the splits ran on.
+    // ---- key split: this split's partial rows (the sum over its key groups,
+    // relative to the row max M, with M and the sum of weights L) go to the
+    // split workspace; split_merge_kernel, launched next on the same stream,
+    // combines the splits.  The kernel boundary orders the writes before the
+    // merge's reads, so no cross-workgroup protocol is needed here.
     const size_t plane = (size_t)a.n_batch * a.n_head_kv * rows_pad;  // rows per split
-    const uint32_t plane_o_bytes = (uint32_t)(plane * HD * 4);
+    float* po = a.part_o + (size_t)split * plane * HD;
+    float* pml = a.part_ml + (size_t)split * plane * 2;
     for (int item = tid; item < QROWS * CHUNKS; item += NT) {
         const int rr = item / CHUNKS, ch = item % CHUNKS;
         const int rbi = rr >> 5, ci = rr & 31;
@@ -766,67 +762,71 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
             Mrow = __builtin_fmaxf(Mrow, sm[wi * 32 + ci]);
         }
         const size_t prow = bg * rows_pad + wg_row0 + rr;  // row within a split plane
-        const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o + split * plane * HD, plane_o_bytes);
-        store16_coherent(ro, (int)((prow * HD + ch * 4) * 4), acc);
-        if (ch == 0) {
-            float* ml = a.part_ml + (split * plane + prow) * 2;
-            __hip_atomic_store(ml, Mrow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    wait_vmcnt<0>();  // this wave's partial rows are complete at the coherent level
-    __syncthreads();
-    if (tid == 0) {
-        int* ticket = a.tickets + bg * a.rowgroups + rg;
-        const int prev =
-            __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = prev == a.n_split - 1;
-        if (last) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-
-    for (int item = tid; item < QROWS * CHUNKS; item += NT) {
-        const int rr = item / CHUNKS, ch = item % CHUNKS;
-        const int rglob = wg_row0 + rr;
-        if (rglob >= rows_total) continue;
-        const size_t prow = bg * rows_pad + rglob;
-        float Mx = -INFINITY;
-        for (int sp = 0; sp < a.n_split; ++sp)
-            Mx = __builtin_fmaxf(Mx, __hip_atomic_load(a.part_ml + (sp * plane + prow) * 2,
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        float L = 0.0f;
-        for (int sp = 0; sp < a.n_split; ++sp) {
-            const float* ml = a.part_ml + (sp * plane + prow) * 2;
-            const float ms = __hip_atomic_load(ml, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float ls = __hip_atomic_load(ml + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float w = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - Mx);
-            L += w * ls;
-            const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o + sp * plane * HD, plane_o_bytes);
-            acc += w * load16_coherent(ro, (int)((prow * HD + ch * 4) * 4));
-        }
-        const int c0 = ch * 4;
-        int hgi, qii;
-        row_split(rglob, S.nq, inv_nq, a.group, hgi, qii);
-        float* orow = S.out + (size_t)qii * a.o_rstride + (size_t)(g * a.group + hgi) * a.hd;
-        const f32x4 val = acc * __builtin_amdgcn_rcpf(L);
-        if (a.hd == HD) {
-            *reinterpret_cast<f32x4*>(orow + c0) = val;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (c0 + e < a.hd) orow[c0 + e] = val[e];
-        }
+        *reinterpret_cast<f32x4*>(po + prow * HD + ch * 4) = acc;
+        if (ch == 0) *reinterpret_cast<float2*>(pml + prow * 2) = make_float2(Mrow, L);
     }
 }
 
-// Fills n ints with zero (the split tickets; a kernel rather than a memset so
-// that it may sit in a captured graph).
-__global__ __launch_bounds__(256) void zero_ints_kernel(int* p, int n) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 0;
+// Combines the key splits of an attention launch: one thread per (row of a
+// split plane, 16-byte chunk of HD).  Row r of (batch b, kv head g) merges the
+// n_split partial states (M_s, L_s, acc_s) as softmax states merge:
+// out = sum_s w_s acc_s / sum_s w_s L_s with w_s = exp2(M_s - max_s M_s) (a
+// split with no visible key has M_s = -inf and weight 0; a row with none at
+// all ends 0 * (1/0) = NaN, as in the unsplit kernel).
+template <int HD>
+__global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
+    constexpr int CHUNKS = HD / 4;
+    constexpr int SG = 4;  // splits whose loads are issued together
+    const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
+    const size_t item = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (item >= plane * CHUNKS) return;
+    const size_t prow = item / CHUNKS;
+    const int ch = (int)(item % CHUNKS);
+    const int bg = (int)(prow / a.part_rows), r = (int)(prow % a.part_rows);
+    const int b = bg / a.n_head_kv, g = bg % a.n_head_kv;
+    const AttnSlot& S = a.slot[b];
+    if (r >= a.group * S.nq) return;
+    float Mx = -INFINITY, Ls = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < a.n_split; s0 += SG) {
+        float m[SG], l[SG];
+        f32x4 o[SG];
+#pragma unroll
+        for (int j = 0; j < SG; ++j) {
+            const int sp = min(s0 + j, a.n_split - 1);
+            const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + ((size_t)sp * plane + prow) * 2);
+            o[j] = *reinterpret_cast<const f32x4*>(a.part_o + ((size_t)sp * plane + prow) * HD + ch * 4);
+            const bool in = s0 + j < a.n_split;
+            m[j] = in ? ml.x : -INFINITY;
+            l[j] = ml.y;
+        }
+        float nm = Mx;
+#pragma unroll
+        for (int j = 0; j < SG; ++j) nm = __builtin_fmaxf(nm, m[j]);
+        if (nm == -INFINITY) continue;  // no visible key in these splits
+        const float f = Mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mx - nm);
+        acc *= f;
+        Ls *= f;
+#pragma unroll
+        for (int j = 0; j < SG; ++j) {
+            const float w = m[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[j] - nm);
+            Ls += w * l[j];
+            acc += w * o[j];
+        }
+        Mx = nm;
+    }
+    int hg, qi;
+    row_split(r, S.nq, __builtin_amdgcn_rcpf((float)S.nq), a.group, hg, qi);
+    float* orow = S.out + (size_t)qi * a.o_rstride + (size_t)(g * a.group + hg) * a.hd;
+    const f32x4 val = acc * __builtin_amdgcn_rcpf(Ls);
+    const int c0 = ch * 4;
+    if (a.hd == HD) {
+        *reinterpret_cast<f32x4*>(orow + c0) = val;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (c0 + e < a.hd) orow[c0 + e] = val[e];
+    }
 }
 
 template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM>
@@ -947,17 +947,6 @@ size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv) {
     return (size_t)p.n_split * rows * ((size_t)p.hd_tile + 2) * sizeof(float);
 }
 
-size_t split_ticket_count(const LaunchPlan& p, int n_batch, int n_head_kv) {
-    return p.n_split <= 1 ? 0 : (size_t)n_batch * n_head_kv * p.rowgroups;
-}
-
-hipError_t zero_ints(int* p, size_t n, hipStream_t st) {
-    if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p,
-                       (int)n);
-    return hipGetLastError();
-}
-
 // ceil(2^32 / d) when n * d < 2^32 for every n < n_max, else 0.
 static uint32_t div_magic(int d, int n_max) {
     if (d < 2 || (uint64_t)n_max * (uint64_t)d >= ((uint64_t)1 << 32)) return 0;
@@ -965,6 +954,7 @@ static uint32_t div_magic(int d, int n_max) {
 }
 
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
+    a.n_wg = p.n_workgroups;
     a.rowgroups = p.rowgroups;
     a.n_split = p.n_split;
     if (p.n_split > 1) {
@@ -974,7 +964,17 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.mg_split = div_magic(a.n_split, p.n_workgroups);
     a.mg_rowgroups = div_magic(a.rowgroups, p.n_workgroups);
     a.mg_hkv = div_magic(a.n_head_kv, p.n_workgroups);
-    return launch_shape(p, a, st);
+    a.part_rows = p.rowgroups * p.rb * 32;
+    hipError_t e = launch_shape(p, a, st);
+    if (e != hipSuccess || p.n_split <= 1) return e;
+    const size_t items = (size_t)a.n_batch * a.n_head_kv * a.part_rows * (p.hd_tile / 4);
+    const dim3 grid((unsigned)((items + 255) / 256));
+    switch (p.hd_tile) {
+        case 64: hipLaunchKernelGGL(split_merge_kernel<64>, grid, dim3(256), 0, st, a); break;
+        case 128: hipLaunchKernelGGL(split_merge_kernel<128>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(split_merge_kernel<256>, grid, dim3(256), 0, st, a); break;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace dr

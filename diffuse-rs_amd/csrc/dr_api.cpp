@@ -96,7 +96,6 @@ struct dr_ctx {
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials
-    DevBuf tickets;                      // key-split arrival counters (kept zero)
     DevBuf q, k, v, kc, vtc, meta, out;  // dr_attention() staging
 };
 
@@ -226,7 +225,7 @@ void dr_ctx_destroy(dr_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    for (DevBuf* b : {&ctx->part, &ctx->tickets, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc,
+    for (DevBuf* b : {&ctx->part, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc,
                       &ctx->meta, &ctx->out})
         release(*b);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
@@ -517,16 +516,6 @@ static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int 
     if (ws > 0) {
         DR_CHECK(ensure(ctx->part, ws));
         a.part_o = static_cast<float*>(ctx->part.p);
-        const size_t tb = dr::split_ticket_count(p, a.n_batch, a.n_head_kv) * sizeof(int);
-        if (tb > ctx->tickets.cap) {
-            // fresh counters start at zero; afterwards every launch leaves
-            // them at zero (the last workgroup of a row group resets its own)
-            DR_CHECK(ensure(ctx->tickets, tb));
-            hipError_t e = dr::zero_ints(static_cast<int*>(ctx->tickets.p),
-                                         ctx->tickets.cap / sizeof(int), ctx->stream);
-            if (e != hipSuccess) return hip_fail(e, "zeroing split tickets");
-        }
-        a.tickets = static_cast<int*>(ctx->tickets.p);
     }
     hipError_t e = dr::launch_attention(p, a, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "attention launch");

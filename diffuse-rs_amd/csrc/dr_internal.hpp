@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace dr {
@@ -32,25 +33,31 @@ struct AttnSlot {
 };
 
 struct AttnArgs {
-    AttnSlot slot[MAX_BATCH];
+    // The scalars of the workgroup decode and of the first loads fill the
+    // first 64 bytes, with batch slot 0 right behind, so the kernel fetches
+    // them with a few wide scalar loads and one wait.
     int n_batch;
-    int n_head, n_head_kv, group;  // group = n_head / n_head_kv
+    int n_head_kv, group;          // group = n_head / n_head_kv
     int hd;                        // actual head_dim (<= the kernel's HD tile)
     int cap;                       // key capacity of K/VT (multiple of KEY_ALIGN)
-    int q_rstride, o_rstride;      // elements between query / output rows
-    float c;                       // scale * log2(e), folded into Q
-    int window;                    // < 0: no sliding window
-    int prefix;                    // < 0: no causal prefix (scalar)
-    const float* qn_w;             // QK-norm gain for Q heads or nullptr
-    float qn_eps;
+    int q_rstride;                 // elements between query rows
     int rowgroups;                 // workgroup row groups per (batch, kv head)
     int n_split;                   // key splits; > 1 writes partials
+    uint32_t mg_split, mg_rowgroups, mg_hkv;  // division magic for the workgroup decode
+    float c;                       // scale * log2(e), folded into Q
+    int n_wg;                      // workgroups in the grid
+    int window;                    // < 0: no sliding window
+    int prefix;                    // < 0: no causal prefix (scalar)
+    int o_rstride;                 // elements between output rows
+    AttnSlot slot[MAX_BATCH];
+    int n_head;
+    const float* qn_w;             // QK-norm gain for Q heads or nullptr
+    float qn_eps;
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
-    uint32_t mg_split, mg_rowgroups, mg_hkv;  // division magic for the workgroup decode
-    int* tickets;                  // [batch*kv head][rowgroups] arrival counters, zero
-                                   // between launches (the last arriver resets its own)
+    int part_rows;                 // rows per (batch, kv head) in a split plane
 };
+static_assert(offsetof(AttnArgs, slot) == 64, "scalar block of AttnArgs is one 64-byte line");
 
 struct StoreArgs {
     const float* k;      // [n][n_head_kv][hd] f32 rows
@@ -111,11 +118,8 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
                           int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
                           int force_split);
 
-// Bytes of split workspace a plan needs (part_o + part_ml), and the number
-// of int tickets (which must be zero before the first launch).
+// Bytes of split workspace a plan needs (part_o + part_ml).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
-size_t split_ticket_count(const LaunchPlan& p, int n_batch, int n_head_kv);
-hipError_t zero_ints(int* p, size_t n, hipStream_t st);
 
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);

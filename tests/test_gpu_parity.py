@@ -293,6 +293,8 @@ def test_gemma_scale_one_error(dev):
 
 @pytest.mark.parametrize("n_split", [1, 2, 3, 5, 8])
 def test_split_count_does_not_change_result(dev, n_split):
+    """Key splits merged by the last workgroup of each row group give the
+    unsplit result."""
     cfg = CONFIGS["C2"]
     say(f"C2 with forced n_split={n_split}")
     dev.ctx.set_split(n_split)
