@@ -208,7 +208,7 @@ struct Geometry {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT>
 __attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD,
                                    Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD))) __global__
 __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
@@ -219,6 +219,9 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
 
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_red[3][NWT];
+    // fused step: each DMA wave's own copy of the K-norm gain (written and
+    // read by that wave only, so no barrier orders it)
+    __shared__ __attribute__((aligned(16))) float s_kn[ACT ? NP : 1][ACT ? HD : 1];
 
     // Every scalar of the decode and the first loads, and batch slot 0, is
     // requested here at once (wide scalar loads, one wait) rather than by one
@@ -335,6 +338,46 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     const int t1 = kt_lo + min((split + 1) * per, ntiles);
     const int nsup = (t1 - t0 + KQ - 1) / KQ;  // super-tiles
 
+    // Tile of slot u (super-tile u) of this wave's key group.  Without ACT,
+    // t0 + u*KQ + kq.  With ACT the fresh tiles (the suffix [ta, t1) of the
+    // range) are staged from f32 rows, which costs the staging wave far more
+    // than a DMA; the softmax does not depend on the key order, so each key
+    // group w takes the fresh tiles ta + j*KQ + w (j < m_w) spread evenly over
+    // its column of slots, phase-shifted by w so the groups stage in turn, and
+    // away from the first NS slots (staged before the loop can overlap them)
+    // when the column has room; the cached tiles fill the remaining slots, a
+    // contiguous block of them per key group.  Every tile of [t0, t1) lands in
+    // exactly one slot.
+    const int kg = compute ? kq : dwave;  // this wave's key group
+    auto group_slots = [&](int cnt, int w) __attribute__((always_inline)) {
+        return cnt > w ? (cnt - w + KQ - 1) / KQ : 0;
+    };
+    const int ta = ACT ? min(max(S.act0 / BN, t0), t1) : t1;  // first fresh tile
+    const int sl_w = group_slots(t1 - t0, kg), m_w = group_slots(t1 - ta, kg);
+    int pc_w = 0;  // cached tiles of the key groups before this one
+#pragma unroll
+    for (int w = 0; w < KQ; ++w)
+        if (w < kg) pc_w += group_slots(t1 - t0, w) - group_slots(t1 - ta, w);
+    const int ulo_w = min(NS, sl_w - m_w), span_w = sl_w - ulo_w;
+    // fresh slots of this key group before slot U: the j whose slot
+    // ulo_w + floor((j*KQ + kg) * span_w / (m_w*KQ)) is below U
+    auto fresh_before = [&](int U) __attribute__((always_inline)) {
+        const int num = (U - ulo_w) * m_w * KQ - kg * span_w;
+        if (m_w == 0 || num <= 0) return 0;
+        return min(m_w, (num + KQ * span_w - 1) / (KQ * span_w));
+    };
+    auto tile_at = [&](int u) __attribute__((always_inline)) {
+        if constexpr (!ACT) {
+            return t0 + u * KQ + kg;
+        } else {
+            // (uniform over the wave: the divisions run on the vector unit,
+            // and the DMA takes the tile offset in a scalar register)
+            const int b0 = fresh_before(u);
+            return __builtin_amdgcn_readfirstlane(fresh_before(u + 1) > b0 ? ta + b0 * KQ + kg
+                                                                           : t0 + pc_w + (u - b0));
+        }
+    };
+
     // ---- DMA plan: instruction j of this wave fills 64 chunks of one tile
     // region (region 2*i is K tile i of the super-tile, 2*i+1 its V^T tile).
     // A wave's instructions cover whole regions or part of one, so the
@@ -344,9 +387,9 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     constexpr bool WHOLE = (NLDW * 64) % CPT == 0;
     static_assert(WHOLE || CPT % (NLDW * 64) == 0, "DMA split");
     const int wreg0 = (dwave * NLDW * 64) / CPT;
-    auto voff_of = [&](int j) __attribute__((always_inline)) -> int {
+    auto voff_of = [&](int j, int ln) __attribute__((always_inline)) -> int {
         const int jreg = WHOLE ? (j * 64) / CPT : 0;
-        const int idx = (WHOLE ? (j * 64) % CPT : (dwave * NLDW * 64) % CPT + j * 64) + lane;
+        const int idx = (WHOLE ? (j * 64) % CPT : (dwave * NLDW * 64) % CPT + j * 64) + ln;
         if (((wreg0 + jreg) & 1) == 0) {
             const int R = idx / KCH, pk = idx % KCH;
             return (((R & ~31) + sigma(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3)) * 2;
@@ -360,15 +403,22 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     int voff[NP > 0 ? 1 : NLDW];
     if constexpr (NP == 0) {
 #pragma unroll
-        for (int j = 0; j < NLDW; ++j) voff[j] = voff_of(j);
+        for (int j = 0; j < NLDW; ++j) voff[j] = voff_of(j, lane);
     }
     const uint32_t plane_bytes = (uint32_t)a.cap * HD * 2;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k + (size_t)g * a.cap * HD, plane_bytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vt + (size_t)g * HD * a.cap, plane_bytes);
 
-    // DMA instructions [j0, j1) of super-tile u into stage st.
-    auto issue_range = [&](int u, int st, int j0, int j1) __attribute__((always_inline)) {
+    // DMA instructions [j0, j1) of super-tile u into stage st (ACT: each DMA
+    // wave fills its own key group, whose tile in super-tile u is tt).
+    auto issue_range = [&](int u, int st, int j0, int j1, int tt) __attribute__((always_inline)) {
         const int cofs = WHOLE ? 0 : (dwave * NLDW * 64) % CPT;  // first chunk in the region
+        // (fused step: an opaque lane index, as for the staged tiles below)
+        int ln = lane;
+        if constexpr (ACT) {
+            asm volatile("" : "+v"(ln));
+            ln &= 63;
+        }
 #pragma unroll
         for (int j = 0; j < NLDW; ++j) {
             if (j < j0 || j >= j1) continue;
@@ -377,16 +427,158 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
             uint16_t* dst = smem + (kqr * NS + st) * SLOT + (reg & 1) * TILE +
                             ((WHOLE ? (j * 64) % CPT : cofs + j * 64) << 3);
             // slots past the range reload the last tile: in bounds, unused
-            const int t = min(t0 + u * KQ + kqr, t1 - 1);
-            const int vo = NP > 0 ? voff_of(j) : voff[NP > 0 ? 0 : j];
+            const int t = ACT ? __builtin_amdgcn_readfirstlane(tt) : min(t0 + u * KQ + kqr, t1 - 1);
+            const int vo = NP > 0 ? voff_of(j, ln) : voff[NP > 0 ? 0 : j];
             if (reg & 1)
                 dma16(rv, dst, vo, t * (BN * 2));
             else
                 dma16(rk, dst, vo, t * (BN * HD * 2));
         }
     };
-    auto issue = [&](int u, int st) __attribute__((always_inline)) {
-        issue_range(u, st, 0, NLDW);
+    auto issue = [&](int u, int st, int tt = 0) __attribute__((always_inline)) {
+        issue_range(u, st, 0, NLDW, tt);
+    };
+
+    // Fused step (ACT): a tile whose keys are the step's fresh rows is staged
+    // by the DMA wave of its key group through registers instead of the DMA:
+    // f32 rows of ka / va, K-normalised when asked, rounded to bf16 and
+    // written as the same permuted, swizzled LDS image the DMA produces (V
+    // transposed on the way).  The workgroup whose row group matches the
+    // tile (one per kv head and key split) also writes the bf16 rows into the
+    // cache: StepCache::store (cache.rs:62-71) of those rows, positions the
+    // launch never reads from the cache.  Staging has two phases so that the
+    // load latency overlaps a super-tile of compute: act_load issues the f32
+    // loads into kx / vx one pipeline iteration ahead, act_write converts and
+    // writes them in the iteration the DMA would have been issued.
+    static_assert(!ACT || (NP > 0 && NP == KQ && NLDW * 64 == 2 * CPT),
+                  "fused step: each DMA wave stages one key group's K and V^T tiles");
+    constexpr int KJ = ACT ? CPT / 64 : 1;             // K chunks per lane
+    constexpr int VJ = ACT ? (HD / 4) * VCH / 64 : 1;  // (4 d x 8 keys) blocks per lane
+    // The lane index as a value the compiler cannot see through: offsets
+    // derived from it are recomputed per use instead of hoisted out of the
+    // producer loop (which holds a staged tile in registers) and spilled.
+    auto opaque_lane = [&]() __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        return ln & 63;  // the range, for the compiler's arithmetic
+    };
+    using KRegs = f32x4[KJ][2];
+    using VRegs = f32x4[VJ][8];
+    // Buffer loads with 32-bit offsets from kv head g's first element; the
+    // range of the resources ends at the pass's last row, so rows past it
+    // read as zeros (the padding of the tile) and every load is issued
+    // without a branch, needing no wait until act_write.
+    auto act_load = [&](int t, KRegs& kx, VRegs& vx) __attribute__((always_inline)) {
+        const int key0 = t * BN - S.act0;
+        const int ln = opaque_lane();
+        const uint32_t nb = (uint32_t)(S.n_act * a.kv_rstride - g * HD) * 4u;
+        const __amdgpu_buffer_rsrc_t rka = make_rsrc(S.ka + (size_t)g * HD, nb);
+        const __amdgpu_buffer_rsrc_t rva = make_rsrc(S.va + (size_t)g * HD, nb);
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+            const int c = ln + 64 * j, R = c / KCH, lc = (c % KCH) ^ swz<KCH>(R);
+            const int off = ((key0 + sigma(R)) * a.kv_rstride + 8 * lc) * 4;
+            kx[j][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rka, off, 0, 0));
+            kx[j][1] =
+                __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rka, off + 16, 0, 0));
+        }
+#pragma unroll
+        for (int jj = 0; jj < VJ; ++jj) {
+            const int pp = ln + 64 * jj, d0 = 4 * (pp / VCH), lv = pp % VCH;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const int off = ((key0 + 8 * lv + kk) * a.kv_rstride + d0) * 4;
+                vx[jj][kk] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rva, off, 0, 0));
+            }
+        }
+    };
+    auto act_write = [&](int t, int st, const KRegs& kx, const VRegs& vx)
+        __attribute__((always_inline)) {
+        uint16_t* kdst = smem + (dwave * NS + st) * SLOT;
+        uint16_t* vdst = kdst + TILE;
+        const int key0 = t * BN;
+        const int ln = opaque_lane();
+        const bool own = ((t - S.act0 / BN) % a.rowgroups) == rg;
+        // cache planes of kv head g, written with 32-bit byte offsets (one
+        // register per address: 64-bit addresses of the 16 row pieces would
+        // not fit beside the staged data)
+        const __amdgpu_buffer_rsrc_t wk = make_rsrc(S.kst + (size_t)g * a.cap * HD, plane_bytes);
+        const __amdgpu_buffer_rsrc_t wv = make_rsrc(S.vst + (size_t)g * HD * a.cap, plane_bytes);
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+            const int c = ln + 64 * j, R = c / KCH, lc = (c % KCH) ^ swz<KCH>(R);
+            f32x4 x0 = kx[j][0], x1 = kx[j][1];
+            if (a.kn_w) {
+                // rms_norm_inplace (ops.rs:106-114) per head row: f32 squares
+                // summed in f64; the KCH lanes holding a row's chunks are
+                // consecutive.
+                double ss = 0.0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sq0 = x0[e] * x0[e];
+                    ss += (double)sq0;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sq1 = x1[e] * x1[e];
+                    ss += (double)sq1;
+                }
+#pragma unroll
+                for (int off = 1; off < KCH; off <<= 1) ss += __shfl_xor(ss, off);
+                const float sc = 1.0f / (float)sqrt(ss / (double)HD + (double)a.kn_eps);
+                const f32x4 w0 = *reinterpret_cast<const f32x4*>(&s_kn[dwave][8 * lc]);
+                const f32x4 w1 = *reinterpret_cast<const f32x4*>(&s_kn[dwave][8 * lc + 4]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x0[e] = x0[e] * sc * w0[e];
+                    x1[e] = x1[e] * sc * w1[e];
+                }
+            }
+            bf16x8 y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[e] = (__bf16)x0[e];
+                y[4 + e] = (__bf16)x1[e];
+            }
+            *reinterpret_cast<bf16x8*>(kdst + c * 8) = y;
+            if (own && key0 + sigma(R) - S.act0 < S.n_act)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, y), wk, ((key0 + sigma(R)) * HD + 8 * lc) * 2, 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < VJ; ++jj) {
+            const int pp = ln + 64 * jj, d0 = 4 * (pp / VCH), lv = pp % VCH;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = d0 + i;
+                bf16x8 y;
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) y[kk] = (__bf16)vx[jj][kk][i];
+                *reinterpret_cast<bf16x8*>(vdst + (d * VCH + (lv ^ swz<VCH>(d))) * 8) = y;
+                if (own)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), wv,
+                                                           (d * a.cap + key0 + 8 * lv) * 2, 0, 0);
+            }
+        }
+    };
+    // What a DMA wave does for super-tile u into stage st before the main
+    // loop: the DMA, or with ACT, both staging phases when its key group's
+    // tile is active (no work when the key group has no tile there).
+    auto fill = [&](int u, int st) __attribute__((always_inline)) {
+        if constexpr (ACT) {
+            if (u >= sl_w) return;
+            const int t = tile_at(u);
+            if (t >= ta) {
+                KRegs kx;
+                VRegs vx;
+                act_load(t, kx, vx);
+                act_write(t, st, kx, vx);
+            } else {
+                issue(u, st, t);
+            }
+            return;
+        }
+        issue(u, st);
     };
 
     // ---- Q: the workgroup's rows, loaded once (coalesced f32x4 row pieces,
@@ -420,9 +612,13 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     }
 
     if (dma) {
+        if constexpr (ACT) {
+            if (a.kn_w)
+                for (int i = lane; i < HD; i += 64) s_kn[dwave][i] = a.kn_w[i];
+        }
 #pragma unroll
         for (int i = 0; i < NS - 1; ++i)
-            if (i < nsup) issue(i, i);
+            if (i < nsup) fill(i, i);
     }
 
     uint16_t* qs = smem + (NS - 1) * SLOT;
@@ -458,253 +654,314 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     auto qfrag = [&](int c) __attribute__((always_inline)) {
         return *reinterpret_cast<const bf16x8*>(qrow_l + (((2 * c + hf) ^ swz<KCH>(col)) << 3));
     };
-    bf16x8 qf[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
-
-    // ---- main loop over super-tiles
-    f32x16 o[ND];
-#pragma unroll
-    for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-    float mu = 0.0f;          // running max m (log2 units), valid once m_set
-    bool m_set = false;
-    float thr = -INFINITY;    // a score above mu + thr moves m
-    float l_lo = 0.0f, l_hi = 0.0f;
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-
-    // O^T += V^T P^T for one tile whose V^T fragments and P are in registers.
-    // Contraction slot 8*hf + j of MFMA hh is key 16*hf + 8*hh + j, in both
-    // operands.
-    auto pv = [&](const bf16x8 (&vf)[ND][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int db = 0; db < ND; ++db) {
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pf[0], o[db], 0, 0, 0);
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pf[1], o[db], 0, 0, 0);
-        }
-    };
-
-    // One super-tile.  A compute wave software-pipelines its tiles: the PV
-    // product of its previous tile (V^T fragments vf and P pin, in registers)
-    // is issued in program order between the VALU instructions of this
-    // tile's softmax, so the matrix core and the VALU work at the same time
-    // (with one compute wave per SIMD nothing else would fill either).  This
-    // tile's P goes to pout, and its V^T fragments replace vf once those
-    // MFMAs have read them (one set of V^T registers, which leaves room for
-    // Q's); the first step multiplies zero fragments.  Without DMA waves (NP == 0)
-    // the DMA of super-tile u+NS-1 is issued in three parts spread over the
-    // compute, so that no wave stalls on a burst of memory instructions in
-    // front of its MFMAs.  Head dim 256 has no registers for a second set of
-    // V^T fragments (Q stays in registers there): its PV product is issued
-    // in the step of its tile, after the softmax (PIPE false).
-    constexpr bool PIPE = HD <= 128;
-    constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
-    auto step = [&](int u, bf16x8 (&vf)[ND][2], const bf16x8 (&pin)[2], bf16x8 (&pout)[2])
-        __attribute__((always_inline)) {
-        const int st = u % NS;
-        if (dma) wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
-        __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
-        const int un = u + NS - 1, stn = (u + NS - 1) % NS;
-        if constexpr (NP > 0) {
-            if (!compute) {
-                if (un < nsup) issue(un, stn);
-                return;
-            }
-        }
-        const bool pf = NP == 0 && un < nsup;
-
-        const int t = t0 + u * KQ + kq;
-        if (t >= t1) {  // this key group has no tile in the last super-tile
-            if (pf) issue(un, stn);
-            if constexpr (PIPE) pv(vf, pin);
-            pout[0] = pout[1] = bf16x8{};  // vf holds finite values: nothing is added
-            return;
-        }
-        const uint16_t* ks = smem + (kq * NS + st) * SLOT;
-        const uint16_t* vs = ks + TILE;
-        const int kbase_t = t * BN;
-
-        // per-key metadata (arbitrary key positions / ids): loaded per tile
-        int kp[16], kqs[16];
-        if constexpr (MODE == MASK_KEYS) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int kidx = min(kbase_t + 16 * hf + i, S.nk - 1);
-                kp[i] = S.kpos ? S.kpos[kidx] : kidx;
-                kqs[i] = S.kseq ? S.kseq[kidx] : 0;
-            }
-        }
-        if (pf) issue_range(un, stn, 0, J1);
-        __builtin_amdgcn_sched_barrier(0);
-
-        // S^T = K Q^T - m: -m enters as the accumulator init, so the scores
-        // come out relative to m.  The K fragments are requested in two
-        // halves, the second while the MFMAs of the first run.
-        f32x16 s;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = -mu;
-        {
-            constexpr int NH = NC / 2;
-            const uint16_t* krow = ks + col * HD;
-            const int sw = swz<KCH>(col);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                bf16x8 kf[NH];
-#pragma unroll
-                for (int c = 0; c < NH; ++c)
-                    kf[c] = *reinterpret_cast<const bf16x8*>(
-                        krow + (((2 * (h * NH + c) + hf) ^ sw) << 3));
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int c = 0; c < NH; ++c)
-                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[h * NH + c], s, 0, 0, 0);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-
-        // this tile's V^T fragments
-        auto read_v = [&]() __attribute__((always_inline)) {
-#pragma unroll
-            for (int db = 0; db < ND; ++db) {
-                const int d = db * 32 + col;
-                const uint16_t* vrow = vs + d * BN;
-                const int sw = swz<VCH>(d);
-                vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
-                vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
-            }
-        };
-        if constexpr (!PIPE) read_v();
-        if (pf) issue_range(un, stn, J1, J2);
-
-        // Masking: s[i] is the score of key t*BN + 16*hf + i.
-        bool full = kbase_t + BN <= S.nk;
-        if constexpr (MODE == MASK_POS) {
-            const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
-                                                 kbase_t + BN - 1 - qmin < a.window);
-            full = full && tiles_can_be_full && win_ok;
-        } else if constexpr (MODE == MASK_KEYS) {
-            full = false;
-        }
-        if (!full) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int kidx = kbase_t + 16 * hf + i;
-                bool vis = kidx < S.nk;
-                if constexpr (MODE == MASK_POS) {
-                    vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
-                } else if constexpr (MODE == MASK_KEYS) {
-                    vis = vis & visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
-                }
-                s[i] = vis ? s[i] : -INFINITY;
-            }
-        }
-
-        // Online softmax with a lazily moved max (scores are relative to mu).
-        float mx = max3(s[0], s[1], s[2]);
-#pragma unroll
-        for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
-        mx = __builtin_fmaxf(mx, s[15]);
-        // The column max over both lane halves decides, so lane and lane^32
-        // move m together.  O is rescaled after the previous tile's PV
-        // product (whose P is relative to the old m) has gone into it, and
-        // before this tile's.
-        const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
-        float alpha = 1.0f;
-        if (moved) {
-            const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-            const bool upd = cm > thr;
-            const float delta = upd ? cm : 0.0f;
-            alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
-            mu += delta;
-            m_set = m_set | upd;
-            thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] -= delta;
-            l_lo *= alpha;
-            l_hi *= alpha;
-        }
-
-        // p = exp2(s) rounded to bf16 in pairs; l sums the rounded values
-        // (what the PV product multiplies), so the weights normalise exactly.
-        // The previous tile's PV MFMAs are interleaved with this VALU work.
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            u32x4 w4;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float p0 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j]);
-                const float p1 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j + 1]);
-                const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
-                w4[j] = __builtin_bit_cast(uint32_t, pr);
-                if (hh == 0)
-                    l_lo = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_lo, false);
-                else
-                    l_hi = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_hi, false);
-            }
-            pout[hh] = __builtin_bit_cast(bf16x8, w4);
-        }
-        if constexpr (PIPE) {
-            pv(vf, pin);
-#pragma unroll
-            for (int i = 0; i < 2 * ND; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (moved) {
-#pragma unroll
-            for (int db = 0; db < ND; ++db) o[db] *= alpha;
-        }
-        if constexpr (PIPE) read_v();
-        if (pf) issue_range(un, stn, J2, NLDW);
-        if constexpr (!PIPE) pv(vf, pout);
-    };
-
-    {
-        bf16x8 vf[ND][2], pfa[2], pfb[2];
-#pragma unroll
-        for (int db = 0; db < ND; ++db) vf[db][0] = vf[db][1] = bf16x8{};
-        pfa[0] = pfa[1] = bf16x8{};
-        int u = 0;
-        for (; u + 1 < nsup; u += 2) {
-            step(u, vf, pfa, pfb);
-            step(u + 1, vf, pfb, pfa);
-        }
-        if (u < nsup) {
-            step(u, vf, pfa, pfb);
-            if (PIPE && compute) pv(vf, pfb);
-        } else if (PIPE && compute) {
-            pv(vf, pfa);
-        }
-    }
-
-    // ---- merge the KQ key groups of each row block through LDS
-    const float l_run = l_lo + l_hi;
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float m_fin = m_set ? mu : -INFINITY;
-    __syncthreads();  // every wave is done with the tile stages
+    // The merge area of the epilogue (it overlays the tile stages).
     float* mrows = reinterpret_cast<float*>(smem);  // [NW][32][ROWF]
     float* sm = mrows + NW * 32 * ROWF;             // [NW][32] running max
     float* sl = sm + NW * 32;                       // [NW][32] scaled sum
-    if (compute && hf == 0) sm[wave * 32 + col] = m_fin;
-    __syncthreads();
-    if (compute) {
-        float M = -INFINITY;
+
+    // Compute waves and DMA-only waves run separate loops with the same
+    // number of barriers, so that none of the compute state (O, P, V^T and Q
+    // fragments) is live in the DMA waves' code, which needs registers of its
+    // own to stage fused-step tiles.
+    if (NP == 0 || compute) {
+        bf16x8 qf[NC];
 #pragma unroll
-        for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + col]);
-        const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
-        // o[db][4j + e] is O^T[d = db*32 + 8j + 4hf + e][col]
-        float* myrow = mrows + (wave * 32 + col) * ROWF;
+        for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
+
+        // ---- main loop over super-tiles
+        f32x16 o[ND];
 #pragma unroll
-        for (int db = 0; db < ND; ++db)
+        for (int db = 0; db < ND; ++db) o[db] = f32x16{};
+        float mu = 0.0f;          // running max m (log2 units), valid once m_set
+        bool m_set = false;
+        float thr = -INFINITY;    // a score above mu + thr moves m
+        float l_lo = 0.0f, l_hi = 0.0f;
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+        // O^T += V^T P^T for one tile whose V^T fragments and P are in registers.
+        // Contraction slot 8*hf + j of MFMA hh is key 16*hf + 8*hh + j, in both
+        // operands.
+        auto pv = [&](const bf16x8 (&vf)[ND][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                f32x4 val;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) val[e] = o[db][4 * j + e] * sc;
-                *reinterpret_cast<f32x4*>(myrow + db * 32 + 8 * j + 4 * hf) = val;
+            for (int db = 0; db < ND; ++db) {
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pf[0], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pf[1], o[db], 0, 0, 0);
             }
-        if (hf == 0) sl[wave * 32 + col] = l_tot * sc;
+        };
+
+        // One super-tile.  A compute wave software-pipelines its tiles: the PV
+        // product of its previous tile (V^T fragments vf and P pin, in registers)
+        // is issued in program order between the VALU instructions of this
+        // tile's softmax, so the matrix core and the VALU work at the same time
+        // (with one compute wave per SIMD nothing else would fill either).  This
+        // tile's P goes to pout, and its V^T fragments replace vf once those
+        // MFMAs have read them (one set of V^T registers, which leaves room for
+        // Q's); the first step multiplies zero fragments.  Without DMA waves (NP == 0)
+        // the DMA of super-tile u+NS-1 is issued in three parts spread over the
+        // compute, so that no wave stalls on a burst of memory instructions in
+        // front of its MFMAs.  Head dim 256 has no registers for a second set of
+        // V^T fragments (Q stays in registers there): its PV product is issued
+        // in the step of its tile, after the softmax (PIPE false).
+        constexpr bool PIPE = HD <= 128;
+        constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
+        auto step = [&](int u, bf16x8 (&vf)[ND][2], const bf16x8 (&pin)[2], bf16x8 (&pout)[2])
+            __attribute__((always_inline)) {
+            const int st = u % NS;
+            if (dma) {
+                // a fused-step super-tile may issue no DMA (staged) or extra
+                // cache stores, so the per-super-tile vmcnt accounting does not
+                // hold: wait for everything
+                if constexpr (ACT)
+                    wait_vmcnt<0>();
+                else
+                    wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
+            }
+            __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
+            const int un = u + NS - 1, stn = (u + NS - 1) % NS;
+            const bool pf = NP == 0 && un < nsup;
+
+            if (t0 + u * KQ + kq >= t1) {  // this key group has no tile in the last super-tile
+                if (pf) issue(un, stn);
+                if constexpr (PIPE) pv(vf, pin);
+                pout[0] = pout[1] = bf16x8{};  // vf holds finite values: nothing is added
+                return;
+            }
+            const int t = tile_at(u);
+            const uint16_t* ks = smem + (kq * NS + st) * SLOT;
+            const uint16_t* vs = ks + TILE;
+            const int kbase_t = t * BN;
+
+            // per-key metadata (arbitrary key positions / ids): loaded per tile
+            int kp[16], kqs[16];
+            if constexpr (MODE == MASK_KEYS) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kidx = min(kbase_t + 16 * hf + i, S.nk - 1);
+                    kp[i] = S.kpos ? S.kpos[kidx] : kidx;
+                    kqs[i] = S.kseq ? S.kseq[kidx] : 0;
+                }
+            }
+            if (pf) issue_range(un, stn, 0, J1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+
+            // S^T = K Q^T - m: -m enters as the accumulator init, so the scores
+            // come out relative to m.  The K fragments are requested in two
+            // halves, the second while the MFMAs of the first run.
+            f32x16 s;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = -mu;
+            {
+                constexpr int NH = NC / 2;
+                const uint16_t* krow = ks + col * HD;
+                const int sw = swz<KCH>(col);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    bf16x8 kf[NH];
+#pragma unroll
+                    for (int c = 0; c < NH; ++c)
+                        kf[c] = *reinterpret_cast<const bf16x8*>(
+                            krow + (((2 * (h * NH + c) + hf) ^ sw) << 3));
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int c = 0; c < NH; ++c)
+                        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[h * NH + c], s, 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+
+            // this tile's V^T fragments
+            auto read_v = [&]() __attribute__((always_inline)) {
+#pragma unroll
+                for (int db = 0; db < ND; ++db) {
+                    const int d = db * 32 + col;
+                    const uint16_t* vrow = vs + d * BN;
+                    const int sw = swz<VCH>(d);
+                    vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
+                    vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
+                }
+            };
+            if constexpr (!PIPE) read_v();
+            if (pf) issue_range(un, stn, J1, J2, 0);
+
+            // Masking: s[i] is the score of key t*BN + 16*hf + i.
+            bool full = kbase_t + BN <= S.nk;
+            if constexpr (MODE == MASK_POS) {
+                const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
+                                                     kbase_t + BN - 1 - qmin < a.window);
+                full = full && tiles_can_be_full && win_ok;
+            } else if constexpr (MODE == MASK_KEYS) {
+                full = false;
+            }
+            if (!full) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kidx = kbase_t + 16 * hf + i;
+                    bool vis = kidx < S.nk;
+                    if constexpr (MODE == MASK_POS) {
+                        vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                    } else if constexpr (MODE == MASK_KEYS) {
+                        vis = vis & visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
+                    }
+                    s[i] = vis ? s[i] : -INFINITY;
+                }
+            }
+
+            // Online softmax with a lazily moved max (scores are relative to mu).
+            float mx = max3(s[0], s[1], s[2]);
+#pragma unroll
+            for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
+            mx = __builtin_fmaxf(mx, s[15]);
+            // The column max over both lane halves decides, so lane and lane^32
+            // move m together.  O is rescaled after the previous tile's PV
+            // product (whose P is relative to the old m) has gone into it, and
+            // before this tile's.
+            const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+            float alpha = 1.0f;
+            if (moved) {
+                const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+                const bool upd = cm > thr;
+                const float delta = upd ? cm : 0.0f;
+                alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+                mu += delta;
+                m_set = m_set | upd;
+                thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] -= delta;
+                l_lo *= alpha;
+                l_hi *= alpha;
+            }
+
+            // p = exp2(s) rounded to bf16 in pairs; l sums the rounded values
+            // (what the PV product multiplies), so the weights normalise exactly.
+            // The previous tile's PV MFMAs are interleaved with this VALU work.
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                u32x4 w4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p0 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j]);
+                    const float p1 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j + 1]);
+                    const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
+                    w4[j] = __builtin_bit_cast(uint32_t, pr);
+                    if (hh == 0)
+                        l_lo = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_lo, false);
+                    else
+                        l_hi = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_hi, false);
+                }
+                pout[hh] = __builtin_bit_cast(bf16x8, w4);
+            }
+            if constexpr (PIPE) {
+                pv(vf, pin);
+#pragma unroll
+                for (int i = 0; i < 2 * ND; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (moved) {
+#pragma unroll
+                for (int db = 0; db < ND; ++db) o[db] *= alpha;
+            }
+            if constexpr (PIPE) read_v();
+            if (pf) issue_range(un, stn, J2, NLDW, 0);
+            if constexpr (!PIPE) pv(vf, pout);
+        };
+
+        {
+            bf16x8 vf[ND][2], pfa[2], pfb[2];
+#pragma unroll
+            for (int db = 0; db < ND; ++db) vf[db][0] = vf[db][1] = bf16x8{};
+            pfa[0] = pfa[1] = bf16x8{};
+            int u = 0;
+            for (; u + 1 < nsup; u += 2) {
+                step(u, vf, pfa, pfb);
+                step(u + 1, vf, pfb, pfa);
+            }
+            if (u < nsup) {
+                step(u, vf, pfa, pfb);
+                if (PIPE) pv(vf, pfb);
+            } else if (PIPE) {
+                pv(vf, pfa);
+            }
+        }
+
+        // ---- merge the KQ key groups of each row block through LDS
+        const float l_run = l_lo + l_hi;
+        const float l_tot = l_run + __shfl_xor(l_run, 32);
+        const float m_fin = m_set ? mu : -INFINITY;
+        __syncthreads();  // every wave is done with the tile stages
+        if (hf == 0) sm[wave * 32 + col] = m_fin;
+        __syncthreads();
+        {
+            float M = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + col]);
+            const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
+            // o[db][4j + e] is O^T[d = db*32 + 8j + 4hf + e][col]
+            float* myrow = mrows + (wave * 32 + col) * ROWF;
+#pragma unroll
+            for (int db = 0; db < ND; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x4 val;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) val[e] = o[db][4 * j + e] * sc;
+                    *reinterpret_cast<f32x4*>(myrow + db * 32 + 8 * j + 4 * hf) = val;
+                }
+            if (hf == 0) sl[wave * 32 + col] = l_tot * sc;
+        }
+    } else if constexpr (ACT) {
+        // A DMA fill is waited for before the next barrier; a staged one is
+        // not (its LDS writes complete before the barrier, and its cache
+        // stores need no wait).  pre: kx / vx hold super-tile un's tile; when
+        // its NLA loads were issued after the DMA, the wait leaves them in
+        // flight (vector memory instructions complete in issue order for
+        // vmcnt; every load of act_load is issued, none is predicated).
+        constexpr int NLA = 2 * KJ + 8 * VJ;
+        static_assert(NLA < 64, "vmcnt range");
+        bool wait_dma = true, pre = false;
+        KRegs kx;
+        VRegs vx;
+        int tnext = NS - 1 < sl_w ? tile_at(NS - 1) : -1;  // tile of slot un
+        for (int u = 0; u < nsup; ++u) {
+            if (wait_dma) {
+                if (pre)
+                    wait_vmcnt<NLA>();
+                else
+                    wait_vmcnt<0>();
+            }
+            __syncthreads();
+            const int un = u + NS - 1;
+            wait_dma = false;
+            if (un < sl_w) {
+                const int tn = tnext;
+                tnext = un + 1 < sl_w ? tile_at(un + 1) : -1;
+                if (tn >= ta) {
+                    if (!pre) act_load(tn, kx, vx);
+                    act_write(tn, un % NS, kx, vx);
+                } else {
+                    issue(un, un % NS, tn);
+                    wait_dma = true;
+                }
+                pre = tnext >= ta;
+                // the next tile's loads go after this tile's conversion (not
+                // interleaved with it: both register sets would be live)
+                __builtin_amdgcn_sched_barrier(0);
+                if (pre) act_load(tnext, kx, vx);
+            }
+        }
+        __syncthreads();  // the two barriers of the compute waves' merge
+        __syncthreads();
+    } else {
+        for (int u = 0; u < nsup; ++u) {
+            wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
+            __syncthreads();
+            const int un = u + NS - 1;
+            if (un < nsup) issue(un, un % NS);
+        }
+        __syncthreads();  // the two barriers of the compute waves' merge
+        __syncthreads();
     }
     __syncthreads();
 
@@ -829,11 +1086,11 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     }
 }
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT>
 hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     constexpr size_t lds = Geometry<HD, RB, KQ, NS, NP>::LDS_BYTES;
     static bool attr_set = false;
-    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QNORM>;
+    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QNORM, ACT>;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -846,15 +1103,31 @@ hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
 
 template <int HD, int RB, int KQ, int NS, int NP>
 hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    // Fused-step instances exist for the shapes whose DMA waves each own one
+    // key group (plan_supports_act), in the cached modes.
+    constexpr bool CAN_ACT = NP > 0 && NP == KQ && RB == 1;
+    if (p.act) {
+        if constexpr (CAN_ACT) {
+            // The fused step runs the position-masked kernel also without a
+            // mask: with no window, prefix or sequence ids its full tiles take
+            // the unmasked path, and the register budget of that build holds
+            // a staged tile across the producer loop.
+            if (p.mask == MASK_KEYS) return hipErrorInvalidValue;
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, true>(p, a, st);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
     switch (p.mask) {
         case MASK_NONE:
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false>(p, a, st);
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, false>(p, a, st);
         case MASK_POS:
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false>(p, a, st);
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false>(p, a, st);
         default:
-            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false>(p, a, st);
+            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false>(p, a, st);
     }
 }
 
@@ -896,7 +1169,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
                           int force_split) {
-    LaunchPlan p;
+    LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : 256);
     p.block_n = BN;
     p.mask = mask;
@@ -939,6 +1212,11 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     p.n_split = split;
     p.n_workgroups = base * split;
     return p;
+}
+
+bool plan_supports_act(const LaunchPlan& p) {
+    const Shape* sh = find_shape(p.hd_tile, p.rb, p.kq);
+    return sh && sh->np > 0 && sh->np == sh->kq && sh->rb == 1 && p.mask != MASK_KEYS;
 }
 
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv) {

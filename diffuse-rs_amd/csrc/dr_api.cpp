@@ -93,6 +93,7 @@ struct dr_ctx {
     int force_split = 0;
     int force_rb = 0;
     int force_kq = 0;
+    int fused_step = 0;  // dr_attention_step may run the fused kernel
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials
@@ -104,7 +105,7 @@ struct dr_pass {
     int* d_pos = nullptr;
     size_t n = 0;
     size_t cap = 0;
-    size_t max_pos = 0;
+    size_t min_pos = 0, max_pos = 0;
 };
 
 struct dr_step_cache {
@@ -156,6 +157,7 @@ int upload_pass(dr_pass* p, const size_t* active, size_t n) {
         DR_HIP(hipStreamSynchronize(p->ctx->stream));
     }
     p->n = n;
+    p->min_pos = n > 0 ? active[0] : 0;
     p->max_pos = mx;
     return DR_OK;
 }
@@ -242,6 +244,7 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
     info->head_dim_tile = ctx->last.hd_tile;
     info->row_blocks = ctx->last.rb;
     info->key_groups = ctx->last.kq;
+    info->fused_step = ctx->last.act ? 1 : 0;
     return DR_OK;
 }
 
@@ -249,6 +252,12 @@ int dr_ctx_set_split(dr_ctx* ctx, int n_split) {
     if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_split: ctx is NULL");
     if (n_split < 0 || n_split > 64) return fail(DR_ERR_INVALID, "n_split %d not in 0..64", n_split);
     ctx->force_split = n_split;
+    return DR_OK;
+}
+
+int dr_ctx_set_fused_step(dr_ctx* ctx, int enable) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_fused_step: ctx is NULL");
+    ctx->fused_step = enable ? 1 : 0;
     return DR_OK;
 }
 
@@ -507,11 +516,13 @@ int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
 
 // ---------------------------------------------------------------- attention
 
-static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int max_nk,
-                          int mask, bool qnorm) {
-    dr::LaunchPlan p =
-        dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qnorm,
-                           ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split);
+static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int max_nq,
+                               int max_nk, int mask, bool qnorm) {
+    return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qnorm,
+                              ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split);
+}
+
+static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
         DR_CHECK(ensure(ctx->part, ws));
@@ -524,6 +535,11 @@ static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int 
     return DR_OK;
 }
 
+static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int max_nk,
+                          int mask, bool qnorm) {
+    return launch_plan(ctx, a, plan_for(ctx, a, hd, max_nq, max_nk, mask, qnorm));
+}
+
 static float scale_log2(float scale) { return scale * 1.4426950408889634f; }
 
 static int opt_to_int(dr_opt_usize o) {
@@ -531,21 +547,23 @@ static int opt_to_int(dr_opt_usize o) {
     return (int)std::min(o.value, MAX_POS);
 }
 
-int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
-                        size_t n_items, size_t n_head, dr_opt_usize sliding_window,
-                        dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
-                        float q_norm_eps) {
-    DR_CHECK(check_slot(cache, layer, 0, "dr_attention_cached"));
-    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "dr_attention_cached: no items");
+// The AttnArgs of a cached attention call over items (q, out, pass per
+// batch slot), validated; max_nq = 0 means every pass is empty.
+static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
+                       size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                       dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                       float q_norm_eps, const char* who, dr::AttnArgs& a, int& max_nq) {
+    DR_CHECK(check_slot(cache, layer, 0, who));
+    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "%s: no items", who);
     if (n_items > cache->n_batch)
-        return fail(DR_ERR_INVALID, "dr_attention_cached: %zu items > cache n_batch %zu", n_items,
+        return fail(DR_ERR_INVALID, "%s: %zu items > cache n_batch %zu", who, n_items,
                     cache->n_batch);
     const size_t hkv = (size_t)cache->hkv[layer];
     const size_t hd = (size_t)cache->hd[layer];
     if (n_head < hkv || n_head % hkv != 0)
         return fail(DR_ERR_INVALID, "n_head %zu is not a multiple of n_head_kv %zu", n_head, hkv);
     dr_ctx* ctx = cache->ctx;
-    dr::AttnArgs a{};
+    a = dr::AttnArgs{};
     a.n_batch = (int)n_items;
     a.n_head = (int)n_head;
     a.n_head_kv = (int)hkv;
@@ -558,7 +576,7 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
     a.prefix = opt_to_int(causal_prefix);
     a.qn_w = q_norm_w;
     a.qn_eps = q_norm_eps;
-    int max_nq = 0;
+    max_nq = 0;
     const int tile = cache->hd_tile[layer];
     for (size_t b = 0; b < n_items; ++b) {
         const dr_batch_item& it = items[b];
@@ -583,12 +601,82 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
         s.qpos_sorted = 1;  // dr_pass positions are strictly ascending
         max_nq = std::max(max_nq, s.nq);
     }
+    return DR_OK;
+}
+
+static int mask_of(dr_opt_usize sliding_window, dr_opt_usize causal_prefix) {
+    return (sliding_window.present || causal_prefix.present) ? dr::MASK_POS : dr::MASK_NONE;
+}
+
+int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
+                        size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                        dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                        float q_norm_eps) {
+    dr::AttnArgs a;
+    int max_nq = 0;
+    DR_CHECK(cached_args(cache, layer, items, n_items, n_head, sliding_window, causal_prefix,
+                         scale, q_norm_w, q_norm_eps, "dr_attention_cached", a, max_nq));
     if (max_nq == 0) return DR_OK;
-    DR_CHECK(use_device(ctx));
-    const int mask =
-        (sliding_window.present || causal_prefix.present) ? dr::MASK_POS : dr::MASK_NONE;
-    return launch_planned(ctx, a, (int)hd, max_nq, (int)cache->n_total, mask,
-                          q_norm_w != nullptr);
+    DR_CHECK(use_device(cache->ctx));
+    return launch_planned(cache->ctx, a, a.hd, max_nq, (int)cache->n_total,
+                          mask_of(sliding_window, causal_prefix), q_norm_w != nullptr);
+}
+
+int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* items,
+                      size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                      dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                      float q_norm_eps, const float* k_norm_w, float k_norm_eps) {
+    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "dr_attention_step: no items");
+    if (n_items > (size_t)dr::MAX_BATCH)
+        return fail(DR_ERR_INVALID, "dr_attention_step: %zu items > %d", n_items, dr::MAX_BATCH);
+    dr_batch_item bi[dr::MAX_BATCH];
+    for (size_t b = 0; b < n_items; ++b) bi[b] = dr_batch_item{items[b].q, items[b].out, items[b].pass};
+    dr::AttnArgs a;
+    int max_nq = 0;
+    DR_CHECK(cached_args(cache, layer, bi, n_items, n_head, sliding_window, causal_prefix, scale,
+                         q_norm_w, q_norm_eps, "dr_attention_step", a, max_nq));
+    for (size_t b = 0; b < n_items; ++b)
+        if (items[b].pass->n > 0 && (!items[b].k || !items[b].v))
+            return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
+    if (max_nq == 0) return DR_OK;
+    DR_CHECK(use_device(cache->ctx));
+    const int mask = mask_of(sliding_window, causal_prefix);
+    dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask,
+                                q_norm_w != nullptr);
+    // One kernel when every pass is the block [n_total - n, n_total) starting
+    // on a 32-key tile, its K/V rows take 32-bit byte offsets (with the last
+    // tile's padding rows), rows are whole tiles of the head dim, the shape
+    // stages tiles per key group, and no sliding window narrows a
+    // workgroup's key range (each active tile is stored by one workgroup of
+    // its kv head, which must visit it).
+    bool fused = cache->ctx->fused_step && a.hd == cache->hd_tile[layer] &&
+                 dr::plan_supports_act(p) && !sliding_window.present;
+    for (size_t b = 0; b < n_items && fused; ++b) {
+        const dr_pass* ps = items[b].pass;
+        fused = ps->n > 0 && ps->max_pos + 1 == cache->n_total && ps->max_pos + 1 - ps->min_pos == ps->n &&
+                ps->min_pos % 32 == 0 && (((uintptr_t)items[b].k | (uintptr_t)items[b].v) & 15) == 0 &&
+                (ps->n + 32) * (size_t)a.n_head_kv * a.hd * sizeof(float) < ((size_t)1 << 31);
+    }
+    if (!fused) {
+        for (size_t b = 0; b < n_items; ++b)
+            DR_CHECK(dr_cache_store(cache, layer, b, items[b].pass, items[b].k, items[b].v,
+                                    k_norm_w, k_norm_eps));
+        return launch_plan(cache->ctx, a, p);
+    }
+    p.act = true;
+    a.kv_rstride = a.n_head_kv * a.hd;
+    a.kn_w = k_norm_w;
+    a.kn_eps = k_norm_eps;
+    for (size_t b = 0; b < n_items; ++b) {
+        dr::AttnSlot& s = a.slot[b];
+        s.ka = items[b].k;
+        s.va = items[b].v;
+        s.kst = cache->k[layer * cache->n_batch + b];
+        s.vst = cache->vt[layer * cache->n_batch + b];
+        s.act0 = (int)items[b].pass->min_pos;
+        s.n_act = (int)items[b].pass->n;
+    }
+    return launch_plan(cache->ctx, a, p);
 }
 
 int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const float* k,

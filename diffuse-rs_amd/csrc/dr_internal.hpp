@@ -30,6 +30,17 @@ struct AttnSlot {
     int nq;
     int nk;
     int qpos_sorted;      // qpos strictly ascending (a dr_pass): key ranges from endpoints
+    // Fused step (LaunchPlan::act): keys at positions [act0, act0 + n_act)
+    // are the step's fresh rows, read as f32 from ka / va ([n_act][kv_rstride],
+    // head g at g*hd) instead of from the cache, and written into the cache
+    // (kst / vst, the same buffers as k / vt) on the way.  act0 is a multiple
+    // of 32 and act0 + n_act == nk.
+    const float* ka;
+    const float* va;
+    uint16_t* kst;
+    uint16_t* vst;
+    int act0;
+    int n_act;
 };
 
 struct AttnArgs {
@@ -56,6 +67,9 @@ struct AttnArgs {
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
     int part_rows;                 // rows per (batch, kv head) in a split plane
+    int kv_rstride;                // fused step: elements between active K/V rows
+    const float* kn_w;             // fused step: K-norm gain for the active rows or nullptr
+    float kn_eps;
 };
 static_assert(offsetof(AttnArgs, slot) == 64, "scalar block of AttnArgs is one 64-byte line");
 
@@ -109,6 +123,7 @@ struct LaunchPlan {
     int n_workgroups;
     int mask;        // MaskMode
     bool qnorm;
+    bool act;        // fused step: active keys read from f32 rows and stored (see AttnSlot)
 };
 
 // Chooses tile sizes and the key split for a problem on a device with n_cu
@@ -117,6 +132,10 @@ struct LaunchPlan {
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
                           int force_split);
+
+// Whether a plan's shape can run the fused step (each DMA wave stages one
+// key group's K and V^T tiles).
+bool plan_supports_act(const LaunchPlan& p);
 
 // Bytes of split workspace a plan needs (part_o + part_ml).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);

@@ -71,6 +71,11 @@ class CBatchItem(ctypes.Structure):
     _fields_ = [("q", ctypes.c_void_p), ("out", ctypes.c_void_p), ("pass_", ctypes.c_void_p)]
 
 
+class CStepItem(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("out", ctypes.c_void_p), ("pass_", ctypes.c_void_p),
+                ("k", ctypes.c_void_p), ("v", ctypes.c_void_p)]
+
+
 class CLaunchInfo(ctypes.Structure):
     _fields_ = [
         ("n_split", ctypes.c_int),
@@ -80,6 +85,7 @@ class CLaunchInfo(ctypes.Structure):
         ("head_dim_tile", ctypes.c_int),
         ("row_blocks", ctypes.c_int),
         ("key_groups", ctypes.c_int),
+        ("fused_step", ctypes.c_int),
     ]
 
 
@@ -108,6 +114,7 @@ _SIGS = {
     "dr_ctx_destroy": (None, [_VP]),
     "dr_ctx_last_launch": (_I, [_VP, ctypes.POINTER(CLaunchInfo)]),
     "dr_ctx_set_split": (_I, [_VP, _I]),
+    "dr_ctx_set_fused_step": (_I, [_VP, _I]),
     "dr_ctx_set_tuning": (_I, [_VP, _I, _I, _I]),
     "dr_pass_create": (_I, [_VP, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
@@ -123,6 +130,7 @@ _SIGS = {
     "dr_cache_set_vicinity": (_I, [_VP, _SZ, _SZ]),
     "dr_cache_initialized": (_I, [_VP, _SZ]),
     "dr_attention_cached": (_I, [_VP, _SZ, ctypes.POINTER(CBatchItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F]),
+    "dr_attention_step": (_I, [_VP, _SZ, ctypes.POINTER(CStepItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F, _VP, _F]),
 }
 
 
@@ -285,6 +293,9 @@ class Context:
     def set_split(self, n_split: int) -> None:
         _check(self.lib.dr_ctx_set_split(self.h, n_split))
 
+    def set_fused_step(self, enable: bool) -> None:
+        _check(self.lib.dr_ctx_set_fused_step(self.h, 1 if enable else 0))
+
     def set_tuning(self, row_blocks: int = 0, key_groups: int = 0, n_split: int = 0) -> None:
         _check(self.lib.dr_ctx_set_tuning(self.h, row_blocks, key_groups, n_split))
 
@@ -402,6 +413,20 @@ class StepCache:
         _check(self.ctx.lib.dr_attention_cached(
             self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
             scale, _ptr(q_norm_w) or None, q_norm_eps))
+
+    def step(self, layer: int, items: Sequence[tuple], n_head: int,
+             sliding_window: Optional[int] = None, causal_prefix: Optional[int] = None,
+             scale: float = 1.0, q_norm_w=None, q_norm_eps: float = 1e-6, k_norm_w=None,
+             k_norm_eps: float = 1e-6) -> None:
+        """One denoise-step layer: items = (q, out, Pass, k, v) per batch slot
+        (device tensors; k/v the pass's active rows).  Stores k/v into the
+        cache and runs the attention (one kernel where the pass allows)."""
+        arr = (CStepItem * len(items))()
+        for i, (q, out, p, k, v) in enumerate(items):
+            arr[i] = CStepItem(_ptr(q), _ptr(out), p.h, _ptr(k), _ptr(v))
+        _check(self.ctx.lib.dr_attention_step(
+            self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
+            scale, _ptr(q_norm_w) or None, q_norm_eps, _ptr(k_norm_w) or None, k_norm_eps))
 
     def close(self) -> None:
         if self.h:

@@ -195,6 +195,34 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
                         dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
                         float q_norm_eps);
 
+/* One batch slot of a denoise-step layer: queries and the active K/V rows. */
+typedef struct {
+    const float* q; /* device, [n_active][n_head][head_dim] f32 */
+    float* out;     /* device, [n_active][n_head * head_dim] f32, overwritten */
+    const dr_pass* pass;
+    const float* k; /* device, [n_active][n_head_kv][head_dim] f32 (RoPE applied) */
+    const float* v; /* device, [n_active][n_head_kv][head_dim] f32 */
+} dr_step_item;
+
+/*
+ * One denoise-step attention layer with its cache update: the per-layer block
+ * of attention_block (src/model/forward.rs:296-343), norm_heads(k, k_norm) +
+ * cache.store(active) + gather(cached) ++ active + attention().  For item b
+ * (cache batch slot b) the active rows k / v are RMS-normalised with
+ * k_norm_w when it is non-NULL (K only), stored into the cache at the
+ * pass's positions, and the queries attend over every position 0..n_total,
+ * the active ones with the rows just given.  This is dr_cache_store per item
+ * followed by dr_attention_cached, or, when dr_ctx_set_fused_step enabled it
+ * and every pass is one block of consecutive positions that starts at a
+ * multiple of 32 and ends at n_total (the canvas of a prompt + canvas
+ * sequence), one kernel that does both.  Other arguments as
+ * dr_attention_cached.
+ */
+int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* items,
+                      size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                      dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                      float q_norm_eps, const float* k_norm_w, float k_norm_eps);
+
 /* Launch configuration of the last attention kernel this context enqueued
  * (for measurement): key splits across workgroups, workgroups, waves per
  * workgroup, keys per tile, head-dim tile, 32-row query blocks and key
@@ -207,11 +235,16 @@ typedef struct {
     int head_dim_tile;
     int row_blocks;
     int key_groups;
+    int fused_step; /* 1 when the launch also stored the step's active rows */
 } dr_launch_info;
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 
 /* Override the key-split heuristic for later calls on ctx (0 = automatic). */
 int dr_ctx_set_split(dr_ctx* ctx, int n_split);
+/* Let dr_attention_step run its single fused kernel (1) or always the cache
+ * store followed by the attention (0, the default: on the MI355X the fused
+ * kernel is the slower of the two at the shapes measured so far). */
+int dr_ctx_set_fused_step(dr_ctx* ctx, int enable);
 /* Override the workgroup shape (32-row query blocks x key groups) and the
  * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
  * to the automatic one. */

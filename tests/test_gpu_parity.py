@@ -17,7 +17,7 @@ import pytest
 
 import dr_attn as dr
 import oracle as orc
-from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, RowsSpec, Shape, as_kernel_sees, closed_form,
+from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, Config, RowsSpec, Shape, as_kernel_sees, closed_form,
                      config_seed, err_stats, golden_cases, materialise)
 
 pytestmark = pytest.mark.gpu
@@ -330,6 +330,163 @@ def test_c2_sixteen_denoise_steps(dev):
             got = dev.get(out)
             want = _oracle_cfg(cfg, Q, np.concatenate([Kp, Kc]), np.concatenate([Vp, Vc]))
             check(got, want, f"C2 step {step}")
+
+
+# Ragged shapes of the fused step (not BASELINE configs).
+STEP_RAGGED = {
+    "R1": Config("ragged_gqa_qknorm_96c+77q_b2", 8, 2, 128, 96, 77, batch=2, qk_norm=True),
+    "R2": Config("hd64_all_fresh_0c+50q", 4, 4, 64, 0, 50),
+    "R3": Config("prompt128_128c+100q", 8, 8, 128, 128, 100),
+}
+
+
+def _step_problem(dev, cfg, cfg_id, n_split=0, fused=True):
+    """Prompt K/V stored once, then one denoise-step layer through
+    StepCache.step (store of the canvas rows + attention).  Returns outputs,
+    inputs, norms, the cache and the launch info."""
+    rng = np.random.default_rng(config_seed(cfg_id, 7))
+    kvs = cfg.n_head_kv * cfg.head_dim
+    n_tot = cfg.n_total
+    cache = dr.StepCache(dev.ctx, n_tot, [cfg.n_head_kv], [cfg.head_dim], n_batch=cfg.batch)
+    p_pr = dr.Pass(dev.ctx, list(range(cfg.n_prompt)))
+    p_can = dr.Pass(dev.ctx, list(range(cfg.n_prompt, n_tot)))
+    qn = kn = None
+    if cfg.qk_norm:
+        g = np.random.default_rng(config_seed(cfg_id) + 100)
+        qn = g.uniform(0.5, 1.5, cfg.head_dim).astype(np.float32)
+        kn = g.uniform(0.5, 1.5, cfg.head_dim).astype(np.float32)
+    knd = dev.put(kn) if kn is not None else None
+    ins, outs, items = [], [], []
+    for b in range(cfg.batch):
+        K = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+        V = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+        Q = rng.standard_normal((cfg.n_canvas, cfg.n_head * cfg.head_dim), dtype=np.float32)
+        if cfg.n_prompt:
+            cache.store(0, p_pr, dev.put(K[:cfg.n_prompt].copy()), dev.put(V[:cfg.n_prompt].copy()),
+                        knd, 1e-6, batch=b)
+        out = dev.empty(cfg.n_canvas * cfg.n_head * cfg.head_dim)
+        items.append((dev.put(Q), out, p_can, dev.put(K[cfg.n_prompt:].copy()),
+                      dev.put(V[cfg.n_prompt:].copy())))
+        outs.append(out)
+        ins.append((Q, K, V))
+    dev.ctx.set_split(n_split)
+    dev.ctx.set_fused_step(fused)
+    try:
+        cache.step(0, items, cfg.n_head, sliding_window=cfg.window, scale=cfg.attn_scale,
+                   q_norm_w=dev.put(qn) if qn is not None else None, q_norm_eps=1e-6,
+                   k_norm_w=knd, k_norm_eps=1e-6)
+        launch = dev.ctx.last_launch()
+    finally:
+        dev.ctx.set_split(0)
+        dev.ctx.set_fused_step(False)
+    got = [dev.get(o) for o in outs]
+    return got, ins, (qn, kn), cache, launch
+
+
+def _normed_bf16(dev, x, w):
+    x = x.reshape(-1).copy()
+    if w is not None:
+        orc.norm_heads(x, w, 1e-6)
+    t = dev.t
+    return t.from_numpy(x).to(t.bfloat16).to(t.float32).numpy()
+
+
+@pytest.mark.parametrize("cid,n_split,fused", [
+    ("C2", 0, True), ("C2", 2, True), ("C3", 0, True), ("C4", 0, True), ("C5S", 0, True),
+    ("C5G", 0, True), ("R1", 0, True), ("R1", 3, True), ("R2", 0, True), ("R3", 0, True),
+    ("C2", 0, False), ("C4", 0, False), ("R1", 0, False)])
+def test_step_vs_oracle_and_cache(dev, cid, n_split, fused):
+    """StepCache.step = norm_heads(k) + cache.store(canvas) + attention over
+    [prompt | canvas] (forward.rs:296-343): the outputs meet the parity bar
+    against the oracle, and afterwards the cache holds bf16 of the (K-normed)
+    canvas rows and still the prompt rows, bit for bit.  With fusion on, C2-C4
+    take the fused kernel (also with a key split: each active tile is stored
+    once); C5 (hd 256, window) and every case with fusion off take the store
+    + attention path.  R1-R3 are ragged
+    fused cases: a partial last tile (rows past the pass staged as zeros and
+    not stored), every key fresh (head dim 64, no prompt), and a first fresh
+    tile right after the pipeline prologue."""
+    cfg = CONFIGS.get(cid) or STEP_RAGGED[cid]
+    cfg_id = list(CONFIGS).index(cid) if cid in CONFIGS else 100 + list(STEP_RAGGED).index(cid)
+    say(f"step {cid} split {n_split} fused {fused} ({cfg.name})")
+    got, ins, (qn, kn), cache, launch = _step_problem(dev, cfg, cfg_id, n_split, fused)
+    say(f"  launch {launch}")
+    assert launch["fused_step"] == (1 if fused and cid not in ("C5S", "C5G") else 0)
+    if n_split:
+        assert launch["n_split"] == n_split
+    kvs = cfg.n_head_kv * cfg.head_dim
+    for b in range(cfg.batch):
+        Q, K, V = ins[b]
+        check(got[b], _oracle_cfg(cfg, Q, K, V, qn, kn), f"{cid} batch {b}")
+        ok, ov = dev.empty(cfg.n_total * kvs), dev.empty(cfg.n_total * kvs)
+        cache.gather(0, list(range(cfg.n_total)), ok, ov, batch=b)
+        assert np.array_equal(dev.get(ok), _normed_bf16(dev, K, kn)), f"{cid} K cache, batch {b}"
+        assert np.array_equal(dev.get(ov), _normed_bf16(dev, V, None)), f"{cid} V cache, batch {b}"
+
+
+def test_step_sixteen_denoise_steps(dev):
+    """configs[1] through StepCache.step: 16 steps with fresh canvas K/V and
+    queries; each step's output against the oracle, and the cache after the
+    last step against its canvas rows."""
+    cfg = CONFIGS["C2"]
+    kvs = cfg.n_head_kv * cfg.head_dim
+    rng = np.random.default_rng(config_seed(1))
+    Kp = rng.standard_normal((cfg.n_prompt, kvs), dtype=np.float32)
+    Vp = rng.standard_normal((cfg.n_prompt, kvs), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, cfg.n_total, [cfg.n_head_kv], [cfg.head_dim])
+    cache.store(0, dr.Pass(dev.ctx, range(cfg.n_prompt)), dev.put(Kp), dev.put(Vp))
+    p_can = dr.Pass(dev.ctx, range(cfg.n_prompt, cfg.n_total))
+    out = dev.empty(cfg.n_canvas * cfg.n_head * cfg.head_dim)
+    dev.ctx.set_fused_step(True)
+    try:
+        for step in range(16):
+            r = np.random.default_rng(config_seed(1, step + 1))
+            Kc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
+            Vc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
+            Q = r.standard_normal((cfg.n_canvas, cfg.n_head * cfg.head_dim), dtype=np.float32)
+            cache.step(0, [(dev.put(Q), out, p_can, dev.put(Kc), dev.put(Vc))], cfg.n_head,
+                       scale=cfg.attn_scale)
+            assert dev.ctx.last_launch()["fused_step"] == 1
+            if step in (0, 7, 15):
+                want = _oracle_cfg(cfg, Q, np.concatenate([Kp, Kc]), np.concatenate([Vp, Vc]))
+                check(dev.get(out), want, f"C2 fused step {step}")
+    finally:
+        dev.ctx.set_fused_step(False)
+    ok, ov = dev.empty(cfg.n_total * kvs), dev.empty(cfg.n_total * kvs)
+    cache.gather(0, list(range(cfg.n_total)), ok, ov)
+    assert np.array_equal(dev.get(ok), _normed_bf16(dev, np.concatenate([Kp, Kc]), None))
+    assert np.array_equal(dev.get(ov), _normed_bf16(dev, np.concatenate([Vp, Vc]), None))
+
+
+def test_step_scattered_pass_falls_back(dev):
+    """A pass that is not one block ending at n_total (the ActiveSplit of a
+    later step) runs as store + attention; the result is the reference's
+    [cached | active] concatenation (forward.rs:312-343)."""
+    rng = np.random.default_rng(43)
+    n_tot, h, hkv, hd = 300, 8, 4, 128
+    kvs = hkv * hd
+    K = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+    V = rng.standard_normal((n_tot, kvs), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, n_tot, [hkv], [hd])
+    cache.store(0, dr.Pass(dev.ctx, range(n_tot)), dev.put(K), dev.put(V))
+    active = sorted(rng.choice(n_tot, 61, replace=False).tolist())
+    cached = [p for p in range(n_tot) if p not in set(active)]
+    Ka = rng.standard_normal((len(active), kvs), dtype=np.float32)
+    Va = rng.standard_normal((len(active), kvs), dtype=np.float32)
+    Q = rng.standard_normal((len(active), h * hd), dtype=np.float32)
+    pa = dr.Pass(dev.ctx, active)
+    out = dev.empty(len(active) * h * hd)
+    dev.ctx.set_fused_step(True)
+    try:
+        cache.step(0, [(dev.put(Q), out, pa, dev.put(Ka), dev.put(Va))], h, scale=0.1)
+    finally:
+        dev.ctx.set_fused_step(False)
+    assert dev.ctx.last_launch()["fused_step"] == 0
+    Kf = np.concatenate([K[cached], Ka]).reshape(-1).copy()
+    Vf = np.concatenate([V[cached], Va]).reshape(-1).copy()
+    s = Shape(len(active), n_tot, h, hkv, hd, scale=0.1)
+    want = oracle_run(s, RowsSpec(active), RowsSpec(cached + active), Q.reshape(-1).copy(), Kf, Vf)
+    check(dev.get(out), want, "scattered pass via step")
 
 
 def test_cache_store_gather_roundtrip(dev):
