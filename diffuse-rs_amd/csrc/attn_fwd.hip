@@ -92,6 +92,21 @@ __device__ __forceinline__ int sigma(int R) {
     return 16 * ((R >> 2) & 1) + 4 * (R >> 3) + (R & 3);
 }
 
+// The same for 16-row waves (16x16x32 MFMA, two 16-key blocks b): A-row R
+// of block b lands in accumulator slot i of lane group g with R = 4*g + i,
+// and the PV product wants lane group g to hold keys 8*g .. 8*g + 7, so
+// kappa(16*b + 4*g + i) = 8*g + 4*b + i.
+__device__ __forceinline__ int kappa(int R) {
+    return 8 * ((R & 15) >> 2) + 4 * (R >> 4) + (R & 3);
+}
+template <bool W16>
+__device__ __forceinline__ int kperm(int R) {
+    if constexpr (W16)
+        return kappa(R);
+    else
+        return sigma(R);
+}
+
 // visible() of attention.rs:36-57, evaluated without branches (bitwise
 // and/or of the three rules) so the per-element mask is a straight-line
 // compare + select; a short-circuit version compiled into divergent control
@@ -177,9 +192,11 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
     return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
 }
 
-template <int HD, int RB, int KQ, int NS, int NP>
+template <int HD, int RB, int KQ, int NS, int NP, bool W16 = false>
 struct Geometry {
-    static constexpr int NW = RB * KQ;         // compute waves per workgroup
+    // W16: two compute waves of 16 query rows per (row block, key group)
+    static constexpr int NE = RB * KQ;         // (row block, key group) pairs: merge entries
+    static constexpr int NW = NE * (W16 ? 2 : 1);  // compute waves per workgroup
     static constexpr int NWT = NW + NP;        // all waves (NP: DMA-only producer waves)
     static constexpr int NT = NWT * 64;
     static constexpr int NDMA = NP > 0 ? NP : NW;  // waves that issue the K/V DMA
@@ -198,7 +215,7 @@ struct Geometry {
     // Q fragments are held in registers for the whole kernel; Q is staged
     // once, through the first slot of the last pipeline stage.
     static constexpr int ROWF = HD + 4;        // f32 row pitch of the merge area
-    static constexpr size_t MERGE_BYTES = ((size_t)NW * 32 * ROWF + 2 * NW * 32) * 4;
+    static constexpr size_t MERGE_BYTES = ((size_t)NE * 32 * ROWF + 2 * NE * 32) * 4;
     static constexpr size_t LDS_BYTES = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
     static constexpr int WAVES_PER_SIMD = (NWT + 3) / 4;
     static_assert(CPT % 64 == 0, "a DMA instruction must stay inside one tile");
@@ -206,13 +223,15 @@ struct Geometry {
     static_assert(NLDW * (NS - 1) < 64, "vmcnt range");
     static_assert(QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(!W16 || (NP > 0 && HD <= 128), "16-row waves: DMA waves, head dim up to 128");
 };
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT>
-__attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD,
-                                   Geometry<HD, RB, KQ, NS, NP>::WAVES_PER_SIMD))) __global__
-__launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
-    using G = Geometry<HD, RB, KQ, NS, NP>;
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT, bool W16>
+__attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD,
+                                   Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD))) __global__
+__launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
+    using G = Geometry<HD, RB, KQ, NS, NP, W16>;
+    static_assert(!(W16 && ACT), "the fused step runs 32-row waves");
     constexpr int NW = G::NW, NWT = G::NWT, NT = G::NT, NC = G::NC, ND = G::ND;
     constexpr int KCH = G::KCH, VCH = G::VCH, TILE = G::TILE, SLOT = G::SLOT;
     constexpr int CPT = G::CPT, NLDW = G::NLDW, ROWF = G::ROWF, QROWS = G::QROWS;
@@ -246,6 +265,8 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     const bool dma = NP == 0 || !compute;
     const int dwave = NP > 0 ? wave - NW : wave;  // index among the DMA waves
     const int rb = wave % RB, kq = (wave / RB) % KQ;
+    // W16: the wave's half of the row block (rows rh*16 .. rh*16 + 15)
+    const int rh = W16 ? wave / (RB * KQ) : 0;
 
     // Workgroup -> (batch, kv head, row group, split).  The hardware deals
     // workgroups round-robin over the 8 XCDs; remapping keeps consecutive
@@ -264,7 +285,7 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     const int rows_total = a.group * S.nq;
     const int wg_row0 = rg * QROWS;
     if (wg_row0 >= rows_total) return;  // uniform over the workgroup and all its splits
-    const int r = wg_row0 + rb * 32 + col;
+    const int r = wg_row0 + rb * 32 + (W16 ? rh * 16 + (lane & 15) : col);
     const bool rvalid = r < rows_total;
     const float inv_nq = __builtin_amdgcn_rcpf((float)S.nq);
     int hg = 0, qi = 0;
@@ -392,7 +413,7 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         const int idx = (WHOLE ? (j * 64) % CPT : (dwave * NLDW * 64) % CPT + j * 64) + ln;
         if (((wreg0 + jreg) & 1) == 0) {
             const int R = idx / KCH, pk = idx % KCH;
-            return (((R & ~31) + sigma(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3)) * 2;
+            return (((R & ~31) + kperm<W16>(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3)) * 2;
         }
         const int d = idx / VCH, pv = idx % VCH;
         return (d * a.cap + ((pv ^ swz<VCH>(d)) << 3)) * 2;
@@ -655,15 +676,225 @@ __launch_bounds__((RB * KQ + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
         return *reinterpret_cast<const bf16x8*>(qrow_l + (((2 * c + hf) ^ swz<KCH>(col)) << 3));
     };
     // The merge area of the epilogue (it overlays the tile stages).
-    float* mrows = reinterpret_cast<float*>(smem);  // [NW][32][ROWF]
-    float* sm = mrows + NW * 32 * ROWF;             // [NW][32] running max
-    float* sl = sm + NW * 32;                       // [NW][32] scaled sum
+    // One entry per (row block, key group) = k * RB + rb.
+    constexpr int NE = G::NE;
+    float* mrows = reinterpret_cast<float*>(smem);  // [NE][32][ROWF]
+    float* sm = mrows + NE * 32 * ROWF;             // [NE][32] running max
+    float* sl = sm + NE * 32;                       // [NE][32] scaled sum
 
     // Compute waves and DMA-only waves run separate loops with the same
     // number of barriers, so that none of the compute state (O, P, V^T and Q
     // fragments) is live in the DMA waves' code, which needs registers of its
     // own to stage fused-step tiles.
-    if (NP == 0 || compute) {
+    if (W16 && compute) {
+        if constexpr (W16) {
+            // 16 query rows per wave on 16x16x32 MFMAs: two compute waves per
+            // SIMD, so the softmax of one overlaps the matrix products of the
+            // other.  Lane (g16, n16): query row n16, contraction / key group
+            // g16.  Same transposed products as the 32-row waves: S^T = K Q^T
+            // in two 16-key blocks, O^T += V^T P^T.
+            constexpr int NC16 = HD / 32;  // contraction steps of 32 along d
+            constexpr int ND16 = HD / 16;  // 16-row blocks of O^T
+            const int n16 = lane & 15, g16 = lane >> 4;
+            const int qr = rb * 32 + rh * 16 + n16;  // query row within the workgroup
+            bf16x8 qf[NC16];
+            {
+                const uint16_t* qrow = qs + qr * HD;
+                const int sw = swz<KCH>(qr & 31);
+#pragma unroll
+                for (int c = 0; c < NC16; ++c)
+                    qf[c] = *reinterpret_cast<const bf16x8*>(qrow + (((4 * c + g16) ^ sw) << 3));
+            }
+            f32x4 o[ND16];
+#pragma unroll
+            for (int db = 0; db < ND16; ++db) o[db] = f32x4{};
+            float mu = 0.0f;  // running max m (log2 units), valid once m_set
+            bool m_set = false;
+            float thr = -INFINITY;  // a score above mu + thr moves m
+            float l_acc = 0.0f;     // this lane's share of the row's weight sum
+            const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+            // O^T += V^T P^T; contraction slot 8*g16 + j is key 8*g16 + j in
+            // both operands.
+            auto pv = [&](const bf16x8 (&vf)[ND16], const bf16x8& pf) __attribute__((always_inline)) {
+#pragma unroll
+                for (int db = 0; db < ND16; ++db)
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pf, o[db], 0, 0, 0);
+            };
+            // One super-tile, software-pipelined like the 32-row step: the
+            // previous tile's PV product is interleaved with this tile's
+            // softmax, and this tile's V^T fragments replace vf afterwards.
+            auto step = [&](int u, bf16x8 (&vf)[ND16], const bf16x8& pin, bf16x8& pout)
+                __attribute__((always_inline)) {
+                const int st = u % NS;
+                __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
+                if (t0 + u * KQ + kq >= t1) {  // this key group has no tile in the last super-tile
+                    pv(vf, pin);
+                    pout = bf16x8{};
+                    return;
+                }
+                const int t = t0 + u * KQ + kq;
+                const uint16_t* ks = smem + (kq * NS + st) * SLOT;
+                const uint16_t* vs = ks + TILE;
+                const int kbase_t = t * BN;
+
+                // score j = 4*b + i of this lane is key kbase_t + 8*g16 + j
+                int kp[8], kqs[8];
+                if constexpr (MODE == MASK_KEYS) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int kidx = min(kbase_t + 8 * g16 + j, S.nk - 1);
+                        kp[j] = S.kpos ? S.kpos[kidx] : kidx;
+                        kqs[j] = S.kseq ? S.kseq[kidx] : 0;
+                    }
+                }
+
+                // S^T = K Q^T - m: block b holds LDS rows 16*b + n16 (keys
+                // kappa of them), -m as the accumulator init.
+                f32x4 s0, s1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s0[i] = s1[i] = -mu;
+                {
+                    const uint16_t* kr0 = ks + n16 * HD;
+                    const uint16_t* kr1 = ks + (16 + n16) * HD;
+                    const int sw0 = swz<KCH>(n16), sw1 = swz<KCH>(16 + n16);
+                    bf16x8 kf0[NC16], kf1[NC16];
+#pragma unroll
+                    for (int c = 0; c < NC16; ++c) {
+                        kf0[c] = *reinterpret_cast<const bf16x8*>(kr0 + (((4 * c + g16) ^ sw0) << 3));
+                        kf1[c] = *reinterpret_cast<const bf16x8*>(kr1 + (((4 * c + g16) ^ sw1) << 3));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int c = 0; c < NC16; ++c) {
+                        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf0[c], qf[c], s0, 0, 0, 0);
+                        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf1[c], qf[c], s1, 0, 0, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+
+                bool full = kbase_t + BN <= S.nk;
+                if constexpr (MODE == MASK_POS) {
+                    const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
+                                                         kbase_t + BN - 1 - qmin < a.window);
+                    full = full && tiles_can_be_full && win_ok;
+                } else if constexpr (MODE == MASK_KEYS) {
+                    full = false;
+                }
+                if (!full) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int kidx = kbase_t + 8 * g16 + j;
+                        bool vis = kidx < S.nk;
+                        if constexpr (MODE == MASK_POS) {
+                            vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                        } else if constexpr (MODE == MASK_KEYS) {
+                            vis = vis & visible(my_qpos, kp[j], my_qseq, kqs[j], a.window, my_pref);
+                        }
+                        if (j < 4)
+                            s0[j] = vis ? s0[j] : -INFINITY;
+                        else
+                            s1[j - 4] = vis ? s1[j - 4] : -INFINITY;
+                    }
+                }
+
+                // Online softmax with a lazily moved max; a row's 32 scores sit
+                // in the four lanes n16 + 16*g16.
+                float mx = max3(s0[0], s0[1], s0[2]);
+                mx = max3(mx, s0[3], s1[0]);
+                mx = max3(mx, s1[1], s1[2]);
+                mx = __builtin_fmaxf(mx, s1[3]);
+                const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+                float alpha = 1.0f;
+                if (moved) {
+                    float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+                    cm = __builtin_fmaxf(cm, __shfl_xor(cm, 32));
+                    const bool upd = cm > thr;
+                    const float delta = upd ? cm : 0.0f;
+                    alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+                    mu += delta;
+                    m_set = m_set | upd;
+                    thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        s0[i] -= delta;
+                        s1[i] -= delta;
+                    }
+                    l_acc *= alpha;
+                }
+
+                // p = exp2(s) rounded to bf16 in pairs; l sums the rounded
+                // values (what the PV product multiplies).
+                u32x4 w4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float x0 = j < 2 ? s0[2 * j] : s1[2 * j - 4];
+                    const float x1 = j < 2 ? s0[2 * j + 1] : s1[2 * j - 3];
+                    const bf16x2 pr = {(__bf16)__builtin_amdgcn_exp2f(x0),
+                                       (__bf16)__builtin_amdgcn_exp2f(x1)};
+                    w4[j] = __builtin_bit_cast(uint32_t, pr);
+                    l_acc = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_acc, false);
+                }
+                pout = __builtin_bit_cast(bf16x8, w4);
+                pv(vf, pin);
+#pragma unroll
+                for (int i = 0; i < ND16; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);  // two VALU / transcendental
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (moved) {
+#pragma unroll
+                    for (int db = 0; db < ND16; ++db) o[db] *= alpha;
+                }
+                // this tile's V^T fragments: rows 16*db + n16, keys 8*g16 ..
+#pragma unroll
+                for (int db = 0; db < ND16; ++db) {
+                    const int d = 16 * db + n16;
+                    vf[db] = *reinterpret_cast<const bf16x8*>(vs + d * BN + ((g16 ^ swz<VCH>(d)) << 3));
+                }
+            };
+
+            {
+                bf16x8 vf[ND16], pa, pb;
+#pragma unroll
+                for (int db = 0; db < ND16; ++db) vf[db] = bf16x8{};
+                pa = bf16x8{};
+                int u = 0;
+                for (; u + 1 < nsup; u += 2) {
+                    step(u, vf, pa, pb);
+                    step(u + 1, vf, pb, pa);
+                }
+                if (u < nsup) {
+                    step(u, vf, pa, pb);
+                    pv(vf, pb);
+                } else {
+                    pv(vf, pa);
+                }
+            }
+
+            // ---- merge the KQ key groups: entry kq * RB + rb, rows rh*16 + n16
+            float l_tot = l_acc + __shfl_xor(l_acc, 16);
+            l_tot += __shfl_xor(l_tot, 32);
+            const float m_fin = m_set ? mu : -INFINITY;
+            const int e = kq * RB + rb, row32 = rh * 16 + n16;
+            __syncthreads();  // every wave is done with the tile stages
+            if (g16 == 0) sm[e * 32 + row32] = m_fin;
+            __syncthreads();
+            {
+                float M = -INFINITY;
+#pragma unroll
+                for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + row32]);
+                const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
+                // o[db][i] is O^T[d = 16*db + 4*g16 + i][n16]
+                float* myrow = mrows + (e * 32 + row32) * ROWF;
+#pragma unroll
+                for (int db = 0; db < ND16; ++db)
+                    *reinterpret_cast<f32x4*>(myrow + 16 * db + 4 * g16) = o[db] * sc;
+                if (g16 == 0) sl[e * 32 + row32] = l_tot * sc;
+            }
+        }
+    } else if (NP == 0 || compute) {
         bf16x8 qf[NC];
 #pragma unroll
         for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
@@ -1086,19 +1317,36 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     }
 }
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT, bool W16 = false>
 hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    constexpr size_t lds = Geometry<HD, RB, KQ, NS, NP>::LDS_BYTES;
+    using G = Geometry<HD, RB, KQ, NS, NP, W16>;
+    constexpr size_t lds = G::LDS_BYTES;
     static bool attr_set = false;
-    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QNORM, ACT>;
+    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QNORM, ACT, W16>;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3((RB * KQ + NP) * 64), lds, st, a);
+    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(G::NT), lds, st, a);
     return hipGetLastError();
+}
+
+// The 16-row-wave builds (no fused step).
+template <int HD, int RB, int KQ, int NS, int NP>
+hipError_t launch_modes16(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    if (p.act) return hipErrorInvalidValue;
+    switch (p.mask) {
+        case MASK_NONE:
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, false, true>(p, a, st);
+        case MASK_POS:
+            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false, true>(p, a, st);
+        default:
+            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false, true>(p, a, st);
+    }
 }
 
 template <int HD, int RB, int KQ, int NS, int NP>
@@ -1136,20 +1384,26 @@ hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 // of KQ x (K + V^T) tiles of 32 keys).
 struct Shape {
     int hd, rb, kq, ns, np;
+    bool w16;  // two 16-row compute waves per (row block, key group)
 };
 constexpr Shape SHAPES[] = {
-    {64, 1, 4, 3, 4}, {64, 2, 2, 4, 4}, {64, 2, 4, 3, 0},
-    {128, 1, 4, 2, 4}, {128, 2, 2, 4, 4}, {128, 2, 4, 2, 0},
-    {256, 2, 2, 2, 0}, {256, 1, 2, 2, 0},  // one wave per SIMD: 512 VGPRs
+    {64, 1, 4, 3, 4, false}, {64, 2, 2, 4, 4, false}, {64, 2, 4, 3, 0, false},
+    {128, 1, 4, 2, 4, false}, {128, 2, 2, 4, 4, false}, {128, 2, 4, 2, 0, false},
+    {128, 1, 4, 2, 4, true},
+    {256, 2, 2, 2, 0, false}, {256, 1, 2, 2, 0, false},  // one wave per SIMD: 512 VGPRs
 };
 
-const Shape* find_shape(int hd_tile, int rb, int kq) {
+const Shape* find_shape(int hd_tile, int rb, int kq, bool w16) {
     for (const Shape& s : SHAPES)
-        if (s.hd == hd_tile && s.rb == rb && s.kq == kq) return &s;
+        if (s.hd == hd_tile && s.rb == rb && s.kq == kq && s.w16 == w16) return &s;
     return nullptr;
 }
 
 hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    if (p.w16) {
+        if (p.hd_tile == 128 && p.rb == 1 && p.kq == 4) return launch_modes16<128, 1, 4, 2, 4>(p, a, st);
+        return hipErrorInvalidValue;
+    }
     const int key = p.hd_tile * 100 + p.rb * 10 + p.kq;
     switch (key) {
         case 6414: return launch_modes<64, 1, 4, 3, 4>(p, a, st);
@@ -1168,7 +1422,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
-                          int force_split) {
+                          int force_split, int force_rows) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : 256);
     p.block_n = BN;
@@ -1183,17 +1437,26 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     int rb = 1;
     int kq = p.hd_tile == 256 ? 2 : 4;
     if (p.hd_tile == 256 && row_blocks >= 2) rb = 2;
+    // Head dim 128 without a mask: two 16-row compute waves per key group
+    // (two compute waves per SIMD; 1-3 % faster on C2-C4, whose loop is bound
+    // by the K/V stream).  The masked builds of that shape spill, so masked
+    // launches keep 32-row waves unless asked.
+    bool w16 = p.hd_tile == 128 && mask == MASK_NONE;
     if (force_rb > 0) rb = force_rb;
     if (force_kq > 0) kq = force_kq;
-    const Shape* sh = find_shape(p.hd_tile, rb, kq);
+    if (force_rows == 16) w16 = true;
+    if (force_rows == 32) w16 = false;
+    const Shape* sh = find_shape(p.hd_tile, rb, kq, w16);
     if (!sh) {
         rb = p.hd_tile == 256 && row_blocks >= 2 ? 2 : 1;
         kq = p.hd_tile == 256 ? 2 : 4;
-        sh = find_shape(p.hd_tile, rb, kq);
+        w16 = false;
+        sh = find_shape(p.hd_tile, rb, kq, w16);
     }
     p.rb = rb;
     p.kq = kq;
-    p.waves = rb * kq + sh->np;
+    p.w16 = w16;
+    p.waves = rb * kq * (w16 ? 2 : 1) + sh->np;
     p.stages = sh->ns;
     p.rowgroups = (row_blocks + rb - 1) / rb;
     if (p.rowgroups < 1) p.rowgroups = 1;
@@ -1215,8 +1478,8 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
 }
 
 bool plan_supports_act(const LaunchPlan& p) {
-    const Shape* sh = find_shape(p.hd_tile, p.rb, p.kq);
-    return sh && sh->np > 0 && sh->np == sh->kq && sh->rb == 1 && p.mask != MASK_KEYS;
+    const Shape* sh = find_shape(p.hd_tile, p.rb, p.kq, p.w16);
+    return sh && !sh->w16 && sh->np > 0 && sh->np == sh->kq && sh->rb == 1 && p.mask != MASK_KEYS;
 }
 
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv) {

@@ -94,6 +94,7 @@ struct dr_ctx {
     int force_rb = 0;
     int force_kq = 0;
     int fused_step = 0;  // dr_attention_step may run the fused kernel
+    int force_rows = 0;  // query rows per compute wave (0: automatic)
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials
@@ -245,6 +246,7 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
     info->row_blocks = ctx->last.rb;
     info->key_groups = ctx->last.kq;
     info->fused_step = ctx->last.act ? 1 : 0;
+    info->rows_per_wave = ctx->last.w16 ? 16 : 32;
     return DR_OK;
 }
 
@@ -252,6 +254,13 @@ int dr_ctx_set_split(dr_ctx* ctx, int n_split) {
     if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_split: ctx is NULL");
     if (n_split < 0 || n_split > 64) return fail(DR_ERR_INVALID, "n_split %d not in 0..64", n_split);
     ctx->force_split = n_split;
+    return DR_OK;
+}
+
+int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_wave_rows: ctx is NULL");
+    if (rows != 0 && rows != 16 && rows != 32) return fail(DR_ERR_INVALID, "rows %d not 0, 16 or 32", rows);
+    ctx->force_rows = rows;
     return DR_OK;
 }
 
@@ -519,7 +528,8 @@ int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
 static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int max_nq,
                                int max_nk, int mask, bool qnorm) {
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qnorm,
-                              ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split);
+                              ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
+                              ctx->force_rows);
 }
 
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
@@ -641,8 +651,12 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
     if (max_nq == 0) return DR_OK;
     DR_CHECK(use_device(cache->ctx));
     const int mask = mask_of(sliding_window, causal_prefix);
-    dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask,
-                                q_norm_w != nullptr);
+    // the fused kernel is built for 32-row waves only
+    dr_ctx* ctx = cache->ctx;
+    const int rows_saved = ctx->force_rows;
+    if (ctx->fused_step && rows_saved == 0) ctx->force_rows = 32;
+    dr::LaunchPlan p = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, q_norm_w != nullptr);
+    ctx->force_rows = rows_saved;
     // One kernel when every pass is the block [n_total - n, n_total) starting
     // on a 32-key tile, its K/V rows take 32-bit byte offsets (with the last
     // tile's padding rows), rows are whole tiles of the head dim, the shape

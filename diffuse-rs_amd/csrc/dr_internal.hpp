@@ -124,14 +124,16 @@ struct LaunchPlan {
     int mask;        // MaskMode
     bool qnorm;
     bool act;        // fused step: active keys read from f32 rows and stored (see AttnSlot)
+    bool w16;        // two 16-row compute waves per (row block, key group)
 };
 
 // Chooses tile sizes and the key split for a problem on a device with n_cu
-// compute units.  force_split > 0 overrides the split heuristic.
-// force_rb / force_kq / force_split > 0 override the heuristic (tuning).
+// compute units.  force_rb / force_kq / force_split > 0 override the
+// heuristic (tuning); force_rows 16 or 32 picks the query rows per compute
+// wave where both are built (0: automatic).
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
-                          int force_split);
+                          int force_split, int force_rows);
 
 // Whether a plan's shape can run the fused step (each DMA wave stages one
 // key group's K and V^T tiles).

@@ -86,6 +86,7 @@ class CLaunchInfo(ctypes.Structure):
         ("row_blocks", ctypes.c_int),
         ("key_groups", ctypes.c_int),
         ("fused_step", ctypes.c_int),
+        ("rows_per_wave", ctypes.c_int),
     ]
 
 
@@ -115,6 +116,7 @@ _SIGS = {
     "dr_ctx_last_launch": (_I, [_VP, ctypes.POINTER(CLaunchInfo)]),
     "dr_ctx_set_split": (_I, [_VP, _I]),
     "dr_ctx_set_fused_step": (_I, [_VP, _I]),
+    "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
     "dr_ctx_set_tuning": (_I, [_VP, _I, _I, _I]),
     "dr_pass_create": (_I, [_VP, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
@@ -292,6 +294,9 @@ class Context:
 
     def set_split(self, n_split: int) -> None:
         _check(self.lib.dr_ctx_set_split(self.h, n_split))
+
+    def set_wave_rows(self, rows: int) -> None:
+        _check(self.lib.dr_ctx_set_wave_rows(self.h, rows))
 
     def set_fused_step(self, enable: bool) -> None:
         _check(self.lib.dr_ctx_set_fused_step(self.h, 1 if enable else 0))

@@ -236,11 +236,15 @@ typedef struct {
     int row_blocks;
     int key_groups;
     int fused_step; /* 1 when the launch also stored the step's active rows */
+    int rows_per_wave; /* query rows per compute wave: 32, or 16 (two waves per row block) */
 } dr_launch_info;
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 
 /* Override the key-split heuristic for later calls on ctx (0 = automatic). */
 int dr_ctx_set_split(dr_ctx* ctx, int n_split);
+/* Query rows per compute wave for later calls on ctx: 16 or 32 where the
+ * head-dim tile builds both, 0 = automatic. */
+int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
 /* Let dr_attention_step run its single fused kernel (1) or always the cache
  * store followed by the attention (0, the default: on the MI355X the fused
  * kernel is the slower of the two at the shapes measured so far). */

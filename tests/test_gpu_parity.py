@@ -291,6 +291,41 @@ def test_gemma_scale_one_error(dev):
     assert np.isfinite(mx) and mx < 1.0
 
 
+@pytest.mark.parametrize("window,prefix", [(None, None), (64, None), (None, 250), (37, 180)])
+def test_wave_rows_16_and_32_vs_oracle(dev, window, prefix):
+    """Both compute-wave shapes of head dim 128 (32 query rows per wave, or
+    two waves of 16 on 16x16x32 MFMAs) against the oracle, unmasked and
+    with windows / causal prefixes, on a GQA problem with a ragged last tile
+    and a ragged last row block."""
+    rng = np.random.default_rng(31)
+    h, hkv, hd, n_p, n_c = 8, 2, 128, 200, 93
+    n_t = n_p + n_c
+    K = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    V = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    Q = rng.standard_normal((n_c, h * hd), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.store(0, dr.Pass(dev.ctx, range(n_t)), dev.put(K), dev.put(V))
+    pc = dr.Pass(dev.ctx, range(n_p, n_t))
+    scale = 1 / math.sqrt(hd)
+    s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, causal_prefix=prefix, scale=scale)
+    qr, kr = RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t)))
+    want = oracle_run(s, qr, kr, *as_kernel_sees(Q.reshape(-1).copy(), K.reshape(-1).copy(),
+                                                 V.reshape(-1).copy(), scale))
+    got = {}
+    try:
+        for rows in (16, 32):
+            dev.ctx.set_wave_rows(rows)
+            out = dev.empty(n_c * h * hd)
+            cache.attention(0, [(dev.put(Q), out, pc)], h, sliding_window=window,
+                            causal_prefix=prefix, scale=scale)
+            assert dev.ctx.last_launch()["rows_per_wave"] == rows
+            got[rows] = dev.get(out)
+            check(got[rows], want, f"rows {rows} window {window} prefix {prefix}")
+    finally:
+        dev.ctx.set_wave_rows(0)
+    assert np.max(np.abs(got[16] - got[32])) < 1e-5
+
+
 @pytest.mark.parametrize("n_split", [1, 2, 3, 5, 8])
 def test_split_count_does_not_change_result(dev, n_split):
     """Key splits merged by the last workgroup of each row group give the
