@@ -129,6 +129,42 @@ def other_configs(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
     return res
 
 
+def qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
+    """The Q/K/V epilogue (bias + QK-norm + RoPE, forward.rs:291-310) on the
+    C4 layer's 512 canvas rows, in graph bursts.  HBM-bound: every element of
+    q, k and v is read and written once (the bias, gains and table rows stay
+    in L2), so GB/s = 2 * 4 * n * (h + 2 hkv) * hd / time."""
+    cfg = CONFIGS["C4"]
+    h, hkv, hd, n = cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.n_canvas
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(99)
+    with torch.cuda.stream(stream):
+        q = torch.randn(n, h * hd, device="cuda", generator=gen)
+        k = torch.randn(n, hkv * hd, device="cuda", generator=gen)
+        v = torch.randn(n, hkv * hd, device="cuda", generator=gen)
+        bq = 0.1 * torch.randn(h * hd, device="cuda", generator=gen)
+        bk = 0.1 * torch.randn(hkv * hd, device="cuda", generator=gen)
+        bv = 0.1 * torch.randn(hkv * hd, device="cuda", generator=gen)
+        qn = torch.rand(hd, device="cuda", generator=gen) + 0.5
+        kn = torch.rand(hd, device="cuda", generator=gen) + 0.5
+    rope = dr.Rope(ctx, cfg.n_total, hd, 10000.0)
+    p_can = dr.Pass(ctx, range(cfg.n_prompt, cfg.n_total))
+
+    def call(i):
+        dr.qkv_epilogue(ctx, p_can, q, k, v, h, hkv, hd, bq, bk, bv, qn, kn, False, 1e-6, rope)
+    ms, _ = attention_only_ms(torch, stream, call, 4, reps)
+    nbytes = 2 * 4 * n * (h + 2 * hkv) * hd
+    gbs = nbytes / (ms / 1e3) / 1e9
+    res = {"workload": f"C4 layer epilogue: {n} rows, {h}+{hkv}+{hkv} heads x {hd}, "
+                       "bias + QK-norm + RoPE (f32, in place)",
+           "us_per_call": round(ms * 1e3, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+           "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    log(f"qkv epilogue: {res}")
+    stream.synchronize()
+    rope.close()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,9 +320,10 @@ def main() -> int:
     # ---- CPU baseline: the C restatement of the reference's attention on this
     # host's cores, on the first step's inputs; its output also checks the
     # GPU result of that step (the measured configuration).
-    others = None
+    others = epi = None
     if not args.no_others:
         others = other_configs(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
+        epi = qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
 
     cpu, parity = None, None
     if not args.no_cpu:
@@ -343,6 +380,7 @@ def main() -> int:
         "gpu_event_ms": round(gpu_ms, 4), "wall_s": round(wall, 4),
         "launch": launch, "parity": parity, "roofline": roofline, "cpu_baseline": cpu,
         "other_configs_attention_only": others,
+        "qkv_epilogue": epi,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -377,6 +377,108 @@ void dr_cache_destroy(dr_step_cache* cache) {
     delete cache;
 }
 
+// ---------------------------------------------------------------- Q/K/V epilogue
+
+struct dr_rope {
+    dr_ctx* ctx = nullptr;
+    size_t max_len = 0, rope_dim = 0;
+    float* d_table = nullptr;  // [max_len][rope_dim/2][2] (sin, cos)
+};
+
+int dr_rope_create(dr_ctx* ctx, size_t max_len, size_t rope_dim, float theta,
+                   const float* freq_factors, dr_rope** out) {
+    if (!ctx || !out) return fail(DR_ERR_INVALID, "dr_rope_create: NULL argument");
+    *out = nullptr;
+    if (rope_dim < 2 || rope_dim % 2 != 0 || rope_dim > 512)
+        return fail(DR_ERR_INVALID, "dr_rope_create: rope_dim %zu not even in 2..512", rope_dim);
+    if (max_len < 1 || max_len > ((size_t)1 << 27) / rope_dim)
+        return fail(DR_ERR_INVALID, "dr_rope_create: max_len %zu not in 1..%zu", max_len,
+                    ((size_t)1 << 27) / rope_dim);
+    // build_rope_cache_ff (ops.rs:396-417), in f32 like Rust's f32::powf /
+    // sin / cos (libm powf / sinf / cosf)
+    const size_t half = rope_dim / 2;
+    std::vector<float> h(max_len * half * 2);
+    for (size_t t = 0; t < max_len; ++t)
+        for (size_t i = 0; i < half; ++i) {
+            const float e = 2.0f * (float)i / (float)rope_dim;
+            float freq = 1.0f / powf(theta, e);
+            if (freq_factors) freq /= freq_factors[i];
+            const float ang = (float)t * freq;
+            h[(t * half + i) * 2] = sinf(ang);
+            h[(t * half + i) * 2 + 1] = cosf(ang);
+        }
+    DR_CHECK(use_device(ctx));
+    dr_rope* r = new dr_rope();
+    r->ctx = ctx;
+    r->max_len = max_len;
+    r->rope_dim = rope_dim;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&r->d_table), h.size() * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMemcpy(r->d_table, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        dr_rope_destroy(r);
+        return hip_fail(e, "RoPE table");
+    }
+    *out = r;
+    return DR_OK;
+}
+
+void dr_rope_destroy(dr_rope* rope) {
+    if (!rope) return;
+    (void)hipSetDevice(rope->ctx->device);
+    (void)hipStreamSynchronize(rope->ctx->stream);
+    if (rope->d_table) (void)hipFree(rope->d_table);
+    delete rope;
+}
+
+int dr_qkv_epilogue(dr_ctx* ctx, const dr_pass* pass, float* q, float* k, float* v, size_t n_head,
+                    size_t n_head_kv, size_t head_dim, const float* bq, const float* bk,
+                    const float* bv, const float* q_norm_w, const float* k_norm_w, int v_norm,
+                    float eps, const dr_rope* rope) {
+    if (!ctx || !pass) return fail(DR_ERR_INVALID, "dr_qkv_epilogue: ctx/pass is NULL");
+    if (pass->ctx != ctx) return fail(DR_ERR_INVALID, "dr_qkv_epilogue: pass uses another context");
+    if (head_dim < 1 || head_dim > 512)
+        return fail(DR_ERR_UNSUPPORTED, "dr_qkv_epilogue: head_dim %zu not in 1..512", head_dim);
+    if (n_head_kv == 0 || n_head % n_head_kv != 0)
+        return fail(DR_ERR_INVALID, "n_head %zu is not a multiple of n_head_kv %zu", n_head, n_head_kv);
+    if (rope) {
+        if (rope->ctx != ctx) return fail(DR_ERR_INVALID, "dr_qkv_epilogue: rope uses another context");
+        if (rope->rope_dim > head_dim)
+            return fail(DR_ERR_INVALID, "rope_dim %zu > head_dim %zu", rope->rope_dim, head_dim);
+        if (pass->n > 0 && pass->max_pos >= rope->max_len)
+            return fail(DR_ERR_INVALID, "position %zu >= the RoPE table's %zu", pass->max_pos,
+                        rope->max_len);
+    }
+    if (pass->n == 0) return DR_OK;
+    if (!q || !k || !v) return fail(DR_ERR_INVALID, "dr_qkv_epilogue: q/k/v is NULL");
+    if (pass->n * (n_head + 2 * n_head_kv) >= (size_t)1 << 31)
+        return fail(DR_ERR_INVALID, "dr_qkv_epilogue: %zu rows x %zu heads is too many", pass->n,
+                    n_head + 2 * n_head_kv);
+    DR_CHECK(use_device(ctx));
+    dr::EpiArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.pos = pass->d_pos;
+    a.n = (int)pass->n;
+    a.n_head = (int)n_head;
+    a.n_head_kv = (int)n_head_kv;
+    a.hd = (int)head_dim;
+    a.bq = bq;
+    a.bk = bk;
+    a.bv = bv;
+    a.qn_w = q_norm_w;
+    a.kn_w = k_norm_w;
+    a.v_norm = v_norm ? 1 : 0;
+    a.eps = eps;
+    a.rope = rope ? rope->d_table : nullptr;
+    a.rot = rope ? (int)rope->rope_dim : 0;
+    a.vec = head_dim % 4 == 0 && (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15) == 0;
+    hipError_t e = dr::launch_epilogue(a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "qkv_epilogue launch");
+    return DR_OK;
+}
+
 static int check_slot(const dr_step_cache* c, size_t layer, size_t batch, const char* who) {
     if (!c) return fail(DR_ERR_INVALID, "%s: cache is NULL", who);
     if (layer >= c->n_layer) return fail(DR_ERR_INVALID, "%s: layer %zu >= %zu", who, layer, c->n_layer);

@@ -104,6 +104,26 @@ struct GatherArgs {
     float* out_v;
 };
 
+// The Q/K/V epilogue of attention_block (forward.rs:291-310), in place on
+// device rows: q [n][n_head*hd], k and v [n][n_head_kv*hd] f32.
+struct EpiArgs {
+    float* q;
+    float* k;
+    float* v;
+    const int* pos;       // [n] sequence positions of the rows (device)
+    int n, n_head, n_head_kv, hd;
+    const float* bq;      // [n_head*hd] or nullptr (add_bias)
+    const float* bk;      // [n_head_kv*hd] or nullptr
+    const float* bv;
+    const float* qn_w;    // [hd] QK-norm gains or nullptr
+    const float* kn_w;
+    int v_norm;           // Gemma: unweighted RMSNorm of each V head
+    float eps;
+    const float* rope;    // [max_len][rot/2][2] (sin, cos) or nullptr
+    int rot;              // rotated dims per head (even, <= hd)
+    int vec;              // q, k, v 16-byte aligned and hd a multiple of 4: vector loads
+};
+
 // Masking mode of an attention launch.
 enum MaskMode : int {
     MASK_NONE = 0,  // every key visible (only the key tail is masked)
@@ -145,5 +165,6 @@ size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
+hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);
 
 }  // namespace dr

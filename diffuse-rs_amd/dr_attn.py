@@ -117,6 +117,11 @@ _SIGS = {
     "dr_ctx_set_split": (_I, [_VP, _I]),
     "dr_ctx_set_fused_step": (_I, [_VP, _I]),
     "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
+    "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
+                            ctypes.POINTER(ctypes.c_void_p)]),
+    "dr_rope_destroy": (None, [_VP]),
+    "dr_qkv_epilogue": (_I, [_VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, ctypes.c_size_t,
+                             ctypes.c_size_t, _VP, _VP, _VP, _VP, _VP, _I, ctypes.c_float, _VP]),
     "dr_ctx_set_tuning": (_I, [_VP, _I, _I, _I]),
     "dr_pass_create": (_I, [_VP, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
@@ -348,6 +353,42 @@ class Pass:
             self.close()
         except Exception:
             pass
+
+
+class Rope:
+    """dr_rope: build_rope_cache_ff's (sin, cos) table (ops.rs:396-417) on the device."""
+
+    def __init__(self, ctx: "Context", max_len: int, rope_dim: int, theta: float,
+                 freq_factors=None):
+        self.ctx = ctx
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+        h = ctypes.c_void_p()
+        _check(ctx.lib.dr_rope_create(ctx.h, max_len, rope_dim, theta,
+                                      ff.ctypes.data if ff is not None else None, ctypes.byref(h)))
+        self.h = h
+        self.rope_dim = rope_dim
+
+    def close(self) -> None:
+        if self.h:
+            self.ctx.lib.dr_rope_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def qkv_epilogue(ctx: "Context", p: "Pass", q, k, v, n_head: int, n_head_kv: int, head_dim: int,
+                 bq=None, bk=None, bv=None, q_norm_w=None, k_norm_w=None, v_norm: bool = False,
+                 eps: float = 1e-6, rope: "Rope | None" = None) -> None:
+    """attention_block's Q/K/V epilogue (forward.rs:291-310) in place on device
+    rows: bias, QK-norm, Gemma V-norm, RoPE at the pass's positions."""
+    _check(ctx.lib.dr_qkv_epilogue(ctx.h, p.h, _ptr(q), _ptr(k), _ptr(v), n_head, n_head_kv,
+                                   head_dim, _ptr(bq) or None, _ptr(bk) or None, _ptr(bv) or None,
+                                   _ptr(q_norm_w) or None, _ptr(k_norm_w) or None,
+                                   1 if v_norm else 0, eps, rope.h if rope is not None else None))
 
 
 def _ptr(t) -> int:

@@ -223,6 +223,32 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
                       dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
                       float q_norm_eps, const float* k_norm_w, float k_norm_eps);
 
+/*
+ * The Q/K/V epilogue of attention_block (src/model/forward.rs:291-310), on
+ * device rows and in place, before dr_attention_step / dr_cache_store +
+ * dr_attention_cached (which are then called without norms):
+ *   add_bias(q, bq), (k, bk), (v, bv)           ops.rs:373-382 (NULL: none)
+ *   norm_heads(q, q_norm_w), (k, k_norm_w)       ops.rs:384-389 (NULL: none)
+ *   Gemma: rms_norm_noscale of each V head       ops.rs:116-124 (v_norm != 0)
+ *   apply_rope(q, k, rope, pass positions)       ops.rs:419-452 (rope NULL: none)
+ * q is [n][n_head][head_dim], k and v [n][n_head_kv][head_dim] f32 (device),
+ * row t at the pass's t-th position; the biases are [heads * head_dim] and
+ * the norm gains [head_dim] (device); eps is rms_norm_eps.  head_dim <= 512.
+ */
+typedef struct dr_rope dr_rope;
+/* build_rope_cache_ff (src/model/ops.rs:396-417; build_rope_cache :391-393
+ * when freq_factors is NULL): the f32 (sin, cos) table of positions
+ * 0..max_len and the rope_dim/2 frequency pairs, built on the host exactly
+ * as the reference builds it and kept on the device.  freq_factors: host,
+ * rope_dim/2 floats, or NULL. */
+int dr_rope_create(dr_ctx* ctx, size_t max_len, size_t rope_dim, float theta,
+                   const float* freq_factors, dr_rope** out);
+void dr_rope_destroy(dr_rope* rope);
+int dr_qkv_epilogue(dr_ctx* ctx, const dr_pass* pass, float* q, float* k, float* v, size_t n_head,
+                    size_t n_head_kv, size_t head_dim, const float* bq, const float* bk,
+                    const float* bv, const float* q_norm_w, const float* k_norm_w, int v_norm,
+                    float eps, const dr_rope* rope);
+
 /* Launch configuration of the last attention kernel this context enqueued
  * (for measurement): key splits across workgroups, workgroups, waves per
  * workgroup, keys per tile, head-dim tile, 32-row query blocks and key

@@ -18,6 +18,10 @@
  *                           n_head*nq tasks, head = task / nq)
  *   or_rms_norm_inplace     src/model/ops.rs:106-114       (f64 sum of f32 squares)
  *   or_norm_heads           src/model/ops.rs:384-389
+ *   or_rms_norm_noscale     src/model/ops.rs:116-124       (Gemma V heads)
+ *   or_add_bias             src/model/ops.rs:373-382
+ *   or_rope_table           src/model/ops.rs:390-417       (build_rope_cache[_ff])
+ *   or_rotate_rows          src/model/ops.rs:419-452       (apply_rope / rotate_rows)
  *   or_cache_store/gather   src/model/cache.rs:62-82       (StepCache::store/gather)
  *   or_split_active         src/model/cache.rs:85-114      (StepCache::split_active)
  *
@@ -226,6 +230,60 @@ void or_rms_norm_inplace(float* x, const float* w, size_t n, float eps) {
 /* norm_heads -- ops.rs:384-389: every hd-wide group of x with the same gain. */
 void or_norm_heads(float* x, size_t len, const float* w, size_t hd, float eps) {
     for (size_t o = 0; o + hd <= len; o += hd) or_rms_norm_inplace(x + o, w, hd, eps);
+}
+
+/* rms_norm_noscale -- ops.rs:116-124: RMSNorm without a gain (Gemma's V heads,
+ * forward.rs:303-308). */
+void or_rms_norm_noscale(float* x, size_t n, float eps) {
+    double ss = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        float sq = x[i] * x[i];
+        ss += (double)sq;
+    }
+    float scale = 1.0f / (float)sqrt(ss / (double)n + (double)eps);
+    for (size_t i = 0; i < n; i++) x[i] *= scale;
+}
+
+/* add_bias -- ops.rs:373-382: the stride-long bias added to each of n rows. */
+void or_add_bias(float* x, const float* b, size_t stride, size_t n) {
+    for (size_t t = 0; t < n; t++)
+        for (size_t i = 0; i < stride; i++) x[t * stride + i] += b[i];
+}
+
+/* build_rope_cache_ff -- ops.rs:396-417 (build_rope_cache, :391-393, is ff =
+ * NULL): for position t < max_len and i < rope_dim/2, freq_i = 1 /
+ * theta^(2i/rope_dim), divided by ff[i] when given, and (sin, cos) of t*freq_i,
+ * all in f32 (Rust's f32::powf / sin / cos are libm's powf / sinf / cosf).
+ * out[(t*half + i)*2] = sin, out[(t*half + i)*2 + 1] = cos. */
+void or_rope_table(float* out, size_t max_len, size_t rope_dim, float theta, const float* ff) {
+    size_t half = rope_dim / 2;
+    for (size_t t = 0; t < max_len; t++)
+        for (size_t i = 0; i < half; i++) {
+            float e = 2.0f * (float)i / (float)rope_dim;
+            float freq = 1.0f / powf(theta, e);
+            if (ff) freq /= ff[i];
+            float ang = (float)t * freq;
+            out[(t * half + i) * 2] = sinf(ang);
+            out[(t * half + i) * 2 + 1] = cosf(ang);
+        }
+}
+
+/* rotate_rows -- ops.rs:433-452 (apply_rope, :419-431, runs it over Q with
+ * n_head and over K with n_head_kv): row t at position pos[t], each head's
+ * first rot dims rotate in pairs (i, i + rot/2). */
+void or_rotate_rows(float* x, const float* table, const size_t* pos, size_t n, size_t heads,
+                    size_t hd, size_t rot) {
+    size_t half = rot / 2;
+    for (size_t t = 0; t < n; t++)
+        for (size_t head = 0; head < heads; head++) {
+            float* row = x + t * heads * hd + head * hd;
+            for (size_t i = 0; i < half; i++) {
+                float sn = table[(pos[t] * half + i) * 2], cs = table[(pos[t] * half + i) * 2 + 1];
+                float a = row[i], b = row[half + i];
+                row[i] = a * cs - b * sn;
+                row[half + i] = a * sn + b * cs;
+            }
+        }
 }
 
 /* StepCache::store -- cache.rs:62-71: row r goes to position positions[r]. */

@@ -70,6 +70,11 @@ def load() -> ctypes.CDLL:
     lib.or_max_threads.restype = ctypes.c_int
     lib.or_rms_norm_inplace.argtypes = [P, P, ctypes.c_size_t, ctypes.c_float]
     lib.or_norm_heads.argtypes = [P, ctypes.c_size_t, P, ctypes.c_size_t, ctypes.c_float]
+    lib.or_rms_norm_noscale.argtypes = [P, ctypes.c_size_t, ctypes.c_float]
+    lib.or_add_bias.argtypes = [P, P, ctypes.c_size_t, ctypes.c_size_t]
+    lib.or_rope_table.argtypes = [P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, P]
+    lib.or_rotate_rows.argtypes = [P, P, c_size_p, ctypes.c_size_t, ctypes.c_size_t,
+                                   ctypes.c_size_t, ctypes.c_size_t]
     lib.or_cache_store.argtypes = [P, P, ctypes.c_size_t, c_size_p, ctypes.c_size_t, P, P]
     lib.or_cache_gather.argtypes = [P, P, ctypes.c_size_t, c_size_p, ctypes.c_size_t, P, P]
     lib.or_split_active.argtypes = [P, P, P, P, ctypes.c_size_t, ctypes.c_size_t,
@@ -147,6 +152,31 @@ def rms_norm_inplace(x: np.ndarray, w: np.ndarray, eps: float) -> None:
 
 def norm_heads(x: np.ndarray, w: np.ndarray, eps: float) -> None:
     load().or_norm_heads(_f32(x).ctypes.data, x.size, _f32(w).ctypes.data, w.size, eps)
+
+
+def rms_norm_noscale(x: np.ndarray, eps: float) -> None:
+    load().or_rms_norm_noscale(_f32(x).ctypes.data, x.size, eps)
+
+
+def add_bias(x: np.ndarray, b: np.ndarray, n: int) -> None:
+    load().or_add_bias(_f32(x).ctypes.data, _f32(b).ctypes.data, b.size, n)
+
+
+def rope_table(max_len: int, rope_dim: int, theta: float, freq_factors=None) -> np.ndarray:
+    """(max_len, rope_dim/2, 2) float32: (sin, cos) per position and pair."""
+    out = np.zeros((max_len, rope_dim // 2, 2), np.float32)
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+    load().or_rope_table(out.ctypes.data, max_len, rope_dim, ctypes.c_float(theta),
+                         ff.ctypes.data if ff is not None else None)
+    return out
+
+
+def rotate_rows(x: np.ndarray, table: np.ndarray, positions: Sequence[int], heads: int, hd: int,
+                rot: int) -> None:
+    keep: list = []
+    t = np.ascontiguousarray(table, np.float32)
+    load().or_rotate_rows(_f32(x).ctypes.data, t.ctypes.data, _arr(positions, keep), len(positions),
+                          heads, hd, rot)
 
 
 def cache_store(ck: np.ndarray, cv: np.ndarray, stride: int, positions: Sequence[int],

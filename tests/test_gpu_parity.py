@@ -620,3 +620,126 @@ def test_partial_active_split_vs_dropin(dev):
     s = Shape(len(active), n_tot, h, hkv, hd, sliding_window=40, scale=0.1)
     want = oracle_run(s, RowsSpec(active), RowsSpec(cached + active), Q.reshape(-1).copy(), Kf, Vf)
     check(got, want, "partial split")
+
+
+# ------------------------------------------------------------- Q/K/V epilogue
+
+def _epilogue_oracle(q, k, v, pos, h, hkv, hd, bq, bk, bv, qn, kn, v_norm, eps, table, rot):
+    """forward.rs:291-310 with the oracle's restatement of each step."""
+    q, k, v = q.copy(), k.copy(), v.copy()
+    n = len(pos)
+    for x, b in ((q, bq), (k, bk), (v, bv)):
+        if b is not None:
+            orc.add_bias(x, b, n)
+    if qn is not None:
+        orc.norm_heads(q, qn, eps)
+    if kn is not None:
+        orc.norm_heads(k, kn, eps)
+    if v_norm:
+        for r in range(n * hkv):
+            seg = v[r * hd:(r + 1) * hd].copy()
+            orc.rms_norm_noscale(seg, eps)
+            v[r * hd:(r + 1) * hd] = seg
+    if table is not None:
+        orc.rotate_rows(q, table, pos, h, hd, rot)
+        orc.rotate_rows(k, table, pos, hkv, hd, rot)
+    return q, k, v
+
+
+@pytest.mark.parametrize("hd,rot,h,hkv,bias,norm,v_norm,ff", [
+    (128, 128, 8, 2, True, True, False, False),
+    (128, 64, 4, 4, True, False, False, False),
+    (128, 128, 4, 2, False, False, False, False),
+    (256, 256, 4, 2, False, True, True, True),
+    (64, 64, 2, 2, True, True, False, False),
+    (96, 32, 3, 1, True, True, True, False),
+    (512, 256, 4, 2, False, True, True, False),
+])
+def test_qkv_epilogue_vs_oracle(dev, hd, rot, h, hkv, bias, norm, v_norm, ff):
+    """The epilogue kernel against the oracle's add_bias / norm_heads /
+    rms_norm_noscale / rotate_rows (bias and rotation are exact: no fused
+    multiply-adds on either side; a norm's f64 sum runs in another order,
+    which may move its f32 scale by an ulp)."""
+    rng = np.random.default_rng(hd * 7 + rot)
+    n, max_len, eps = 37, 3000, 1e-6
+    pos = sorted(rng.choice(max_len, n, replace=False).tolist())
+    q = rng.standard_normal(n * h * hd).astype(np.float32)
+    k = rng.standard_normal(n * hkv * hd).astype(np.float32)
+    v = rng.standard_normal(n * hkv * hd).astype(np.float32)
+    mk = lambda m: rng.standard_normal(m).astype(np.float32) if bias else None  # noqa: E731
+    bq, bk, bv = mk(h * hd), mk(hkv * hd), mk(hkv * hd)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    ffv = rng.uniform(1.0, 8.0, rot // 2).astype(np.float32) if ff else None
+    theta = 10000.0 if hd != 256 else 1e6
+    table = orc.rope_table(max_len, rot, theta, ffv)
+    want = _epilogue_oracle(q, k, v, pos, h, hkv, hd, bq, bk, bv, qn, kn, v_norm, eps, table, rot)
+    say(f"epilogue hd {hd} rot {rot} h {h}/{hkv} bias {bias} norm {norm} v_norm {v_norm} ff {ff}")
+    rope = dr.Rope(dev.ctx, max_len, rot, theta, ffv)
+    p = dr.Pass(dev.ctx, pos)
+    dq, dk, dv = dev.put(q), dev.put(k), dev.put(v)
+    put = lambda x: dev.put(x) if x is not None else None  # noqa: E731
+    dr.qkv_epilogue(dev.ctx, p, dq, dk, dv, h, hkv, hd, put(bq), put(bk), put(bv), put(qn),
+                    put(kn), v_norm, eps, rope)
+    for name, g, w in zip("qkv", (dev.get(dq), dev.get(dk), dev.get(dv)), want):
+        if not (norm or (v_norm and name == "v")):
+            assert np.array_equal(g, w), name
+        else:
+            rel = np.abs(g - w) / np.maximum(np.abs(w), 1e-30)
+            assert np.max(rel) <= 2.0**-22 or np.max(np.abs(g - w)) < 1e-6, (name, np.max(rel))
+            say(f"  {name}: {np.count_nonzero(g != w)} of {g.size} differ by an ulp")
+
+
+def test_qkv_epilogue_then_step_vs_oracle(dev):
+    """C4-like layer (16/16 heads, hd 128, QK-norm) with biases and RoPE:
+    epilogue, then the step (store + attention without norms), against the
+    oracle's epilogue and attention; the cache then holds bf16 of the
+    oracle's K and V rows, bit for bit."""
+    rng = np.random.default_rng(41)
+    h, hkv, hd, n_p, n_c, eps = 16, 16, 128, 512, 256, 1e-6
+    n_t = n_p + n_c
+    kvs = hkv * hd
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    bq = (0.1 * rng.standard_normal(h * hd)).astype(np.float32)
+    bk = (0.1 * rng.standard_normal(kvs)).astype(np.float32)
+    bv = (0.1 * rng.standard_normal(kvs)).astype(np.float32)
+    table = orc.rope_table(n_t, hd, 10000.0)
+    rope = dr.Rope(dev.ctx, n_t, hd, 10000.0)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    K = rng.standard_normal(n_t * kvs).astype(np.float32)
+    V = rng.standard_normal(n_t * kvs).astype(np.float32)
+    Q = rng.standard_normal(n_c * h * hd).astype(np.float32)
+    put = dev.put
+    kp, vp = K[:n_p * kvs].copy(), V[:n_p * kvs].copy()
+    kc, vc = K[n_p * kvs:].copy(), V[n_p * kvs:].copy()
+    # prompt pass through the same epilogue (its q rows are not needed)
+    p_pr = dr.Pass(dev.ctx, range(n_p))
+    qdummy = np.zeros(n_p * h * hd, np.float32)
+    _, kp_o, vp_o = _epilogue_oracle(qdummy, kp, vp, list(range(n_p)), h, hkv, hd, bq, bk, bv,
+                                     qn, kn, False, eps, table, hd)
+    dq0, dkp, dvp = put(qdummy), put(kp), put(vp)
+    dr.qkv_epilogue(dev.ctx, p_pr, dq0, dkp, dvp, h, hkv, hd, put(bq), put(bk), put(bv), put(qn),
+                    put(kn), False, eps, rope)
+    cache.store(0, p_pr, dkp, dvp)
+    # canvas step
+    canvas = list(range(n_p, n_t))
+    p_c = dr.Pass(dev.ctx, canvas)
+    q_o, kc_o, vc_o = _epilogue_oracle(Q, kc, vc, canvas, h, hkv, hd, bq, bk, bv, qn, kn, False,
+                                       eps, table, hd)
+    dq, dk, dv = put(Q), put(kc), put(vc)
+    dr.qkv_epilogue(dev.ctx, p_c, dq, dk, dv, h, hkv, hd, put(bq), put(bk), put(bv), put(qn),
+                    put(kn), False, eps, rope)
+    out = dev.empty(n_c * h * hd)
+    cache.step(0, [(dq, out, p_c, dk, dv)], h, scale=1 / math.sqrt(hd))
+    s = Shape(n_c, n_t, h, hkv, hd, scale=1 / math.sqrt(hd))
+    Kf = np.concatenate([kp_o, kc_o])
+    Vf = np.concatenate([vp_o, vc_o])
+    want = oracle_run(s, RowsSpec(canvas), RowsSpec(list(range(n_t))), q_o, Kf, Vf)
+    check(dev.get(out), want, "epilogue + step vs oracle")
+    ok, ov = dev.empty(n_t * kvs), dev.empty(n_t * kvs)
+    cache.gather(0, list(range(n_t)), ok, ov)
+    # bf16 of the oracle's rows (an ulp of f32 from the norm's sum order can
+    # move a bf16 rounding only at an exact tie, which these inputs avoid)
+    assert np.array_equal(dev.get(ok), _normed_bf16(dev, Kf, None))
+    assert np.array_equal(dev.get(ov), _normed_bf16(dev, Vf, None))

@@ -270,6 +270,117 @@ def test_norm_heads_matches_f64():
     assert np.max(np.abs(x - want)) < 1e-5
 
 
+# ------------------------------------------------- QKV epilogue: bias, V-norm, RoPE
+
+def test_rms_norm_noscale_closed_forms():
+    # ops.rs:116-124: all-equal c -> sign(c) / sqrt(1 + eps/c^2); unit RMS and
+    # a positive multiple of the input for random rows
+    for c in (2.5, -0.125):
+        x = np.full(256, c, np.float32)
+        orc.rms_norm_noscale(x, 1e-6)
+        assert np.max(np.abs(x - np.sign(c) / math.sqrt(1 + 1e-6 / c**2))) < 1e-6
+    rng = np.random.default_rng(5)
+    x0 = rng.standard_normal(256).astype(np.float32) * 3.0
+    x = x0.copy()
+    orc.rms_norm_noscale(x, 0.0)
+    assert abs(math.sqrt(np.mean(x.astype(np.float64) ** 2)) - 1.0) < 1e-6
+    ratio = x / x0
+    assert np.all(ratio > 0) and np.ptp(ratio) < 1e-6
+
+
+def test_add_bias_is_rowwise_addition():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((7, 96)).astype(np.float32)
+    b = rng.standard_normal(96).astype(np.float32)
+    want = x + b
+    y = x.reshape(-1).copy()
+    orc.add_bias(y, b, 7)
+    assert np.array_equal(y.reshape(7, 96), want)
+
+
+def test_rope_table_matches_f64_trig():
+    # ops.rs:396-417: freq_i = theta^(-2i/d) (/ ff_i), angle t*freq_i.  The
+    # f32 angle carries a relative rounding error of ~2^-23 per operation,
+    # so the bound grows with the angle.
+    d, theta, T = 128, 10000.0, 4096
+    tab = orc.rope_table(T, d, theta)
+    i = np.arange(d // 2, dtype=np.float64)
+    freq = theta ** (-2.0 * i / d)
+    t = np.arange(T, dtype=np.float64)[:, None]
+    ang = t * freq[None, :]
+    tol = 4 * 2.0**-23 * (ang + 1.0) + 1e-7
+    assert np.all(np.abs(tab[:, :, 0] - np.sin(ang)) <= tol)
+    assert np.all(np.abs(tab[:, :, 1] - np.cos(ang)) <= tol)
+    # freq factors divide the frequency: the angle at 2t with factor 2 is the
+    # plain angle at t
+    ff = np.full(d // 2, 2.0, np.float32)
+    tab2 = orc.rope_table(T, d, theta, ff)
+    assert np.max(np.abs(tab2[0:T:2] - tab[: T // 2])) < 1e-3
+    assert np.array_equal(tab[0, :, 0], np.zeros(d // 2, np.float32))
+    assert np.array_equal(tab[0, :, 1], np.ones(d // 2, np.float32))
+
+
+def test_rotate_rows_pairs_signs_and_invariants():
+    d, rot, heads = 128, 128, 3
+    tab = orc.rope_table(512, rot, 10000.0)
+    half = rot // 2
+    # unit vectors: e_i -> cos at i, sin at i+half; e_{half+i} -> -sin at i,
+    # cos at i+half (the pairing (i, i+half) and the rotation's sign)
+    for i in (0, 5, half - 1):
+        for pos in (1, 77, 300):
+            x = np.zeros(d, np.float32)
+            x[i] = 1.0
+            orc.rotate_rows(x, tab, [pos], 1, d, rot)
+            sn, cs = tab[pos, i]
+            nz = np.flatnonzero(x)
+            assert set(nz.tolist()) <= {i, half + i}
+            assert x[i] == cs and x[half + i] == sn
+            y = np.zeros(d, np.float32)
+            y[half + i] = 1.0
+            orc.rotate_rows(y, tab, [pos], 1, d, rot)
+            assert y[i] == -sn and y[half + i] == cs
+    rng = np.random.default_rng(7)
+    x0 = rng.standard_normal((4, heads, d)).astype(np.float32)
+    pos = [0, 3, 200, 511]
+    x = x0.reshape(-1).copy()
+    orc.rotate_rows(x, tab, pos, heads, d, rot)
+    x = x.reshape(4, heads, d)
+    assert np.array_equal(x[0], x0[0])  # position 0 is the identity
+    n0 = x0[..., :half] ** 2 + x0[..., half:] ** 2
+    n1 = x[..., :half] ** 2 + x[..., half:] ** 2
+    assert np.max(np.abs(n1 - n0) / (n0 + 1e-3)) < 1e-5  # pair norms kept
+    # relative position: <R(q, m), R(k, n)> depends only on m - n
+    q0 = rng.standard_normal(d).astype(np.float32)
+    k0 = rng.standard_normal(d).astype(np.float32)
+
+    def dot_at(m, n):
+        q = q0.copy()
+        k = k0.copy()
+        orc.rotate_rows(q, tab, [m], 1, d, rot)
+        orc.rotate_rows(k, tab, [n], 1, d, rot)
+        return float(np.dot(q.astype(np.float64), k.astype(np.float64)))
+    for m, n, s in ((10, 3, 40), (50, 60, 7), (5, 5, 100)):
+        assert abs(dot_at(m, n) - dot_at(m + s, n + s)) < 2e-3 * math.sqrt(d)
+    assert abs(dot_at(10, 3) - dot_at(10, 4)) > 1e-2  # and it does depend on m - n
+
+
+def test_rotate_rows_partial_rotary():
+    d, rot = 128, 64
+    tab = orc.rope_table(64, rot, 500.0)
+    rng = np.random.default_rng(8)
+    x0 = rng.standard_normal((2, 2, d)).astype(np.float32)
+    x = x0.reshape(-1).copy()
+    orc.rotate_rows(x, tab, [9, 33], 2, d, rot)
+    x = x.reshape(2, 2, d)
+    assert np.array_equal(x[..., rot:], x0[..., rot:])  # the rest untouched
+    assert np.max(np.abs(x[..., :rot] - x0[..., :rot])) > 1e-2
+    # a rotation by the table's angle in each (i, i + rot/2) plane
+    a, b = x0[1, 1, :rot // 2], x0[1, 1, rot // 2:rot]
+    sn, cs = tab[33, :, 0], tab[33, :, 1]
+    assert np.max(np.abs(x[1, 1, :rot // 2] - (a * cs - b * sn))) < 1e-6
+    assert np.max(np.abs(x[1, 1, rot // 2:rot] - (a * sn + b * cs))) < 1e-6
+
+
 # ------------------------------------------------- StepCache
 
 def test_cache_store_gather_roundtrip():
