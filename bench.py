@@ -155,12 +155,36 @@ def qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
     ms, _ = attention_only_ms(torch, stream, call, 4, reps)
     nbytes = 2 * 4 * n * (h + 2 * hkv) * hd
     gbs = nbytes / (ms / 1e3) / 1e9
+    # the whole C4 layer step: plain (no epilogue), the epilogue folded into
+    # the store and the attention, and the separate pass followed by the step
+    n_t = cfg.n_total
+    with torch.cuda.stream(stream):
+        Kp = torch.randn(n_t, hkv * hd, device="cuda", generator=gen)
+        Vp = torch.randn(n_t, hkv * hd, device="cuda", generator=gen)
+        out = torch.empty(n * h * hd, device="cuda")
+    cache = dr.StepCache(ctx, n_t, [hkv], [hd])
+    cache.store(0, dr.Pass(ctx, range(n_t)), Kp, Vp, k_norm_w=kn)
+    sc = cfg.attn_scale
+    item = [(q, out, p_can, k, v)]
+    plain, _ = attention_only_ms(torch, stream, lambda i: cache.step(
+        0, item, h, scale=sc, q_norm_w=qn, k_norm_w=kn), 4, reps)
+    folded, _ = attention_only_ms(torch, stream, lambda i: cache.step_epi(
+        0, item, h, scale=sc, bq=bq, bk=bk, bv=bv, q_norm_w=qn, k_norm_w=kn, rope=rope), 4, reps)
+
+    def two_pass(i):
+        dr.qkv_epilogue(ctx, p_can, q, k, v, h, hkv, hd, bq, bk, bv, qn, kn, False, 1e-6, rope)
+        cache.step(0, item, h, scale=sc)
+    both, _ = attention_only_ms(torch, stream, two_pass, 4, reps)
     res = {"workload": f"C4 layer epilogue: {n} rows, {h}+{hkv}+{hkv} heads x {hd}, "
                        "bias + QK-norm + RoPE (f32, in place)",
            "us_per_call": round(ms * 1e3, 3), "bytes": nbytes, "gbs": round(gbs, 1),
-           "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+           "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+           "c4_step_us": {"no_epilogue": round(plain * 1e3, 3),
+                          "epilogue_in_store_and_attention": round(folded * 1e3, 3),
+                          "epilogue_pass_then_step": round(both * 1e3, 3)}}
     log(f"qkv epilogue: {res}")
     stream.synchronize()
+    del cache
     rope.close()
     return res
 

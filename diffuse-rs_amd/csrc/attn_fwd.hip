@@ -85,6 +85,17 @@ __device__ __forceinline__ int swz(int row) {
     }
 }
 
+// RoPE's rotation of one pair (ops.rs:447-448), without fused multiply-adds
+// as Rust evaluates it.
+__device__ __forceinline__ float rope_lo(float a, float b, float sn, float cs) {
+#pragma clang fp contract(off)
+    return a * cs - b * sn;
+}
+__device__ __forceinline__ float rope_hi(float a, float b, float sn, float cs) {
+#pragma clang fp contract(off)
+    return a * sn + b * cs;
+}
+
 // Key offset (within a 32-key block) stored in LDS row R of the block.  The
 // MFMA puts A-row R in accumulator slot i of lane half hf with
 // R = 8*(i/4) + 4*hf + (i%4); sigma(R) = 16*hf + i places key 16*hf + i there.
@@ -616,19 +627,55 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
         return (it * NWT + wave) * RPI + lane / LPR;
     };
     f32x4 xq[QIT];
+    // the epilogue's Q part (bias, RoPE), when asked: its operands are
+    // requested with the rows
+    f32x4 bq4[QIT];
+    float2 rq[QIT][4];
+    const int rhalf = a.rot / 2;
+    int qp[QIT];  // the rows' positions, requested before the rows (RoPE's table index)
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
         const int rr = wg_row0 + q_lrow(it);
         const bool ok = q_lrow(it) < QROWS && rr < rows_total;
         int hgq = 0, qiq = 0;
         if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
+        qp[it] = (a.rope && ok) ? (S.qpos0 >= 0 ? S.qpos0 + qiq : S.qpos[qiq]) : 0;
+    }
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+        const int rr = wg_row0 + q_lrow(it);
+        const bool ok = q_lrow(it) < QROWS && rr < rows_total;
+        int hgq = 0, qiq = 0;
+        if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
+        const int qh = g * a.group + hgq;
         const float* qrow = static_cast<const float*>(S.q) + (size_t)qiq * a.q_rstride +
-                            (size_t)(g * a.group + hgq) * a.hd;
+                            (size_t)qh * a.hd;
         if (ok && a.hd == HD) {
             xq[it] = *reinterpret_cast<const f32x4*>(qrow + d0);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) xq[it][e] = (ok && d0 + e < a.hd) ? qrow[d0 + e] : 0.0f;
+        }
+        if (a.qb) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                bq4[it][e] = (ok && d0 + e < a.hd) ? a.qb[(size_t)qh * a.hd + d0 + e] : 0.0f;
+        }
+        if (a.rope) {
+            // dims d0 .. d0+3 lie on one side of rot/2 (a multiple of 4): their
+            // four (sin, cos) pairs are 32 contiguous bytes of the table
+            const int j0 = d0 < rhalf ? d0 : d0 - rhalf;
+            if (ok && d0 < a.rot) {
+                const f32x4* t = reinterpret_cast<const f32x4*>(a.rope + ((size_t)qp[it] * rhalf + j0) * 2);
+                const f32x4 t0 = t[0], t1 = t[1];
+                rq[it][0] = make_float2(t0[0], t0[1]);
+                rq[it][1] = make_float2(t0[2], t0[3]);
+                rq[it][2] = make_float2(t1[0], t1[1]);
+                rq[it][3] = make_float2(t1[2], t1[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rq[it][e] = make_float2(0.0f, 1.0f);
+            }
         }
     }
 
@@ -646,6 +693,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
         f32x4 x = xq[it];
+        if (a.qb) x += bq4[it];  // add_bias (ops.rs:373-382)
         if constexpr (QNORM) {
             // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
             double ss = 0.0;
@@ -660,6 +708,20 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (d0 + e < a.hd) x[e] = x[e] * sc * a.qn_w[d0 + e];
+        }
+        if (a.rope) {
+            // rotate_rows (ops.rs:433-452): dim d < rot pairs with d +- rot/2,
+            // which this row's lane (d +- rot/2)/4 holds (rot is a multiple of 8)
+            const int src = d0 < a.rot ? (d0 < rhalf ? lane + rhalf / 4 : lane - rhalf / 4) : lane;
+            f32x4 xp;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xp[e] = __shfl(x[e], src);
+            if (d0 < a.rot) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    x[e] = d0 < rhalf ? rope_lo(x[e], xp[e], rq[it][e].x, rq[it][e].y)
+                                      : rope_hi(xp[e], x[e], rq[it][e].x, rq[it][e].y);
+            }
         }
         bf16x4 y;
 #pragma unroll

@@ -109,6 +109,12 @@ struct dr_pass {
     size_t min_pos = 0, max_pos = 0;
 };
 
+struct dr_rope {
+    dr_ctx* ctx = nullptr;
+    size_t max_len = 0, rope_dim = 0;
+    float* d_table = nullptr;  // [max_len][rope_dim/2][2] (sin, cos)
+};
+
 struct dr_step_cache {
     struct Slot {
         std::vector<int32_t> prev_seq, last_changed;
@@ -379,11 +385,6 @@ void dr_cache_destroy(dr_step_cache* cache) {
 
 // ---------------------------------------------------------------- Q/K/V epilogue
 
-struct dr_rope {
-    dr_ctx* ctx = nullptr;
-    size_t max_len = 0, rope_dim = 0;
-    float* d_table = nullptr;  // [max_len][rope_dim/2][2] (sin, cos)
-};
 
 int dr_rope_create(dr_ctx* ctx, size_t max_len, size_t rope_dim, float theta,
                    const float* freq_factors, dr_rope** out) {
@@ -486,8 +487,20 @@ static int check_slot(const dr_step_cache* c, size_t layer, size_t batch, const 
     return DR_OK;
 }
 
+// StepCache::store (cache.rs:62-71) of a pass's rows, with the K / V part of
+// the Q/K/V epilogue (forward.rs:291-310) applied on the way when asked.
+static int store_rows(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
+                      const float* k, const float* v, const float* k_norm_w, float eps,
+                      const float* kb, const float* vb, int v_norm, const dr_rope* rope);
+
 int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
                    const float* k, const float* v, const float* k_norm_w, float eps) {
+    return store_rows(cache, layer, batch, pass, k, v, k_norm_w, eps, nullptr, nullptr, 0, nullptr);
+}
+
+static int store_rows(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
+                      const float* k, const float* v, const float* k_norm_w, float eps,
+                      const float* kb, const float* vb, int v_norm, const dr_rope* rope) {
     DR_CHECK(check_slot(cache, layer, batch, "dr_cache_store"));
     if (!pass) return fail(DR_ERR_INVALID, "dr_cache_store: pass is NULL");
     if (pass->ctx != cache->ctx) return fail(DR_ERR_INVALID, "dr_cache_store: pass and cache use different contexts");
@@ -501,6 +514,7 @@ int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pa
     a.k = k;
     a.v = v;
     a.pos = pass->d_pos;
+    a.pos0 = pass->max_pos - pass->min_pos + 1 == pass->n ? (int)pass->min_pos : -1;
     a.n = (int)pass->n;
     a.n_head_kv = cache->hkv[layer];
     a.hd = cache->hd[layer];
@@ -512,6 +526,11 @@ int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pa
     a.vec = a.hd == cache->hd_tile[layer] && (((uintptr_t)k | (uintptr_t)v) & 15) == 0;
     a.batch = (int)batch;
     a.n_batch = (int)cache->n_batch;
+    a.kb = kb;
+    a.vb = vb;
+    a.v_norm = v_norm ? 1 : 0;
+    a.rope = rope ? rope->d_table : nullptr;
+    a.rot = rope ? (int)rope->rope_dim : 0;
     hipError_t e = dr::launch_store(cache->hd_tile[layer], a, cache->ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "kv_store launch");
     return DR_OK;
@@ -711,6 +730,8 @@ static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* 
         s.nq = (int)it.pass->n;
         s.nk = (int)cache->n_total;
         s.qpos_sorted = 1;  // dr_pass positions are strictly ascending
+        const dr_pass* ps = it.pass;
+        s.qpos0 = ps->n > 0 && ps->max_pos - ps->min_pos + 1 == ps->n ? (int)ps->min_pos : -1;
         max_nq = std::max(max_nq, s.nq);
     }
     return DR_OK;
@@ -792,6 +813,49 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
         s.act0 = (int)items[b].pass->min_pos;
         s.n_act = (int)items[b].pass->n;
     }
+    return launch_plan(cache->ctx, a, p);
+}
+
+int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item* items,
+                          size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                          dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi) {
+    if (!epi) return fail(DR_ERR_INVALID, "dr_attention_step_epi: epi is NULL");
+    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "dr_attention_step_epi: no items");
+    if (n_items > (size_t)dr::MAX_BATCH)
+        return fail(DR_ERR_INVALID, "dr_attention_step_epi: %zu items > %d", n_items, dr::MAX_BATCH);
+    const dr_rope* rope = epi->rope;
+    if (rope) {
+        if (!cache || rope->ctx != cache->ctx)
+            return fail(DR_ERR_INVALID, "dr_attention_step_epi: rope uses another context");
+        if (rope->rope_dim % 8 != 0)
+            return fail(DR_ERR_UNSUPPORTED, "rope_dim %zu is not a multiple of 8 (use dr_qkv_epilogue)",
+                        rope->rope_dim);
+        if (layer < cache->n_layer && rope->rope_dim > (size_t)cache->hd[layer])
+            return fail(DR_ERR_INVALID, "rope_dim %zu > head_dim %d", rope->rope_dim, cache->hd[layer]);
+        for (size_t b = 0; b < n_items; ++b)
+            if (items[b].pass && items[b].pass->n > 0 && items[b].pass->max_pos >= rope->max_len)
+                return fail(DR_ERR_INVALID, "item %zu: position %zu >= the RoPE table's %zu", b,
+                            items[b].pass->max_pos, rope->max_len);
+    }
+    dr_batch_item bi[dr::MAX_BATCH];
+    for (size_t b = 0; b < n_items; ++b) bi[b] = dr_batch_item{items[b].q, items[b].out, items[b].pass};
+    dr::AttnArgs a;
+    int max_nq = 0;
+    DR_CHECK(cached_args(cache, layer, bi, n_items, n_head, sliding_window, causal_prefix, scale,
+                         epi->q_norm_w, epi->eps, "dr_attention_step_epi", a, max_nq));
+    for (size_t b = 0; b < n_items; ++b) {
+        if (items[b].pass->n > 0 && (!items[b].k || !items[b].v))
+            return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
+        DR_CHECK(store_rows(cache, layer, b, items[b].pass, items[b].k, items[b].v, epi->k_norm_w,
+                            epi->eps, epi->bk, epi->bv, epi->v_norm, rope));
+    }
+    if (max_nq == 0) return DR_OK;
+    a.qb = epi->bq;
+    a.rope = rope ? rope->d_table : nullptr;
+    a.rot = rope ? (int)rope->rope_dim : 0;
+    const int mask = mask_of(sliding_window, causal_prefix);
+    dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask,
+                                epi->q_norm_w != nullptr);
     return launch_plan(cache->ctx, a, p);
 }
 
@@ -931,6 +995,7 @@ int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const
     bool sorted = true;
     for (size_t i = 1; i < nq && sorted; ++i) sorted = qr.pos[i] > qr.pos[i - 1];
     sl.qpos_sorted = sorted ? 1 : 0;
+    sl.qpos0 = -1;  // the drop-in reads each row's position
     const int mask = !masked ? dr::MASK_NONE
                              : ((has_kpos || has_kseq) ? dr::MASK_KEYS : dr::MASK_POS);
     DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, mask, false));

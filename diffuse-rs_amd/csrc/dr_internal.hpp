@@ -30,6 +30,7 @@ struct AttnSlot {
     int nq;
     int nk;
     int qpos_sorted;      // qpos strictly ascending (a dr_pass): key ranges from endpoints
+    int qpos0;            // >= 0: qpos[i] == qpos0 + i (contiguous), read without a load
     // Fused step (LaunchPlan::act): keys at positions [act0, act0 + n_act)
     // are the step's fresh rows, read as f32 from ka / va ([n_act][kv_rstride],
     // head g at g*hd) instead of from the cache, and written into the cache
@@ -70,6 +71,11 @@ struct AttnArgs {
     int kv_rstride;                // fused step: elements between active K/V rows
     const float* kn_w;             // fused step: K-norm gain for the active rows or nullptr
     float kn_eps;
+    // the Q/K/V epilogue's Q part (forward.rs:291-310): bias before the
+    // QK-norm, RoPE after it, at the query rows' positions (qpos)
+    const float* qb;               // [n_head*hd] or nullptr
+    const float* rope;             // [max_len][rot/2][2] (sin, cos) table or nullptr
+    int rot;                       // rotated dims (a multiple of 8)
 };
 static_assert(offsetof(AttnArgs, slot) == 64, "scalar block of AttnArgs is one 64-byte line");
 
@@ -90,6 +96,13 @@ struct StoreArgs {
     int batch, n_batch;  // batch slot of the cache (n_batch 0 counts as 1): picks the XCDs
     // set by launch_store: workgroup -> (kv head, head-dim chunk, row block)
     int n_rb, per_xcd, xcd_lo, xcd_n;
+    // the Q/K/V epilogue's K / V part (forward.rs:291-310), all optional
+    const float* kb;     // [n_head_kv*hd] K bias
+    const float* vb;     // [n_head_kv*hd] V bias
+    int v_norm;          // Gemma: unweighted RMSNorm of each V head (eps kn_eps)
+    const float* rope;   // [max_len][rot/2][2] (sin, cos) table, or nullptr
+    int rot;             // rotated dims per head
+    int pos0;            // >= 0: pos[r] == pos0 + r (contiguous rows), read without a load
 };
 
 struct GatherArgs {

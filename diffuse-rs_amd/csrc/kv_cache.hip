@@ -34,6 +34,17 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
     return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// RoPE's rotation of one pair (ops.rs:447-448), without fused multiply-adds
+// as Rust evaluates it.
+__device__ __forceinline__ float rope_lo(float a, float b, float sn, float cs) {
+#pragma clang fp contract(off)
+    return a * cs - b * sn;
+}
+__device__ __forceinline__ float rope_hi(float a, float b, float sn, float cs) {
+#pragma clang fp contract(off)
+    return a * sn + b * cs;
+}
+
 constexpr int SR = 64;   // rows per store workgroup: one 128-byte line of a V^T row
 constexpr int SD = 64;   // head-dim entries per store workgroup: one 128-byte line of a K row
 constexpr int SPT = 16;  // consecutive values per thread (4 threads per row, 256 threads)
@@ -87,39 +98,147 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
                 xv[i][e] = in ? a.v[row + d] : 0.0f;
             }
     }
-    const int pos = ok ? (a.pos ? a.pos[r] : r) : 0;
+    const int pos = ok ? (a.pos0 >= 0 ? a.pos0 + r : (a.pos ? a.pos[r] : r)) : 0;
+    // RoPE's (sin, cos) pairs of this thread's 16 dims, requested with the
+    // rows: when rot/2 is a multiple of 16 they lie on one side of it, 32
+    // contiguous floats of the position's table row
+    const int rhalf = a.rot / 2;
+    const bool tab_vec = a.rope && rhalf % SPT == 0 && d0 < a.rot;
+    f32x4 tv[SPT / 2];
+    if (tab_vec && ok) {
+        const int j0 = d0 < rhalf ? d0 : d0 - rhalf;
+        const f32x4* t = reinterpret_cast<const f32x4*>(a.rope + ((size_t)pos * rhalf + j0) * 2);
+#pragma unroll
+        for (int i = 0; i < SPT / 2; ++i) tv[i] = t[i];
+    }
 
-    if (a.kn_w) {
-        // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64 over
-        // the whole row; this thread covers entries part*16 + [0,16) of every
-        // 64-wide chunk.
-        double ss = 0.0;
-#pragma unroll
-        for (int i = 0; i < V4; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float sq = xk[i][e] * xk[i][e];
-                ss += (double)sq;
-            }
-        for (int c = 0; c < NDC; ++c) {
-            if (c == dc) continue;
-            const int e0 = c * SD + part * SPT;
-            for (int e = 0; e < SPT; ++e) {
-                const float x = (ok && e0 + e < a.hd) ? a.k[row + e0 + e] : 0.0f;
-                const float sq = x * x;
-                ss += (double)sq;
-            }
-        }
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        const float sc = 1.0f / (float)sqrt(ss / (double)a.hd + (double)a.kn_eps);
+    // The Q/K/V epilogue's K and V part (forward.rs:291-310), when asked:
+    // add_bias (ops.rs:373-382), then K's RMSNorm with the gain / V's
+    // without one (Gemma, ops.rs:116-124), then RoPE on K (ops.rs:433-452).
+    const float* kb = a.kb ? a.kb + (size_t)g * a.hd : nullptr;
+    const float* vb = a.vb ? a.vb + (size_t)g * a.hd : nullptr;
+    if (kb || vb) {
 #pragma unroll
         for (int i = 0; i < V4; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d = d0 + 4 * i + e;
-                if (d < a.hd) xk[i][e] = xk[i][e] * sc * a.kn_w[d];
+                if (d < a.hd) {
+                    if (kb) xk[i][e] += kb[d];
+                    if (vb) xv[i][e] += vb[d];
+                }
             }
+    }
+    // The row's other 64-wide chunks at this thread's 16 entries (bias
+    // added), read once: the norms sum over the whole row, and with RoPE a
+    // dim's partner (d +- rot/2) lies in one of them when rot/2 is a multiple
+    // of 64.
+    const bool need_ko = a.kn_w || a.rope;
+    f32x4 ko[NDC][V4], vo[NDC][V4];
+    auto load_other = [&](f32x4 (&xo)[NDC][V4], const float* src, const float* bias)
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NDC; ++c) {
+            if (c == dc) continue;
+            const int e0 = c * SD + part * SPT;
+            if (ok && a.vec) {
+#pragma unroll
+                for (int i = 0; i < V4; ++i) {
+                    xo[c][i] = *reinterpret_cast<const f32x4*>(src + row + e0 + 4 * i);
+                    if (bias) xo[c][i] += *reinterpret_cast<const f32x4*>(bias + e0 + 4 * i);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < V4; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int d = e0 + 4 * i + e;
+                        float v = (ok && d < a.hd) ? src[row + d] : 0.0f;
+                        if (bias && d < a.hd) v += bias[d];
+                        xo[c][i][e] = v;
+                    }
+            }
+        }
+    };
+    if (need_ko) load_other(ko, a.k, kb);
+    if (a.v_norm) load_other(vo, a.v, vb);
+    // rms_norm_inplace (ops.rs:106-114) / rms_norm_noscale: f32 squares
+    // summed in f64 over the whole row
+    auto row_scale = [&](const f32x4 (&x)[V4], const f32x4 (&xo)[NDC][V4], float eps)
+        __attribute__((always_inline)) {
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < NDC; ++c)
+#pragma unroll
+            for (int i = 0; i < V4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xv = c == dc ? x[i][e] : xo[c][i][e];
+                    const float sq = xv * xv;
+                    ss += (double)sq;
+                }
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        return 1.0f / (float)sqrt(ss / (double)a.hd + (double)eps);
+    };
+    float ksc = 1.0f;
+    if (a.kn_w) {
+        ksc = row_scale(xk, ko, a.kn_eps);
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = d0 + 4 * i + e;
+                if (d < a.hd) xk[i][e] = xk[i][e] * ksc * a.kn_w[d];
+            }
+    }
+    if (a.v_norm) {
+        const float vsc = row_scale(xv, vo, a.kn_eps);
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] *= vsc;
+    }
+    if (a.rope && ok) {
+        // the partner's value with the same bias and norm, then the pair
+        // rotates (rotate_rows, ops.rs:433-452)
+        const int half = a.rot / 2;
+        const float* tab = a.rope + (size_t)pos * half * 2;
+        const bool chunked = half % SD == 0;  // partner = same entry of chunk dc +- half/SD
+        // (the thread's 16 dims lie on one side of half, so one chunk)
+        const int pc = chunked ? (d0 < half ? dc + half / SD : dc - half / SD) : 0;
+        f32x4 yk[V4];
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = d0 + 4 * i + e;
+                yk[i][e] = xk[i][e];
+                if (d >= a.rot) continue;
+                const int pd = d < half ? d + half : d - half;
+                float xp;
+                if (chunked) {
+                    xp = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < NDC; ++c)
+                        if (c == pc) xp = ko[c][i][e];  // pc != dc
+                } else {
+                    xp = a.k[row + pd];
+                    if (kb) xp += kb[pd];
+                }
+                if (a.kn_w) xp = xp * ksc * a.kn_w[pd];
+                const int j = d < half ? d : pd;
+                float2 t;
+                if (tab_vec) {
+                    const int k4 = 4 * i + e;  // pair k4 of the 16: floats 2*k4, 2*k4+1
+                    t = make_float2(tv[k4 / 2][2 * (k4 % 2)], tv[k4 / 2][2 * (k4 % 2) + 1]);
+                } else {
+                    t = *reinterpret_cast<const float2*>(tab + 2 * j);
+                }
+                yk[i][e] = d < half ? rope_lo(xk[i][e], xp, t.x, t.y) : rope_hi(xp, xk[i][e], t.x, t.y);
+            }
+#pragma unroll
+        for (int i = 0; i < V4; ++i) xk[i] = yk[i];
     }
     if (ok) {
         uint16_t* dst = a.kc + ((size_t)g * a.cap + pos) * HD + d0;

@@ -76,6 +76,12 @@ class CStepItem(ctypes.Structure):
                 ("k", ctypes.c_void_p), ("v", ctypes.c_void_p)]
 
 
+class CEpilogue(ctypes.Structure):
+    _fields_ = [("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
+                ("q_norm_w", ctypes.c_void_p), ("k_norm_w", ctypes.c_void_p),
+                ("v_norm", ctypes.c_int), ("eps", ctypes.c_float), ("rope", ctypes.c_void_p)]
+
+
 class CLaunchInfo(ctypes.Structure):
     _fields_ = [
         ("n_split", ctypes.c_int),
@@ -120,6 +126,9 @@ _SIGS = {
     "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
                             ctypes.POINTER(ctypes.c_void_p)]),
     "dr_rope_destroy": (None, [_VP]),
+    "dr_attention_step_epi": (_I, [_VP, ctypes.c_size_t, ctypes.POINTER(CStepItem), ctypes.c_size_t,
+                                   ctypes.c_size_t, OptUsize, OptUsize, ctypes.c_float,
+                                   ctypes.POINTER(CEpilogue)]),
     "dr_qkv_epilogue": (_I, [_VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, ctypes.c_size_t,
                              ctypes.c_size_t, _VP, _VP, _VP, _VP, _VP, _I, ctypes.c_float, _VP]),
     "dr_ctx_set_tuning": (_I, [_VP, _I, _I, _I]),
@@ -473,6 +482,22 @@ class StepCache:
         _check(self.ctx.lib.dr_attention_step(
             self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
             scale, _ptr(q_norm_w) or None, q_norm_eps, _ptr(k_norm_w) or None, k_norm_eps))
+
+    def step_epi(self, layer: int, items: Sequence[tuple], n_head: int,
+                 sliding_window: Optional[int] = None, causal_prefix: Optional[int] = None,
+                 scale: float = 1.0, bq=None, bk=None, bv=None, q_norm_w=None, k_norm_w=None,
+                 v_norm: bool = False, eps: float = 1e-6, rope: "Rope | None" = None) -> None:
+        """step() with the Q/K/V epilogue (forward.rs:291-310) folded into the
+        store and the attention; the item buffers are only read."""
+        arr = (CStepItem * len(items))()
+        for i, (q, out, p, k, v) in enumerate(items):
+            arr[i] = CStepItem(_ptr(q), _ptr(out), p.h, _ptr(k), _ptr(v))
+        epi = CEpilogue(_ptr(bq) or None, _ptr(bk) or None, _ptr(bv) or None,
+                        _ptr(q_norm_w) or None, _ptr(k_norm_w) or None, 1 if v_norm else 0, eps,
+                        rope.h.value if rope is not None else None)
+        _check(self.ctx.lib.dr_attention_step_epi(
+            self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
+            scale, ctypes.byref(epi)))
 
     def close(self) -> None:
         if self.h:

@@ -249,6 +249,28 @@ int dr_qkv_epilogue(dr_ctx* ctx, const dr_pass* pass, float* q, float* k, float*
                     const float* bv, const float* q_norm_w, const float* k_norm_w, int v_norm,
                     float eps, const dr_rope* rope);
 
+/* The operands of the Q/K/V epilogue (all device pointers, NULL = none). */
+typedef struct {
+    const float* bq;       /* [n_head * head_dim] */
+    const float* bk;       /* [n_head_kv * head_dim] */
+    const float* bv;       /* [n_head_kv * head_dim] */
+    const float* q_norm_w; /* [head_dim] */
+    const float* k_norm_w; /* [head_dim] */
+    int v_norm;            /* Gemma: unweighted RMSNorm of each V head */
+    float eps;             /* rms_norm_eps */
+    const dr_rope* rope;   /* rope_dim a multiple of 8 */
+} dr_epilogue;
+/* dr_attention_step with the Q/K/V epilogue of attention_block
+ * (src/model/forward.rs:291-343) folded into its passes: each item's k / v
+ * rows get bias, norm and (K) RoPE inside the cache store, and its q rows get
+ * bias, QK-norm and RoPE where the attention reads them, at the pass's
+ * positions.  No separate pass over q, k or v; the item buffers are read,
+ * never written.  Same result as dr_qkv_epilogue followed by
+ * dr_attention_step. */
+int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item* items,
+                          size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                          dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi);
+
 /* Launch configuration of the last attention kernel this context enqueued
  * (for measurement): key splits across workgroups, workgroups, waves per
  * workgroup, keys per tile, head-dim tile, 32-row query blocks and key

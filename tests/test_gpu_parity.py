@@ -743,3 +743,73 @@ def test_qkv_epilogue_then_step_vs_oracle(dev):
     # move a bf16 rounding only at an exact tie, which these inputs avoid)
     assert np.array_equal(dev.get(ok), _normed_bf16(dev, Kf, None))
     assert np.array_equal(dev.get(ov), _normed_bf16(dev, Vf, None))
+
+
+@pytest.mark.parametrize("h,hkv,hd,rot,n_p,n_c,batch,norm,v_norm,window,theta", [
+    (16, 16, 128, 128, 512, 256, 1, True, False, None, 10000.0),   # C4-like, QK-norm
+    (8, 2, 128, 64, 200, 93, 2, False, False, None, 500000.0),     # GQA, partial rotary, CFG pair
+    (8, 4, 256, 256, 300, 120, 1, True, True, 128, 10000.0),       # Gemma-like: V-norm, window
+])
+def test_step_epi_vs_oracle(dev, h, hkv, hd, rot, n_p, n_c, batch, norm, v_norm, window, theta):
+    """dr_attention_step_epi (the Q/K/V epilogue folded into the cache store
+    and the attention prologue) against the oracle's epilogue + attention,
+    and the cache against bf16 of the oracle's K / V rows."""
+    rng = np.random.default_rng(hd + rot + batch)
+    eps = 1e-6
+    n_t = n_p + n_c
+    kvs = hkv * hd
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    bq = (0.1 * rng.standard_normal(h * hd)).astype(np.float32)
+    bk = (0.1 * rng.standard_normal(kvs)).astype(np.float32)
+    bv = (0.1 * rng.standard_normal(kvs)).astype(np.float32)
+    table = orc.rope_table(n_t, rot, theta)
+    rope = dr.Rope(dev.ctx, n_t, rot, theta)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd], n_batch=batch)
+    p_pr = dr.Pass(dev.ctx, range(n_p))
+    canvas = list(range(n_p, n_t))
+    p_c = dr.Pass(dev.ctx, canvas)
+    put = lambda x: dev.put(x) if x is not None else None  # noqa: E731
+    scale = 1 / math.sqrt(hd)
+    items, outs, wants = [], [], []
+    for b in range(batch):
+        K = rng.standard_normal(n_t * kvs).astype(np.float32)
+        V = rng.standard_normal(n_t * kvs).astype(np.float32)
+        Q = rng.standard_normal(n_c * h * hd).astype(np.float32)
+        kp, vp = K[:n_p * kvs].copy(), V[:n_p * kvs].copy()
+        kc, vc = K[n_p * kvs:].copy(), V[n_p * kvs:].copy()
+        # the prompt rows go through the two-pass path: epilogue, then store
+        qd = np.zeros(n_p * h * hd, np.float32)
+        dq0, dkp, dvp = put(qd), put(kp), put(vp)
+        dr.qkv_epilogue(dev.ctx, p_pr, dq0, dkp, dvp, h, hkv, hd, put(bq), put(bk), put(bv),
+                        put(qn), put(kn), v_norm, eps, rope)
+        cache.store(0, p_pr, dkp, dvp, batch=b)
+        _, kp_o, vp_o = _epilogue_oracle(qd, kp, vp, list(range(n_p)), h, hkv, hd, bq, bk, bv, qn,
+                                         kn, v_norm, eps, table, rot)
+        q_o, kc_o, vc_o = _epilogue_oracle(Q, kc, vc, canvas, h, hkv, hd, bq, bk, bv, qn, kn,
+                                           v_norm, eps, table, rot)
+        s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, scale=scale)
+        Kf, Vf = np.concatenate([kp_o, kc_o]), np.concatenate([vp_o, vc_o])
+        wants.append((oracle_run(s, RowsSpec(canvas), RowsSpec(list(range(n_t))), q_o, Kf, Vf),
+                      Kf, Vf))
+        out = dev.empty(n_c * h * hd)
+        outs.append(out)
+        items.append((put(Q), out, p_c, put(kc), put(vc)))
+    say(f"step_epi h {h}/{hkv} hd {hd} rot {rot} batch {batch} norm {norm} v_norm {v_norm} "
+        f"window {window}")
+    cache.step_epi(0, items, h, sliding_window=window, scale=scale, bq=put(bq), bk=put(bk),
+                   bv=put(bv), q_norm_w=put(qn), k_norm_w=put(kn), v_norm=v_norm, eps=eps,
+                   rope=rope)
+    for b in range(batch):
+        want, Kf, Vf = wants[b]
+        check(dev.get(outs[b]), want, f"batch {b} vs oracle")
+        ok, ov = dev.empty(n_t * kvs), dev.empty(n_t * kvs)
+        cache.gather(0, list(range(n_t)), ok, ov, batch=b)
+        gk, gv = dev.get(ok), dev.get(ov)
+        wk, wv = _normed_bf16(dev, Kf, None), _normed_bf16(dev, Vf, None)
+        # bf16 of the same f32 rows; a norm's f64 sum in another order can
+        # move an f32 value by an ulp, which changes its bf16 rounding only
+        # at an exact tie
+        for name, g_, w_ in (("K", gk, wk), ("V", gv, wv)):
+            bad = np.count_nonzero(g_ != w_)
+            assert bad <= 2 and np.max(np.abs(g_ - w_)) <= 2.0**-7 * np.max(np.abs(w_)), (name, bad)
