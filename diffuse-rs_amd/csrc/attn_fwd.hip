@@ -237,7 +237,7 @@ struct Geometry {
     static_assert(!W16 || (NP > 0 && HD <= 128), "16-row waves: DMA waves, head dim up to 128");
 };
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT, bool W16>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool ACT, bool W16>
 __attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD,
                                    Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD))) __global__
 __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
@@ -627,19 +627,25 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
         return (it * NWT + wave) * RPI + lane / LPR;
     };
     f32x4 xq[QIT];
-    // the epilogue's Q part (bias, RoPE), when asked: its operands are
-    // requested with the rows
+    // The epilogue's Q part (QEPI kernels only; bias, QK-norm and RoPE each
+    // where its operand is given): its operands are requested with the rows.
+    // Kernels without QEPI carry none of this code.
     f32x4 bq4[QIT];
     float2 rq[QIT][4];
-    const int rhalf = a.rot / 2;
+    const int rhalf = QEPI ? a.rot / 2 : 0;
+    const bool qbias = QEPI && a.qb != nullptr;
+    const bool qrope = QEPI && a.rope != nullptr;
     int qp[QIT];  // the rows' positions, requested before the rows (RoPE's table index)
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
-        const int rr = wg_row0 + q_lrow(it);
-        const bool ok = q_lrow(it) < QROWS && rr < rows_total;
-        int hgq = 0, qiq = 0;
-        if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
-        qp[it] = (a.rope && ok) ? (S.qpos0 >= 0 ? S.qpos0 + qiq : S.qpos[qiq]) : 0;
+        qp[it] = 0;
+        if constexpr (QEPI) {
+            const int rr = wg_row0 + q_lrow(it);
+            const bool ok = q_lrow(it) < QROWS && rr < rows_total;
+            int hgq = 0, qiq = 0;
+            if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
+            qp[it] = (qrope && ok) ? (S.qpos0 >= 0 ? S.qpos0 + qiq : S.qpos[qiq]) : 0;
+        }
     }
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
@@ -656,12 +662,12 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
 #pragma unroll
             for (int e = 0; e < 4; ++e) xq[it][e] = (ok && d0 + e < a.hd) ? qrow[d0 + e] : 0.0f;
         }
-        if (a.qb) {
+        if (qbias) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 bq4[it][e] = (ok && d0 + e < a.hd) ? a.qb[(size_t)qh * a.hd + d0 + e] : 0.0f;
         }
-        if (a.rope) {
+        if (qrope) {
             // dims d0 .. d0+3 lie on one side of rot/2 (a multiple of 4): their
             // four (sin, cos) pairs are 32 contiguous bytes of the table
             const int j0 = d0 < rhalf ? d0 : d0 - rhalf;
@@ -693,8 +699,8 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
         f32x4 x = xq[it];
-        if (a.qb) x += bq4[it];  // add_bias (ops.rs:373-382)
-        if constexpr (QNORM) {
+        if (qbias) x += bq4[it];  // add_bias (ops.rs:373-382)
+        if (QEPI && a.qn_w) {
             // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
             double ss = 0.0;
 #pragma unroll
@@ -709,7 +715,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
             for (int e = 0; e < 4; ++e)
                 if (d0 + e < a.hd) x[e] = x[e] * sc * a.qn_w[d0 + e];
         }
-        if (a.rope) {
+        if (qrope) {
             // rotate_rows (ops.rs:433-452): dim d < rot pairs with d +- rot/2,
             // which this row's lane (d +- rot/2)/4 holds (rot is a multiple of 8)
             const int src = d0 < a.rot ? (d0 < rhalf ? lane + rhalf / 4 : lane - rhalf / 4) : lane;
@@ -1379,12 +1385,12 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     }
 }
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QNORM, bool ACT, bool W16 = false>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool ACT, bool W16 = false>
 hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     using G = Geometry<HD, RB, KQ, NS, NP, W16>;
     constexpr size_t lds = G::LDS_BYTES;
     static bool attr_set = false;
-    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QNORM, ACT, W16>;
+    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QEPI, ACT, W16>;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1401,10 +1407,10 @@ hipError_t launch_modes16(const LaunchPlan& p, const AttnArgs& a, hipStream_t st
     if (p.act) return hipErrorInvalidValue;
     switch (p.mask) {
         case MASK_NONE:
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false, true>(p, a, st)
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false, true>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, false, true>(p, a, st);
         case MASK_POS:
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false, true>(p, a, st)
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false, true>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false, true>(p, a, st);
         default:
             return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false, true>(p, a, st);
@@ -1423,7 +1429,7 @@ hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
             // the unmasked path, and the register budget of that build holds
             // a staged tile across the producer loop.
             if (p.mask == MASK_KEYS) return hipErrorInvalidValue;
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, true>(p, a, st)
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, true>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, true>(p, a, st);
         } else {
             return hipErrorInvalidValue;
@@ -1431,10 +1437,10 @@ hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
     }
     switch (p.mask) {
         case MASK_NONE:
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false>(p, a, st)
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, false>(p, a, st);
         case MASK_POS:
-            return p.qnorm ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false>(p, a, st)
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false>(p, a, st);
         default:
             return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false>(p, a, st);
@@ -1483,13 +1489,13 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 }  // namespace
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
+                          int mask, bool qepi, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : 256);
     p.block_n = BN;
     p.mask = mask;
-    p.qnorm = qnorm && mask != MASK_KEYS;
+    p.qepi = qepi && mask != MASK_KEYS;
     const int cus = n_cu > 0 ? n_cu : 256;
     const int row_blocks = (group * max_nq + 31) / 32;  // per (batch, kv head)
     const int ntiles = (max_nk + BN - 1) / BN;

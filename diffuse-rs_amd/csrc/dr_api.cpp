@@ -647,8 +647,8 @@ int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
 // ---------------------------------------------------------------- attention
 
 static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int max_nq,
-                               int max_nk, int mask, bool qnorm) {
-    return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qnorm,
+                               int max_nk, int mask, bool qepi) {
+    return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
                               ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
                               ctx->force_rows);
 }
@@ -667,8 +667,8 @@ static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
 }
 
 static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int max_nk,
-                          int mask, bool qnorm) {
-    return launch_plan(ctx, a, plan_for(ctx, a, hd, max_nq, max_nk, mask, qnorm));
+                          int mask, bool qepi) {
+    return launch_plan(ctx, a, plan_for(ctx, a, hd, max_nq, max_nk, mask, qepi));
 }
 
 static float scale_log2(float scale) { return scale * 1.4426950408889634f; }
@@ -855,7 +855,7 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
     a.rot = rope ? (int)rope->rope_dim : 0;
     const int mask = mask_of(sliding_window, causal_prefix);
     dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask,
-                                epi->q_norm_w != nullptr);
+                                epi->q_norm_w || epi->bq || rope);
     return launch_plan(cache->ctx, a, p);
 }
 

@@ -155,7 +155,7 @@ struct LaunchPlan {
     int rowgroups;   // workgroups per (batch, kv head) and split
     int n_workgroups;
     int mask;        // MaskMode
-    bool qnorm;
+    bool qepi;       // Q epilogue compiled in: bias, QK-norm, RoPE, each where its operand is given
     bool act;        // fused step: active keys read from f32 rows and stored (see AttnSlot)
     bool w16;        // two 16-row compute waves per (row block, key group)
 };
@@ -165,7 +165,7 @@ struct LaunchPlan {
 // heuristic (tuning); force_rows 16 or 32 picks the query rows per compute
 // wave where both are built (0: automatic).
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, bool qnorm, int n_cu, int force_rb, int force_kq,
+                          int mask, bool qepi, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows);
 
 // Whether a plan's shape can run the fused step (each DMA wave stages one
