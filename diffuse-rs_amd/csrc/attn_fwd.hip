@@ -205,9 +205,13 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 
 template <int HD, int RB, int KQ, int NS, int NP, bool W16 = false>
 struct Geometry {
-    // W16: two compute waves of 16 query rows per (row block, key group)
+    // W16: two compute waves of 16 query rows per (row block, key group).
+    // DS (head dim 512): two compute waves per (row block, key group) that
+    // split the head dim: each holds Q and O for its 256-wide half, and the
+    // two halves of every score are summed through LDS.
+    static constexpr bool DS = HD > 256;
     static constexpr int NE = RB * KQ;         // (row block, key group) pairs: merge entries
-    static constexpr int NW = NE * (W16 ? 2 : 1);  // compute waves per workgroup
+    static constexpr int NW = NE * ((W16 || DS) ? 2 : 1);  // compute waves per workgroup
     static constexpr int NWT = NW + NP;        // all waves (NP: DMA-only producer waves)
     static constexpr int NT = NWT * 64;
     static constexpr int NDMA = NP > 0 ? NP : NW;  // waves that issue the K/V DMA
@@ -222,7 +226,9 @@ struct Geometry {
     static constexpr int NLDW = STAGE / 8 / (NDMA * 64);  // DMA instructions per DMA wave
                                                           // and super-tile
     static constexpr int QROWS = RB * 32;      // query rows per workgroup
-    static constexpr size_t STAGE_BYTES = (size_t)NS * STAGE * 2;
+    // DS: each compute wave's partial scores (32 x 32 f32), after the stages
+    static constexpr size_t XCH_BYTES = DS ? (size_t)NW * 64 * 16 * 4 : 0;
+    static constexpr size_t STAGE_BYTES = (size_t)NS * STAGE * 2 + XCH_BYTES;
     // Q fragments are held in registers for the whole kernel; Q is staged
     // once, through the first slot of the last pipeline stage.
     static constexpr int ROWF = HD + 4;        // f32 row pitch of the merge area
@@ -235,12 +241,13 @@ struct Geometry {
     static_assert(QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
     static_assert(!W16 || (NP > 0 && HD <= 128), "16-row waves: DMA waves, head dim up to 128");
+    static_assert(!DS || (HD == 512 && !W16 && NP == 0), "head-dim split: head dim 512, no DMA waves");
 };
 
 template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool ACT, bool W16>
 __attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD,
                                    Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD))) __global__
-__launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
+__launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     using G = Geometry<HD, RB, KQ, NS, NP, W16>;
     static_assert(!(W16 && ACT), "the fused step runs 32-row waves");
     constexpr int NW = G::NW, NWT = G::NWT, NT = G::NT, NC = G::NC, ND = G::ND;
@@ -618,7 +625,11 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
     // RMS-normalised when asked, times scale*log2(e), rounded to bf16 and
     // stored in the B-operand layout in stage NS-1 (first written by the DMA
     // of super-tile NS-1, issued after the barrier at the top of the loop).
-    constexpr int LPR = HD / 4;       // lanes per row (f32x4 each)
+    // A lane holds PPL f32x4 pieces of a row, at d0 + p*HW (head dim 512:
+    // two, so that a row fits one wave).
+    constexpr int PPL = HD > 256 ? 2 : 1;
+    constexpr int HW = HD / PPL;
+    constexpr int LPR = HW / 4;       // lanes per row
     constexpr int RPI = 64 / LPR;     // rows per wave instruction
     constexpr int QIT = (QROWS + NWT * RPI - 1) / (NWT * RPI);  // row groups per wave
     const int d0 = (lane % LPR) * 4;
@@ -626,117 +637,167 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
     auto q_lrow = [&](int it) __attribute__((always_inline)) {
         return (it * NWT + wave) * RPI + lane / LPR;
     };
-    f32x4 xq[QIT];
     // The epilogue's Q part (QEPI kernels only; bias, QK-norm and RoPE each
     // where its operand is given): its operands are requested with the rows.
-    // Kernels without QEPI carry none of this code.
-    f32x4 bq4[QIT];
-    float2 rq[QIT][4];
+    // Kernels without QEPI carry none of this code.  Rows are loaded and
+    // written in batches of QB iterations (all at once except with the
+    // epilogue at head dim 512, whose operands would not fit the registers).
+    constexpr int QB = (QEPI && PPL > 1) ? (QIT < 4 ? QIT : 4) : QIT;
     const int rhalf = QEPI ? a.rot / 2 : 0;
     const bool qbias = QEPI && a.qb != nullptr;
     const bool qrope = QEPI && a.rope != nullptr;
-    int qp[QIT];  // the rows' positions, requested before the rows (RoPE's table index)
+    uint16_t* const qs = smem + (NS - 1) * SLOT;
+    auto q_batch = [&](const int ib) __attribute__((always_inline)) {
+        f32x4 xq[QB][PPL];
+        f32x4 bq4[QB][PPL];
+        float2 rq[QB][PPL][4];
+        int qp[QB];  // the rows' positions, requested before the rows (RoPE's table index)
 #pragma unroll
-    for (int it = 0; it < QIT; ++it) {
-        qp[it] = 0;
-        if constexpr (QEPI) {
+        for (int ii = 0; ii < QB; ++ii) {
+            const int it = ib + ii;
+            qp[ii] = 0;
+            if constexpr (QEPI) {
+                const int rr = wg_row0 + q_lrow(it);
+                const bool ok = it < QIT && q_lrow(it) < QROWS && rr < rows_total;
+                int hgq = 0, qiq = 0;
+                if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
+                qp[ii] = (qrope && ok) ? (S.qpos0 >= 0 ? S.qpos0 + qiq : S.qpos[qiq]) : 0;
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < QB; ++ii) {
+            const int it = ib + ii;
             const int rr = wg_row0 + q_lrow(it);
-            const bool ok = q_lrow(it) < QROWS && rr < rows_total;
+            const bool ok = it < QIT && q_lrow(it) < QROWS && rr < rows_total;
             int hgq = 0, qiq = 0;
             if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
-            qp[it] = (qrope && ok) ? (S.qpos0 >= 0 ? S.qpos0 + qiq : S.qpos[qiq]) : 0;
-        }
-    }
+            const int qh = g * a.group + hgq;
+            const float* qrow = static_cast<const float*>(S.q) + (size_t)qiq * a.q_rstride +
+                                (size_t)qh * a.hd;
 #pragma unroll
-    for (int it = 0; it < QIT; ++it) {
-        const int rr = wg_row0 + q_lrow(it);
-        const bool ok = q_lrow(it) < QROWS && rr < rows_total;
-        int hgq = 0, qiq = 0;
-        if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
-        const int qh = g * a.group + hgq;
-        const float* qrow = static_cast<const float*>(S.q) + (size_t)qiq * a.q_rstride +
-                            (size_t)qh * a.hd;
-        if (ok && a.hd == HD) {
-            xq[it] = *reinterpret_cast<const f32x4*>(qrow + d0);
-        } else {
+            for (int pc = 0; pc < PPL; ++pc) {
+                const int dp = d0 + pc * HW;
+                if (ok && a.hd == HD) {
+                    xq[ii][pc] = *reinterpret_cast<const f32x4*>(qrow + dp);
+                } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xq[it][e] = (ok && d0 + e < a.hd) ? qrow[d0 + e] : 0.0f;
-        }
-        if (qbias) {
+                    for (int e = 0; e < 4; ++e) xq[ii][pc][e] = (ok && dp + e < a.hd) ? qrow[dp + e] : 0.0f;
+                }
+                if (qbias) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                bq4[it][e] = (ok && d0 + e < a.hd) ? a.qb[(size_t)qh * a.hd + d0 + e] : 0.0f;
-        }
-        if (qrope) {
-            // dims d0 .. d0+3 lie on one side of rot/2 (a multiple of 4): their
-            // four (sin, cos) pairs are 32 contiguous bytes of the table
-            const int j0 = d0 < rhalf ? d0 : d0 - rhalf;
-            if (ok && d0 < a.rot) {
-                const f32x4* t = reinterpret_cast<const f32x4*>(a.rope + ((size_t)qp[it] * rhalf + j0) * 2);
-                const f32x4 t0 = t[0], t1 = t[1];
-                rq[it][0] = make_float2(t0[0], t0[1]);
-                rq[it][1] = make_float2(t0[2], t0[3]);
-                rq[it][2] = make_float2(t1[0], t1[1]);
-                rq[it][3] = make_float2(t1[2], t1[3]);
-            } else {
+                    for (int e = 0; e < 4; ++e)
+                        bq4[ii][pc][e] = (ok && dp + e < a.hd) ? a.qb[(size_t)qh * a.hd + dp + e] : 0.0f;
+                }
+                if (qrope) {
+                    // dims dp .. dp+3 lie on one side of rot/2 (a multiple of 4):
+                    // their four (sin, cos) pairs are 32 contiguous bytes of the table
+                    const int j0 = dp < rhalf ? dp : dp - rhalf;
+                    if (ok && dp < a.rot) {
+                        const f32x4* t =
+                            reinterpret_cast<const f32x4*>(a.rope + ((size_t)qp[ii] * rhalf + j0) * 2);
+                        const f32x4 t0 = t[0], t1 = t[1];
+                        rq[ii][pc][0] = make_float2(t0[0], t0[1]);
+                        rq[ii][pc][1] = make_float2(t0[2], t0[3]);
+                        rq[ii][pc][2] = make_float2(t1[0], t1[1]);
+                        rq[ii][pc][3] = make_float2(t1[2], t1[3]);
+                    } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) rq[it][e] = make_float2(0.0f, 1.0f);
+                        for (int e = 0; e < 4; ++e) rq[ii][pc][e] = make_float2(0.0f, 1.0f);
+                    }
+                }
             }
         }
-    }
 
-    if (dma) {
-        if constexpr (ACT) {
-            if (a.kn_w)
-                for (int i = lane; i < HD; i += 64) s_kn[dwave][i] = a.kn_w[i];
-        }
+        if (ib == 0 && dma) {  // (first batch only)
+            if constexpr (ACT) {
+                if (a.kn_w)
+                    for (int i = lane; i < HD; i += 64) s_kn[dwave][i] = a.kn_w[i];
+            }
 #pragma unroll
-        for (int i = 0; i < NS - 1; ++i)
-            if (i < nsup) fill(i, i);
-    }
+            for (int i = 0; i < NS - 1; ++i)
+                if (i < nsup) fill(i, i);
+        }
 
-    uint16_t* qs = smem + (NS - 1) * SLOT;
 #pragma unroll
-    for (int it = 0; it < QIT; ++it) {
-        f32x4 x = xq[it];
-        if (qbias) x += bq4[it];  // add_bias (ops.rs:373-382)
-        if (QEPI && a.qn_w) {
-            // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
-            double ss = 0.0;
+        for (int ii = 0; ii < QB; ++ii) {
+            const int it = ib + ii;
+            f32x4 x[PPL];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float sq = x[e] * x[e];
-                ss += (double)sq;
+            for (int pc = 0; pc < PPL; ++pc) {
+                x[pc] = xq[ii][pc];
+                if (qbias) x[pc] += bq4[ii][pc];  // add_bias (ops.rs:373-382)
             }
+            if (QEPI && a.qn_w) {
+                // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
+                double ss = 0.0;
 #pragma unroll
-            for (int off = 1; off < LPR; off <<= 1) ss += __shfl_xor(ss, off);
-            const float sc = 1.0f / (float)sqrt(ss / (double)a.hd + (double)a.qn_eps);
+                for (int pc = 0; pc < PPL; ++pc)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (d0 + e < a.hd) x[e] = x[e] * sc * a.qn_w[d0 + e];
-        }
-        if (qrope) {
-            // rotate_rows (ops.rs:433-452): dim d < rot pairs with d +- rot/2,
-            // which this row's lane (d +- rot/2)/4 holds (rot is a multiple of 8)
-            const int src = d0 < a.rot ? (d0 < rhalf ? lane + rhalf / 4 : lane - rhalf / 4) : lane;
-            f32x4 xp;
+                    for (int e = 0; e < 4; ++e) {
+                        const float sq = x[pc][e] * x[pc][e];
+                        ss += (double)sq;
+                    }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xp[e] = __shfl(x[e], src);
-            if (d0 < a.rot) {
+                for (int off = 1; off < LPR; off <<= 1) ss += __shfl_xor(ss, off);
+                const float sc = 1.0f / (float)sqrt(ss / (double)a.hd + (double)a.qn_eps);
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    x[e] = d0 < rhalf ? rope_lo(x[e], xp[e], rq[it][e].x, rq[it][e].y)
-                                      : rope_hi(xp[e], x[e], rq[it][e].x, rq[it][e].y);
+                for (int pc = 0; pc < PPL; ++pc)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (d0 + pc * HW + e < a.hd) x[pc][e] = x[pc][e] * sc * a.qn_w[d0 + pc * HW + e];
+            }
+            if (qrope) {
+                // rotate_rows (ops.rs:433-452): dim d < rot pairs with d +- rot/2,
+                // held by piece (d +- rot/2) / HW of this row's lane
+                // ((d +- rot/2) % HW) / 4 (rot is a multiple of 8)
+                f32x4 xp[PPL];
+#pragma unroll
+                for (int pc = 0; pc < PPL; ++pc) {
+                    const int dp = d0 + pc * HW;
+                    const int dq = dp < rhalf ? dp + rhalf : dp - rhalf;
+                    const int src = dp < a.rot ? lane - lane % LPR + (dq % HW) / 4 : lane;
+                    const int pq = dp < a.rot ? dq / HW : pc;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float v = __shfl(x[0][e], src);
+                        if constexpr (PPL > 1) {
+                            const float v1 = __shfl(x[1][e], src);
+                            v = pq == 0 ? v : v1;
+                        }
+                        xp[pc][e] = v;
+                    }
+                }
+#pragma unroll
+                for (int pc = 0; pc < PPL; ++pc) {
+                    const int dp = d0 + pc * HW;
+                    if (dp < a.rot) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            x[pc][e] = dp < rhalf
+                                           ? rope_lo(x[pc][e], xp[pc][e], rq[ii][pc][e].x, rq[ii][pc][e].y)
+                                           : rope_hi(xp[pc][e], x[pc][e], rq[ii][pc][e].x, rq[ii][pc][e].y);
+                    }
+                }
+            }
+            const int lr = q_lrow(it);  // row within the workgroup
+            const int rl = lr & 31;     // row within its row block (the swizzle key)
+#pragma unroll
+            for (int pc = 0; pc < PPL; ++pc) {
+                const int dp = d0 + pc * HW;
+                bf16x4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = (__bf16)(x[pc][e] * a.c);
+                if (it < QIT && lr < QROWS)
+                    *reinterpret_cast<bf16x4*>(qs + lr * HD + (((dp >> 3) ^ swz<KCH>(rl)) << 3) +
+                                               (dp & 7)) = y;
             }
         }
-        bf16x4 y;
+    };
+    if constexpr (QB == QIT) {
+        q_batch(0);
+    } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (__bf16)(x[e] * a.c);
-        const int lr = q_lrow(it);  // row within the workgroup
-        const int rl = lr & 31;     // row within its row block (the swizzle key)
-        if (lr < QROWS)
-            *reinterpret_cast<bf16x4*>(qs + lr * HD + (((d0 >> 3) ^ swz<KCH>(rl)) << 3) +
-                                       (d0 & 7)) = y;
+        for (int ib = 0; ib < QIT; ib += QB) q_batch(ib);
     }
     __syncthreads();
     const uint16_t* qrow_l = qs + (rb * 32 + col) * HD;
@@ -962,253 +1023,453 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(cons
                 if (g16 == 0) sl[e * 32 + row32] = l_tot * sc;
             }
         }
-    } else if (NP == 0 || compute) {
-        bf16x8 qf[NC];
+    } else if (G::DS && compute) {
+        if constexpr (G::DS) {
+            // Head dim 512: the wave pair (rb, dh = 0 / 1) shares 32 query rows
+            // and splits the head dim.  Wave dh holds the Q fragments and the
+            // O^T rows of dims [256 dh, 256 dh + 256): it computes its half of
+            // every score, the two halves meet in LDS, and both waves add them
+            // (IEEE addition commutes, so both hold the same scores and take
+            // the same softmax steps) before each multiplies P into its half
+            // of V^T.  One key group, so every wave reads every tile.
+            static_assert(KQ == 1, "head-dim split: one key group");
+            constexpr int NCH = NC / 2;  // contraction steps of this wave's half
+            constexpr int NDH = ND / 2;  // 32-row blocks of this wave's half of O^T
+            const int dh = wave / (RB * KQ);
+            const int partner = (wave + RB * KQ) % NW;
+            float* xch = reinterpret_cast<float*>(smem + NS * G::STAGE);  // [NW][4][64] f32x4
+            bf16x8 qf[NCH];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
+            for (int c = 0; c < NCH; ++c) qf[c] = qfrag(dh * NCH + c);
 
-        // ---- main loop over super-tiles
-        f32x16 o[ND];
+            f32x16 o[NDH];
 #pragma unroll
-        for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-        float mu = 0.0f;          // running max m (log2 units), valid once m_set
-        bool m_set = false;
-        float thr = -INFINITY;    // a score above mu + thr moves m
-        float l_lo = 0.0f, l_hi = 0.0f;
-        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+            for (int db = 0; db < NDH; ++db) o[db] = f32x16{};
+            float mu = 0.0f;  // running max m (log2 units), valid once m_set
+            bool m_set = false;
+            float thr = -INFINITY;  // a score above mu + thr moves m
+            float l_lo = 0.0f, l_hi = 0.0f;
+            const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+            constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
 
-        // O^T += V^T P^T for one tile whose V^T fragments and P are in registers.
-        // Contraction slot 8*hf + j of MFMA hh is key 16*hf + 8*hh + j, in both
-        // operands.
-        auto pv = [&](const bf16x8 (&vf)[ND][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
+            for (int u = 0; u < nsup; ++u) {
+                const int st = u % NS;
+                wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
+                __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
+                const int un = u + NS - 1, stn = (u + NS - 1) % NS;
+                const bool pf = un < nsup;
+                const int t = t0 + u;
+                const uint16_t* ks = smem + st * SLOT;
+                const uint16_t* vs = ks + TILE;
+                const int kbase_t = t * BN;
+                int kp[16], kqs[16];
+                if constexpr (MODE == MASK_KEYS) {
 #pragma unroll
-            for (int db = 0; db < ND; ++db) {
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pf[0], o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pf[1], o[db], 0, 0, 0);
-            }
-        };
-
-        // One super-tile.  A compute wave software-pipelines its tiles: the PV
-        // product of its previous tile (V^T fragments vf and P pin, in registers)
-        // is issued in program order between the VALU instructions of this
-        // tile's softmax, so the matrix core and the VALU work at the same time
-        // (with one compute wave per SIMD nothing else would fill either).  This
-        // tile's P goes to pout, and its V^T fragments replace vf once those
-        // MFMAs have read them (one set of V^T registers, which leaves room for
-        // Q's); the first step multiplies zero fragments.  Without DMA waves (NP == 0)
-        // the DMA of super-tile u+NS-1 is issued in three parts spread over the
-        // compute, so that no wave stalls on a burst of memory instructions in
-        // front of its MFMAs.  Head dim 256 has no registers for a second set of
-        // V^T fragments (Q stays in registers there): its PV product is issued
-        // in the step of its tile, after the softmax (PIPE false).
-        constexpr bool PIPE = HD <= 128;
-        constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
-        auto step = [&](int u, bf16x8 (&vf)[ND][2], const bf16x8 (&pin)[2], bf16x8 (&pout)[2])
-            __attribute__((always_inline)) {
-            const int st = u % NS;
-            if (dma) {
-                // a fused-step super-tile may issue no DMA (staged) or extra
-                // cache stores, so the per-super-tile vmcnt accounting does not
-                // hold: wait for everything
-                if constexpr (ACT)
-                    wait_vmcnt<0>();
-                else
-                    wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
-            }
-            __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
-            const int un = u + NS - 1, stn = (u + NS - 1) % NS;
-            const bool pf = NP == 0 && un < nsup;
-
-            if (t0 + u * KQ + kq >= t1) {  // this key group has no tile in the last super-tile
-                if (pf) issue(un, stn);
-                if constexpr (PIPE) pv(vf, pin);
-                pout[0] = pout[1] = bf16x8{};  // vf holds finite values: nothing is added
-                return;
-            }
-            const int t = tile_at(u);
-            const uint16_t* ks = smem + (kq * NS + st) * SLOT;
-            const uint16_t* vs = ks + TILE;
-            const int kbase_t = t * BN;
-
-            // per-key metadata (arbitrary key positions / ids): loaded per tile
-            int kp[16], kqs[16];
-            if constexpr (MODE == MASK_KEYS) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kidx = min(kbase_t + 16 * hf + i, S.nk - 1);
-                    kp[i] = S.kpos ? S.kpos[kidx] : kidx;
-                    kqs[i] = S.kseq ? S.kseq[kidx] : 0;
+                    for (int i = 0; i < 16; ++i) {
+                        const int kidx = min(kbase_t + 16 * hf + i, S.nk - 1);
+                        kp[i] = S.kpos ? S.kpos[kidx] : kidx;
+                        kqs[i] = S.kseq ? S.kseq[kidx] : 0;
+                    }
                 }
-            }
-            if (pf) issue_range(un, stn, 0, J1, 0);
-            __builtin_amdgcn_sched_barrier(0);
+                if (pf) issue_range(un, stn, 0, J1, 0);
+                __builtin_amdgcn_sched_barrier(0);
 
-            // S^T = K Q^T - m: -m enters as the accumulator init, so the scores
-            // come out relative to m.  The K fragments are requested in two
-            // halves, the second while the MFMAs of the first run.
-            f32x16 s;
+                // this half of S^T = K Q^T; wave 0 of the pair starts from -m
+                f32x16 s;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = -mu;
-            {
-                constexpr int NH = NC / 2;
-                const uint16_t* krow = ks + col * HD;
-                const int sw = swz<KCH>(col);
+                for (int i = 0; i < 16; ++i) s[i] = dh == 0 ? -mu : 0.0f;
+                {
+                    constexpr int NH = NCH / 2;
+                    const uint16_t* krow = ks + col * HD;
+                    const int sw = swz<KCH>(col);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    bf16x8 kf[NH];
+                    for (int h = 0; h < 2; ++h) {
+                        bf16x8 kf[NH];
 #pragma unroll
-                    for (int c = 0; c < NH; ++c)
-                        kf[c] = *reinterpret_cast<const bf16x8*>(
-                            krow + (((2 * (h * NH + c) + hf) ^ sw) << 3));
-                    __builtin_amdgcn_sched_barrier(0);
+                        for (int c = 0; c < NH; ++c)
+                            kf[c] = *reinterpret_cast<const bf16x8*>(
+                                krow + (((2 * (dh * NCH + h * NH + c) + hf) ^ sw) << 3));
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int c = 0; c < NH; ++c)
-                        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[h * NH + c], s, 0, 0, 0);
+                        for (int c = 0; c < NH; ++c)
+                            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[h * NH + c], s, 0, 0, 0);
+                    }
                 }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-
-            // this tile's V^T fragments
-            auto read_v = [&]() __attribute__((always_inline)) {
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    f32x4* mine = reinterpret_cast<f32x4*>(xch) + wave * 256;
 #pragma unroll
-                for (int db = 0; db < ND; ++db) {
-                    const int d = db * 32 + col;
+                    for (int j = 0; j < 4; ++j)
+                        mine[j * 64 + lane] = f32x4{s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]};
+                }
+                // this half of V^T, read while the partner finishes its scores
+                bf16x8 vf[NDH][2];
+#pragma unroll
+                for (int db = 0; db < NDH; ++db) {
+                    const int d = (dh * NDH + db) * 32 + col;
                     const uint16_t* vrow = vs + d * BN;
                     const int sw = swz<VCH>(d);
                     vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
                     vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
                 }
-            };
-            if constexpr (!PIPE) read_v();
-            if (pf) issue_range(un, stn, J1, J2, 0);
-
-            // Masking: s[i] is the score of key t*BN + 16*hf + i.
-            bool full = kbase_t + BN <= S.nk;
-            if constexpr (MODE == MASK_POS) {
-                const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
-                                                     kbase_t + BN - 1 - qmin < a.window);
-                full = full && tiles_can_be_full && win_ok;
-            } else if constexpr (MODE == MASK_KEYS) {
-                full = false;
-            }
-            if (!full) {
+                if (pf) issue_range(un, stn, J1, J2, 0);
+                __syncthreads();  // both halves of every score are in LDS
+                {
+                    const f32x4* theirs = reinterpret_cast<const f32x4*>(xch) + partner * 256;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kidx = kbase_t + 16 * hf + i;
-                    bool vis = kidx < S.nk;
-                    if constexpr (MODE == MASK_POS) {
-                        vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
-                    } else if constexpr (MODE == MASK_KEYS) {
-                        vis = vis & visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
+                    for (int j = 0; j < 4; ++j) {
+                        const f32x4 x = theirs[j * 64 + lane];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) s[4 * j + e] += x[e];
                     }
-                    s[i] = vis ? s[i] : -INFINITY;
+                }
+
+                // Masking: s[i] is the score of key t*BN + 16*hf + i.
+                bool full = kbase_t + BN <= S.nk;
+                if constexpr (MODE == MASK_POS) {
+                    const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
+                                                         kbase_t + BN - 1 - qmin < a.window);
+                    full = full && tiles_can_be_full && win_ok;
+                } else if constexpr (MODE == MASK_KEYS) {
+                    full = false;
+                }
+                if (!full) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int kidx = kbase_t + 16 * hf + i;
+                        bool vis = kidx < S.nk;
+                        if constexpr (MODE == MASK_POS) {
+                            vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                        } else if constexpr (MODE == MASK_KEYS) {
+                            vis = vis & visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
+                        }
+                        s[i] = vis ? s[i] : -INFINITY;
+                    }
+                }
+
+                // Online softmax with a lazily moved max, as in the 32-row step.
+                float mx = max3(s[0], s[1], s[2]);
+#pragma unroll
+                for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
+                mx = __builtin_fmaxf(mx, s[15]);
+                const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+                if (moved) {
+                    const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+                    const bool upd = cm > thr;
+                    const float delta = upd ? cm : 0.0f;
+                    const float alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+                    mu += delta;
+                    m_set = m_set | upd;
+                    thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[i] -= delta;
+                    l_lo *= alpha;
+                    l_hi *= alpha;
+#pragma unroll
+                    for (int db = 0; db < NDH; ++db) o[db] *= alpha;
+                }
+                bf16x8 pw[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    u32x4 w4;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float p0 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j]);
+                        const float p1 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j + 1]);
+                        const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
+                        w4[j] = __builtin_bit_cast(uint32_t, pr);
+                        if (hh == 0)
+                            l_lo = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_lo, false);
+                        else
+                            l_hi = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_hi, false);
+                    }
+                    pw[hh] = __builtin_bit_cast(bf16x8, w4);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (pf) issue_range(un, stn, J2, NLDW, 0);
+#pragma unroll
+                for (int db = 0; db < NDH; ++db) {
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pw[0], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pw[1], o[db], 0, 0, 0);
                 }
             }
 
-            // Online softmax with a lazily moved max (scores are relative to mu).
-            float mx = max3(s[0], s[1], s[2]);
+            // ---- merge: the pair's two halves form one entry's row
+            const float l_run = l_lo + l_hi;
+            const float l_tot = l_run + __shfl_xor(l_run, 32);
+            const float m_fin = m_set ? mu : -INFINITY;
+            const int ent = kq * RB + rb;
+            __syncthreads();  // every wave is done with the tile stages and the exchange
+            if (hf == 0 && dh == 0) sm[ent * 32 + col] = m_fin;
+            __syncthreads();
+            {
+                float M = -INFINITY;
 #pragma unroll
-            for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
-            mx = __builtin_fmaxf(mx, s[15]);
-            // The column max over both lane halves decides, so lane and lane^32
-            // move m together.  O is rescaled after the previous tile's PV
-            // product (whose P is relative to the old m) has gone into it, and
-            // before this tile's.
-            const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
-            float alpha = 1.0f;
-            if (moved) {
-                const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-                const bool upd = cm > thr;
-                const float delta = upd ? cm : 0.0f;
-                alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
-                mu += delta;
-                m_set = m_set | upd;
-                thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+                for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + col]);
+                const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
+                // o[db][4j + e] is O^T[d = 256 dh + db*32 + 8j + 4hf + e][col]
+                float* myrow = mrows + (ent * 32 + col) * ROWF + dh * (HD / 2);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) s[i] -= delta;
-                l_lo *= alpha;
-                l_hi *= alpha;
-            }
-
-            // p = exp2(s) rounded to bf16 in pairs; l sums the rounded values
-            // (what the PV product multiplies), so the weights normalise exactly.
-            // The previous tile's PV MFMAs are interleaved with this VALU work.
+                for (int db = 0; db < NDH; ++db)
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                u32x4 w4;
+                    for (int j = 0; j < 4; ++j) {
+                        f32x4 val;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p0 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j]);
-                    const float p1 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j + 1]);
-                    const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
-                    w4[j] = __builtin_bit_cast(uint32_t, pr);
-                    if (hh == 0)
-                        l_lo = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_lo, false);
-                    else
-                        l_hi = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_hi, false);
-                }
-                pout[hh] = __builtin_bit_cast(bf16x8, w4);
-            }
-            if constexpr (PIPE) {
-                pv(vf, pin);
-#pragma unroll
-                for (int i = 0; i < 2 * ND; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (moved) {
-#pragma unroll
-                for (int db = 0; db < ND; ++db) o[db] *= alpha;
-            }
-            if constexpr (PIPE) read_v();
-            if (pf) issue_range(un, stn, J2, NLDW, 0);
-            if constexpr (!PIPE) pv(vf, pout);
-        };
-
-        {
-            bf16x8 vf[ND][2], pfa[2], pfb[2];
-#pragma unroll
-            for (int db = 0; db < ND; ++db) vf[db][0] = vf[db][1] = bf16x8{};
-            pfa[0] = pfa[1] = bf16x8{};
-            int u = 0;
-            for (; u + 1 < nsup; u += 2) {
-                step(u, vf, pfa, pfb);
-                step(u + 1, vf, pfb, pfa);
-            }
-            if (u < nsup) {
-                step(u, vf, pfa, pfb);
-                if (PIPE) pv(vf, pfb);
-            } else if (PIPE) {
-                pv(vf, pfa);
+                        for (int e = 0; e < 4; ++e) val[e] = o[db][4 * j + e] * sc;
+                        *reinterpret_cast<f32x4*>(myrow + db * 32 + 8 * j + 4 * hf) = val;
+                    }
+                if (hf == 0 && dh == 0) sl[ent * 32 + col] = l_tot * sc;
             }
         }
+    } else if (NP == 0 || compute) {
+        if constexpr (!G::DS) {
+            bf16x8 qf[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
 
-        // ---- merge the KQ key groups of each row block through LDS
-        const float l_run = l_lo + l_hi;
-        const float l_tot = l_run + __shfl_xor(l_run, 32);
-        const float m_fin = m_set ? mu : -INFINITY;
-        __syncthreads();  // every wave is done with the tile stages
-        if (hf == 0) sm[wave * 32 + col] = m_fin;
-        __syncthreads();
-        {
-            float M = -INFINITY;
+            // ---- main loop over super-tiles
+            f32x16 o[ND];
 #pragma unroll
-            for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + col]);
-            const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
-            // o[db][4j + e] is O^T[d = db*32 + 8j + 4hf + e][col]
-            float* myrow = mrows + (wave * 32 + col) * ROWF;
+            for (int db = 0; db < ND; ++db) o[db] = f32x16{};
+            float mu = 0.0f;          // running max m (log2 units), valid once m_set
+            bool m_set = false;
+            float thr = -INFINITY;    // a score above mu + thr moves m
+            float l_lo = 0.0f, l_hi = 0.0f;
+            const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+            // O^T += V^T P^T for one tile whose V^T fragments and P are in registers.
+            // Contraction slot 8*hf + j of MFMA hh is key 16*hf + 8*hh + j, in both
+            // operands.
+            auto pv = [&](const bf16x8 (&vf)[ND][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int db = 0; db < ND; ++db)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f32x4 val;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) val[e] = o[db][4 * j + e] * sc;
-                    *reinterpret_cast<f32x4*>(myrow + db * 32 + 8 * j + 4 * hf) = val;
+                for (int db = 0; db < ND; ++db) {
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pf[0], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pf[1], o[db], 0, 0, 0);
                 }
-            if (hf == 0) sl[wave * 32 + col] = l_tot * sc;
+            };
+
+            // One super-tile.  A compute wave software-pipelines its tiles: the PV
+            // product of its previous tile (V^T fragments vf and P pin, in registers)
+            // is issued in program order between the VALU instructions of this
+            // tile's softmax, so the matrix core and the VALU work at the same time
+            // (with one compute wave per SIMD nothing else would fill either).  This
+            // tile's P goes to pout, and its V^T fragments replace vf once those
+            // MFMAs have read them (one set of V^T registers, which leaves room for
+            // Q's); the first step multiplies zero fragments.  Without DMA waves (NP == 0)
+            // the DMA of super-tile u+NS-1 is issued in three parts spread over the
+            // compute, so that no wave stalls on a burst of memory instructions in
+            // front of its MFMAs.  Head dim 256 has no registers for a second set of
+            // V^T fragments (Q stays in registers there): its PV product is issued
+            // in the step of its tile, after the softmax (PIPE false).
+            constexpr bool PIPE = HD <= 128;
+            constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
+            auto step = [&](int u, bf16x8 (&vf)[ND][2], const bf16x8 (&pin)[2], bf16x8 (&pout)[2])
+                __attribute__((always_inline)) {
+                const int st = u % NS;
+                if (dma) {
+                    // a fused-step super-tile may issue no DMA (staged) or extra
+                    // cache stores, so the per-super-tile vmcnt accounting does not
+                    // hold: wait for everything
+                    if constexpr (ACT)
+                        wait_vmcnt<0>();
+                    else
+                        wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
+                }
+                __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
+                const int un = u + NS - 1, stn = (u + NS - 1) % NS;
+                const bool pf = NP == 0 && un < nsup;
+
+                if (t0 + u * KQ + kq >= t1) {  // this key group has no tile in the last super-tile
+                    if (pf) issue(un, stn);
+                    if constexpr (PIPE) pv(vf, pin);
+                    pout[0] = pout[1] = bf16x8{};  // vf holds finite values: nothing is added
+                    return;
+                }
+                const int t = tile_at(u);
+                const uint16_t* ks = smem + (kq * NS + st) * SLOT;
+                const uint16_t* vs = ks + TILE;
+                const int kbase_t = t * BN;
+
+                // per-key metadata (arbitrary key positions / ids): loaded per tile
+                int kp[16], kqs[16];
+                if constexpr (MODE == MASK_KEYS) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int kidx = min(kbase_t + 16 * hf + i, S.nk - 1);
+                        kp[i] = S.kpos ? S.kpos[kidx] : kidx;
+                        kqs[i] = S.kseq ? S.kseq[kidx] : 0;
+                    }
+                }
+                if (pf) issue_range(un, stn, 0, J1, 0);
+                __builtin_amdgcn_sched_barrier(0);
+
+                // S^T = K Q^T - m: -m enters as the accumulator init, so the scores
+                // come out relative to m.  The K fragments are requested in two
+                // halves, the second while the MFMAs of the first run.
+                f32x16 s;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] = -mu;
+                {
+                    constexpr int NH = NC / 2;
+                    const uint16_t* krow = ks + col * HD;
+                    const int sw = swz<KCH>(col);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        bf16x8 kf[NH];
+#pragma unroll
+                        for (int c = 0; c < NH; ++c)
+                            kf[c] = *reinterpret_cast<const bf16x8*>(
+                                krow + (((2 * (h * NH + c) + hf) ^ sw) << 3));
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int c = 0; c < NH; ++c)
+                            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[h * NH + c], s, 0, 0, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+
+                // this tile's V^T fragments
+                auto read_v = [&]() __attribute__((always_inline)) {
+#pragma unroll
+                    for (int db = 0; db < ND; ++db) {
+                        const int d = db * 32 + col;
+                        const uint16_t* vrow = vs + d * BN;
+                        const int sw = swz<VCH>(d);
+                        vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
+                        vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
+                    }
+                };
+                if constexpr (!PIPE) read_v();
+                if (pf) issue_range(un, stn, J1, J2, 0);
+
+                // Masking: s[i] is the score of key t*BN + 16*hf + i.
+                bool full = kbase_t + BN <= S.nk;
+                if constexpr (MODE == MASK_POS) {
+                    const bool win_ok = a.window < 0 || (qmax - kbase_t < a.window &&
+                                                         kbase_t + BN - 1 - qmin < a.window);
+                    full = full && tiles_can_be_full && win_ok;
+                } else if constexpr (MODE == MASK_KEYS) {
+                    full = false;
+                }
+                if (!full) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int kidx = kbase_t + 16 * hf + i;
+                        bool vis = kidx < S.nk;
+                        if constexpr (MODE == MASK_POS) {
+                            vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                        } else if constexpr (MODE == MASK_KEYS) {
+                            vis = vis & visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
+                        }
+                        s[i] = vis ? s[i] : -INFINITY;
+                    }
+                }
+
+                // Online softmax with a lazily moved max (scores are relative to mu).
+                float mx = max3(s[0], s[1], s[2]);
+#pragma unroll
+                for (int i = 3; i < 15; i += 2) mx = max3(mx, s[i], s[i + 1]);
+                mx = __builtin_fmaxf(mx, s[15]);
+                // The column max over both lane halves decides, so lane and lane^32
+                // move m together.  O is rescaled after the previous tile's PV
+                // product (whose P is relative to the old m) has gone into it, and
+                // before this tile's.
+                const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+                float alpha = 1.0f;
+                if (moved) {
+                    const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+                    const bool upd = cm > thr;
+                    const float delta = upd ? cm : 0.0f;
+                    alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+                    mu += delta;
+                    m_set = m_set | upd;
+                    thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[i] -= delta;
+                    l_lo *= alpha;
+                    l_hi *= alpha;
+                }
+
+                // p = exp2(s) rounded to bf16 in pairs; l sums the rounded values
+                // (what the PV product multiplies), so the weights normalise exactly.
+                // The previous tile's PV MFMAs are interleaved with this VALU work.
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    u32x4 w4;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float p0 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j]);
+                        const float p1 = __builtin_amdgcn_exp2f(s[8 * hh + 2 * j + 1]);
+                        const bf16x2 pr = {(__bf16)p0, (__bf16)p1};
+                        w4[j] = __builtin_bit_cast(uint32_t, pr);
+                        if (hh == 0)
+                            l_lo = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_lo, false);
+                        else
+                            l_hi = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_hi, false);
+                    }
+                    pout[hh] = __builtin_bit_cast(bf16x8, w4);
+                }
+                if constexpr (PIPE) {
+                    pv(vf, pin);
+#pragma unroll
+                    for (int i = 0; i < 2 * ND; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (moved) {
+#pragma unroll
+                    for (int db = 0; db < ND; ++db) o[db] *= alpha;
+                }
+                if constexpr (PIPE) read_v();
+                if (pf) issue_range(un, stn, J2, NLDW, 0);
+                if constexpr (!PIPE) pv(vf, pout);
+            };
+
+            {
+                bf16x8 vf[ND][2], pfa[2], pfb[2];
+#pragma unroll
+                for (int db = 0; db < ND; ++db) vf[db][0] = vf[db][1] = bf16x8{};
+                pfa[0] = pfa[1] = bf16x8{};
+                int u = 0;
+                for (; u + 1 < nsup; u += 2) {
+                    step(u, vf, pfa, pfb);
+                    step(u + 1, vf, pfb, pfa);
+                }
+                if (u < nsup) {
+                    step(u, vf, pfa, pfb);
+                    if (PIPE) pv(vf, pfb);
+                } else if (PIPE) {
+                    pv(vf, pfa);
+                }
+            }
+
+            // ---- merge the KQ key groups of each row block through LDS
+            const float l_run = l_lo + l_hi;
+            const float l_tot = l_run + __shfl_xor(l_run, 32);
+            const float m_fin = m_set ? mu : -INFINITY;
+            __syncthreads();  // every wave is done with the tile stages
+            if (hf == 0) sm[wave * 32 + col] = m_fin;
+            __syncthreads();
+            {
+                float M = -INFINITY;
+#pragma unroll
+                for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + col]);
+                const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
+                // o[db][4j + e] is O^T[d = db*32 + 8j + 4hf + e][col]
+                float* myrow = mrows + (wave * 32 + col) * ROWF;
+#pragma unroll
+                for (int db = 0; db < ND; ++db)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        f32x4 val;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) val[e] = o[db][4 * j + e] * sc;
+                        *reinterpret_cast<f32x4*>(myrow + db * 32 + 8 * j + 4 * hf) = val;
+                    }
+                if (hf == 0) sl[wave * 32 + col] = l_tot * sc;
+            }
         }
     } else if constexpr (ACT) {
         // A DMA fill is waited for before the next barrier; a staged one is
@@ -1459,6 +1720,7 @@ constexpr Shape SHAPES[] = {
     {128, 1, 4, 2, 4, false}, {128, 2, 2, 4, 4, false}, {128, 2, 4, 2, 0, false},
     {128, 1, 4, 2, 4, true},
     {256, 2, 2, 2, 0, false}, {256, 1, 2, 2, 0, false},  // one wave per SIMD: 512 VGPRs
+    {512, 2, 1, 2, 0, false},  // head-dim split: a wave pair per row block, one wave per SIMD
 };
 
 const Shape* find_shape(int hd_tile, int rb, int kq, bool w16) {
@@ -1482,6 +1744,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
         case 12824: return launch_modes<128, 2, 4, 2, 0>(p, a, st);
         case 25622: return launch_modes<256, 2, 2, 2, 0>(p, a, st);
         case 25612: return launch_modes<256, 1, 2, 2, 0>(p, a, st);
+        case 51221: return launch_modes<512, 2, 1, 2, 0>(p, a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1492,7 +1755,7 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
                           int mask, bool qepi, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows) {
     LaunchPlan p{};
-    p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : 256);
+    p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
     p.block_n = BN;
     p.mask = mask;
     p.qepi = qepi && mask != MASK_KEYS;
@@ -1502,9 +1765,10 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     // Head dims up to 128: one row block of four key groups with four DMA
     // waves (two waves per SIMD).  256: two row blocks of two key groups,
     // one wave per SIMD (the accumulators need the whole register file).
+    // 512: two row blocks, each a wave pair that splits the head dim.
     int rb = 1;
-    int kq = p.hd_tile == 256 ? 2 : 4;
-    if (p.hd_tile == 256 && row_blocks >= 2) rb = 2;
+    int kq = p.hd_tile == 256 ? 2 : (p.hd_tile == 512 ? 1 : 4);
+    if ((p.hd_tile == 256 && row_blocks >= 2) || p.hd_tile == 512) rb = 2;
     // Head dim 128 without a mask: two 16-row compute waves per key group
     // (two compute waves per SIMD; 1-3 % faster on C2-C4, whose loop is bound
     // by the K/V stream).  The masked builds of that shape spill, so masked
@@ -1516,15 +1780,15 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     if (force_rows == 32) w16 = false;
     const Shape* sh = find_shape(p.hd_tile, rb, kq, w16);
     if (!sh) {
-        rb = p.hd_tile == 256 && row_blocks >= 2 ? 2 : 1;
-        kq = p.hd_tile == 256 ? 2 : 4;
+        rb = (p.hd_tile == 256 && row_blocks >= 2) || p.hd_tile == 512 ? 2 : 1;
+        kq = p.hd_tile == 256 ? 2 : (p.hd_tile == 512 ? 1 : 4);
         w16 = false;
         sh = find_shape(p.hd_tile, rb, kq, w16);
     }
     p.rb = rb;
     p.kq = kq;
     p.w16 = w16;
-    p.waves = rb * kq * (w16 ? 2 : 1) + sh->np;
+    p.waves = rb * kq * ((w16 || p.hd_tile == 512) ? 2 : 1) + sh->np;
     p.stages = sh->ns;
     p.rowgroups = (row_blocks + rb - 1) / rb;
     if (p.rowgroups < 1) p.rowgroups = 1;
@@ -1581,7 +1845,9 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     switch (p.hd_tile) {
         case 64: hipLaunchKernelGGL(split_merge_kernel<64>, grid, dim3(256), 0, st, a); break;
         case 128: hipLaunchKernelGGL(split_merge_kernel<128>, grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL(split_merge_kernel<256>, grid, dim3(256), 0, st, a); break;
+        case 256: hipLaunchKernelGGL(split_merge_kernel<256>, grid, dim3(256), 0, st, a); break;
+        case 512: hipLaunchKernelGGL(split_merge_kernel<512>, grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

@@ -79,7 +79,7 @@ void release(DevBuf& b) {
     b.cap = 0;
 }
 
-int hd_tile_for(size_t hd) { return hd <= 64 ? 64 : (hd <= 128 ? 128 : 256); }
+int hd_tile_for(size_t hd) { return hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512)); }
 
 size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
@@ -334,8 +334,8 @@ int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n
         if (n_head_kv[l] < 1 || n_head_kv[l] > 4096)
             return fail(DR_ERR_INVALID, "layer %zu: n_head_kv %zu invalid", l, n_head_kv[l]);
         if (head_dim[l] < 1) return fail(DR_ERR_INVALID, "layer %zu: head_dim is 0", l);
-        if (head_dim[l] > 256)
-            return fail(DR_ERR_UNSUPPORTED, "layer %zu: head_dim %zu > 256 not built", l,
+        if (head_dim[l] > 512)
+            return fail(DR_ERR_UNSUPPORTED, "layer %zu: head_dim %zu > 512 not built", l,
                         head_dim[l]);
     }
     DR_CHECK(use_device(ctx));
@@ -872,7 +872,7 @@ int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const
     if (nq == 0 || h == 0 || hd == 0) return DR_OK;  // no (head, query) task writes anything
     if (hkv == 0 || h % hkv != 0)
         return fail(DR_ERR_INVALID, "n_head %zu is not a multiple of n_head_kv %zu", h, hkv);
-    if (hd > 256) return fail(DR_ERR_UNSUPPORTED, "head_dim %zu > 256 not built", hd);
+    if (hd > 512) return fail(DR_ERR_UNSUPPORTED, "head_dim %zu > 512 not built", hd);
     if (!out || !q) return fail(DR_ERR_INVALID, "out/q is NULL");
     if (q_len < nq * h * hd) return fail(DR_ERR_INVALID, "q.len() %zu < %zu", q_len, nq * h * hd);
     if (nk > 0) {

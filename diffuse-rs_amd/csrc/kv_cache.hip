@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
 
 hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
     if (args.n <= 0) return hipSuccess;
-    if (hd_tile != 64 && hd_tile != 128 && hd_tile != 256) return hipErrorInvalidValue;
+    if (hd_tile != 64 && hd_tile != 128 && hd_tile != 256 && hd_tile != 512) return hipErrorInvalidValue;
     StoreArgs a = args;
     // Batch slot b of nb: the attention launch puts the slot's kv heads on
     // XCDs [8b/nb, 8(b+1)/nb).
@@ -314,7 +314,8 @@ hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
     switch (hd_tile) {
         case 64: hipLaunchKernelGGL(kv_store_kernel<64>, grid, dim3(256), 0, st, a); break;
         case 128: hipLaunchKernelGGL(kv_store_kernel<128>, grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(256), 0, st, a); break;
+        case 256: hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(kv_store_kernel<512>, grid, dim3(256), 0, st, a); break;
     }
     return hipGetLastError();
 }
@@ -328,6 +329,7 @@ hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st) {
         case 64: hipLaunchKernelGGL(kv_gather_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, st, a); break;
         case 128: hipLaunchKernelGGL(kv_gather_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, st, a); break;
         case 256: hipLaunchKernelGGL(kv_gather_kernel<256>, dim3((unsigned)blocks), dim3(256), 0, st, a); break;
+        case 512: hipLaunchKernelGGL(kv_gather_kernel<512>, dim3((unsigned)blocks), dim3(256), 0, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

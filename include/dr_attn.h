@@ -32,7 +32,7 @@ typedef enum {
     DR_ERR_NO_DEVICE = 2,   /* no HIP device visible */
     DR_ERR_OOM = 3,         /* device allocation failed */
     DR_ERR_HIP = 4,         /* a HIP runtime call failed */
-    DR_ERR_UNSUPPORTED = 5  /* valid for the reference, not built here (e.g. head_dim > 256) */
+    DR_ERR_UNSUPPORTED = 5  /* valid for the reference, not built here (e.g. head_dim > 512) */
 } dr_status;
 
 /* Option<usize>: present == 0 means None. */

@@ -69,8 +69,8 @@ def test_invalid_shapes_rejected(lib):
     # per-row prefix shorter than nq (the reference's qr.prefix[i] panics)
     rc, _ = _call(S(2, 3, 2, 2, 8), qprefix=[1])
     assert rc == dr.DR_ERR_INVALID
-    # head_dim > 256 is valid for the reference but not built here
-    rc, _ = _call(S(1, 1, 1, 1, 512))
+    # head_dim > 512 is valid for the reference but not built here
+    rc, _ = _call(S(1, 1, 1, 1, 516))
     assert rc == dr.DR_ERR_UNSUPPORTED
 
 

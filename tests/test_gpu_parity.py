@@ -554,7 +554,7 @@ def test_cache_gather_is_bf16_of_store(dev):
 
 
 @pytest.mark.parametrize("hd,n,n_tot", [(64, 70, 200), (96, 129, 150), (128, 64, 64),
-                                        (256, 33, 90)])
+                                        (256, 33, 90), (512, 70, 100), (320, 17, 40)])
 def test_cache_store_k_norm_is_bf16_of_oracle(dev, hd, n, n_tot):
     """norm_heads(k, k_norm) + cache.store (forward.rs:300-302, 318-320): the
     gathered K equals bf16 of the oracle's rms_norm_inplace (ops.rs:106-114)
