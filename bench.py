@@ -89,13 +89,15 @@ def attention_only_ms(torch, stream, call, n_calls: int, reps: int):
 
 
 def other_configs(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
-    """Attention-only TFLOP/s of the other BASELINE.json configs (synthetic
-    N(0,1) inputs, same graph-burst timing as the roofline)."""
+    """Attention-only TFLOP/s of the other BASELINE.json configs and of a
+    real DiffusionGemma global layer at head dim 512 (synthetic N(0,1)
+    inputs, same graph-burst timing as the roofline)."""
     res = {}
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
-    for name in ("C3", "C4", "C5S", "C5G"):
-        cfg = CONFIGS[name]
+    from helpers import EXTRA_CONFIGS
+    for name in ("C3", "C4", "C5S", "C5G", "G512"):
+        cfg = CONFIGS[name] if name in CONFIGS else EXTRA_CONFIGS[name]
         h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
         n_t, n_c = cfg.n_total, cfg.n_canvas
         with torch.cuda.stream(stream):

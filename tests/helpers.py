@@ -227,6 +227,13 @@ CONFIGS = {
     "C5G": Config("gemma_global_4096c+256q", 16, 8, 256, 4096, 256),
 }
 
+# Shapes outside BASELINE.json's configs that the path also serves.
+# G512: a real DiffusionGemma global layer (docs/diffusiongemma.md:11-12): 16
+# query heads over 2 KV heads at head dim 512, full attention, C5's context.
+EXTRA_CONFIGS = {
+    "G512": Config("diffusiongemma_global_hd512_4096c+256q", 16, 2, 512, 4096, 256),
+}
+
 
 def config_seed(cfg_id: int, step: int = 0) -> int:
     return 0xD1FF0000 + cfg_id + 1000 * step
