@@ -191,6 +191,50 @@ def qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
     return res
 
 
+def split_active_timing(torch, dr, ctx, stream, reps: int = 200) -> dict:
+    """StepCache::split_active (cache.rs:85-114) per call, host wall time:
+    on the device from device tokens (the two counts come back by one small
+    copy), against the host split of host tokens plus the upload of the
+    active list into a pass (what a step needs before its launches)."""
+    import time
+    res = {}
+    for n in (768, 4352):
+        rng = torch.Generator()
+        rng.manual_seed(n)
+        seq = torch.randint(5, 30000, (n,), generator=rng, dtype=torch.int32)
+        seq[n // 3:] = 4
+        prev = seq.clone()
+        prev[n // 3::7] = 9  # a seventh of the canvas changed since the last step
+        mask = (seq == 4).to(torch.uint8)
+        cache = dr.StepCache(ctx, n, [1], [64])
+        with torch.cuda.stream(stream):
+            d_seq, d_mask, d_prev = seq.cuda(), mask.cuda(), prev.cuda()
+        pa, pc = dr.Pass(ctx, []), dr.Pass(ctx, [])
+        cache.update_seq_dev(d_prev)
+        stream.synchronize()
+        for _ in range(10):
+            cache.split_active_dev(d_seq, d_mask, n, 5, pa, pc)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            na, _ = cache.split_active_dev(d_seq, d_mask, n, 5, pa, pc)
+        dev_us = (time.perf_counter() - t0) / reps * 1e6
+        cache.update_seq(prev.numpy())
+        seq_h, mask_h = seq.numpy(), mask.numpy()
+        ph = dr.Pass(ctx, [])
+        for _ in range(10):
+            act, _ = cache.split_active(seq_h, mask_h, 5)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            act, _ = cache.split_active(seq_h, mask_h, 5)
+            ph.set(act)
+        host_us = (time.perf_counter() - t0) / reps * 1e6
+        res[str(n)] = {"n_active": na, "device_us": round(dev_us, 1),
+                       "host_split_and_upload_us": round(host_us, 1)}
+        del cache
+    log(f"split_active: {res}")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -346,10 +390,11 @@ def main() -> int:
     # ---- CPU baseline: the C restatement of the reference's attention on this
     # host's cores, on the first step's inputs; its output also checks the
     # GPU result of that step (the measured configuration).
-    others = epi = None
+    others = epi = split = None
     if not args.no_others:
         others = other_configs(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
         epi = qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
+        split = split_active_timing(torch, dr, ctx, stream)
 
     cpu, parity = None, None
     if not args.no_cpu:
@@ -407,6 +452,7 @@ def main() -> int:
         "launch": launch, "parity": parity, "roofline": roofline, "cpu_baseline": cpu,
         "other_configs_attention_only": others,
         "qkv_epilogue": epi,
+        "split_active": split,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -117,7 +117,13 @@ struct dr_rope {
 
 struct dr_step_cache {
     struct Slot {
+        // split_active's state (cache.rs:31-34).  It lives on the host, or,
+        // once a device-side call has used it, in d_prev / d_lc until a host
+        // call takes it back (dev_state says which copy is current).
         std::vector<int32_t> prev_seq, last_changed;
+        int32_t* d_prev = nullptr;
+        int32_t* d_lc = nullptr;
+        bool dev_state = false;
         bool initialized = false;
         size_t vicinity = 0;
     };
@@ -126,12 +132,29 @@ struct dr_step_cache {
     std::vector<int> hkv, hd, hd_tile;
     std::vector<uint16_t*> k, vt;  // [layer * n_batch + batch]
     std::vector<Slot> slot;
+    int32_t* d_meta = nullptr;     // [6] device-side split results
+    int32_t* h_meta = nullptr;     // [6] pinned host copy
 };
 
 namespace {
 
 int use_device(const dr_ctx* ctx) {
     DR_HIP(hipSetDevice(ctx->device));
+    return DR_OK;
+}
+
+// Capacity for n positions in a pass's device array (contents not kept).
+int reserve_pass(dr_pass* p, size_t n) {
+    if (n <= p->cap) return DR_OK;
+    DR_CHECK(use_device(p->ctx));
+    if (p->d_pos) {
+        hipError_t e = hipFree(p->d_pos);
+        p->d_pos = nullptr;
+        p->cap = 0;
+        if (e != hipSuccess) return hip_fail(e, "hipFree");
+    }
+    DR_HIP(hipMalloc(&p->d_pos, n * sizeof(int32_t)));
+    p->cap = n;
     return DR_OK;
 }
 
@@ -148,16 +171,7 @@ int upload_pass(dr_pass* p, const size_t* active, size_t n) {
         mx = std::max(mx, active[i]);
     }
     DR_CHECK(use_device(p->ctx));
-    if (n > p->cap) {
-        if (p->d_pos) {
-            hipError_t e = hipFree(p->d_pos);
-            p->d_pos = nullptr;
-            p->cap = 0;
-            if (e != hipSuccess) return hip_fail(e, "hipFree");
-        }
-        DR_HIP(hipMalloc(&p->d_pos, n * sizeof(int32_t)));
-        p->cap = n;
-    }
+    DR_CHECK(reserve_pass(p, n));
     if (n > 0) {
         DR_HIP(hipMemcpyAsync(p->d_pos, h.data(), n * sizeof(int32_t), hipMemcpyHostToDevice,
                               p->ctx->stream));
@@ -309,6 +323,20 @@ int dr_pass_set(dr_pass* pass, const size_t* active, size_t n_active) {
 
 size_t dr_pass_len(const dr_pass* pass) { return pass ? pass->n : 0; }
 
+int dr_pass_positions(const dr_pass* pass, size_t* out, size_t cap) {
+    if (!pass) return fail(DR_ERR_INVALID, "dr_pass_positions: pass is NULL");
+    if (cap < pass->n) return fail(DR_ERR_INVALID, "dr_pass_positions: cap %zu < %zu", cap, pass->n);
+    if (pass->n == 0) return DR_OK;
+    if (!out) return fail(DR_ERR_INVALID, "dr_pass_positions: out is NULL");
+    DR_CHECK(use_device(pass->ctx));
+    std::vector<int32_t> h(pass->n);
+    DR_HIP(hipMemcpyAsync(h.data(), pass->d_pos, pass->n * sizeof(int32_t), hipMemcpyDeviceToHost,
+                          pass->ctx->stream));
+    DR_HIP(hipStreamSynchronize(pass->ctx->stream));
+    for (size_t i = 0; i < pass->n; ++i) out[i] = (size_t)h[i];
+    return DR_OK;
+}
+
 void dr_pass_destroy(dr_pass* pass) {
     if (!pass) return;
     if (pass->d_pos) {
@@ -380,6 +408,12 @@ void dr_cache_destroy(dr_step_cache* cache) {
         if (p) (void)hipFree(p);
     for (uint16_t* p : cache->vt)
         if (p) (void)hipFree(p);
+    for (auto& s : cache->slot) {
+        if (s.d_prev) (void)hipFree(s.d_prev);
+        if (s.d_lc) (void)hipFree(s.d_lc);
+    }
+    if (cache->d_meta) (void)hipFree(cache->d_meta);
+    if (cache->h_meta) (void)hipHostFree(cache->h_meta);
     delete cache;
 }
 
@@ -570,6 +604,112 @@ int dr_cache_gather(dr_step_cache* cache, size_t layer, size_t batch, const size
     return DR_OK;
 }
 
+namespace {
+
+// Makes the device copy of a slot's split state current.
+int state_to_device(dr_step_cache* c, dr_step_cache::Slot& s) {
+    if (s.dev_state) return DR_OK;
+    DR_CHECK(use_device(c->ctx));
+    const size_t bytes = std::max(c->n_total, (size_t)1) * sizeof(int32_t);
+    if (!s.d_prev) DR_HIP(hipMalloc(&s.d_prev, bytes));
+    if (!s.d_lc) DR_HIP(hipMalloc(&s.d_lc, bytes));
+    if (c->n_total > 0) {
+        DR_HIP(hipMemcpyAsync(s.d_prev, s.prev_seq.data(), c->n_total * sizeof(int32_t),
+                              hipMemcpyHostToDevice, c->ctx->stream));
+        DR_HIP(hipMemcpyAsync(s.d_lc, s.last_changed.data(), c->n_total * sizeof(int32_t),
+                              hipMemcpyHostToDevice, c->ctx->stream));
+        DR_HIP(hipStreamSynchronize(c->ctx->stream));
+    }
+    s.dev_state = true;
+    return DR_OK;
+}
+
+// Makes the host copy of a slot's split state current.
+int state_to_host(dr_step_cache* c, dr_step_cache::Slot& s) {
+    if (!s.dev_state) return DR_OK;
+    DR_CHECK(use_device(c->ctx));
+    if (c->n_total > 0) {
+        DR_HIP(hipMemcpyAsync(s.prev_seq.data(), s.d_prev, c->n_total * sizeof(int32_t),
+                              hipMemcpyDeviceToHost, c->ctx->stream));
+        DR_HIP(hipMemcpyAsync(s.last_changed.data(), s.d_lc, c->n_total * sizeof(int32_t),
+                              hipMemcpyDeviceToHost, c->ctx->stream));
+        DR_HIP(hipStreamSynchronize(c->ctx->stream));
+    }
+    s.dev_state = false;
+    return DR_OK;
+}
+
+}  // namespace
+
+int dr_cache_update_seq_dev(dr_step_cache* cache, size_t batch, const int32_t* seq, size_t n) {
+    if (!cache) return fail(DR_ERR_INVALID, "dr_cache_update_seq_dev: cache is NULL");
+    if (batch >= cache->n_batch)
+        return fail(DR_ERR_INVALID, "dr_cache_update_seq_dev: batch %zu >= %zu", batch, cache->n_batch);
+    if (n != cache->n_total)
+        return fail(DR_ERR_INVALID, "dr_cache_update_seq_dev: length %zu != n_total %zu", n, cache->n_total);
+    if (n > 0 && !seq) return fail(DR_ERR_INVALID, "dr_cache_update_seq_dev: seq is NULL");
+    auto& s = cache->slot[batch];
+    DR_CHECK(state_to_device(cache, s));
+    if (n > 0)
+        DR_HIP(hipMemcpyAsync(s.d_prev, seq, n * sizeof(int32_t), hipMemcpyDeviceToDevice,
+                              cache->ctx->stream));
+    s.initialized = true;
+    return DR_OK;
+}
+
+int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t* seq,
+                              const uint8_t* is_masked, size_t n, size_t step, dr_pass* active,
+                              dr_pass* cached, size_t* n_active, size_t* n_cached) {
+    if (!cache) return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: cache is NULL");
+    if (batch >= cache->n_batch)
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: batch %zu >= %zu", batch, cache->n_batch);
+    if (n > cache->n_total)
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: length %zu > n_total %zu", n, cache->n_total);
+    if (n > 0 && (!seq || !is_masked))
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: seq / is_masked is NULL");
+    if (!active || !cached || active == cached)
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: need two distinct passes");
+    if (active->ctx != cache->ctx || cached->ctx != cache->ctx)
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: pass from another context");
+    if (!n_active || !n_cached) return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: NULL count");
+    if (step > (size_t)std::numeric_limits<int32_t>::max() - 8)
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: step too large");
+    auto& s = cache->slot[batch];
+    if (s.vicinity > (size_t)std::numeric_limits<int32_t>::max())
+        return fail(DR_ERR_INVALID, "dr_cache_split_active_dev: vicinity too large");
+    DR_CHECK(state_to_device(cache, s));
+    DR_CHECK(reserve_pass(active, std::max(n, (size_t)1)));
+    DR_CHECK(reserve_pass(cached, std::max(n, (size_t)1)));
+    if (!cache->d_meta) DR_HIP(hipMalloc(&cache->d_meta, 6 * sizeof(int32_t)));
+    if (!cache->h_meta) DR_HIP(hipHostMalloc(&cache->h_meta, 6 * sizeof(int32_t)));
+    dr::SplitArgs a{};
+    a.seq = seq;
+    a.is_masked = is_masked;
+    a.prev_seq = s.d_prev;
+    a.last_changed = s.d_lc;
+    a.active = active->d_pos;
+    a.cached = cached->d_pos;
+    a.meta = cache->d_meta;
+    a.n = (int)n;
+    a.step = (int)step;
+    a.vicinity = (int)s.vicinity;
+    hipStream_t st = cache->ctx->stream;
+    hipError_t e = dr::launch_split_active(a, st);
+    if (e != hipSuccess) return hip_fail(e, "split_active launch");
+    DR_HIP(hipMemcpyAsync(cache->h_meta, cache->d_meta, 6 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    DR_HIP(hipStreamSynchronize(st));
+    const int32_t* m = cache->h_meta;
+    active->n = (size_t)m[0];
+    active->min_pos = m[0] > 0 ? (size_t)m[2] : 0;
+    active->max_pos = m[0] > 0 ? (size_t)m[3] : 0;
+    cached->n = (size_t)m[1];
+    cached->min_pos = m[1] > 0 ? (size_t)m[4] : 0;
+    cached->max_pos = m[1] > 0 ? (size_t)m[5] : 0;
+    *n_active = active->n;
+    *n_cached = cached->n;
+    return DR_OK;
+}
+
 int dr_cache_update_seq(dr_step_cache* cache, size_t batch, const int32_t* seq, size_t n) {
     if (!cache) return fail(DR_ERR_INVALID, "dr_cache_update_seq: cache is NULL");
     if (batch >= cache->n_batch) return fail(DR_ERR_INVALID, "dr_cache_update_seq: batch %zu >= %zu", batch, cache->n_batch);
@@ -577,6 +717,7 @@ int dr_cache_update_seq(dr_step_cache* cache, size_t batch, const int32_t* seq, 
         return fail(DR_ERR_INVALID, "dr_cache_update_seq: length %zu != n_total %zu", n, cache->n_total);
     if (n > 0 && !seq) return fail(DR_ERR_INVALID, "dr_cache_update_seq: seq is NULL");
     auto& s = cache->slot[batch];
+    DR_CHECK(state_to_host(cache, s));
     std::copy(seq, seq + n, s.prev_seq.begin());
     s.initialized = true;
     return DR_OK;
@@ -629,6 +770,7 @@ int dr_cache_split_active(dr_step_cache* cache, size_t batch, const int32_t* seq
     if (n > cache->n_total)
         return fail(DR_ERR_INVALID, "dr_cache_split_active: length %zu > n_total %zu", n, cache->n_total);
     auto& s = cache->slot[batch];
+    DR_CHECK(state_to_host(cache, s));
     return dr_split_active(s.prev_seq.data(), s.last_changed.data(), seq, is_masked, n, step,
                            s.vicinity, active, n_active, cached, n_cached);
 }

@@ -137,6 +137,20 @@ struct EpiArgs {
     int vec;              // q, k, v 16-byte aligned and hd a multiple of 4: vector loads
 };
 
+// StepCache::split_active (cache.rs:85-114) of one batch slot on the device.
+struct SplitArgs {
+    const int* seq;        // [n] this step's tokens
+    const uint8_t* is_masked;  // [n]
+    const int* prev_seq;   // [n] the tokens of the last update_seq
+    int* last_changed;     // [n] step of each position's last change (-1: never); updated
+    int* active;           // [n] out: active positions, ascending
+    int* cached;           // [n] out: cached positions, ascending
+    int* meta;             // [6] out: n_active, n_cached, first/last active, first/last cached
+    int n;
+    int step;
+    int vicinity;
+};
+
 // Masking mode of an attention launch.
 enum MaskMode : int {
     MASK_NONE = 0,  // every key visible (only the key tail is masked)
@@ -179,5 +193,6 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
 hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);
+hipError_t launch_split_active(const SplitArgs& a, hipStream_t st);
 
 }  // namespace dr

@@ -135,6 +135,7 @@ _SIGS = {
     "dr_pass_create": (_I, [_VP, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
     "dr_pass_len": (_SZ, [_VP]),
+    "dr_pass_positions": (_I, [_VP, c_size_p, _SZ]),
     "dr_pass_destroy": (None, [_VP]),
     "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_cache_destroy": (None, [_VP]),
@@ -144,6 +145,8 @@ _SIGS = {
     "dr_cache_split_active": (_I, [_VP, _SZ, _VP, _VP, _SZ, _SZ, c_size_p, c_size_p, c_size_p, c_size_p]),
     "dr_split_active": (_I, [_VP, _VP, _VP, _VP, _SZ, _SZ, _SZ, c_size_p, c_size_p, c_size_p, c_size_p]),
     "dr_cache_set_vicinity": (_I, [_VP, _SZ, _SZ]),
+    "dr_cache_update_seq_dev": (_I, [_VP, _SZ, _VP, _SZ]),
+    "dr_cache_split_active_dev": (_I, [_VP, _SZ, _VP, _VP, _SZ, _SZ, _VP, _VP, c_size_p, c_size_p]),
     "dr_cache_initialized": (_I, [_VP, _SZ]),
     "dr_attention_cached": (_I, [_VP, _SZ, ctypes.POINTER(CBatchItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F]),
     "dr_attention_step": (_I, [_VP, _SZ, ctypes.POINTER(CStepItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F, _VP, _F]),
@@ -352,6 +355,12 @@ class Pass:
     def __len__(self) -> int:
         return self.ctx.lib.dr_pass_len(self.h)
 
+    def positions(self) -> list:
+        n = len(self)
+        out = np.zeros(max(n, 1), dtype=np.uintp)
+        _check(self.ctx.lib.dr_pass_positions(self.h, out.ctypes.data_as(c_size_p), out.size))
+        return [int(x) for x in out[:n]]
+
     def close(self) -> None:
         if self.h:
             self.ctx.lib.dr_pass_destroy(self.h)
@@ -451,6 +460,21 @@ class StepCache:
             act.ctypes.data_as(c_size_p), ctypes.byref(na), cac.ctypes.data_as(c_size_p),
             ctypes.byref(nc)))
         return [int(x) for x in act[: na.value]], [int(x) for x in cac[: nc.value]]
+
+    def update_seq_dev(self, seq, batch: int = 0) -> None:
+        """update_seq from a device int32 tensor of n_total tokens."""
+        _check(self.ctx.lib.dr_cache_update_seq_dev(self.h, batch, _ptr(seq), self.n_total))
+
+    def split_active_dev(self, seq, is_masked, n: int, step: int, active: Pass, cached: Pass,
+                         batch: int = 0) -> tuple:
+        """split_active on the device (cache.rs:85-114): seq (int32) and
+        is_masked (uint8) are device tensors of n entries; the active and cached
+        positions land in the two passes.  Returns (n_active, n_cached)."""
+        na, nc = ctypes.c_size_t(), ctypes.c_size_t()
+        _check(self.ctx.lib.dr_cache_split_active_dev(
+            self.h, batch, _ptr(seq), _ptr(is_masked), n, step, active.h, cached.h,
+            ctypes.byref(na), ctypes.byref(nc)))
+        return na.value, nc.value
 
     def set_vicinity(self, vicinity: int, batch: int = 0) -> None:
         _check(self.ctx.lib.dr_cache_set_vicinity(self.h, batch, vicinity))

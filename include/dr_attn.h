@@ -122,6 +122,10 @@ int dr_pass_create(dr_ctx* ctx, const size_t* active, size_t n_active, dr_pass**
 /* Replace the positions (e.g. for the next denoise step); synchronous upload. */
 int dr_pass_set(dr_pass* pass, const size_t* active, size_t n_active);
 size_t dr_pass_len(const dr_pass* pass);
+/* Copy the pass's positions (ascending) into out (host, room for cap
+ * entries, cap >= dr_pass_len); waits for the context's stream.  Reads back
+ * what dr_cache_split_active_dev wrote (ActiveSplit's lists, cache.rs:7-10). */
+int dr_pass_positions(const dr_pass* pass, size_t* out, size_t cap);
 void dr_pass_destroy(dr_pass* pass);
 
 /*
@@ -166,6 +170,22 @@ int dr_cache_split_active(dr_step_cache* cache, size_t batch, const int32_t* seq
 int dr_split_active(const int32_t* prev_seq, int32_t* last_changed, const int32_t* seq,
                     const uint8_t* is_masked, size_t n, size_t step, size_t vicinity,
                     size_t* active, size_t* n_active, size_t* cached, size_t* n_cached);
+/* StepCache::update_seq (cache.rs:56-59) from a device array seq [n_total]
+ * (int32), ordered on the context's stream. */
+int dr_cache_update_seq_dev(dr_step_cache* cache, size_t batch, const int32_t* seq, size_t n);
+/* StepCache::split_active (cache.rs:85-114) computed on the device from
+ * device arrays seq [n] (int32) and is_masked [n] (uint8): the active
+ * positions are written into pass `active` and the cached ones into pass
+ * `cached` (their device position arrays, ascending), ready for
+ * dr_attention_cached / dr_cache_store / dr_attention_step, with no host
+ * loop and no upload of index lists.  The two counts come back through one
+ * small device-to-host copy (the launches that follow are sized by them).
+ * The slot's split state (cache.rs:29-31) moves to the device on first use
+ * and back on the next host-side dr_cache_split_active / dr_cache_update_seq,
+ * so the two kinds of call may be mixed on one slot. */
+int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t* seq,
+                              const uint8_t* is_masked, size_t n, size_t step, dr_pass* active,
+                              dr_pass* cached, size_t* n_active, size_t* n_cached);
 /* StepCache.vicinity (cache.rs:37-41). */
 int dr_cache_set_vicinity(dr_step_cache* cache, size_t batch, size_t vicinity);
 /* StepCache.initialized (cache.rs:33). */
