@@ -916,12 +916,21 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
     if (max_nq == 0) return DR_OK;
     DR_CHECK(use_device(cache->ctx));
     const int mask = mask_of(sliding_window, causal_prefix);
-    // the fused kernel is built for 32-row waves only
     dr_ctx* ctx = cache->ctx;
-    const int rows_saved = ctx->force_rows;
-    if (ctx->fused_step && rows_saved == 0) ctx->force_rows = 32;
     dr::LaunchPlan p = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, q_norm_w != nullptr);
-    ctx->force_rows = rows_saved;
+    // The fused kernel is built for one row block of 32-row waves and four
+    // key groups with their DMA waves; when asked for, plan that shape too
+    // (p stays the plan of the unfused store + attention).
+    dr::LaunchPlan pf = p;
+    if (ctx->fused_step && !dr::plan_supports_act(p) && ctx->force_rb == 0 && ctx->force_kq == 0) {
+        const int rows_saved = ctx->force_rows;
+        ctx->force_rb = 1;
+        ctx->force_kq = 4;
+        if (rows_saved == 0) ctx->force_rows = 32;
+        pf = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, q_norm_w != nullptr);
+        ctx->force_rb = ctx->force_kq = 0;
+        ctx->force_rows = rows_saved;
+    }
     // One kernel when every pass is the block [n_total - n, n_total) starting
     // on a 32-key tile, its K/V rows take 32-bit byte offsets (with the last
     // tile's padding rows), rows are whole tiles of the head dim, the shape
@@ -929,7 +938,7 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
     // workgroup's key range (each active tile is stored by one workgroup of
     // its kv head, which must visit it).
     bool fused = cache->ctx->fused_step && a.hd == cache->hd_tile[layer] &&
-                 dr::plan_supports_act(p) && !sliding_window.present;
+                 dr::plan_supports_act(pf) && !sliding_window.present;
     for (size_t b = 0; b < n_items && fused; ++b) {
         const dr_pass* ps = items[b].pass;
         fused = ps->n > 0 && ps->max_pos + 1 == cache->n_total && ps->max_pos + 1 - ps->min_pos == ps->n &&
@@ -942,6 +951,7 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
                                     k_norm_w, k_norm_eps));
         return launch_plan(cache->ctx, a, p);
     }
+    p = pf;
     p.act = true;
     a.kv_rstride = a.n_head_kv * a.hd;
     a.kn_w = k_norm_w;
