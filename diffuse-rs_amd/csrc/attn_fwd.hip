@@ -240,7 +240,7 @@ struct Geometry {
     static_assert(NLDW * (NS - 1) < 64, "vmcnt range");
     static_assert(QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-    static_assert(!W16 || (NP > 0 && HD <= 128), "16-row waves: DMA waves, head dim up to 128");
+    static_assert(!W16 || HD <= 256, "16-row waves: head dim up to 256");
     static_assert(!DS || (HD == 512 && !W16 && NP == 0), "head-dim split: head dim 512, no DMA waves");
 };
 
@@ -853,15 +853,28 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
             // One super-tile, software-pipelined like the 32-row step: the
             // previous tile's PV product is interleaved with this tile's
             // softmax, and this tile's V^T fragments replace vf afterwards.
+            // Without DMA waves (NP == 0, head dim 256) the compute waves wait
+            // for and issue the K/V DMA themselves, in three parts spread over
+            // the step as the 32-row step does.
+            constexpr int J1 = NLDW / 4, J2 = NLDW / 2;
+            // Head dim 256 has no registers for V^T fragments held across a
+            // step: its PV product runs in the tile's own step, the fragments
+            // read in two halves (PIPE16 false).
+            constexpr bool PIPE16 = HD <= 128;
             auto step = [&](int u, bf16x8 (&vf)[ND16], const bf16x8& pin, bf16x8& pout)
                 __attribute__((always_inline)) {
                 const int st = u % NS;
+                if constexpr (NP == 0) wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
                 __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
+                const int un = u + NS - 1, stn = (u + NS - 1) % NS;
+                const bool pf = NP == 0 && un < nsup;
                 if (t0 + u * KQ + kq >= t1) {  // this key group has no tile in the last super-tile
-                    pv(vf, pin);
+                    if (pf) issue(un, stn);
+                    if constexpr (PIPE16) pv(vf, pin);
                     pout = bf16x8{};
                     return;
                 }
+                if (pf) issue_range(un, stn, 0, J1, 0);
                 const int t = t0 + u * KQ + kq;
                 const uint16_t* ks = smem + (kq * NS + st) * SLOT;
                 const uint16_t* vs = ks + TILE;
@@ -884,23 +897,31 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s0[i] = s1[i] = -mu;
                 {
+                    // (head dim 256: the K fragments in two halves, the second
+                    // read while the MFMAs of the first run)
+                    constexpr int NKH = HD > 128 ? 2 : 1, NCH = NC16 / NKH;
                     const uint16_t* kr0 = ks + n16 * HD;
                     const uint16_t* kr1 = ks + (16 + n16) * HD;
                     const int sw0 = swz<KCH>(n16), sw1 = swz<KCH>(16 + n16);
-                    bf16x8 kf0[NC16], kf1[NC16];
 #pragma unroll
-                    for (int c = 0; c < NC16; ++c) {
-                        kf0[c] = *reinterpret_cast<const bf16x8*>(kr0 + (((4 * c + g16) ^ sw0) << 3));
-                        kf1[c] = *reinterpret_cast<const bf16x8*>(kr1 + (((4 * c + g16) ^ sw1) << 3));
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+                    for (int h = 0; h < NKH; ++h) {
+                        bf16x8 kf0[NCH], kf1[NCH];
 #pragma unroll
-                    for (int c = 0; c < NC16; ++c) {
-                        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf0[c], qf[c], s0, 0, 0, 0);
-                        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf1[c], qf[c], s1, 0, 0, 0);
+                        for (int c = 0; c < NCH; ++c) {
+                            const int cc = h * NCH + c;
+                            kf0[c] = *reinterpret_cast<const bf16x8*>(kr0 + (((4 * cc + g16) ^ sw0) << 3));
+                            kf1[c] = *reinterpret_cast<const bf16x8*>(kr1 + (((4 * cc + g16) ^ sw1) << 3));
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int c = 0; c < NCH; ++c) {
+                            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf0[c], qf[h * NCH + c], s0, 0, 0, 0);
+                            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf1[c], qf[h * NCH + c], s1, 0, 0, 0);
+                        }
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                if (pf) issue_range(un, stn, J1, J2, 0);
 
                 bool full = kbase_t + BN <= S.nk;
                 if constexpr (MODE == MASK_POS) {
@@ -965,22 +986,41 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
                     l_acc = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_acc, false);
                 }
                 pout = __builtin_bit_cast(bf16x8, w4);
-                pv(vf, pin);
+                if constexpr (PIPE16) {
+                    pv(vf, pin);
 #pragma unroll
-                for (int i = 0; i < ND16; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);  // two VALU / transcendental
+                    for (int i = 0; i < ND16; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);  // two VALU / transcendental
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if (moved) {
 #pragma unroll
                     for (int db = 0; db < ND16; ++db) o[db] *= alpha;
                 }
+                if (pf) issue_range(un, stn, J2, NLDW, 0);
                 // this tile's V^T fragments: rows 16*db + n16, keys 8*g16 ..
-#pragma unroll
-                for (int db = 0; db < ND16; ++db) {
+                auto vfrag = [&](int db) __attribute__((always_inline)) {
                     const int d = 16 * db + n16;
-                    vf[db] = *reinterpret_cast<const bf16x8*>(vs + d * BN + ((g16 ^ swz<VCH>(d)) << 3));
+                    return *reinterpret_cast<const bf16x8*>(vs + d * BN + ((g16 ^ swz<VCH>(d)) << 3));
+                };
+                if constexpr (PIPE16) {
+#pragma unroll
+                    for (int db = 0; db < ND16; ++db) vf[db] = vfrag(db);
+                } else {
+                    constexpr int NVH = ND16 / 2;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        bf16x8 vh[NVH];
+#pragma unroll
+                        for (int i = 0; i < NVH; ++i) vh[i] = vfrag(h * NVH + i);
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int i = 0; i < NVH; ++i)
+                            o[h * NVH + i] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh[i], pout, o[h * NVH + i], 0, 0, 0);
+                    }
                 }
             };
 
@@ -996,8 +1036,8 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
                 }
                 if (u < nsup) {
                     step(u, vf, pa, pb);
-                    pv(vf, pb);
-                } else {
+                    if constexpr (PIPE16) pv(vf, pb);
+                } else if constexpr (PIPE16) {
                     pv(vf, pa);
                 }
             }
@@ -1222,7 +1262,9 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
             }
         }
     } else if (NP == 0 || compute) {
-        if constexpr (!G::DS) {
+        // (16-row and head-dim-split builds never reach this branch: every
+        // compute wave took one of the two above)
+        if constexpr (!G::DS && !W16) {
             bf16x8 qf[NC];
 #pragma unroll
             for (int c = 0; c < NC; ++c) qf[c] = qfrag(c);
@@ -1718,7 +1760,7 @@ struct Shape {
 constexpr Shape SHAPES[] = {
     {64, 1, 4, 3, 4, false}, {64, 2, 2, 4, 4, false}, {64, 2, 4, 3, 0, false},
     {128, 1, 4, 2, 4, false}, {128, 2, 2, 4, 4, false}, {128, 2, 4, 2, 0, false},
-    {128, 1, 4, 2, 4, true},
+    {128, 1, 4, 2, 4, true}, {256, 2, 2, 2, 0, true},
     {256, 2, 2, 2, 0, false}, {256, 1, 2, 2, 0, false},  // one wave per SIMD: 512 VGPRs
     {512, 2, 1, 2, 0, false},  // head-dim split: a wave pair per row block, one wave per SIMD
 };
@@ -1732,6 +1774,7 @@ const Shape* find_shape(int hd_tile, int rb, int kq, bool w16) {
 hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     if (p.w16) {
         if (p.hd_tile == 128 && p.rb == 1 && p.kq == 4) return launch_modes16<128, 1, 4, 2, 4>(p, a, st);
+        if (p.hd_tile == 256 && p.rb == 2 && p.kq == 2) return launch_modes16<256, 2, 2, 2, 0>(p, a, st);
         return hipErrorInvalidValue;
     }
     const int key = p.hd_tile * 100 + p.rb * 10 + p.kq;
@@ -1773,7 +1816,11 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     // (two compute waves per SIMD; 1-3 % faster on C2-C4, whose loop is bound
     // by the K/V stream).  The masked builds of that shape spill, so masked
     // launches keep 32-row waves unless asked.
-    bool w16 = p.hd_tile == 128 && mask == MASK_NONE;
+    // Head dim 256 (two row blocks, two key groups): 16-row waves under every
+    // mask (200-222 VGPRs, so two compute waves per SIMD, which issue their
+    // own DMA): C5's sliding and global layers take 29.0 and 36.3 us against
+    // 33.7 and 41.4 with one 32-row wave per SIMD.
+    bool w16 = (p.hd_tile == 128 && mask == MASK_NONE) || (p.hd_tile == 256 && rb == 2 && kq == 2);
     // Head dims up to 128 with more one-row-block workgroups than CUs (C3's
     // 448 on 256): two row blocks of 32-row waves and four key groups, with
     // the compute waves issuing the DMA (RB 2, KQ 4, NP 0).  That fills the
