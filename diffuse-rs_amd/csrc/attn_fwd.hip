@@ -211,7 +211,7 @@ struct Geometry {
     // two halves of every score are summed through LDS.
     static constexpr bool DS = HD > 256;
     static constexpr int NE = RB * KQ;         // (row block, key group) pairs: merge entries
-    static constexpr int NW = NE * ((W16 || DS) ? 2 : 1);  // compute waves per workgroup
+    static constexpr int NW = NE * (W16 ? 2 : 1) * (DS ? 2 : 1);  // compute waves per workgroup
     static constexpr int NWT = NW + NP;        // all waves (NP: DMA-only producer waves)
     static constexpr int NT = NWT * 64;
     static constexpr int NDMA = NP > 0 ? NP : NW;  // waves that issue the K/V DMA
@@ -227,7 +227,7 @@ struct Geometry {
                                                           // and super-tile
     static constexpr int QROWS = RB * 32;      // query rows per workgroup
     // DS: each compute wave's partial scores (32 x 32 f32), after the stages
-    static constexpr size_t XCH_BYTES = DS ? (size_t)NW * 64 * 16 * 4 : 0;
+    static constexpr size_t XCH_BYTES = DS ? (size_t)NW * 64 * (W16 ? 8 : 16) * 4 : 0;
     static constexpr size_t STAGE_BYTES = (size_t)NS * STAGE * 2 + XCH_BYTES;
     // Q fragments are held in registers for the whole kernel; Q is staged
     // once, through the first slot of the last pipeline stage.
@@ -240,14 +240,15 @@ struct Geometry {
     static_assert(NLDW * (NS - 1) < 64, "vmcnt range");
     static_assert(QROWS * HD <= SLOT, "Q staging must fit in one tile slot");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-    static_assert(!W16 || HD <= 256, "16-row waves: head dim up to 256");
-    static_assert(!DS || (HD == 512 && !W16 && NP == 0), "head-dim split: head dim 512, no DMA waves");
+    static_assert(!W16 || HD <= 256 || DS, "16-row waves: head dim up to 256, or split");
+    static_assert(!DS || (HD == 512 && NP == 0 && KQ == 1),
+                  "head-dim split: head dim 512, one key group, no DMA waves");
 };
 
 template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool ACT, bool W16>
 __attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD,
                                    Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD))) __global__
-__launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
+__launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     using G = Geometry<HD, RB, KQ, NS, NP, W16>;
     static_assert(!(W16 && ACT), "the fused step runs 32-row waves");
     constexpr int NW = G::NW, NWT = G::NWT, NT = G::NT, NC = G::NC, ND = G::ND;
@@ -284,7 +285,7 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
     const int dwave = NP > 0 ? wave - NW : wave;  // index among the DMA waves
     const int rb = wave % RB, kq = (wave / RB) % KQ;
     // W16: the wave's half of the row block (rows rh*16 .. rh*16 + 15)
-    const int rh = W16 ? wave / (RB * KQ) : 0;
+    const int rh = W16 ? (wave / (RB * KQ)) % 2 : 0;
 
     // Workgroup -> (batch, kv head, row group, split).  The hardware deals
     // workgroups round-robin over the 8 XCDs; remapping keeps consecutive
@@ -822,21 +823,30 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
             // other.  Lane (g16, n16): query row n16, contraction / key group
             // g16.  Same transposed products as the 32-row waves: S^T = K Q^T
             // in two 16-key blocks, O^T += V^T P^T.
+            // Head dim 512 (WDS): the head dim is also split, as in the
+            // 32-row head-dim-split branch below: wave dh holds Q and O^T of
+            // dims [256 dh, 256 dh + 256), and the two halves of the scores
+            // meet in LDS after the QK^T product.
+            constexpr bool WDS = G::DS;
             constexpr int NC16 = HD / 32;  // contraction steps of 32 along d
             constexpr int ND16 = HD / 16;  // 16-row blocks of O^T
+            constexpr int NCW = WDS ? NC16 / 2 : NC16;  // this wave's contraction steps
+            constexpr int NDW = WDS ? ND16 / 2 : ND16;  // this wave's 16-row blocks of O^T
+            const int dh = WDS ? wave / (RB * KQ * 2) : 0;
+            const int c0 = dh * NCW, db0 = dh * NDW;
             const int n16 = lane & 15, g16 = lane >> 4;
             const int qr = rb * 32 + rh * 16 + n16;  // query row within the workgroup
-            bf16x8 qf[NC16];
+            bf16x8 qf[NCW];
             {
                 const uint16_t* qrow = qs + qr * HD;
                 const int sw = swz<KCH>(qr & 31);
 #pragma unroll
-                for (int c = 0; c < NC16; ++c)
-                    qf[c] = *reinterpret_cast<const bf16x8*>(qrow + (((4 * c + g16) ^ sw) << 3));
+                for (int c = 0; c < NCW; ++c)
+                    qf[c] = *reinterpret_cast<const bf16x8*>(qrow + (((4 * (c0 + c) + g16) ^ sw) << 3));
             }
-            f32x4 o[ND16];
+            f32x4 o[NDW];
 #pragma unroll
-            for (int db = 0; db < ND16; ++db) o[db] = f32x4{};
+            for (int db = 0; db < NDW; ++db) o[db] = f32x4{};
             float mu = 0.0f;  // running max m (log2 units), valid once m_set
             bool m_set = false;
             float thr = -INFINITY;  // a score above mu + thr moves m
@@ -845,9 +855,9 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
 
             // O^T += V^T P^T; contraction slot 8*g16 + j is key 8*g16 + j in
             // both operands.
-            auto pv = [&](const bf16x8 (&vf)[ND16], const bf16x8& pf) __attribute__((always_inline)) {
+            auto pv = [&](const bf16x8 (&vf)[NDW], const bf16x8& pf) __attribute__((always_inline)) {
 #pragma unroll
-                for (int db = 0; db < ND16; ++db)
+                for (int db = 0; db < NDW; ++db)
                     o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pf, o[db], 0, 0, 0);
             };
             // One super-tile, software-pipelined like the 32-row step: the
@@ -861,7 +871,7 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
             // step: its PV product runs in the tile's own step, the fragments
             // read in two halves (PIPE16 false).
             constexpr bool PIPE16 = HD <= 128;
-            auto step = [&](int u, bf16x8 (&vf)[ND16], const bf16x8& pin, bf16x8& pout)
+            auto step = [&](int u, bf16x8 (&vf)[NDW], const bf16x8& pin, bf16x8& pout)
                 __attribute__((always_inline)) {
                 const int st = u % NS;
                 if constexpr (NP == 0) wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
@@ -895,11 +905,11 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
                 // kappa of them), -m as the accumulator init.
                 f32x4 s0, s1;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s0[i] = s1[i] = -mu;
+                for (int i = 0; i < 4; ++i) s0[i] = s1[i] = (WDS && dh != 0) ? 0.0f : -mu;
                 {
                     // (head dim 256: the K fragments in two halves, the second
                     // read while the MFMAs of the first run)
-                    constexpr int NKH = HD > 128 ? 2 : 1, NCH = NC16 / NKH;
+                    constexpr int NKH = HD > 128 ? 2 : 1, NCH = NCW / NKH;
                     const uint16_t* kr0 = ks + n16 * HD;
                     const uint16_t* kr1 = ks + (16 + n16) * HD;
                     const int sw0 = swz<KCH>(n16), sw1 = swz<KCH>(16 + n16);
@@ -908,7 +918,7 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
                         bf16x8 kf0[NCH], kf1[NCH];
 #pragma unroll
                         for (int c = 0; c < NCH; ++c) {
-                            const int cc = h * NCH + c;
+                            const int cc = c0 + h * NCH + c;
                             kf0[c] = *reinterpret_cast<const bf16x8*>(kr0 + (((4 * cc + g16) ^ sw0) << 3));
                             kf1[c] = *reinterpret_cast<const bf16x8*>(kr1 + (((4 * cc + g16) ^ sw1) << 3));
                         }
@@ -922,6 +932,19 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if (pf) issue_range(un, stn, J1, J2, 0);
+                if constexpr (WDS) {
+                    // both halves of every score through LDS; the pair adds
+                    // them (IEEE addition commutes: both get the same sums)
+                    float* xch = reinterpret_cast<float*>(smem + NS * G::STAGE);
+                    f32x4* mine = reinterpret_cast<f32x4*>(xch) + wave * 128;
+                    mine[lane] = s0;
+                    mine[64 + lane] = s1;
+                    __syncthreads();
+                    const f32x4* theirs =
+                        reinterpret_cast<const f32x4*>(xch) + ((wave + RB * KQ * 2) % NW) * 128;
+                    s0 += theirs[lane];
+                    s1 += theirs[64 + lane];
+                }
 
                 bool full = kbase_t + BN <= S.nk;
                 if constexpr (MODE == MASK_POS) {
@@ -997,19 +1020,19 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
                 __builtin_amdgcn_sched_barrier(0);
                 if (moved) {
 #pragma unroll
-                    for (int db = 0; db < ND16; ++db) o[db] *= alpha;
+                    for (int db = 0; db < NDW; ++db) o[db] *= alpha;
                 }
                 if (pf) issue_range(un, stn, J2, NLDW, 0);
-                // this tile's V^T fragments: rows 16*db + n16, keys 8*g16 ..
+                // this tile's V^T fragments: rows 16*(db0 + db) + n16, keys 8*g16 ..
                 auto vfrag = [&](int db) __attribute__((always_inline)) {
-                    const int d = 16 * db + n16;
+                    const int d = 16 * (db0 + db) + n16;
                     return *reinterpret_cast<const bf16x8*>(vs + d * BN + ((g16 ^ swz<VCH>(d)) << 3));
                 };
                 if constexpr (PIPE16) {
 #pragma unroll
-                    for (int db = 0; db < ND16; ++db) vf[db] = vfrag(db);
+                    for (int db = 0; db < NDW; ++db) vf[db] = vfrag(db);
                 } else {
-                    constexpr int NVH = ND16 / 2;
+                    constexpr int NVH = NDW / 2;
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         bf16x8 vh[NVH];
@@ -1025,9 +1048,9 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
             };
 
             {
-                bf16x8 vf[ND16], pa, pb;
+                bf16x8 vf[NDW], pa, pb;
 #pragma unroll
-                for (int db = 0; db < ND16; ++db) vf[db] = bf16x8{};
+                for (int db = 0; db < NDW; ++db) vf[db] = bf16x8{};
                 pa = bf16x8{};
                 int u = 0;
                 for (; u + 1 < nsup; u += 2) {
@@ -1048,23 +1071,23 @@ __launch_bounds__((RB * KQ * ((W16 || HD > 256) ? 2 : 1) + NP) * 64) void attn_f
             const float m_fin = m_set ? mu : -INFINITY;
             const int e = kq * RB + rb, row32 = rh * 16 + n16;
             __syncthreads();  // every wave is done with the tile stages
-            if (g16 == 0) sm[e * 32 + row32] = m_fin;
+            if (g16 == 0 && dh == 0) sm[e * 32 + row32] = m_fin;
             __syncthreads();
             {
                 float M = -INFINITY;
 #pragma unroll
                 for (int k = 0; k < KQ; ++k) M = __builtin_fmaxf(M, sm[(k * RB + rb) * 32 + row32]);
                 const float sc = (m_fin == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_fin - M);
-                // o[db][i] is O^T[d = 16*db + 4*g16 + i][n16]
-                float* myrow = mrows + (e * 32 + row32) * ROWF;
+                // o[db][i] is O^T[d = 16*(db0 + db) + 4*g16 + i][n16]
+                float* myrow = mrows + (e * 32 + row32) * ROWF + 16 * db0;
 #pragma unroll
-                for (int db = 0; db < ND16; ++db)
+                for (int db = 0; db < NDW; ++db)
                     *reinterpret_cast<f32x4*>(myrow + 16 * db + 4 * g16) = o[db] * sc;
-                if (g16 == 0) sl[e * 32 + row32] = l_tot * sc;
+                if (g16 == 0 && dh == 0) sl[e * 32 + row32] = l_tot * sc;
             }
         }
     } else if (G::DS && compute) {
-        if constexpr (G::DS) {
+        if constexpr (G::DS && !W16) {
             // Head dim 512: the wave pair (rb, dh = 0 / 1) shares 32 query rows
             // and splits the head dim.  Wave dh holds the Q fragments and the
             // O^T rows of dims [256 dh, 256 dh + 256): it computes its half of
@@ -1763,6 +1786,7 @@ constexpr Shape SHAPES[] = {
     {128, 1, 4, 2, 4, true}, {256, 2, 2, 2, 0, true},
     {256, 2, 2, 2, 0, false}, {256, 1, 2, 2, 0, false},  // one wave per SIMD: 512 VGPRs
     {512, 2, 1, 2, 0, false},  // head-dim split: a wave pair per row block, one wave per SIMD
+    {512, 2, 1, 2, 0, true},   // ... and with 16-row waves: 8 compute waves, two per SIMD
 };
 
 const Shape* find_shape(int hd_tile, int rb, int kq, bool w16) {
@@ -1775,6 +1799,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
     if (p.w16) {
         if (p.hd_tile == 128 && p.rb == 1 && p.kq == 4) return launch_modes16<128, 1, 4, 2, 4>(p, a, st);
         if (p.hd_tile == 256 && p.rb == 2 && p.kq == 2) return launch_modes16<256, 2, 2, 2, 0>(p, a, st);
+        if (p.hd_tile == 512 && p.rb == 2 && p.kq == 1) return launch_modes16<512, 2, 1, 2, 0>(p, a, st);
         return hipErrorInvalidValue;
     }
     const int key = p.hd_tile * 100 + p.rb * 10 + p.kq;
@@ -1820,7 +1845,10 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     // mask (200-222 VGPRs, so two compute waves per SIMD, which issue their
     // own DMA): C5's sliding and global layers take 29.0 and 36.3 us against
     // 33.7 and 41.4 with one 32-row wave per SIMD.
-    bool w16 = (p.hd_tile == 128 && mask == MASK_NONE) || (p.hd_tile == 256 && rb == 2 && kq == 2);
+    // Head dim 512: 16-row waves that also split the head dim (8 compute
+    // waves, 204-232 VGPRs): the G512 global layer takes 74.3 us against 93.2.
+    bool w16 = (p.hd_tile == 128 && mask == MASK_NONE) || (p.hd_tile == 256 && rb == 2 && kq == 2) ||
+               p.hd_tile == 512;
     // Head dims up to 128 with more one-row-block workgroups than CUs (C3's
     // 448 on 256): two row blocks of 32-row waves and four key groups, with
     // the compute waves issuing the DMA (RB 2, KQ 4, NP 0).  That fills the
@@ -1845,7 +1873,7 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     p.rb = rb;
     p.kq = kq;
     p.w16 = w16;
-    p.waves = rb * kq * ((w16 || p.hd_tile == 512) ? 2 : 1) + sh->np;
+    p.waves = rb * kq * (w16 ? 2 : 1) * (p.hd_tile == 512 ? 2 : 1) + sh->np;
     p.stages = sh->ns;
     p.rowgroups = (row_blocks + rb - 1) / rb;
     if (p.rowgroups < 1) p.rowgroups = 1;

@@ -87,7 +87,7 @@ def test_hd512_global_layer_cached_vs_oracle(dev, n_split):
     finally:
         dev.ctx.set_split(0)
     say(f"  launch {info}")
-    assert info["head_dim_tile"] == 512 and info["waves_per_wg"] == 4
+    assert info["head_dim_tile"] == 512 and info["waves_per_wg"] == 8 and info["rows_per_wave"] == 16
     if n_split:
         assert info["n_split"] == n_split
     check(dev.get(out), want, f"global layer split {info['n_split']}")

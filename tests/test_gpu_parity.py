@@ -291,13 +291,14 @@ def test_gemma_scale_one_error(dev):
     assert np.isfinite(mx) and mx < 1.0
 
 
-@pytest.mark.parametrize("hd", [128, 256])
+@pytest.mark.parametrize("hd", [128, 256, 512])
 @pytest.mark.parametrize("window,prefix", [(None, None), (64, None), (None, 250), (37, 180)])
 def test_wave_rows_16_and_32_vs_oracle(dev, hd, window, prefix):
-    """Both compute-wave shapes of head dims 128 and 256 (32 query rows per
-    wave, or two waves of 16 on 16x16x32 MFMAs) against the oracle, unmasked
-    and with windows / causal prefixes, on a GQA problem with a ragged last
-    tile and a ragged last row block."""
+    """Both compute-wave shapes of head dims 128, 256 and 512 (32 query rows
+    per wave, or two waves of 16 on 16x16x32 MFMAs; at 512 each also split
+    over the head dim) against the oracle, unmasked and with windows /
+    causal prefixes, on a GQA problem with a ragged last tile and a ragged
+    last row block."""
     rng = np.random.default_rng(31)
     h, hkv, n_p, n_c = 8, 2, 200, 93
     n_t = n_p + n_c
