@@ -68,6 +68,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BN = 32;                     // keys per tile (one MFMA key block)
+static_assert(BN == VT_KEYS, "a key tile is one V^T tile of the cache");
 constexpr float RESCALE_THRESHOLD = 8.0f;  // log2 units
 
 // 16-byte-chunk swizzle for an LDS row holding CH chunks.  Keeps 8 (32-bank
@@ -435,7 +436,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             return (((R & ~31) + kperm<W16>(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3)) * 2;
         }
         const int d = idx / VCH, pv = idx % VCH;
-        return (d * a.cap + ((pv ^ swz<VCH>(d)) << 3)) * 2;
+        return (d * BN + ((pv ^ swz<VCH>(d)) << 3)) * 2;  // within the V^T tile
     };
     // Compute waves that also issue DMA keep the offsets in registers; DMA
     // waves recompute them per super-tile (they have the issue slots to
@@ -469,8 +470,9 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             // slots past the range reload the last tile: in bounds, unused
             const int t = ACT ? __builtin_amdgcn_readfirstlane(tt) : min(t0 + u * KQ + kqr, t1 - 1);
             const int vo = NP > 0 ? voff_of(j, ln) : voff[NP > 0 ? 0 : j];
+            // (K tile t and V^T tile t both start at byte t * BN * HD * 2)
             if (reg & 1)
-                dma16(rv, dst, vo, t * (BN * 2));
+                dma16(rv, dst, vo, t * (BN * HD * 2));
             else
                 dma16(rk, dst, vo, t * (BN * HD * 2));
         }
@@ -597,7 +599,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                 *reinterpret_cast<bf16x8*>(vdst + (d * VCH + (lv ^ swz<VCH>(d))) * 8) = y;
                 if (own)
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), wv,
-                                                           (d * a.cap + key0 + 8 * lv) * 2, 0, 0);
+                                                           (key0 * HD + d * BN + 8 * lv) * 2, 0, 0);
             }
         }
     };

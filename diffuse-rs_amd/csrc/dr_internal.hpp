@@ -12,11 +12,17 @@ namespace dr {
 // load never leaves the allocation.
 constexpr int KEY_ALIGN = 64;
 constexpr int MAX_BATCH = 8;
+// V^T is stored key-tile-major: [n_head_kv][cap / VT_KEYS][HD][VT_KEYS], so
+// the V^T tile of keys [32 t, 32 t + 32) is one contiguous HD x 32 block
+// (whole cache lines for the DMA) and element (g, d, p) sits at
+// (g * cap + (p / 32) * 32) * HD + d * 32 + p % 32.
+constexpr int VT_KEYS = 32;
 
 // One batch slot of an attention launch.  K is [n_head_kv][cap][HD] bf16
-// (row = key index), VT is [n_head_kv][HD][cap] bf16 (V transposed so that a
-// d-row holds consecutive keys).  Key index j has sequence position kpos[j]
-// (kpos == nullptr: position j) and sequence id kseq[j] (nullptr: 0).
+// (row = key index), VT is V transposed in 32-key tiles,
+// [n_head_kv][cap / 32][HD][32] bf16 (a tile's d-row holds its 32 keys).
+// Key index j has sequence position kpos[j] (kpos == nullptr: position j)
+// and sequence id kseq[j] (nullptr: 0).
 struct AttnSlot {
     const void* q;        // [nq][q_rstride] f32, head h at h*hd
     float* out;           // [nq][o_rstride] f32
@@ -89,7 +95,7 @@ struct StoreArgs {
     int hd;              // actual head_dim (<= HD tile; tail zero-filled)
     int cap;
     uint16_t* kc;        // [n_head_kv][cap][HD] bf16 bits
-    uint16_t* vtc;       // [n_head_kv][HD][cap] bf16 bits
+    uint16_t* vtc;       // [n_head_kv][cap / VT_KEYS][HD][VT_KEYS] bf16 bits
     const float* kn_w;   // K-norm gain or nullptr
     float kn_eps;
     int vec;             // rows may be read as 16-byte pieces (hd == HD tile, aligned)

@@ -3,11 +3,13 @@
 //
 // Layout per (layer, batch slot), for n_head_kv heads and capacity `cap`
 // positions (a multiple of 64), HD = the head-dim tile (64/128/256):
-//   K  : [n_head_kv][cap][HD]   row = sequence position
-//   V^T: [n_head_kv][HD][cap]   V transposed: a d-row holds all positions
-// The attention kernel stages both as 16-byte row loads; V^T is exactly the
+//   K  : [n_head_kv][cap][HD]              row = sequence position
+//   V^T: [n_head_kv][cap/32][HD][32]       V transposed per 32-key tile: a
+//                                          tile's d-row holds its 32 positions
+// The attention kernel stages both as 16-byte loads; V^T is exactly the
 // operand orientation the P.V MFMA needs, so the transpose is paid once per
-// stored row instead of once per attention tile.
+// stored row instead of once per attention tile, and a key tile of either is
+// one contiguous block (whole cache lines for the DMA).
 //
 // store:  StepCache::store (cache.rs:62-71) -- f32 rows -> bf16 at their
 //         positions, optionally after per-head RMSNorm of K (norm_heads,
@@ -264,19 +266,24 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
     const int rfirst = r0 + p0;
     if (rfirst >= a.n) return;
     const int cnt = min(SPT, a.n - rfirst);
-    uint16_t* drow = a.vtc + ((size_t)g * HD + dc * SD + dl) * a.cap;
+    const int dv = dc * SD + dl;  // this thread's d-row
+    // V^T element (g, dv, p): tile p / VT_KEYS, offset p % VT_KEYS in its d-row
+    uint16_t* vplane = a.vtc + (size_t)g * HD * a.cap + (size_t)dv * VT_KEYS;
+    auto vt_at = [&](int p) __attribute__((always_inline)) {
+        return vplane + (size_t)(p / VT_KEYS) * (HD * VT_KEYS) + p % VT_KEYS;
+    };
     const int q0 = a.pos ? a.pos[rfirst] : rfirst;
     // pos is strictly ascending, so equal endpoint distance means contiguous.
     const bool contiguous = cnt == SPT && (q0 & 7) == 0 &&
                             (a.pos == nullptr || a.pos[rfirst + SPT - 1] - q0 == SPT - 1);
     const uint16_t* t = &tile[dl][p0];
     if (contiguous) {
+        // 8 positions from a multiple of 8 never cross a 32-key tile
 #pragma unroll
         for (int h = 0; h < SPT / 8; ++h)
-            *reinterpret_cast<u32x4*>(drow + q0 + 8 * h) =
-                *reinterpret_cast<const u32x4*>(t + 8 * h);
+            *reinterpret_cast<u32x4*>(vt_at(q0 + 8 * h)) = *reinterpret_cast<const u32x4*>(t + 8 * h);
     } else {
-        for (int e = 0; e < cnt; ++e) drow[a.pos ? a.pos[rfirst + e] : rfirst + e] = t[e];
+        for (int e = 0; e < cnt; ++e) *vt_at(a.pos ? a.pos[rfirst + e] : rfirst + e) = t[e];
     }
 }
 
@@ -292,7 +299,8 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
         const int r = (int)(rg / a.n_head_kv);
         const int pos = a.pos[r];
         a.out_k[idx] = bf2f(a.kc[((size_t)g * a.cap + pos) * HD + d]);
-        a.out_v[idx] = bf2f(a.vtc[((size_t)g * HD + d) * a.cap + pos]);
+        a.out_v[idx] = bf2f(a.vtc[((size_t)g * a.cap + (size_t)(pos / VT_KEYS) * VT_KEYS) * HD +
+                                  (size_t)d * VT_KEYS + pos % VT_KEYS]);
     }
 }
 
