@@ -1,8 +1,10 @@
 """StepCache::split_active (src/model/cache.rs:85-114) on the device
-(dr_cache_split_active_dev), against the host restatement dr_split_active,
-which tests/test_abi.py pins to the reference's own test case: the same
-active / cached lists, bit for bit, step after step, and passes that drive
-the cached attention exactly as host-built ones do.  Needs an MI355X.
+(dr_cache_split_active_dev), against the oracle's or_split_active, which
+tests/test_oracle.py pins to the reference's own test case (tests.rs:39-68)
+and to its vicinity and decay rules: the same active / cached lists, bit for
+bit, step after step; host and device calls mixed on one slot; and passes
+that drive the cached attention exactly as host-built ones do.  Needs an
+MI355X.
 """
 from __future__ import annotations
 
@@ -12,6 +14,7 @@ import numpy as np
 import pytest
 
 import dr_attn as dr
+import oracle as orc
 
 from test_gpu_parity import check, dev, say, torch  # noqa: F401
 
@@ -38,7 +41,7 @@ def _next_seq(rng, seq, n_prompt):
 
 @pytest.mark.parametrize("n_total,n,vicinity", [(768, 768, 0), (3000, 3000, 5),
                                                 (4352, 4000, 64), (100, 37, 1000), (2048, 2048, 1)])
-def test_split_active_dev_matches_host(dev, n_total, n, vicinity):
+def test_split_active_dev_matches_oracle(dev, n_total, n, vicinity):
     rng = np.random.default_rng(n_total + vicinity)
     n_prompt = n // 3
     cache = dr.StepCache(dev.ctx, n_total, [1], [64])
@@ -50,7 +53,7 @@ def test_split_active_dev_matches_host(dev, n_total, n, vicinity):
     pa, pc = dr.Pass(dev.ctx, []), dr.Pass(dev.ctx, [])
     for step in range(10):
         is_masked = (seq == MASK).astype(np.uint8)
-        want_a, want_c = dr.split_active(prev, lc, seq, is_masked, step, vicinity)
+        want_a, want_c = orc.split_active(prev, lc, seq, is_masked, step, vicinity)
         na, nc = cache.split_active_dev(dev.put(seq), dev.put(is_masked), n, step, pa, pc)
         say(f"n {n} vicinity {vicinity} step {step}: {na} active, {nc} cached")
         assert (na, nc) == (len(want_a), len(want_c))
@@ -65,8 +68,8 @@ def test_split_active_dev_matches_host(dev, n_total, n, vicinity):
 
 
 def test_split_state_moves_between_host_and_device(dev):
-    """Host and device calls mixed on one slot give the stateless host
-    sequence of splits: the state (prev_seq, last_changed) follows the call."""
+    """Host and device calls mixed on one slot give the oracle's sequence of
+    splits: the state (prev_seq, last_changed) follows the call."""
     rng = np.random.default_rng(77)
     n = 1500
     cache = dr.StepCache(dev.ctx, n, [1], [64])
@@ -78,7 +81,7 @@ def test_split_state_moves_between_host_and_device(dev):
     pa, pc = dr.Pass(dev.ctx, []), dr.Pass(dev.ctx, [])
     for step in range(12):
         is_masked = (seq == MASK).astype(np.uint8)
-        want = dr.split_active(prev, lc, seq, is_masked, step, 3)
+        want = orc.split_active(prev, lc, seq, is_masked, step, 3)
         if step % 3 == 0:
             got = cache.split_active(seq, is_masked, step)
         else:
