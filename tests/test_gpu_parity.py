@@ -815,3 +815,42 @@ def test_step_epi_vs_oracle(dev, h, hkv, hd, rot, n_p, n_c, batch, norm, v_norm,
         for name, g_, w_ in (("K", gk, wk), ("V", gv, wv)):
             bad = np.count_nonzero(g_ != w_)
             assert bad <= 2 and np.max(np.abs(g_ - w_)) <= 2.0**-7 * np.max(np.abs(w_)), (name, bad)
+
+
+@pytest.mark.parametrize("h,hkv,hd,batch,window,prefix", [
+    (28, 4, 128, 2, 96, None),    # 448 one-row-block workgroups: the RB 2 x KQ 4 shape, masked
+    (28, 4, 128, 2, None, 700),   # the same shape under a causal prefix
+    (8, 4, 256, 2, None, None),   # 16-row waves at hd 256, two batch slots
+    (16, 2, 512, 2, 300, None),   # hd 512 split waves with a window, two batch slots
+])
+def test_batched_plans_vs_oracle(dev, h, hkv, hd, batch, window, prefix):
+    """Launch shapes the planner picks for batched (CFG-pair) problems, under
+    masks, against the oracle per batch slot."""
+    rng = np.random.default_rng(h * 1000 + hd + (window or 0))
+    n_p, n_c = 600, 256
+    n_t = n_p + n_c
+    kvs = hkv * hd
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd], n_batch=batch)
+    p_all = dr.Pass(dev.ctx, range(n_t))
+    pc = dr.Pass(dev.ctx, range(n_p, n_t))
+    scale = 1 / math.sqrt(hd)
+    items, ins, outs = [], [], []
+    for b in range(batch):
+        K = rng.standard_normal((n_t, kvs), dtype=np.float32)
+        V = rng.standard_normal((n_t, kvs), dtype=np.float32)
+        Q = rng.standard_normal((n_c, h * hd), dtype=np.float32)
+        cache.store(0, p_all, dev.put(K), dev.put(V), batch=b)
+        out = dev.empty(n_c * h * hd)
+        items.append((dev.put(Q), out, pc))
+        ins.append((Q, K, V))
+        outs.append(out)
+    cache.attention(0, items, h, sliding_window=window, causal_prefix=prefix, scale=scale)
+    info = dev.ctx.last_launch()
+    say(f"h {h}/{hkv} hd {hd} batch {batch} window {window} prefix {prefix}: launch {info}")
+    s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, causal_prefix=prefix, scale=scale)
+    qr, kr = RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t)))
+    for b in range(batch):
+        Q, K, V = ins[b]
+        want = oracle_run(s, qr, kr, *as_kernel_sees(Q.reshape(-1).copy(), K.reshape(-1).copy(),
+                                                     V.reshape(-1).copy(), scale))
+        check(dev.get(outs[b]), want, f"batch {b}")
