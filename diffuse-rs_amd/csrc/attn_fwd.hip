@@ -1741,6 +1741,7 @@ hipError_t launch_modes16(const LaunchPlan& p, const AttnArgs& a, hipStream_t st
             return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false, true>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false, true>(p, a, st);
         default:
+            if (p.qepi) return hipErrorInvalidValue;
             return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false, true>(p, a, st);
     }
 }
@@ -1771,6 +1772,7 @@ hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
             return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false>(p, a, st)
                            : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false>(p, a, st);
         default:
+            if (p.qepi) return hipErrorInvalidValue;
             return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false>(p, a, st);
     }
 }
@@ -1786,8 +1788,8 @@ constexpr Shape SHAPES[] = {
     {64, 1, 4, 3, 4, false}, {64, 2, 2, 4, 4, false}, {64, 2, 4, 3, 0, false},
     {128, 1, 4, 2, 4, false}, {128, 2, 2, 4, 4, false}, {128, 2, 4, 2, 0, false},
     {128, 1, 4, 2, 4, true}, {256, 2, 2, 2, 0, true},
-    {256, 2, 2, 2, 0, false}, {256, 1, 2, 2, 0, false},  // one wave per SIMD: 512 VGPRs
-    {512, 2, 1, 2, 0, false},  // head-dim split: a wave pair per row block, one wave per SIMD
+    {256, 2, 2, 2, 0, false}, {256, 1, 2, 2, 0, false},  // 32-row waves: one per SIMD, 512 VGPRs
+    {512, 2, 1, 2, 0, false},  // head-dim split, 32-row waves: a pair per row block, one per SIMD
     {512, 2, 1, 2, 0, true},   // ... and with 16-row waves: 8 compute waves, two per SIMD
 };
 
@@ -1828,13 +1830,14 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
     p.block_n = BN;
     p.mask = mask;
-    p.qepi = qepi && mask != MASK_KEYS;
+    p.qepi = qepi;  // (no key-masked build carries the Q epilogue: its launch fails)
     const int cus = n_cu > 0 ? n_cu : 256;
     const int row_blocks = (group * max_nq + 31) / 32;  // per (batch, kv head)
     const int ntiles = (max_nk + BN - 1) / BN;
     // Head dims up to 128: one row block of four key groups with four DMA
     // waves (two waves per SIMD).  256: two row blocks of two key groups,
-    // one wave per SIMD (the accumulators need the whole register file).
+    // one 32-row wave per SIMD (the accumulators need the whole register
+    // file), or the 16-row form (below).
     // 512: two row blocks, each a wave pair that splits the head dim.
     int rb = 1;
     int kq = p.hd_tile == 256 ? 2 : (p.hd_tile == 512 ? 1 : 4);

@@ -165,7 +165,7 @@ enum MaskMode : int {
 };
 
 struct LaunchPlan {
-    int hd_tile;     // 64, 128 or 256
+    int hd_tile;     // 64, 128, 256 or 512
     int block_n;     // keys per tile (one MFMA key block is 32)
     int rb;          // row blocks (32 query rows each) per workgroup
     int kq;          // key groups per workgroup (merged in LDS)

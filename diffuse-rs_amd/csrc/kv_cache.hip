@@ -2,7 +2,7 @@
 // src/model/cache.rs:25-115), bf16, position-indexed.
 //
 // Layout per (layer, batch slot), for n_head_kv heads and capacity `cap`
-// positions (a multiple of 64), HD = the head-dim tile (64/128/256):
+// positions (a multiple of 64), HD = the head-dim tile (64/128/256/512):
 //   K  : [n_head_kv][cap][HD]              row = sequence position
 //   V^T: [n_head_kv][cap/32][HD][32]       V transposed per 32-key tile: a
 //                                          tile's d-row holds its 32 positions
