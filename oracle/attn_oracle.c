@@ -24,6 +24,17 @@
  *   or_rotate_rows          src/model/ops.rs:419-452       (apply_rope / rotate_rows)
  *   or_cache_store/gather   src/model/cache.rs:62-82       (StepCache::store/gather)
  *   or_split_active         src/model/cache.rs:85-114      (StepCache::split_active)
+ *   or_f16_to_f32           src/kernels.rs:46-69           (f16_to_f32)
+ *   or_quantize_q8k         src/kernels.rs:79-122          (quantize_rows_q8_k)
+ *   or_dequant_q4k          src/kernels.rs:186-215         (dequantize_q4k_row)
+ *   or_dequant_q6k          src/kernels.rs:129-163         (dequantize_q6k_row)
+ *   or_vec_dot_q4k_q8k      src/kernels.rs:228-308         (the scalar Q4_K x Q8_K
+ *                           dot of the reference's tests, candle-core 0.8.4's
+ *                           BlockQ4K::vec_dot_unopt)
+ *   or_vec_dot_q6k_q8k      src/kernels.rs:313-347         (ggml's generic Q6_K dot)
+ *   or_qmatmul              src/model/matmul.rs:120-148    (native_matmul:
+ *                           out[t*rows + r] = vec_dot(weight row r, act row t)),
+ *                           plus residual_add, src/model/ops.rs:365-370
  *
  * Numerics follow Rust semantics: no FMA contraction outside the explicit
  * _mm256_fmadd_ps calls (build with -ffp-contract=off), f32::exp = libm expf,
@@ -337,4 +348,217 @@ void or_split_active(const int32_t* prev_seq, int32_t* last_changed, const int32
     *n_active = na;
     *n_cached = nc;
     free(act);
+}
+
+
+/* ---------------------------------------------------------------------------
+ * Quantized matmul: Q4_K / Q6_K weight rows against Q8_K activation rows.
+ * Block layouts (src/kernels.rs:9-41): Q4_K 144 bytes {u16 d, u16 dmin,
+ * u8 scales[12], u8 qs[128]}; Q6_K 210 bytes {u8 ql[128], u8 qh[64],
+ * i8 scales[16], u16 d}; Q8_K 292 bytes {f32 d, i8 qs[256], i16 bsums[16]}.
+ * ------------------------------------------------------------------------- */
+#define OR_QK 256
+
+typedef struct {
+    float d;
+    int8_t qs[OR_QK];
+    int16_t bsums[OR_QK / 16];
+} or_q8k_t;
+
+/* f16_to_f32 -- src/kernels.rs:46-69 (subnormals normalised by shifting). */
+float or_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1Fu, mant = h & 0x3FFu;
+    uint32_t bits;
+    if (ex == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            uint32_t e = 0, m = mant;
+            while ((m & 0x400u) == 0) {
+                m <<= 1;
+                e++;
+            }
+            bits = (sign << 31) | ((113u - e) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (ex == 31) {
+        bits = (sign << 31) | (0xFFu << 23) | (mant ? 0x7FFFFFu : 0u);
+    } else {
+        bits = (sign << 31) | ((ex + 127u - 15u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* quantize_rows_q8_k -- src/kernels.rs:79-122: per 256-value block, the
+ * first value of largest magnitude sets iscale = -128 / max; q = round(iscale
+ * x) (half away from zero, as f32::round) capped at 127; d = 1 / iscale;
+ * bsums are the sums of 16 consecutive q.  An all-zero block has d = 0. */
+void or_quantize_q8k(const float* src, size_t n, size_t cols, or_q8k_t* dst) {
+    const size_t nb = cols / OR_QK;
+    for (size_t t = 0; t < n; t++)
+        for (size_t b = 0; b < nb; b++) {
+            const float* xs = src + t * cols + b * OR_QK;
+            or_q8k_t* blk = dst + t * nb + b;
+            float mx = 0.0f, amax = 0.0f;
+            for (int j = 0; j < OR_QK; j++)
+                if (amax < fabsf(xs[j])) {
+                    amax = fabsf(xs[j]);
+                    mx = xs[j];
+                }
+            memset(blk, 0, sizeof(*blk));
+            if (amax == 0.0f) continue;
+            const float iscale = -128.0f / mx;
+            for (int j = 0; j < OR_QK; j++) {
+                float v = roundf(iscale * xs[j]);
+                blk->qs[j] = (int8_t)(v < 127.0f ? v : 127.0f);
+            }
+            for (int j = 0; j < OR_QK / 16; j++) {
+                int32_t sm = 0;
+                for (int i = 0; i < 16; i++) sm += blk->qs[j * 16 + i];
+                blk->bsums[j] = (int16_t)sm;
+            }
+            blk->d = 1.0f / iscale;
+        }
+}
+
+/* The 6-bit scales and mins of a Q4_K block (src/kernels.rs:193-201): the 12
+ * packed bytes unpacked into sc[8] and mn[8]. */
+static void q4k_scales(const uint8_t* packed, uint8_t sc[8], uint8_t mn[8]) {
+    uint32_t u[4];
+    memcpy(u, packed, 12);
+    const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+    u[3] = ((u[2] >> 4) & k2) | (((u[1] >> 6) & k3) << 4);
+    const uint32_t aux = u[1] & k1;
+    u[1] = (u[2] & k2) | (((u[0] >> 6) & k3) << 4);
+    u[2] = aux;
+    u[0] &= k1;
+    memcpy(sc, u, 8);
+    memcpy(mn, (const uint8_t*)u + 8, 8);
+}
+
+/* dequantize_q4k_row -- src/kernels.rs:186-215. */
+void or_dequant_q4k(const uint8_t* blocks, size_t nb, float* out) {
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* x = blocks + b * 144;
+        uint16_t hd, hm;
+        memcpy(&hd, x, 2);
+        memcpy(&hm, x + 2, 2);
+        const float d = or_f16_to_f32(hd), dmin = or_f16_to_f32(hm);
+        uint8_t sc[8], mn[8];
+        q4k_scales(x + 4, sc, mn);
+        const uint8_t* qs = x + 16;
+        for (int j = 0; j < 4; j++)
+            for (int k = 0; k < 32; k++) {
+                const uint8_t q = qs[j * 32 + k];
+                out[b * OR_QK + 64 * j + k] = d * (float)sc[2 * j] * (float)(q & 0xF) - dmin * (float)mn[2 * j];
+                out[b * OR_QK + 64 * j + 32 + k] =
+                    d * (float)sc[2 * j + 1] * (float)(q >> 4) - dmin * (float)mn[2 * j + 1];
+            }
+    }
+}
+
+/* The 256 signed 6-bit values of a Q6_K block (src/kernels.rs:135-147). */
+static void q6k_values(const uint8_t* x, int8_t a[OR_QK]) {
+    const uint8_t *ql = x, *qh = x + 128;
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *l8 = ql + 64 * half, *h8 = qh + 32 * half;
+        int8_t* o = a + 128 * half;
+        for (int l = 0; l < 32; l++) {
+            o[l] = (int8_t)((l8[l] & 0xF) | ((h8[l] & 3) << 4)) - 32;
+            o[l + 32] = (int8_t)((l8[l + 32] & 0xF) | (((h8[l] >> 2) & 3) << 4)) - 32;
+            o[l + 64] = (int8_t)((l8[l] >> 4) | (((h8[l] >> 4) & 3) << 4)) - 32;
+            o[l + 96] = (int8_t)((l8[l + 32] >> 4) | (((h8[l] >> 6) & 3) << 4)) - 32;
+        }
+    }
+}
+
+/* dequantize_q6k_row -- src/kernels.rs:129-163: d * scale[j / 16] * value. */
+void or_dequant_q6k(const uint8_t* blocks, size_t nb, float* out) {
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* x = blocks + b * 210;
+        uint16_t hd;
+        memcpy(&hd, x + 208, 2);
+        const float d = or_f16_to_f32(hd);
+        const int8_t* sc = (const int8_t*)(x + 192);
+        int8_t a[OR_QK];
+        q6k_values(x, a);
+        for (int j = 0; j < OR_QK; j++) out[b * OR_QK + j] = d * (float)sc[j / 16] * (float)a[j];
+    }
+}
+
+/* Q4_K x Q8_K (src/kernels.rs:228-308): integer products gathered into eight
+ * lanes (element i of the block goes to lane i % 8), each sub-block of 32
+ * times its scale; per block sums[l] += d * aux32[l] and sumf -= dmin * sumi
+ * (sumi = bsums . mins), with d = f16(x.d) * y.d and dmin = f16(x.dmin) *
+ * y.d; finally sumf + sums[0] + ... + sums[7]. */
+float or_vec_dot_q4k_q8k(const uint8_t* x, const or_q8k_t* y, size_t nb) {
+    float sums[8] = {0}, sumf = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* xb = x + b * 144;
+        const or_q8k_t* yb = y + b;
+        int8_t a[OR_QK];
+        const uint8_t* q4 = xb + 16;
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) {
+                a[64 * j + l] = (int8_t)(q4[32 * j + l] & 0xF);
+                a[64 * j + 32 + l] = (int8_t)(q4[32 * j + l] >> 4);
+            }
+        uint8_t sc[8], mn[8];
+        q4k_scales(xb + 4, sc, mn);
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; j++) sumi += (int32_t)yb->bsums[j] * (int32_t)mn[j / 2];
+        int32_t aux32[8] = {0};
+        for (int i = 0; i < OR_QK; i++) aux32[i % 8] += (int32_t)sc[i / 32] * ((int32_t)yb->qs[i] * a[i]);
+        uint16_t hd, hm;
+        memcpy(&hd, xb, 2);
+        memcpy(&hm, xb + 2, 2);
+        const float d = or_f16_to_f32(hd) * yb->d;
+        for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
+        const float dmin = or_f16_to_f32(hm) * yb->d;
+        sumf -= dmin * (float)sumi;
+    }
+    float tot = 0.0f;  /* sums.iter().sum(): a left fold from zero, added last */
+    for (int l = 0; l < 8; l++) tot += sums[l];
+    return sumf + tot;
+}
+
+/* Q6_K x Q8_K (src/kernels.rs:313-347): per block sumf += d * sumi with d =
+ * f16(x.d) * y.d and sumi = sum_j scale[j] * sum of 16 products. */
+float or_vec_dot_q6k_q8k(const uint8_t* x, const or_q8k_t* y, size_t nb) {
+    float sumf = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* xb = x + b * 210;
+        const or_q8k_t* yb = y + b;
+        int8_t a[OR_QK];
+        q6k_values(xb, a);
+        const int8_t* sc = (const int8_t*)(xb + 192);
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; j++)
+            for (int k = 0; k < 16; k++) sumi += (int32_t)sc[j] * (int32_t)a[16 * j + k] * (int32_t)yb->qs[16 * j + k];
+        uint16_t hd;
+        memcpy(&hd, xb + 208, 2);
+        sumf += or_f16_to_f32(hd) * yb->d * (float)sumi;
+    }
+    return sumf;
+}
+
+/* native_matmul (src/model/matmul.rs:120-148) over f32 activations quantized
+ * to Q8_K (ActScratch::q8k, matmul.rs:64-71): out[t*rows + r] = vec_dot(weight
+ * row r, activation row t); with residual (non-NULL), then residual_add
+ * (ops.rs:365-370): out += residual.  wtype 12 = Q4_K, 14 = Q6_K (GGML ids). */
+void or_qmatmul(int wtype, const uint8_t* w, size_t rows, size_t cols, const float* act, size_t n,
+                float* out, const float* residual) {
+    const size_t nb = cols / OR_QK, bb = wtype == 12 ? 144 : 210;
+    or_q8k_t* q = (or_q8k_t*)malloc((n * nb > 0 ? n * nb : 1) * sizeof(or_q8k_t));
+    or_quantize_q8k(act, n, cols, q);
+#pragma omp parallel for schedule(static)
+    for (long long r = 0; r < (long long)rows; r++)
+        for (size_t t = 0; t < n; t++) {
+            const uint8_t* wr = w + (size_t)r * nb * bb;
+            float v = wtype == 12 ? or_vec_dot_q4k_q8k(wr, q + t * nb, nb) : or_vec_dot_q6k_q8k(wr, q + t * nb, nb);
+            if (residual) v += residual[t * rows + (size_t)r];
+            out[t * rows + (size_t)r] = v;
+        }
+    free(q);
 }

@@ -76,6 +76,17 @@ def load() -> ctypes.CDLL:
     lib.or_rotate_rows.argtypes = [P, P, c_size_p, ctypes.c_size_t, ctypes.c_size_t,
                                    ctypes.c_size_t, ctypes.c_size_t]
     lib.or_cache_store.argtypes = [P, P, ctypes.c_size_t, c_size_p, ctypes.c_size_t, P, P]
+    lib.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.or_f16_to_f32.restype = ctypes.c_float
+    lib.or_quantize_q8k.argtypes = [P, ctypes.c_size_t, ctypes.c_size_t, P]
+    lib.or_dequant_q4k.argtypes = [P, ctypes.c_size_t, P]
+    lib.or_dequant_q6k.argtypes = [P, ctypes.c_size_t, P]
+    lib.or_vec_dot_q4k_q8k.argtypes = [P, P, ctypes.c_size_t]
+    lib.or_vec_dot_q4k_q8k.restype = ctypes.c_float
+    lib.or_vec_dot_q6k_q8k.argtypes = [P, P, ctypes.c_size_t]
+    lib.or_vec_dot_q6k_q8k.restype = ctypes.c_float
+    lib.or_qmatmul.argtypes = [ctypes.c_int, P, ctypes.c_size_t, ctypes.c_size_t, P, ctypes.c_size_t,
+                               P, P]
     lib.or_cache_gather.argtypes = [P, P, ctypes.c_size_t, c_size_p, ctypes.c_size_t, P, P]
     lib.or_split_active.argtypes = [P, P, P, P, ctypes.c_size_t, ctypes.c_size_t,
                                     ctypes.c_size_t, c_size_p, c_size_p, c_size_p, c_size_p]
@@ -207,3 +218,52 @@ def split_active(prev_seq, last_changed: np.ndarray, seq, is_masked, step: int,
                            m_a.ctypes.data, n, step, vicinity, act.ctypes.data_as(c_size_p),
                            ctypes.byref(na), cac.ctypes.data_as(c_size_p), ctypes.byref(nc))
     return [int(x) for x in act[: na.value]], [int(x) for x in cac[: nc.value]]
+
+
+# ---- quantized matmul (src/kernels.rs, src/model/matmul.rs) -----------------
+
+QK_K = 256
+Q4K_BYTES, Q6K_BYTES = 144, 210
+WTYPE_Q4K, WTYPE_Q6K = 12, 14  # GGML type ids
+# Q8_K block, 292 bytes (src/kernels.rs:37-41)
+Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (QK_K,)), ("bsums", "<i2", (QK_K // 16,))])
+assert Q8K_DTYPE.itemsize == 292
+
+
+def f16_to_f32(h: int) -> float:
+    return float(load().or_f16_to_f32(h))
+
+
+def quantize_q8k(x: np.ndarray, n: int, cols: int) -> np.ndarray:
+    """quantize_rows_q8_k: n rows of cols f32 -> n * cols / 256 Q8_K blocks."""
+    src = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(n * cols // QK_K, Q8K_DTYPE)
+    load().or_quantize_q8k(src.ctypes.data, n, cols, out.ctypes.data)
+    return out
+
+
+def dequant(wtype: int, blocks: np.ndarray, nb: int) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, np.uint8)
+    out = np.zeros(nb * QK_K, np.float32)
+    fn = load().or_dequant_q4k if wtype == WTYPE_Q4K else load().or_dequant_q6k
+    fn(b.ctypes.data, nb, out.ctypes.data)
+    return out
+
+
+def vec_dot(wtype: int, x_blocks: np.ndarray, y_blocks: np.ndarray, nb: int) -> float:
+    xb = np.ascontiguousarray(x_blocks, np.uint8)
+    yb = np.ascontiguousarray(y_blocks, Q8K_DTYPE)
+    fn = load().or_vec_dot_q4k_q8k if wtype == WTYPE_Q4K else load().or_vec_dot_q6k_q8k
+    return float(fn(xb.ctypes.data, yb.ctypes.data, nb))
+
+
+def qmatmul(wtype: int, w: np.ndarray, rows: int, cols: int, act: np.ndarray, n: int,
+            residual: "np.ndarray | None" = None) -> np.ndarray:
+    """native_matmul + residual_add: out[t, r] = vec_dot(w row r, q8k(act row t)) (+ residual)."""
+    wb = np.ascontiguousarray(w, np.uint8)
+    a = np.ascontiguousarray(act, np.float32)
+    out = np.zeros(n * rows, np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    load().or_qmatmul(wtype, wb.ctypes.data, rows, cols, a.ctypes.data, n, out.ctypes.data,
+                      None if res is None else res.ctypes.data)
+    return out

@@ -439,3 +439,115 @@ def test_bf16_round_known_values():
     r = bf16_round(np.random.default_rng(0).standard_normal(1000).astype(np.float32))
     assert np.array_equal(bf16_round(r), r)
     assert np.all(r.view(np.uint32) & 0xFFFF == 0)
+
+
+# ---- quantized matmul pieces (src/kernels.rs, src/model/matmul.rs) ----------
+
+def test_f16_to_f32_reference_vectors():
+    # kernels.rs:350-372 (test_f16_to_f32): numpy float16 reference values
+    cases = [(0x0000, 0.0), (0x0001, 5.9604645e-8), (0x0200, 3.0517578e-5), (0x03FF, 6.097555e-5),
+             (0x0400, 6.1035156e-5), (0x3C00, 1.0), (0xC000, -2.0), (0x8001, -5.9604645e-8)]
+    for h, want in cases:
+        got = orc.f16_to_f32(h)
+        assert abs(got - want) <= abs(want) * 1e-6, (hex(h), got, want)
+        # and numpy's own decode of every one of them
+        assert got == float(np.array([h], np.uint16).view(np.float16)[0])
+    assert math.isinf(orc.f16_to_f32(0x7C00)) and math.isnan(orc.f16_to_f32(0x7C01))
+    allh = np.arange(0, 0x7C00, 97, dtype=np.uint16)
+    assert all(orc.f16_to_f32(int(h)) == float(np.float16(allh.view(np.float16)[i]))
+               for i, h in enumerate(allh))
+
+
+def test_q8k_quantize_invariants():
+    rng = np.random.default_rng(81)
+    x = (rng.standard_normal(4 * 512) * rng.uniform(0.01, 50, 4 * 512)).astype(np.float32)
+    x[256:512] = 0.0  # an all-zero block
+    x[777] = -3.0 * np.abs(x[768:1024]).max()  # its block's largest magnitude, negative
+    q = orc.quantize_q8k(x, 4, 512)
+    assert orc.Q8K_DTYPE.itemsize == 292  # kernels.rs:374-379
+    xb = x.reshape(-1, 256)
+    for b in range(q.size):
+        d, qs = float(q["d"][b]), q["qs"][b].astype(np.int32)
+        if not np.any(xb[b]):
+            assert d == 0.0 and not np.any(qs)
+            continue
+        i = int(np.argmax(np.abs(xb[b])))  # first index of the largest magnitude
+        assert qs[i] == -128
+        assert np.all(np.abs(xb[b] - d * qs) <= abs(d) * 0.5 * (1 + 1e-5) + 1e-30)
+        assert np.array_equal(q["bsums"][b], qs.reshape(16, 16).sum(1).astype(np.int16))
+    assert q["d"][3] > 0  # a negative extreme gives a positive d (iscale = -128 / max)
+
+
+def _q4k_ref_block():
+    # kernels.rs:425-437 (test_q4k_nonzero)
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.uint16(0x3800).tobytes(), np.uint8)
+    b[4:16] = [(i * 5 + 1) & 0x3F for i in range(12)]
+    b[16:] = [(i * 7 + 3) & 0xFF for i in range(128)]
+    return b
+
+
+def _q6k_ref_block():
+    # kernels.rs:398-423 (test_q6k_vs_dequantize)
+    b = np.zeros(210, np.uint8)
+    b[:128] = [(i * 7 + 3) & 0xFF for i in range(128)]
+    b[128:192] = [(i * 13 + 5) & 0xFF for i in range(64)]
+    b[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    b[208:210] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    return b
+
+
+def _ref_q8():
+    q = np.zeros(1, orc.Q8K_DTYPE)
+    q["d"] = np.float32(1.0 / 127.0)
+    qs = np.clip(np.arange(256) * 3 - 128, -128, 127).astype(np.int8)
+    q["qs"][0] = qs
+    q["bsums"][0] = qs.astype(np.int16).reshape(16, 16).sum(1)
+    return q
+
+
+@pytest.mark.parametrize("wtype", [orc.WTYPE_Q4K, orc.WTYPE_Q6K])
+def test_quantized_dot_equals_dequantized_dot(wtype):
+    """The reference's own cross-check (kernels.rs:398-437): the integer dot
+    equals dequantize-then-dot, on its block patterns and on random blocks."""
+    nbytes = orc.Q4K_BYTES if wtype == orc.WTYPE_Q4K else orc.Q6K_BYTES
+    blocks = [_q4k_ref_block() if wtype == orc.WTYPE_Q4K else _q6k_ref_block()]
+    ys = [_ref_q8()]
+    rng = np.random.default_rng(82 + wtype)
+    for _ in range(6):
+        b = rng.integers(0, 256, nbytes, dtype=np.uint8)
+        dpos = 0 if wtype == orc.WTYPE_Q4K else 208
+        b[dpos:dpos + 2] = np.frombuffer(np.float16(rng.uniform(0.001, 0.05)).tobytes(), np.uint8)
+        if wtype == orc.WTYPE_Q4K:
+            b[2:4] = np.frombuffer(np.float16(rng.uniform(0.001, 0.05)).tobytes(), np.uint8)
+        blocks.append(b)
+        ys.append(orc.quantize_q8k(rng.standard_normal(256).astype(np.float32), 1, 256))
+    for b, y in zip(blocks, ys):
+        got = orc.vec_dot(wtype, b, y, 1)
+        w = orc.dequant(wtype, b, 1).astype(np.float64)
+        want = float(np.dot(w, y["qs"][0].astype(np.float64)) * float(y["d"][0]))
+        assert np.isfinite(got) and abs(got) > 1e-6
+        assert abs(got - want) <= 1e-4 * max(abs(want), 1e-3), (got, want)
+
+
+def test_q4k_scales_and_mins_closed_form():
+    """Q4_K with every nibble q, d = 1, dmin = 1 and per-sub-block scale s_j and
+    min m_j dequantizes to s_j * q - m_j; sub-block j's scale lands on it (a
+    transposed unpack of the 12 packed bytes would not)."""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    sc = [1, 2, 3, 4, 5, 6, 7, 63]
+    mn = [0, 1, 2, 3, 10, 20, 30, 40]
+    pk = np.zeros(12, np.uint8)  # get_scale_min_k4 packing
+    for j in range(4):
+        pk[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        pk[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        pk[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    b[4:16] = pk
+    b[16:] = 0x53  # low nibble 3, high nibble 5
+    w = orc.dequant(orc.WTYPE_Q4K, b, 1)
+    for j in range(8):
+        q = 3 if j % 2 == 0 else 5
+        assert np.all(w[32 * j:32 * j + 32] == np.float32(sc[j] * q - mn[j])), j
