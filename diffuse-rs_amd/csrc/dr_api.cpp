@@ -99,6 +99,7 @@ struct dr_ctx {
     bool has_last = false;
     DevBuf part;                         // key-split partials
     DevBuf q, k, v, kc, vtc, meta, out;  // dr_attention() staging
+    DevBuf q8k;                          // dr_qmatmul's Q8_K activations
 };
 
 struct dr_pass {
@@ -249,7 +250,7 @@ void dr_ctx_destroy(dr_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (DevBuf* b : {&ctx->part, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc,
-                      &ctx->meta, &ctx->out})
+                      &ctx->meta, &ctx->out, &ctx->q8k})
         release(*b);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
@@ -707,6 +708,36 @@ int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t*
     cached->max_pos = m[1] > 0 ? (size_t)m[5] : 0;
     *n_active = active->n;
     *n_cached = cached->n;
+    return DR_OK;
+}
+
+int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
+               size_t n, float* out, const float* residual) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_qmatmul: ctx is NULL");
+    if (wtype != DR_WTYPE_Q4K && wtype != DR_WTYPE_Q6K)
+        return fail(DR_ERR_UNSUPPORTED, "dr_qmatmul: weight type %d not built (Q4_K = 12, Q6_K = 14)", wtype);
+    if (cols == 0 || cols % 256 != 0)
+        return fail(DR_ERR_INVALID, "dr_qmatmul: cols %zu is not a positive multiple of 256", cols);
+    if (n == 0 || rows == 0) return DR_OK;
+    if (!w || !act || !out) return fail(DR_ERR_INVALID, "dr_qmatmul: NULL w / act / out");
+    const size_t nb = cols / 256;
+    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || n * nb > (size_t)INT32_MAX ||
+        n > (size_t)INT32_MAX / 32)
+        return fail(DR_ERR_INVALID, "dr_qmatmul: %zu x %zu x %zu too large", n, rows, cols);
+    DR_CHECK(use_device(ctx));
+    DR_CHECK(ensure(ctx->q8k, n * nb * sizeof(dr::Q8KBlock)));
+    dr::QmmArgs a{};
+    a.wtype = wtype;
+    a.w = w;
+    a.rows = (int)rows;
+    a.cols = (int)cols;
+    a.act = act;
+    a.n = (int)n;
+    a.q8 = static_cast<dr::Q8KBlock*>(ctx->q8k.p);
+    a.out = out;
+    a.residual = residual;
+    hipError_t e = dr::launch_qmatmul(a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "qmatmul launch");
     return DR_OK;
 }
 

@@ -157,6 +157,27 @@ struct SplitArgs {
     int vicinity;
 };
 
+// A Q8_K block (src/kernels.rs:37-41): 292 bytes.
+struct Q8KBlock {
+    float d;
+    int8_t qs[256];
+    int16_t bsums[16];
+};
+static_assert(sizeof(Q8KBlock) == 292, "Q8_K block layout");
+
+// native_matmul (src/model/matmul.rs:120-148) + residual_add (ops.rs:365-370):
+// out[t * rows + r] = vec_dot(w row r, q8k(act row t)) (+ residual).
+struct QmmArgs {
+    int wtype;               // 12 = Q4_K, 14 = Q6_K
+    const void* w;           // rows * cols/256 blocks
+    int rows, cols;          // cols a multiple of 256
+    const float* act;        // [n][cols]
+    int n;
+    Q8KBlock* q8;            // workspace: n * cols/256 blocks
+    float* out;              // [n][rows]
+    const float* residual;   // [n][rows] or nullptr (may alias out)
+};
+
 // Masking mode of an attention launch.
 enum MaskMode : int {
     MASK_NONE = 0,  // every key visible (only the key tail is masked)
@@ -200,5 +221,6 @@ hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
 hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);
 hipError_t launch_split_active(const SplitArgs& a, hipStream_t st);
+hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st);
 
 }  // namespace dr

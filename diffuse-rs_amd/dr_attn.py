@@ -136,6 +136,7 @@ _SIGS = {
     "dr_pass_set": (_I, [_VP, c_size_p, _SZ]),
     "dr_pass_len": (_SZ, [_VP]),
     "dr_pass_positions": (_I, [_VP, c_size_p, _SZ]),
+    "dr_qmatmul": (_I, [_VP, _I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP]),
     "dr_pass_destroy": (None, [_VP]),
     "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_cache_destroy": (None, [_VP]),
@@ -533,3 +534,14 @@ class StepCache:
             self.close()
         except Exception:
             pass
+
+
+WTYPE_Q4K, WTYPE_Q6K = 12, 14
+
+
+def qmatmul(ctx: Context, wtype: int, w, rows: int, cols: int, act, n: int, out,
+            residual=None) -> None:
+    """Wo on k-quant weights (matmul.rs:94-148) + residual_add (ops.rs:365-370):
+    device tensors; w holds rows * cols/256 GGUF blocks."""
+    _check(ctx.lib.dr_qmatmul(ctx.h, wtype, _ptr(w), rows, cols, _ptr(act), n, _ptr(out),
+                              _ptr(residual) or None))

@@ -291,6 +291,23 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
                           size_t n_items, size_t n_head, dr_opt_usize sliding_window,
                           dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi);
 
+/* ---- the projection after the attention: Wo on GGUF k-quant weights */
+#define DR_WTYPE_Q4K 12 /* GGML type ids */
+#define DR_WTYPE_Q6K 14
+/* MatWeight::forward for Q4_K / Q6_K weights (src/model/matmul.rs:94-106):
+ * the activations are quantized to Q8_K (ActScratch::q8k, matmul.rs:64-71,
+ * quantize_rows_q8_k of src/kernels.rs:79-122) and native_matmul
+ * (matmul.rs:120-148) takes out[t*rows + r] = vec_dot(weight row r,
+ * activation row t); with residual non-NULL, residual_add (ops.rs:365-370)
+ * follows, as attention_block does after Wo (src/model/forward.rs:345-350).
+ * w: rows x cols/256 GGUF blocks (144 bytes for Q4_K, 210 for Q6_K), act
+ * [n][cols], out and residual [n][rows] f32, all device pointers on the
+ * context's stream; residual may equal out.  cols must be a multiple of 256.
+ * Each output is the reference's scalar block dot (src/kernels.rs:228-347),
+ * operation for operation. */
+int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
+               size_t n, float* out, const float* residual);
+
 /* Launch configuration of the last attention kernel this context enqueued
  * (for measurement): key splits across workgroups, workgroups, waves per
  * workgroup, keys per tile, head-dim tile, 32-row query blocks and key
