@@ -42,6 +42,7 @@ sys.path.insert(0, str(ROOT / "tests"))
 METRIC = "attn TFLOP/s & % bf16 MFMA peak per denoise step, LLaDA-8B shape, 1 MI355X"
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0  # dense int8 MFMA
 
 
 def log(msg: str) -> None:
@@ -235,6 +236,40 @@ def split_active_timing(torch, dr, ctx, stream, reps: int = 200) -> dict:
     return res
 
 
+def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
+    """Wo + residual on Q4_K weights (dr_qmatmul) at LLaDA-8B's shape for the
+    C2 step: 256 canvas rows x 4096 x 4096, synthetic blocks.  Ops = 2 * n *
+    rows * cols (the int8 products and their sums), against MI355X's dense
+    int8 MFMA peak; bytes = Q4_K weights + f32 activations in + residual in +
+    out.  The CPU baseline leg times the oracle on the same call."""
+    import numpy as np
+    n, rows, cols = 256, 4096, 4096
+    rng = np.random.default_rng(7)
+    nb = cols // 256
+    w = rng.integers(0, 256, (rows * nb, 144), dtype=np.uint8)
+    w[:, 0:4] = np.float16(rng.uniform(1e-4, 0.02, (rows * nb, 2))).view(np.uint8).reshape(-1, 4)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    res = rng.standard_normal((n, rows)).astype(np.float32)
+    with torch.cuda.stream(stream):
+        dw = torch.from_numpy(w.reshape(-1)).cuda()
+        dx = torch.from_numpy(x).cuda()
+        dres = torch.from_numpy(res).cuda()
+        out = torch.empty(n * rows, device="cuda")
+    stream.synchronize()
+
+    def call(i):
+        dr.qmatmul(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dres)
+    ms, _ = attention_only_ms(torch, stream, call, 4, reps)
+    ops = 2.0 * n * rows * cols
+    nbytes = rows * nb * 144 + 4 * n * cols + 8 * n * rows
+    res_d = {"workload": f"LLaDA-8B Wo + residual: {n} rows x {rows} x {cols}, Q4_K weights, Q8_K activations",
+             "us_per_call": round(ms * 1e3, 3), "int_tops": round(ops / (ms / 1e3) / 1e12, 2),
+             "frac_of_int8_mfma_peak": round(ops / (ms / 1e3) / 1e12 / PEAK_INT8_TOPS, 4),
+             "bytes": nbytes, "gbs": round(nbytes / (ms / 1e3) / 1e9, 1)}
+    log(f"qmatmul: {res_d}")
+    return res_d, (w.reshape(-1), rows, cols, x, n, res)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -390,11 +425,12 @@ def main() -> int:
     # ---- CPU baseline: the C restatement of the reference's attention on this
     # host's cores, on the first step's inputs; its output also checks the
     # GPU result of that step (the measured configuration).
-    others = epi = split = None
+    others = epi = split = qmm = qmm_inputs = None
     if not args.no_others:
         others = other_configs(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
         epi = qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
         split = split_active_timing(torch, dr, ctx, stream)
+        qmm, qmm_inputs = qmatmul_timing(torch, dr, ctx, stream, max(4, min(64, args.steps // 32)))
 
     cpu, parity = None, None
     if not args.no_cpu:
@@ -426,6 +462,12 @@ def main() -> int:
         t = time.perf_counter()
         orc.attention(out_c, qf, kf, vf, s, qr, kr, threads=1)
         per1 = time.perf_counter() - t
+        if qmm is not None:
+            # the same Wo call through the oracle's native_matmul + residual_add
+            t = time.perf_counter()
+            orc.qmatmul(orc.WTYPE_Q4K, *qmm_inputs)
+            qmm["cpu_oracle_ms"] = round((time.perf_counter() - t) * 1e3, 1)
+            qmm["cpu_oracle_threads"] = threads
         cpu = {"value": round(flops / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
                "kind": "port",
                "sample": f"{reps} C2 attention calls (256 q x 768 k x 32 heads, hd 128, f32) "
@@ -453,6 +495,7 @@ def main() -> int:
         "other_configs_attention_only": others,
         "qkv_epilogue": epi,
         "split_active": split,
+        "wo_qmatmul": qmm,
     }
     print(json.dumps(line), flush=True)
     return 0

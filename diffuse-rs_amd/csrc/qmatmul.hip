@@ -128,10 +128,12 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
 #pragma clang fp contract(off)
     constexpr bool Q4 = WT == 12;
     constexpr int WB = Q4 ? Q4K_BYTES : Q6K_BYTES;
-    __shared__ uint32_t s_w[TR][64];
+    // (weight-row arrays padded by one word: a wave's 32 lanes read 32
+    // different rows at the same column, which would otherwise share a bank)
+    __shared__ uint32_t s_w[TR][65];
     __shared__ uint32_t s_x[TT][64];
-    __shared__ int s_sc[TR][16];    // Q4_K: sc[0..7], mn[8..15]; Q6_K: scales[16]
-    __shared__ float s_wd[TR][2];   // f16 d (and dmin) of the weight block
+    __shared__ int s_sc[TR][17];    // Q4_K: sc[0..7], mn[8..15]; Q6_K: scales[16]
+    __shared__ float s_wd[TR][3];   // f16 d (and dmin) of the weight block
     __shared__ float s_xd[TT];      // Q8_K d
     __shared__ int s_bs[TT][16];    // Q8_K bsums
 
@@ -157,15 +159,20 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
             const int rr = tid >> 2, part = tid & 3, r = r0 + rr;
             const uint8_t* blk = W + ((size_t)min(r, a.rows - 1) * nb + b) * WB;
             if constexpr (Q4) {
-                // qs bytes 32 part .. 32 part + 31: sub-blocks 2 part (low
-                // nibbles) and 2 part + 1 (high nibbles)
-                const uint8_t* q = blk + 16 + 32 * part;
+                // qs bytes 32 part .. 32 part + 31 (two 16-byte loads: blocks
+                // are 144 bytes, so 16-byte aligned): sub-blocks 2 part (low
+                // nibbles) and 2 part + 1 (high nibbles); byte 8 g + l goes to
+                // byte g of dword l
+                const uint4* q = reinterpret_cast<const uint4*>(blk + 16 + 32 * part);
+                const uint4 v0 = q[0], v1 = q[1];
+                const uint32_t qd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
                 for (int l = 0; l < 8; ++l) {
                     uint32_t lo = 0, hi = 0;
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        const uint32_t byte = q[8 * g + l];
+                        const int k = 8 * g + l;
+                        const uint32_t byte = (qd[k >> 2] >> (8 * (k & 3))) & 0xFF;
                         lo |= (byte & 0xF) << (8 * g);
                         hi |= (byte >> 4) << (8 * g);
                     }
@@ -173,15 +180,20 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
                     s_w[rr][8 * (2 * part + 1) + l] = hi;
                 }
                 if (part == 0) {
+                    const uint4 h = *reinterpret_cast<const uint4*>(blk);  // d, dmin, scales[12]
+                    uint8_t hb[16];
+                    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) hb[i] = (hw[i >> 2] >> (8 * (i & 3))) & 0xFF;
                     uint8_t sc[8], mn[8];
-                    q4k_unpack_scales(blk + 4, sc, mn);
+                    q4k_unpack_scales(hb + 4, sc, mn);
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         s_sc[rr][i] = sc[i];
                         s_sc[rr][8 + i] = mn[i];
                     }
-                    s_wd[rr][0] = f16_bits_to_f32(blk[0] | (blk[1] << 8));
-                    s_wd[rr][1] = f16_bits_to_f32(blk[2] | (blk[3] << 8));
+                    s_wd[rr][0] = f16_bits_to_f32(h.x & 0xFFFF);
+                    s_wd[rr][1] = f16_bits_to_f32(h.x >> 16);
                 }
             } else {
                 // values 64 part .. 64 part + 63 (src/kernels.rs:135-147):
@@ -217,19 +229,29 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
         {
             const int tt = tid >> 3, j = tid & 7, t = t0 + tt;
             const Q8KBlock* xb = a.q8 + (size_t)min(t, a.n - 1) * nb + b;
-            const int8_t* qs = xb->qs + 32 * j;
+            // sub-block j's 32 values as 8 dword loads (Q8_K blocks are 292
+            // bytes: 4-byte aligned)
+            const uint32_t* qw = reinterpret_cast<const uint32_t*>(xb->qs + 32 * j);
+            uint32_t qd[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qd[i] = qw[i];
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
                 uint32_t v = 0;
+                if constexpr (Q4) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int src = Q4 ? 8 * g + l : 4 * l + g;
-                    v |= (uint32_t)(uint8_t)qs[src] << (8 * g);
+                    for (int g = 0; g < 4; ++g) {
+                        const int k = 8 * g + l;
+                        v |= ((qd[k >> 2] >> (8 * (k & 3))) & 0xFF) << (8 * g);
+                    }
+                } else {
+                    v = qd[l];
                 }
                 s_x[tt][8 * j + l] = v;
             }
-            s_bs[tt][2 * j] = xb->bsums[2 * j];
-            s_bs[tt][2 * j + 1] = xb->bsums[2 * j + 1];
+            const uint32_t bs = *reinterpret_cast<const uint32_t*>(xb->bsums + 2 * j);
+            s_bs[tt][2 * j] = (int16_t)(bs & 0xFFFF);
+            s_bs[tt][2 * j + 1] = (int16_t)(bs >> 16);
             if (j == 0) s_xd[tt] = xb->d;
         }
         __syncthreads();
@@ -244,16 +266,25 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int sc0 = s_sc[2 * rg][j], sc1 = s_sc[2 * rg + 1][j];
+                // the sub-block's 64 independent dot4s first, then their
+                // scaling (a scaled product right behind its dot4 stalls)
+                int p[8][8];
 #pragma unroll
                 for (int l = 0; l < 8; ++l) {
                     const int w0 = s_w[2 * rg][8 * j + l], w1 = s_w[2 * rg + 1][8 * j + l];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const int xv = s_x[4 * tg + k][8 * j + l];
-                        aux[k][l] += sc0 * __builtin_amdgcn_sdot4(w0, xv, 0, false);
-                        aux[4 + k][l] += sc1 * __builtin_amdgcn_sdot4(w1, xv, 0, false);
+                        p[k][l] = __builtin_amdgcn_sdot4(w0, xv, 0, false);
+                        p[4 + k][l] = __builtin_amdgcn_sdot4(w1, xv, 0, false);
                     }
                 }
+                // (scales <= 63 and |dot4| <= 4 * 15 * 128: exact in the
+                // full-rate 24-bit multiply)
+#pragma unroll
+                for (int o = 0; o < 8; ++o)
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) aux[o][l] += __mul24(o < 4 ? sc0 : sc1, p[o][l]);
             }
 #pragma unroll
             for (int o = 0; o < 8; ++o) {
@@ -277,7 +308,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
                     int p = 0;
 #pragma unroll
                     for (int k = 0; k < 4; ++k) p = __builtin_amdgcn_sdot4(s_w[rr][4 * j + k], s_x[tt][4 * j + k], p, false);
-                    sumi += s_sc[rr][j] * p;
+                    sumi += __mul24(s_sc[rr][j], p);  // |scale| <= 128, |p| <= 4 * 32 * 128
                 }
                 const float d = s_wd[rr][0] * s_xd[tt];
                 sumf[o] += d * (float)sumi;
