@@ -720,6 +720,8 @@ int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, 
         return fail(DR_ERR_INVALID, "dr_qmatmul: cols %zu is not a positive multiple of 256", cols);
     if (n == 0 || rows == 0) return DR_OK;
     if (!w || !act || !out) return fail(DR_ERR_INVALID, "dr_qmatmul: NULL w / act / out");
+    if (wtype == DR_WTYPE_Q4K && ((uintptr_t)w & 15))
+        return fail(DR_ERR_INVALID, "dr_qmatmul: Q4_K blocks must start 16-byte aligned (16-byte loads)");
     const size_t nb = cols / 256;
     if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || n * nb > (size_t)INT32_MAX ||
         n > (size_t)INT32_MAX / 32)

@@ -302,7 +302,8 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
  * follows, as attention_block does after Wo (src/model/forward.rs:345-350).
  * w: rows x cols/256 GGUF blocks (144 bytes for Q4_K, 210 for Q6_K), act
  * [n][cols], out and residual [n][rows] f32, all device pointers on the
- * context's stream; residual may equal out.  cols must be a multiple of 256.
+ * context's stream; residual may equal out.  cols must be a multiple of 256,
+ * and Q4_K blocks must start 16-byte aligned.
  * Each output is the reference's scalar block dot (src/kernels.rs:228-347),
  * operation for operation. */
 int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,

@@ -89,3 +89,6 @@ def test_qmatmul_rejects_bad_shapes(dev):
         dr.qmatmul(dev.ctx, 13, dev.put(w), 1, 256, dev.put(x), 1, out)  # Q5_K: not built
     with pytest.raises(dr.DrError):
         dr.qmatmul(dev.ctx, orc.WTYPE_Q4K, dev.put(w), 1, 200, dev.put(x), 1, out)  # cols % 256
+    w2 = dev.put(np.zeros(160, np.uint8))
+    with pytest.raises(dr.DrError):  # Q4_K blocks off a 16-byte boundary
+        dr.qmatmul(dev.ctx, orc.WTYPE_Q4K, w2.data_ptr() + 4, 1, 256, dev.put(x), 1, out)
