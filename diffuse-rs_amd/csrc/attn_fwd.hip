@@ -52,157 +52,13 @@
 // (16 B per lane) free of bank conflicts.  Q is loaded once per workgroup
 // (coalesced f32 rows, RMS-normalised when asked, scaled, rounded to bf16)
 // into the LDS of the last pipeline stage, before that stage is first used.
-#include "dr_internal.hpp"
+#include "attn_common.hpp"
 
 #include <limits.h>
 #include <math.h>
 
 namespace dr {
 namespace {
-
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int BN = 32;                     // keys per tile (one MFMA key block)
-static_assert(BN == VT_KEYS, "a key tile is one V^T tile of the cache");
-constexpr float RESCALE_THRESHOLD = 8.0f;  // log2 units
-
-// 16-byte-chunk swizzle for an LDS row holding CH chunks.  Keeps 8 (32-bank
-// LDS) or 16 (64-bank LDS) consecutive rows read at the same logical chunk on
-// distinct banks.
-template <int CH>
-__device__ __forceinline__ int swz(int row) {
-    if constexpr (CH >= 16) {
-        return row & 15;
-    } else if constexpr (CH == 8) {
-        return (row & 7) ^ ((row >> 3) & 1);
-    } else {
-        static_assert(CH == 4, "unsupported row width");
-        return ((row >> 1) ^ (row >> 3)) & 3;
-    }
-}
-
-// RoPE's rotation of one pair (ops.rs:447-448), without fused multiply-adds
-// as Rust evaluates it.
-__device__ __forceinline__ float rope_lo(float a, float b, float sn, float cs) {
-#pragma clang fp contract(off)
-    return a * cs - b * sn;
-}
-__device__ __forceinline__ float rope_hi(float a, float b, float sn, float cs) {
-#pragma clang fp contract(off)
-    return a * sn + b * cs;
-}
-
-// Key offset (within a 32-key block) stored in LDS row R of the block.  The
-// MFMA puts A-row R in accumulator slot i of lane half hf with
-// R = 8*(i/4) + 4*hf + (i%4); sigma(R) = 16*hf + i places key 16*hf + i there.
-__device__ __forceinline__ int sigma(int R) {
-    return 16 * ((R >> 2) & 1) + 4 * (R >> 3) + (R & 3);
-}
-
-// The same for 16-row waves (16x16x32 MFMA, two 16-key blocks b): A-row R
-// of block b lands in accumulator slot i of lane group g with R = 4*g + i,
-// and the PV product wants lane group g to hold keys 8*g .. 8*g + 7, so
-// kappa(16*b + 4*g + i) = 8*g + 4*b + i.
-__device__ __forceinline__ int kappa(int R) {
-    return 8 * ((R & 15) >> 2) + 4 * (R >> 4) + (R & 3);
-}
-template <bool W16>
-__device__ __forceinline__ int kperm(int R) {
-    if constexpr (W16)
-        return kappa(R);
-    else
-        return sigma(R);
-}
-
-// visible() of attention.rs:36-57, evaluated without branches (bitwise
-// and/or of the three rules) so the per-element mask is a straight-line
-// compare + select; a short-circuit version compiled into divergent control
-// flow that lost masked elements.
-__device__ __forceinline__ bool visible(int qpos, int kpos, int qseq, int kseq, int window,
-                                        int prefix) {
-    const bool same_seq = qseq == kseq;
-    const bool in_band = (window < 0) | (abs(qpos - kpos) < window);
-    const bool causal_ok = (prefix < 0) | (qpos >= prefix) | (kpos <= qpos);
-    return same_seq & in_band & causal_ok;
-}
-
-// Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit
-// data format, no swizzle).  Loads at offsets >= bytes return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-
-// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane i
-// reads rsrc + soff + voff and writes lds_base + 16*i.  Kept in a __device__
-// helper: used directly in a kernel body, an LDS-DMA builtin made the host
-// compilation pass drop the kernel's launch stub.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds_base, int voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
-                                             16, voff, soff, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Waits until at most `pending` super-tiles (each NI vector-memory
-// instructions) issued after the current one are still in flight.
-template <int NI, int NS>
-__device__ __forceinline__ void wait_tiles(int pending) {
-    if constexpr (NS >= 4) {
-        if (pending >= 2) {
-            wait_vmcnt<2 * NI>();
-            return;
-        }
-    }
-    if constexpr (NS >= 3) {
-        if (pending >= 1) {
-            wait_vmcnt<NI>();
-            return;
-        }
-    }
-    wait_vmcnt<0>();
-}
-
-// (head in group, query index) of packed row r = hg * nq + qi.  MHA rows are
-// the queries themselves; otherwise a float reciprocal estimate (exact to +-1
-// for r < 2^24) is corrected once, instead of an integer division.
-__device__ __forceinline__ void row_split(int r, int nq, float inv_nq, int group, int& hg,
-                                          int& qi) {
-    if (group == 1) {
-        hg = 0;
-        qi = r;
-        return;
-    }
-    int h = (int)((float)r * inv_nq);
-    int q = r - h * nq;
-    if (q < 0) {
-        --h;
-        q += nq;
-    } else if (q >= nq) {
-        ++h;
-        q -= nq;
-    }
-    hg = h;
-    qi = q;
-}
-
-// n / d for the workgroup decode: mul-high by m = ceil(2^32 / d), exact when
-// n * d < 2^32 (the host passes m = 0 where that is not guaranteed).
-__device__ __forceinline__ int udiv(int n, int d, uint32_t m) {
-    return m ? (int)__umulhi((uint32_t)n, m) : n / d;
-}
-
-__device__ __forceinline__ float max3(float a, float b, float c) {
-    return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
-}
 
 template <int HD, int RB, int KQ, int NS, int NP, bool W16 = false>
 struct Geometry {
@@ -1824,16 +1680,55 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 }  // namespace
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, bool qepi, int n_cu, int force_rb, int force_kq,
-                          int force_split, int force_rows) {
+                          int mask, int qepi, int n_cu, int force_rb, int force_kq,
+                          int force_split, int force_rows, int force_kernel) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
     p.block_n = BN;
     p.mask = mask;
-    p.qepi = qepi;  // (no key-masked build carries the Q epilogue: its launch fails)
+    p.qepi = qepi != QEPI_NONE;  // (no key-masked build carries the Q epilogue: its launch fails)
+    p.kernel = KERNEL_STAGED;
     const int cus = n_cu > 0 ? n_cu : 256;
     const int row_blocks = (group * max_nq + 31) / 32;  // per (batch, kv head)
     const int ntiles = (max_nk + BN - 1) / BN;
+    // Head dim exactly 128 without per-key metadata and without the Q bias /
+    // RoPE: the per-wave key streams of attn_ring_kernel (one 32-row block
+    // per workgroup, 8 key groups).  A 32-row workgroup pulls every K/V byte
+    // of its key range through its CU's L2 link (64 B/clk), so the call is
+    // bound by that stream; independent per-wave DMA keeps it nearer that
+    // rate than the staged kernel's shared super-tiles.  When one-block
+    // workgroups would take more than one round of the CUs (C3's GQA rows:
+    // 448 blocks on 256 CUs), the staged kernel's 64-row workgroups read
+    // each K/V tile once for twice the rows and win, so it keeps them.
+    const int ring_blocks = n_batch * n_head_kv * row_blocks;
+    const bool ring_ok = hd == 128 && mask != MASK_KEYS && qepi != QEPI_FULL;
+    const bool ring_auto = ring_blocks <= cus;
+    if (ring_ok && (force_kernel == KERNEL_STREAMS || (force_kernel == KERNEL_AUTO && ring_auto)) &&
+        force_rb <= 0 && force_kq <= 0 && force_rows <= 0) {
+        p.kernel = KERNEL_STREAMS;
+        p.rb = 1;
+        p.kq = 8;
+        p.w16 = false;
+        p.waves = 8;
+        p.stages = 1;
+        p.qepi = false;  // the Q norm is a runtime operand of the kernel
+        p.rowgroups = row_blocks < 1 ? 1 : row_blocks;
+        const int base = n_batch * n_head_kv * p.rowgroups;
+        int split = 1;
+        if (force_split > 0) {
+            split = force_split;
+        } else if (2 * base <= cus) {
+            // too few workgroups for the CUs: split the keys, keeping a tile
+            // for each of a split's waves
+            split = cus / base;
+            const int max_split = ntiles / 8 > 1 ? ntiles / 8 : 1;
+            if (split > max_split) split = max_split;
+        }
+        if (split < 1) split = 1;
+        p.n_split = split;
+        p.n_workgroups = base * split;
+        return p;
+    }
     // Head dims up to 128: one row block of four key groups with four DMA
     // waves (two waves per SIMD).  256: two row blocks of two key groups,
     // one 32-row wave per SIMD (the accumulators need the whole register
@@ -1928,7 +1823,7 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.mg_rowgroups = div_magic(a.rowgroups, p.n_workgroups);
     a.mg_hkv = div_magic(a.n_head_kv, p.n_workgroups);
     a.part_rows = p.rowgroups * p.rb * 32;
-    hipError_t e = launch_shape(p, a, st);
+    hipError_t e = p.kernel == KERNEL_STREAMS ? launch_ring(p, a, st) : launch_shape(p, a, st);
     if (e != hipSuccess || p.n_split <= 1) return e;
     const size_t items = (size_t)a.n_batch * a.n_head_kv * a.part_rows * (p.hd_tile / 4);
     const dim3 grid((unsigned)((items + 255) / 256));

@@ -1,0 +1,578 @@
+// attn_ring.hip -- denoise-step attention at head dim 128 with per-wave key
+// streams (gfx950, MI355X).
+//
+// Computes the reference's attention() (src/model/attention.rs:101-186) for
+// one row block of 32 query rows per workgroup: every (query row, head) of the
+// block against the keys visible to it (visible(), :36-57), with an online
+// softmax.  Same operands, cache layout and numerics as attn_fwd_kernel; the
+// difference is how the K/V stream reaches the matrix cores.
+//
+// A workgroup of 32 query rows reads every K/V byte of its key range from L2
+// once, 384 KB per call at LLaDA-8B's 768 keys, so the L2 -> CU stream (64 B
+// per clock per CU on MI355X) bounds the call, not the MFMAs.  The stream
+// reaches that rate only with several waves issuing loads independently.
+// So each of the workgroup's 8 waves is a key group of its own: wave w owns the
+// 32-key tiles w, w + 8, w + 16, ... of the range and runs all 32 query rows
+// against them.  It moves each of its tiles into its own slice of LDS with
+// buffer_load ... lds (K tile and V^T tile in separate 8 KB buffers) and
+// waits on its own vmcnt, so no workgroup barrier sits in the key loop.  The
+// next K tile is requested as soon as the QK^T product has read the current
+// one, the next V^T tile as soon as the PV product has.  The 8 partial softmax
+// states of each row are merged through LDS at the end, which also stages
+// coalesced full-row output stores.
+//
+// Per wave and tile (32 keys x 32 query rows), on v_mfma_f32_32x32x16_bf16:
+//   S^T = K Q^T - m   A = K (LDS rows permuted by sigma), B = Q^T (registers)
+//   O^T += V^T P^T    A = V^T (LDS), B = P^T straight from the S^T registers
+// Lane (col, half) owns query row col and keys 16*half .. 16*half + 15 of the
+// tile, so the softmax row statistics need one exchange with lane ^ 32.
+// Softmax runs in the log2 domain with the lazily moved maximum of
+// attn_fwd.hip (m moves only when a score exceeds it by more than 8); l sums
+// the bf16-rounded p that the PV product multiplies.  A row with no visible
+// key ends with l = 0 and writes NaN, as attention.rs:181-185 does.
+#include "attn_common.hpp"
+
+#include <limits.h>
+#include <math.h>
+
+namespace dr {
+namespace {
+
+constexpr int RW = 8;             // waves (key groups) per workgroup
+constexpr int RHD = 128;          // head dim of the kernel
+constexpr int RT = BN * RHD;      // bf16 elements per K tile (and per V^T tile)
+constexpr int R_KCH = RHD / 8;    // 16-byte chunks per K row
+constexpr int R_VCH = BN / 8;     // 16-byte chunks per V^T row
+constexpr int RING_BYTES = RW * 2 * RT * 2;           // per wave: K tile + V^T tile
+constexpr int Q_BYTES = 32 * RHD * 2;                 // the block's Q rows, bf16
+constexpr int ML_OFF = RING_BYTES + Q_BYTES;          // [RW][32] max, then [RW][32] sum
+constexpr int RING_LDS = ML_OFF + 2 * RW * 32 * 4;
+static_assert(32 * RHD * 4 == 2 * RT * 2, "a wave's O^T partial fills its K + V^T buffers");
+static_assert(RING_LDS <= 160 * 1024, "LDS budget");
+
+template <int MODE>
+__global__ __launch_bounds__(RW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_ring_kernel(const AttnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    __shared__ int s_red[3];
+
+    AttnSlot S = a.slot[0];
+    const float* qn_w = a.qn_w;
+    asm volatile("" : "+s"(S.q), "+s"(S.out), "+s"(S.qpos), "+s"(S.qseq), "+s"(S.qprefix),
+                 "+s"(S.k), "+s"(S.vt), "+s"(S.nq), "+s"(S.nk), "+s"(S.qpos_sorted), "+s"(qn_w)
+                 : "s"(a.n_batch), "s"(a.n_head_kv), "s"(a.group), "s"(a.cap),
+                   "s"(a.q_rstride), "s"(a.rowgroups), "s"(a.n_split), "s"(a.mg_split),
+                   "s"(a.mg_rowgroups), "s"(a.mg_hkv), "s"(a.c), "s"(a.n_wg), "s"(a.window),
+                   "s"(a.prefix));
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, hf = lane >> 5;
+
+    // Workgroup -> (batch, kv head, row group, split); consecutive logical
+    // ids (the row groups of one kv head) share an XCD and its L2.
+    const int nwg = a.n_wg;
+    const int hw = blockIdx.x;
+    const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
+    int split = 0, rg, b = 0, g;
+    if (a.n_split == 1 && a.n_batch == 1) {
+        g = udiv(lid, a.rowgroups, a.mg_rowgroups);
+        rg = lid - g * a.rowgroups;
+    } else {
+        const int q1 = udiv(lid, a.n_split, a.mg_split);
+        split = lid - q1 * a.n_split;
+        const int q2 = udiv(q1, a.rowgroups, a.mg_rowgroups);
+        rg = q1 - q2 * a.rowgroups;
+        b = udiv(q2, a.n_head_kv, a.mg_hkv);
+        g = q2 - b * a.n_head_kv;
+        if (a.n_batch > 1) S = a.slot[b];
+    }
+
+    const int rows_total = a.group * S.nq;
+    const int wg_row0 = rg * 32;
+    if (wg_row0 >= rows_total) return;  // uniform over the workgroup and all its splits
+    const float inv_nq = __builtin_amdgcn_rcpf((float)S.nq);
+    // (head in group, query index) of packed row r; MHA rows are the queries
+    auto split_row = [&](int r, int& hgo, int& qio) __attribute__((always_inline)) {
+        if (a.group == 1) {
+            hgo = 0;
+            qio = r;
+        } else {
+            row_split(r, S.nq, inv_nq, a.group, hgo, qio);
+        }
+    };
+
+    // ---- Q rows first: they gate the first MFMA.  Thread tid holds f32x4
+    // pieces d0 and d0 + 64 of workgroup row tid / 16 (rows past the block
+    // load row 0 and are zeroed later: no branch, so nothing issued below
+    // waits for these loads).
+    const int qlr = tid >> 4;
+    const int qd0 = (tid & 15) * 4;
+    const int qr = wg_row0 + qlr;
+    const bool qok = qr < rows_total;
+    f32x4 xq[2], wq[2];
+    {
+        int qhg, qqi;
+        split_row(qok ? qr : 0, qhg, qqi);
+        const float* qrow = static_cast<const float*>(S.q) + (size_t)qqi * a.q_rstride +
+                            (size_t)(g * a.group + qhg) * RHD;
+        xq[0] = gload<f32x4>(qrow + qd0);
+        xq[1] = gload<f32x4>(qrow + qd0 + 64);
+        if (qn_w) {  // the QK-norm gains of these dims
+            wq[0] = gload<f32x4>(qn_w + qd0);
+            wq[1] = gload<f32x4>(qn_w + qd0 + 64);
+        }
+    }
+
+    // ---- the query row of this lane's column, its mask state, and the
+    // workgroup's key-tile range (MASK_POS: the band its rows can see)
+    const int r = wg_row0 + col;
+    const bool rvalid = r < rows_total;
+    int hg = 0, qi = 0;
+    if (rvalid) split_row(r, hg, qi);
+    int kt_lo = 0, kt_hi = (S.nk + BN - 1) / BN;
+    int my_qpos = 0, my_qseq = 0, my_pref = -1;
+    int qmin = 0, qmax = 0;
+    bool tiles_can_be_full = MODE == MASK_NONE;
+    if constexpr (MODE == MASK_POS) {
+        my_qpos = gload<int>(S.qpos + (rvalid ? qi : 0));
+        if (S.qseq) my_qseq = gload<int>(S.qseq + (rvalid ? qi : 0));
+        my_pref = S.qprefix ? (rvalid ? gload<int>(S.qprefix + qi) : -1) : a.prefix;
+        bool prefix_free;
+        if (S.qpos_sorted && S.qprefix == nullptr) {
+            // ascending positions: the extremes sit at the ends of the block
+            // (the whole pass if it spans heads), read with scalar loads
+            const int r1 = min(wg_row0 + 32, rows_total) - 1;
+            const int h0 = wg_row0 / S.nq, h1 = r1 / S.nq;
+            const int lo = h0 == h1 ? wg_row0 - h0 * S.nq : 0;
+            const int hi = h0 == h1 ? r1 - h0 * S.nq : S.nq - 1;
+            qmin = *(const __attribute__((address_space(4))) int*)(S.qpos + lo);
+            qmax = *(const __attribute__((address_space(4))) int*)(S.qpos + hi);
+            prefix_free = a.prefix < 0 || qmin >= a.prefix;
+        } else {
+            int vmin = rvalid ? my_qpos : INT_MAX;
+            int vmax = rvalid ? my_qpos : INT_MIN;
+            int pref_row = (rvalid && my_pref >= 0 && my_qpos < my_pref) ? 1 : 0;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                vmin = min(vmin, __shfl_xor(vmin, off));
+                vmax = max(vmax, __shfl_xor(vmax, off));
+                pref_row |= __shfl_xor(pref_row, off);
+            }
+            // every wave holds the same 32 rows: wave 0's reduction is the workgroup's
+            if (wave == 0 && lane == 0) {
+                s_red[0] = vmin;
+                s_red[1] = vmax;
+                s_red[2] = pref_row;
+            }
+            __syncthreads();
+            qmin = s_red[0];
+            qmax = s_red[1];
+            prefix_free = s_red[2] == 0;
+        }
+        tiles_can_be_full = prefix_free && S.qseq == nullptr;
+        if (a.window >= 0) {
+            const long lo = max(0L, (long)qmin - a.window + 1);
+            const long hi = min((long)S.nk, (long)qmax + a.window);
+            if (hi <= lo) {
+                kt_lo = kt_hi = 0;
+            } else {
+                kt_lo = (int)(lo / BN);
+                kt_hi = (int)((hi + BN - 1) / BN);
+            }
+        }
+    }
+    int t0 = kt_lo, t1 = kt_hi;
+    if (a.n_split > 1) {
+        const int ntiles = kt_hi - kt_lo;
+        const int per = (ntiles + a.n_split - 1) / a.n_split;
+        t0 = kt_lo + min(split * per, ntiles);
+        t1 = kt_lo + min((split + 1) * per, ntiles);
+    }
+    const int nt = t1 - t0;  // tiles of this workgroup: t0 + j, j < nt
+
+    // ---- the K / V^T planes of kv head g, and this wave's DMA offsets.
+    // K tile t is rows [32t, 32t + 32) of [cap][128]; the V^T tile of the
+    // same keys is the 128 x 32 block at the same byte offset of the V^T
+    // plane.  LDS row R of a K tile holds key sigma(R) with its 16-byte
+    // chunks XOR-swizzled by R, V^T row d its chunks swizzled by d; lane i of
+    // DMA instruction j fills LDS chunk 64 j + i, so it reads the global
+    // chunk that belongs there.  Each instruction reads 1 KB of whole rows.
+    const uint32_t plane_bytes = (uint32_t)a.cap * RHD * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k + (size_t)g * a.cap * RHD, plane_bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vt + (size_t)g * RHD * a.cap, plane_bytes);
+    int kvo[8], vvo[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int idx = j * 64 + lane;
+        const int R = idx / R_KCH, pk = idx % R_KCH;
+        kvo[j] = (sigma(R) * RHD + ((pk ^ swz<R_KCH>(R)) << 3)) * 2;
+        const int d = idx / R_VCH, pv = idx % R_VCH;
+        vvo[j] = (d * BN + ((pv ^ swz<R_VCH>(d)) << 3)) * 2;
+    }
+    uint16_t* const kbuf = smem + wave * 2 * RT;
+    uint16_t* const vbuf = kbuf + RT;
+    auto issue_k = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16(rk, kbuf + j * 512, kvo[j], t * (BN * RHD * 2));
+    };
+    auto issue_v = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16(rv, vbuf + j * 512, vvo[j], t * (BN * RHD * 2));
+    };
+    auto issue_v_to_k = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16(rv, kbuf + j * 512, vvo[j], t * (BN * RHD * 2));
+    };
+    // Wave w takes tiles t0 + w, t0 + w + RW, ...: a fixed assignment, so
+    // every call sums each row's keys in the same order (bit-identical
+    // results run to run; claiming tiles dynamically balanced the waves'
+    // finishing times but made the summation order depend on timing).
+    // (The first DMA is issued even when the wave has no tile: past the
+    // range the descriptor's bounds check returns zeros.)
+    issue_k(t0 + wave);
+    issue_v(t0 + wave);
+
+    // QK-norm (rms_norm_inplace, ops.rs:106-114): f32 squares summed in f64
+    // over the 16 lanes of the row, then x * scale * w.
+    if (qn_w) {
+        double ss = 0.0;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sq = xq[p][e] * xq[p][e];
+                ss += (double)sq;
+            }
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off);
+        const float sc = 1.0f / (float)sqrt(ss / (double)RHD + (double)a.qn_eps);
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
+                xq[p][e] = xq[p][e] * sc * wq[p][e];
+            }
+    }
+    uint16_t* const qs = smem + RING_BYTES / 2;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int d = qd0 + 64 * p;
+        bf16x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (__bf16)(qok ? xq[p][e] * a.c : 0.0f);
+        *reinterpret_cast<bf16x4*>(qs + qlr * RHD + (((d >> 3) ^ swz<R_KCH>(qlr)) << 3) + (d & 7)) = y;
+    }
+    lds_barrier();  // (the first K/V tiles stay in flight)
+    // Q^T fragments, held for the whole key loop: lane (col, hf) supplies
+    // row col, dims 16 c + 8 hf .. + 8 of contraction step c
+    bf16x8 qf[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        qf[c] = *reinterpret_cast<const bf16x8*>(qs + col * RHD + (((2 * c + hf) ^ swz<R_KCH>(col)) << 3));
+
+    f32x16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+    float mu = 0.0f;        // running max m (log2 units), valid once m_set
+    bool m_set = false;
+    float thr = -INFINITY;  // a score above mu + thr moves m
+    float l_acc = 0.0f;     // this lane's share (its 16 keys per tile) of the row's sum
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+    // V^T fragments of a tile: lane (col, hf) supplies row d = 32 db + col,
+    // keys 16 hf + 8 sl .. + 8 of key slice sl (the P^T slice it holds)
+    auto read_v = [&](const uint16_t* vsrc, bf16x8 (&vf)[4][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 32 * db + col;
+            const uint16_t* vrow = vsrc + d * BN;
+            const int sw = swz<R_VCH>(d);
+            vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
+            vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
+        }
+    };
+    auto pv = [&](const bf16x8 (&vf)[4][2], const bf16x8 (&pp)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pp[0], o[db], 0, 0, 0);
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pp[1], o[db], 0, 0, 0);
+        }
+    };
+
+    // Software pipeline over this wave's tiles: step i runs QK^T of tile i
+    // and its softmax, and the PV product of tile i - 1 interleaved with the
+    // exponentials (one MFMA per few VALU instructions, in one basic block),
+    // so the matrix core and the VALU overlap inside the wave.  O holds tile
+    // i - 1's product relative to the max before tile i; it is rescaled
+    // after that product when tile i moves the max.  DMA order: K0 V0 | K1 |
+    // K2 V1 | K3 V2 | ... (the next K tile once QK^T has read the buffer, the
+    // next V^T tile once PV has); the last tile's V^T goes to the K buffer as
+    // soon as its QK^T has read that, so its latency overlaps the last
+    // softmax instead of trailing it.  Step 0 has no PV and is peeled off.
+    f32x16 negm;  // -m in every slot: the accumulator input of QK^T
+#pragma unroll
+    for (int e = 0; e < 16; ++e) negm[e] = 0.0f;
+    // S^T = K Q^T - m of the tile in the K buffer
+    auto qk = [&]() __attribute__((always_inline)) {
+        const uint16_t* krow = kbuf + col * RHD;
+        const int sw = swz<R_KCH>(col);
+        f32x16 sacc = negm;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            bf16x8 kf[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                kf[c] = *reinterpret_cast<const bf16x8*>(krow + (((2 * (4 * h + c) + hf) ^ sw) << 3));
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c], qf[4 * h + c], sacc, 0, 0, 0);
+        }
+        return sacc;
+    };
+    // masking, and the lazily moved max: returns whether m moved (then O
+    // must be scaled by alpha once the pending PV product is in)
+    auto mask_and_max = [&](f32x16& sv, int tt, float& alpha) __attribute__((always_inline)) {
+        // slot e is key 32 tt + 16 hf + e
+        const int kbase = tt * BN;
+        bool full = kbase + BN <= S.nk;
+        if constexpr (MODE == MASK_POS) {
+            const bool win_ok =
+                a.window < 0 || (qmax - kbase < a.window && kbase + BN - 1 - qmin < a.window);
+            full = full && tiles_can_be_full && win_ok;
+        }
+        if (!full) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int kidx = kbase + 16 * hf + e;
+                bool vis = kidx < S.nk;
+                if constexpr (MODE == MASK_POS)
+                    vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                sv[e] = vis ? sv[e] : -INFINITY;
+            }
+        }
+        float mx = max3(sv[0], sv[1], sv[2]);
+        mx = max3(mx, sv[3], sv[4]);
+        mx = max3(mx, sv[5], sv[6]);
+        mx = max3(mx, sv[7], sv[8]);
+        mx = max3(mx, sv[9], sv[10]);
+        mx = max3(mx, sv[11], sv[12]);
+        mx = max3(mx, sv[13], sv[14]);
+        mx = __builtin_fmaxf(mx, sv[15]);
+        const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+        alpha = 1.0f;
+        if (moved) {
+            const float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+            const bool upd = cm > thr;
+            const float delta = upd ? cm : 0.0f;
+            alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+            mu += delta;
+            m_set = m_set | upd;
+            thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                sv[e] -= delta;
+                negm[e] = -mu;
+            }
+            l_acc *= alpha;
+        }
+        return moved;
+    };
+    // p = exp2(s) rounded to bf16 in pairs (P^T slice sl = slots 8 sl ..
+    // 8 sl + 7), l += the rounded p
+    auto softmax_p = [&](const f32x16& sv, u32x4 (&pw)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bf16x2 pr = {(__bf16)__builtin_amdgcn_exp2f(sv[8 * sl + 2 * j]),
+                                   (__bf16)__builtin_amdgcn_exp2f(sv[8 * sl + 2 * j + 1])};
+                pw[sl][j] = __builtin_bit_cast(uint32_t, pr);
+                l_acc = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_acc, false);
+            }
+    };
+    // (keeps p and l computed before this point: the exponentials stay in
+    // the block of the PV product they are interleaved with)
+    auto pin = [&](const u32x4 (&pw)[2]) __attribute__((always_inline)) {
+        asm volatile("" ::"v"(pw[0][0]), "v"(pw[0][1]), "v"(pw[0][2]), "v"(pw[0][3]), "v"(pw[1][0]),
+                     "v"(pw[1][1]), "v"(pw[1][2]), "v"(pw[1][3]), "v"(l_acc));
+    };
+
+    u32x4 pprev[2];
+    bool last_in_k = false;  // the last tile's V^T is in the K buffer
+    int t = wave < nt ? t0 + wave : -1;  // the current tile (uniform over the wave)
+    if (t >= 0) {
+        // step 0: K tile 0 has landed when only V^T tile 0 is outstanding
+        wait_vmcnt<8>();
+        f32x16 sv = qk();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const int tn = t + RW < t1 ? t + RW : -1;
+        if (tn >= 0) issue_k(tn);
+        float alpha;
+        mask_and_max(sv, t, alpha);  // (O is still zero: no rescale)
+        softmax_p(sv, pprev);
+        t = tn;
+    }
+    for (int i = 1; t >= 0; ++i) {
+        // K tile i has landed: outstanding after it is V^T tile i - 1 (8
+        // instructions), except at i = 1, where V^T 0 was issued before K 1
+        if (i == 1)
+            wait_vmcnt<0>();
+        else
+            wait_vmcnt<8>();
+        f32x16 sv = qk();
+        // every K fragment is in registers: the K buffer takes the next tile,
+        // or this last tile's V^T
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const int tn = t + RW < t1 ? t + RW : -1;
+        if (tn >= 0)
+            issue_k(tn);
+        else
+            issue_v_to_k(t);
+        // V^T tile i - 1 (the pending PV product's operand) has landed: after
+        // it only the DMA just issued is outstanding
+        wait_vmcnt<8>();
+        bf16x8 vf[4][2];
+        read_v(vbuf, vf);
+        float alpha;
+        const bool moved = mask_and_max(sv, t, alpha);
+        // the PV product of tile i - 1, interleaved with tile i's exponentials
+        u32x4 pcur[2];
+        softmax_p(sv, pcur);
+        {
+            const bf16x8 pp[2] = {__builtin_bit_cast(bf16x8, pprev[0]), __builtin_bit_cast(bf16x8, pprev[1])};
+            pv(vf, pp);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
+        }
+        pin(pcur);
+        __builtin_amdgcn_sched_barrier(0);
+        if (moved) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        }
+        pprev[0] = pcur[0];
+        pprev[1] = pcur[1];
+        // the V^T buffer is free once its fragments are in registers: it
+        // takes this tile's V^T (the last tile's went to the K buffer)
+        if (tn >= 0) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue_v(t);
+        }
+        last_in_k = true;
+        t = tn;
+    }
+    // the last tile's PV product (a wave without tiles multiplies zeros)
+    wait_vmcnt<0>();
+    {
+        bf16x8 vf[4][2];
+        read_v(last_in_k ? kbuf : vbuf, vf);
+        const bf16x8 pp[2] = {wave < nt ? __builtin_bit_cast(bf16x8, pprev[0]) : bf16x8{},
+                              wave < nt ? __builtin_bit_cast(bf16x8, pprev[1]) : bf16x8{}};
+        pv(vf, pp);
+    }
+
+    // ---- merge the RW key groups of each row.  A wave's K and V^T buffers
+    // are its own and free once its last PV product has read them: its O^T
+    // (32 rows x 128 f32, 16 KB) goes there right away, while other waves
+    // may still be in their loops, with (m, l) beside the other rows'
+    // statistics.  After one barrier every thread finishes a row: wave w's
+    // partial is weighted by exp2(m_w - M), M the row's largest m, and
+    // O = sum_w w_w O_w / sum_w w_w l_w.  16-byte chunk c of row q sits at
+    // chunk c ^ q of its 512-byte row, so both the writes (lanes spread over
+    // rows) and the reads (lanes spread over chunks) hit distinct banks.
+    float* const sm = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + ML_OFF);  // [RW][32]
+    float* const sl = sm + RW * 32;                                                    // [RW][32]
+    const float l_tot = l_acc + __shfl_xor(l_acc, 32);
+    if (hf == 0) {
+        sm[wave * 32 + col] = m_set ? mu : -INFINITY;
+        sl[wave * 32 + col] = l_tot;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (the last V^T fragments are read)
+    {
+        // o[db][e] is O^T[d = 32 db + 8 (e / 4) + 4 hf + e % 4][col]: chunk
+        // 8 db + 2 (e / 4) + hf of row col
+        float* myrow = reinterpret_cast<float*>(kbuf) + col * RHD;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(myrow + 4 * ((8 * db + 2 * j + hf) ^ col)) =
+                    f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
+    }
+    lds_barrier();
+    // thread tid: row rr = tid / 16, chunks ch and ch + 16
+    {
+        const int rr = tid >> 4, ch = tid & 15;
+        const int row = wg_row0 + rr;
+        if (row < rows_total) {
+            float mw[RW];
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < RW; ++w) {
+                mw[w] = sm[w * 32 + rr];
+                M = __builtin_fmaxf(M, mw[w]);
+            }
+            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+            float L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < RW; ++w) {
+                const float wt = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+                const float* prow = reinterpret_cast<const float*>(smem + w * 2 * RT) + rr * RHD;
+                acc0 += wt * *reinterpret_cast<const f32x4*>(prow + 4 * (ch ^ rr));
+                acc1 += wt * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + 16) ^ rr));
+                L += wt * sl[w * 32 + rr];
+            }
+            if (a.n_split > 1) {
+                // this split's partial row, for split_merge_kernel: the sum
+                // relative to the row max M, and (M, L)
+                const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
+                const size_t prow =
+                    (size_t)split * plane + (size_t)(b * a.n_head_kv + g) * a.part_rows + row;
+                gstore(a.part_o + prow * RHD + 4 * ch, acc0);
+                gstore(a.part_o + prow * RHD + 4 * (ch + 16), acc1);
+                if (ch == 0) gstore(a.part_ml + prow * 2, make_float2(M, L));
+            } else {
+                int ohg, oqi;
+                split_row(row, ohg, oqi);
+                float* orow = S.out + (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
+                const float il = __builtin_amdgcn_rcpf(L);
+                gstore(orow + 4 * ch, acc0 * il);
+                gstore(orow + 4 * (ch + 16), acc1 * il);
+            }
+        }
+    }
+}
+
+template <int MODE>
+hipError_t launch_ring_mode(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    static bool attr_set = false;
+    auto fn = attn_ring_kernel<MODE>;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, RING_LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(RW * 64), RING_LDS, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    if (p.hd_tile != RHD || a.hd != RHD || p.act || a.qb || a.rope) return hipErrorInvalidValue;
+    switch (p.mask) {
+        case MASK_NONE: return launch_ring_mode<MASK_NONE>(p, a, st);
+        case MASK_POS: return launch_ring_mode<MASK_POS>(p, a, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace dr

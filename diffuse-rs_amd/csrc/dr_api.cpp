@@ -95,6 +95,7 @@ struct dr_ctx {
     int force_kq = 0;
     int fused_step = 0;  // dr_attention_step may run the fused kernel
     int force_rows = 0;  // query rows per compute wave (0: automatic)
+    int force_kernel = 0;  // dr::KernelKind (0: automatic)
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials
@@ -268,6 +269,7 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
     info->key_groups = ctx->last.kq;
     info->fused_step = ctx->last.act ? 1 : 0;
     info->rows_per_wave = ctx->last.w16 ? 16 : 32;
+    info->kernel = ctx->last.kernel;
     return DR_OK;
 }
 
@@ -282,6 +284,14 @@ int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows) {
     if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_wave_rows: ctx is NULL");
     if (rows != 0 && rows != 16 && rows != 32) return fail(DR_ERR_INVALID, "rows %d not 0, 16 or 32", rows);
     ctx->force_rows = rows;
+    return DR_OK;
+}
+
+int dr_ctx_set_kernel(dr_ctx* ctx, int kernel) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_kernel: ctx is NULL");
+    if (kernel < DR_KERNEL_AUTO || kernel > DR_KERNEL_STREAMS)
+        return fail(DR_ERR_INVALID, "kernel %d not DR_KERNEL_AUTO, _STAGED or _STREAMS", kernel);
+    ctx->force_kernel = kernel;
     return DR_OK;
 }
 
@@ -822,10 +832,10 @@ int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
 // ---------------------------------------------------------------- attention
 
 static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int max_nq,
-                               int max_nk, int mask, bool qepi) {
+                               int max_nk, int mask, int qepi) {
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
                               ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
-                              ctx->force_rows);
+                              ctx->force_rows, ctx->force_kernel);
 }
 
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
@@ -842,7 +852,7 @@ static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
 }
 
 static int launch_planned(dr_ctx* ctx, dr::AttnArgs& a, int hd, int max_nq, int max_nk,
-                          int mask, bool qepi) {
+                          int mask, int qepi) {
     return launch_plan(ctx, a, plan_for(ctx, a, hd, max_nq, max_nk, mask, qepi));
 }
 
@@ -927,7 +937,8 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
     if (max_nq == 0) return DR_OK;
     DR_CHECK(use_device(cache->ctx));
     return launch_planned(cache->ctx, a, a.hd, max_nq, (int)cache->n_total,
-                          mask_of(sliding_window, causal_prefix), q_norm_w != nullptr);
+                          mask_of(sliding_window, causal_prefix),
+                          q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
 }
 
 int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* items,
@@ -950,7 +961,8 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
     DR_CHECK(use_device(cache->ctx));
     const int mask = mask_of(sliding_window, causal_prefix);
     dr_ctx* ctx = cache->ctx;
-    dr::LaunchPlan p = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, q_norm_w != nullptr);
+    const int qepi = q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE;
+    dr::LaunchPlan p = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
     // The fused kernel is built for one row block of 32-row waves and four
     // key groups with their DMA waves; when asked for, plan that shape too
     // (p stays the plan of the unfused store + attention).
@@ -960,7 +972,7 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
         ctx->force_rb = 1;
         ctx->force_kq = 4;
         if (rows_saved == 0) ctx->force_rows = 32;
-        pf = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, q_norm_w != nullptr);
+        pf = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
         ctx->force_rb = ctx->force_kq = 0;
         ctx->force_rows = rows_saved;
     }
@@ -1039,8 +1051,8 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
     a.rope = rope ? rope->d_table : nullptr;
     a.rot = rope ? (int)rope->rope_dim : 0;
     const int mask = mask_of(sliding_window, causal_prefix);
-    dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask,
-                                epi->q_norm_w || epi->bq || rope);
+    const int qepi = (epi->bq || rope) ? dr::QEPI_FULL : (epi->q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
+    dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
     return launch_plan(cache->ctx, a, p);
 }
 
@@ -1183,7 +1195,7 @@ int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const
     sl.qpos0 = -1;  // the drop-in reads each row's position
     const int mask = !masked ? dr::MASK_NONE
                              : ((has_kpos || has_kseq) ? dr::MASK_KEYS : dr::MASK_POS);
-    DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, mask, false));
+    DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, mask, dr::QEPI_NONE));
     DR_HIP(hipMemcpyAsync(out, ctx->out.p, qb, hipMemcpyDeviceToHost, st));
     DR_HIP(hipStreamSynchronize(st));
     return DR_OK;

@@ -199,6 +199,25 @@ struct LaunchPlan {
     bool qepi;       // Q epilogue compiled in: bias, QK-norm, RoPE, each where its operand is given
     bool act;        // fused step: active keys read from f32 rows and stored (see AttnSlot)
     bool w16;        // two 16-row compute waves per (row block, key group)
+    int kernel;      // KERNEL_STAGED (attn_fwd_kernel) or KERNEL_STREAMS (attn_ring_kernel)
+};
+
+// Attention kernel families.  STAGED: attn_fwd_kernel, the workgroup's waves
+// share super-tiles of K/V staged in LDS (every head dim, mask mode, the Q
+// epilogue and the fused step).  STREAMS: attn_ring_kernel, head dim 128,
+// each wave streams its own key tiles (no mask or MASK_POS, Q norm only).
+enum KernelKind : int {
+    KERNEL_AUTO = 0,
+    KERNEL_STAGED = 1,
+    KERNEL_STREAMS = 2,
+};
+
+// What of the Q/K/V epilogue the attention prologue applies to Q: nothing,
+// the QK-norm only, or also the bias and RoPE.
+enum QEpilogue : int {
+    QEPI_NONE = 0,
+    QEPI_NORM = 1,
+    QEPI_FULL = 2,
 };
 
 // Chooses tile sizes and the key split for a problem on a device with n_cu
@@ -206,8 +225,8 @@ struct LaunchPlan {
 // heuristic (tuning); force_rows 16 or 32 picks the query rows per compute
 // wave where both are built (0: automatic).
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, bool qepi, int n_cu, int force_rb, int force_kq,
-                          int force_split, int force_rows);
+                          int mask, int qepi, int n_cu, int force_rb, int force_kq,
+                          int force_split, int force_rows, int force_kernel);
 
 // Whether a plan's shape can run the fused step (each DMA wave stages one
 // key group's K and V^T tiles).
@@ -217,6 +236,7 @@ bool plan_supports_act(const LaunchPlan& p);
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
 
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
+hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
 hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);

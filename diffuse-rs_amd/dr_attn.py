@@ -27,6 +27,7 @@ LIB_PATH = HERE / "lib" / "libdr_attn.so"
 HEADER_PATH = HERE.parent / "include" / "dr_attn.h"
 
 DR_OK, DR_ERR_INVALID, DR_ERR_NO_DEVICE, DR_ERR_OOM, DR_ERR_HIP, DR_ERR_UNSUPPORTED = range(6)
+KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS = range(3)
 STATUS_NAMES = {
     DR_OK: "DR_OK",
     DR_ERR_INVALID: "DR_ERR_INVALID",
@@ -93,6 +94,7 @@ class CLaunchInfo(ctypes.Structure):
         ("key_groups", ctypes.c_int),
         ("fused_step", ctypes.c_int),
         ("rows_per_wave", ctypes.c_int),
+        ("kernel", ctypes.c_int),
     ]
 
 
@@ -123,6 +125,7 @@ _SIGS = {
     "dr_ctx_set_split": (_I, [_VP, _I]),
     "dr_ctx_set_fused_step": (_I, [_VP, _I]),
     "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
+    "dr_ctx_set_kernel": (_I, [_VP, _I]),
     "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
                             ctypes.POINTER(ctypes.c_void_p)]),
     "dr_rope_destroy": (None, [_VP]),
@@ -315,6 +318,10 @@ class Context:
 
     def set_wave_rows(self, rows: int) -> None:
         _check(self.lib.dr_ctx_set_wave_rows(self.h, rows))
+
+    def set_kernel(self, kernel: int) -> None:
+        """KERNEL_AUTO, KERNEL_STAGED or KERNEL_STREAMS (dr_ctx_set_kernel)."""
+        _check(self.lib.dr_ctx_set_kernel(self.h, kernel))
 
     def set_fused_step(self, enable: bool) -> None:
         _check(self.lib.dr_ctx_set_fused_step(self.h, 1 if enable else 0))

@@ -323,6 +323,7 @@ typedef struct {
     int key_groups;
     int fused_step; /* 1 when the launch also stored the step's active rows */
     int rows_per_wave; /* query rows per compute wave: 32, or 16 (two waves per row block) */
+    int kernel; /* DR_KERNEL_STAGED or DR_KERNEL_STREAMS: which attention kernel ran */
 } dr_launch_info;
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 
@@ -331,6 +332,19 @@ int dr_ctx_set_split(dr_ctx* ctx, int n_split);
 /* Query rows per compute wave for later calls on ctx: 16 or 32 where the
  * head-dim tile builds both, 0 = automatic. */
 int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
+/* Attention kernel families, for dr_ctx_set_kernel and dr_launch_info.kernel.
+ * STAGED: the workgroup's waves share K/V super-tiles staged in LDS (every
+ * head dim and mask, the Q bias / RoPE epilogue, the fused step).  STREAMS:
+ * head dim 128 only; each wave streams its own key tiles into LDS with no
+ * workgroup barrier in the key loop (no mask or position masks, Q norm). */
+#define DR_KERNEL_AUTO 0
+#define DR_KERNEL_STAGED 1
+#define DR_KERNEL_STREAMS 2
+/* Pick the kernel family for later calls on ctx: DR_KERNEL_AUTO (the
+ * planner: STREAMS wherever it applies), or force STAGED / STREAMS (STREAMS
+ * falls back to STAGED where it does not apply).  A tuning knob, for
+ * measurement and tests. */
+int dr_ctx_set_kernel(dr_ctx* ctx, int kernel);
 /* Let dr_attention_step run its single fused kernel (1) or always the cache
  * store followed by the attention (0, the default: on the MI355X the fused
  * kernel is the slower of the two at the shapes measured so far). */
