@@ -8,6 +8,7 @@
 #include "dr_attn.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -73,6 +74,22 @@ int ensure(DevBuf& b, size_t bytes) {
     return DR_OK;
 }
 
+// The growing workspaces that kernel launches take (key-split partials, Q8_K
+// activations).  A hipGraph captured on the context keeps the buffer pointer
+// it was captured with, so a workspace is never freed or moved while the
+// context lives: a larger request allocates a new buffer (at least twice the
+// old size) and retires the old one, which dr_ctx_destroy frees.
+int grow(DevBuf& b, size_t bytes, std::vector<void*>& retired) {
+    if (bytes <= b.cap) return DR_OK;
+    const size_t nb = std::max({bytes, 2 * b.cap, (size_t)4096});
+    void* p = nullptr;
+    DR_HIP(hipMalloc(&p, nb));
+    if (b.p) retired.push_back(b.p);
+    b.p = p;
+    b.cap = nb;
+    return DR_OK;
+}
+
 void release(DevBuf& b) {
     if (b.p) (void)hipFree(b.p);
     b.p = nullptr;
@@ -98,9 +115,14 @@ struct dr_ctx {
     int force_kernel = 0;  // dr::KernelKind (0: automatic)
     dr::LaunchPlan last{};
     bool has_last = false;
-    DevBuf part;                         // key-split partials
+    DevBuf part;                         // key-split partials (grow() only)
     DevBuf q, k, v, kc, vtc, meta, out;  // dr_attention() staging
-    DevBuf q8k;                          // dr_qmatmul's Q8_K activations
+    DevBuf q8k;                          // dr_qmatmul's Q8_K activations (grow() only)
+    std::vector<void*> retired;          // workspaces replaced by larger ones
+    // dr_ctx_destroy's reference plus one per pass, cache and RoPE table made
+    // on the context: it is freed when the last of them is destroyed, so the
+    // objects that use it may be destroyed before or after it
+    std::atomic<int> refs{1};
 };
 
 struct dr_pass {
@@ -246,15 +268,29 @@ int dr_ctx_synchronize(dr_ctx* ctx) {
     return DR_OK;
 }
 
-void dr_ctx_destroy(dr_ctx* ctx) {
-    if (!ctx) return;
+namespace {
+
+void ctx_free(dr_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (DevBuf* b : {&ctx->part, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc,
                       &ctx->meta, &ctx->out, &ctx->q8k})
         release(*b);
+    for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
+}
+
+}  // namespace
+
+static void ctx_retain(dr_ctx* ctx) { ctx->refs.fetch_add(1, std::memory_order_relaxed); }
+
+static void ctx_release(dr_ctx* ctx) {
+    if (ctx->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) ctx_free(ctx);
+}
+
+void dr_ctx_destroy(dr_ctx* ctx) {
+    if (ctx) ctx_release(ctx);
 }
 
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
@@ -318,6 +354,7 @@ int dr_pass_create(dr_ctx* ctx, const size_t* active, size_t n_active, dr_pass**
     *out = nullptr;
     dr_pass* p = new dr_pass();
     p->ctx = ctx;
+    ctx_retain(ctx);
     int rc = upload_pass(p, active, n_active);
     if (rc != DR_OK) {
         dr_pass_destroy(p);
@@ -350,12 +387,14 @@ int dr_pass_positions(const dr_pass* pass, size_t* out, size_t cap) {
 
 void dr_pass_destroy(dr_pass* pass) {
     if (!pass) return;
+    dr_ctx* ctx = pass->ctx;
     if (pass->d_pos) {
-        (void)hipSetDevice(pass->ctx->device);
-        (void)hipStreamSynchronize(pass->ctx->stream);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
         (void)hipFree(pass->d_pos);
     }
     delete pass;
+    ctx_release(ctx);
 }
 
 // ---------------------------------------------------------------- cache
@@ -380,6 +419,7 @@ int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n
     DR_CHECK(use_device(ctx));
     dr_step_cache* c = new dr_step_cache();
     c->ctx = ctx;
+    ctx_retain(ctx);
     c->n_total = n_total;
     c->cap = round_up(std::max(n_total, (size_t)1), dr::KEY_ALIGN);
     c->n_layer = n_layer;
@@ -425,7 +465,9 @@ void dr_cache_destroy(dr_step_cache* cache) {
     }
     if (cache->d_meta) (void)hipFree(cache->d_meta);
     if (cache->h_meta) (void)hipHostFree(cache->h_meta);
+    dr_ctx* ctx = cache->ctx;
     delete cache;
+    ctx_release(ctx);
 }
 
 // ---------------------------------------------------------------- Q/K/V epilogue
@@ -456,6 +498,7 @@ int dr_rope_create(dr_ctx* ctx, size_t max_len, size_t rope_dim, float theta,
     DR_CHECK(use_device(ctx));
     dr_rope* r = new dr_rope();
     r->ctx = ctx;
+    ctx_retain(ctx);
     r->max_len = max_len;
     r->rope_dim = rope_dim;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&r->d_table), h.size() * sizeof(float));
@@ -474,7 +517,9 @@ void dr_rope_destroy(dr_rope* rope) {
     (void)hipSetDevice(rope->ctx->device);
     (void)hipStreamSynchronize(rope->ctx->stream);
     if (rope->d_table) (void)hipFree(rope->d_table);
+    dr_ctx* ctx = rope->ctx;
     delete rope;
+    ctx_release(ctx);
 }
 
 int dr_qkv_epilogue(dr_ctx* ctx, const dr_pass* pass, float* q, float* k, float* v, size_t n_head,
@@ -737,7 +782,7 @@ int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, 
         n > (size_t)INT32_MAX / 32)
         return fail(DR_ERR_INVALID, "dr_qmatmul: %zu x %zu x %zu too large", n, rows, cols);
     DR_CHECK(use_device(ctx));
-    DR_CHECK(ensure(ctx->q8k, n * nb * sizeof(dr::Q8KBlock)));
+    DR_CHECK(grow(ctx->q8k, n * nb * sizeof(dr::Q8KBlock), ctx->retired));
     dr::QmmArgs a{};
     a.wtype = wtype;
     a.w = w;
@@ -841,7 +886,7 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
-        DR_CHECK(ensure(ctx->part, ws));
+        DR_CHECK(grow(ctx->part, ws, ctx->retired));
         a.part_o = static_cast<float*>(ctx->part.p);
     }
     hipError_t e = dr::launch_attention(p, a, ctx->stream);

@@ -236,6 +236,7 @@ bool plan_supports_act(const LaunchPlan& p);
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
 
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
+
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);

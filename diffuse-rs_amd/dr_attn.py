@@ -295,7 +295,9 @@ def split_active(prev_seq: np.ndarray, last_changed: np.ndarray, seq, is_masked,
 
 
 class Context:
-    """dr_ctx: one device and one HIP stream."""
+    """dr_ctx: one device and one HIP stream.  (Passes, RoPE tables and
+    caches made on it hold the C context alive, so the garbage collector may
+    finalize these objects in any order.)"""
 
     def __init__(self, device: int = 0):
         self.lib = load()

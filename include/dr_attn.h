@@ -109,6 +109,11 @@ int dr_ctx_set_stream(dr_ctx* ctx, void* stream);
 /* The hipStream_t the context enqueues on. */
 void* dr_ctx_stream(dr_ctx* ctx);
 int dr_ctx_synchronize(dr_ctx* ctx);
+/* Release the caller's hold on ctx.  Every pass, cache and RoPE table made on
+ * ctx holds it too: its stream and workspaces are freed once ctx and all of
+ * them have been destroyed, in any order (a garbage collector may finalize
+ * the context first).  Workspaces that grew are freed only here, never while
+ * a captured hipGraph could still use them. */
 void dr_ctx_destroy(dr_ctx* ctx);
 
 /*
