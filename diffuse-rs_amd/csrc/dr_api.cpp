@@ -243,6 +243,13 @@ int dr_ctx_create(int device, dr_ctx** out) {
         return hip_fail(e, "hipStreamCreateWithFlags");
     }
     c->stream = c->own;
+    // this device's address of the fixed scratch (dr_attention_cached_noalloc)
+    e = dr::scratch_init(device);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    }
     e = hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device);
     if (e != hipSuccess) {
         (void)hipStreamDestroy(c->own);
@@ -883,11 +890,24 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
                               ctx->force_rows, ctx->force_kernel);
 }
 
-static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p) {
+// Launches plan p.  The key-split partials go to the context's workspace,
+// or with fixed_ws to the library's fixed device scratch (no allocation: a
+// plan that needs more than it holds is an error).
+static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws = false) {
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
-        DR_CHECK(grow(ctx->part, ws, ctx->retired));
-        a.part_o = static_cast<float*>(ctx->part.p);
+        if (fixed_ws) {
+            if (ws > dr::scratch_bytes())
+                return fail(DR_ERR_INVALID,
+                            "dr_attention_cached_noalloc: the plan's %d key splits need %zu bytes of "
+                            "workspace, more than the fixed %zu",
+                            p.n_split, ws, dr::scratch_bytes());
+            a.part_o = static_cast<float*>(dr::scratch_ptr(ctx->device));
+            if (!a.part_o) return fail(DR_ERR_HIP, "the device scratch of device %d is not set up", ctx->device);
+        } else {
+            DR_CHECK(grow(ctx->part, ws, ctx->retired));
+            a.part_o = static_cast<float*>(ctx->part.p);
+        }
     }
     hipError_t e = dr::launch_attention(p, a, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "attention launch");
@@ -984,6 +1004,22 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
     return launch_planned(cache->ctx, a, a.hd, max_nq, (int)cache->n_total,
                           mask_of(sliding_window, causal_prefix),
                           q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
+}
+
+int dr_attention_cached_noalloc(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
+                                size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                                dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                                float q_norm_eps) {
+    dr::AttnArgs a;
+    int max_nq = 0;
+    DR_CHECK(cached_args(cache, layer, items, n_items, n_head, sliding_window, causal_prefix,
+                         scale, q_norm_w, q_norm_eps, "dr_attention_cached_noalloc", a, max_nq));
+    if (max_nq == 0) return DR_OK;
+    DR_CHECK(use_device(cache->ctx));
+    const dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total,
+                                      mask_of(sliding_window, causal_prefix),
+                                      q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
+    return launch_plan(cache->ctx, a, p, true);
 }
 
 int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* items,

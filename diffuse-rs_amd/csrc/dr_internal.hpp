@@ -237,6 +237,13 @@ size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
 
 hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st);
 
+// The fixed device workspace of the allocation-free entry point
+// (scratch.hip): its size, the set-up that takes this device's address of it
+// (once per device, with the device current), and that address (nullptr
+// before scratch_init succeeded on the device).
+size_t scratch_bytes();
+hipError_t scratch_init(int device);
+void* scratch_ptr(int device);
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);

@@ -153,6 +153,8 @@ _SIGS = {
     "dr_cache_split_active_dev": (_I, [_VP, _SZ, _VP, _VP, _SZ, _SZ, _VP, _VP, c_size_p, c_size_p]),
     "dr_cache_initialized": (_I, [_VP, _SZ]),
     "dr_attention_cached": (_I, [_VP, _SZ, ctypes.POINTER(CBatchItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F]),
+    "dr_attention_cached_noalloc": (_I, [_VP, _SZ, ctypes.POINTER(CBatchItem), _SZ, _SZ, OptUsize, OptUsize, _F,
+                                         _VP, _F]),
     "dr_attention_step": (_I, [_VP, _SZ, ctypes.POINTER(CStepItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F, _VP, _F]),
 }
 
@@ -494,14 +496,17 @@ class StepCache:
 
     def attention(self, layer: int, items: Sequence[tuple], n_head: int,
                   sliding_window: Optional[int] = None, causal_prefix: Optional[int] = None,
-                  scale: float = 1.0, q_norm_w=None, q_norm_eps: float = 1e-6) -> None:
-        """items: sequence of (q, out, Pass) per batch slot (device tensors)."""
+                  scale: float = 1.0, q_norm_w=None, q_norm_eps: float = 1e-6,
+                  noalloc: bool = False) -> None:
+        """items: sequence of (q, out, Pass) per batch slot (device tensors).
+        noalloc: dr_attention_cached_noalloc (the library's fixed device
+        scratch instead of the context's workspace)."""
         arr = (CBatchItem * len(items))()
         for i, (q, out, p) in enumerate(items):
             arr[i] = CBatchItem(_ptr(q), _ptr(out), p.h)
-        _check(self.ctx.lib.dr_attention_cached(
-            self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
-            scale, _ptr(q_norm_w) or None, q_norm_eps))
+        fn = self.ctx.lib.dr_attention_cached_noalloc if noalloc else self.ctx.lib.dr_attention_cached
+        _check(fn(self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
+                  scale, _ptr(q_norm_w) or None, q_norm_eps))
 
     def step(self, layer: int, items: Sequence[tuple], n_head: int,
              sliding_window: Optional[int] = None, causal_prefix: Optional[int] = None,

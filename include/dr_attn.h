@@ -220,6 +220,27 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
                         dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
                         float q_norm_eps);
 
+/*
+ * dr_attention_cached without allocating: the same arguments, checks,
+ * kernels and results, but the key-split partials (the only device memory
+ * the call uses beyond its inputs and outputs) go to a fixed 64 MiB device
+ * array that the library holds on every GPU it runs on until the process
+ * ends, instead of the context's growing workspace.  No hipMalloc, hipFree
+ * or allocating library routine runs in the call, so it can be made under
+ * hipGraph capture, in serving loops and in harnesses that forbid
+ * allocation.  A plan whose splits need more than 64 MiB (far beyond the
+ * configurations here: DiffusionGemma's 512-wide global layer needs 34 MB)
+ * returns DR_ERR_INVALID.  Nothing in the array needs to start at zero.
+ * Every call on a GPU shares that GPU's array, so calls that overlap on one
+ * GPU (different streams or host threads) race; calls on one stream do not.
+ * This entry point has no counterpart in the reference; it is for callers
+ * that cannot allocate.
+ */
+int dr_attention_cached_noalloc(dr_step_cache* cache, size_t layer, const dr_batch_item* items,
+                                size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                                dr_opt_usize causal_prefix, float scale, const float* q_norm_w,
+                                float q_norm_eps);
+
 /* One batch slot of a denoise-step layer: queries and the active K/V rows. */
 typedef struct {
     const float* q; /* device, [n_active][n_head][head_dim] f32 */
