@@ -3,26 +3,30 @@
 
 Workload ("C2"): LLaDA-8B shape, 32 query heads =
 32 KV heads, head_dim 128, 512 cached prompt rows + 256 canvas rows, batch 1,
-bidirectional, scale 1/sqrt(128).  The prompt K/V is stored in the bf16 KV
-cache once.  One *step* = store the step's 256 fresh canvas K/V rows into the
-cache (f32 -> bf16, by position) + attention of the 256 canvas queries over
-all 768 keys (the attention_block sequence of forward.rs:312-343).  Inputs
-(16 distinct canvas sets, f32 N(0,1), seeded) are resident in HBM before the
-timed region.
+bidirectional, scale 1/sqrt(128).  The cache holds LLaDA-8B's 32 layers
+(32 x 12 MiB of bf16 K/V, more than the 256 MB Infinity Cache), each with the
+prompt K/V stored once.  Step i works on layer i mod 32: store the step's 256
+fresh canvas K/V rows into that layer's cache (f32 -> bf16, by position) +
+attention of the 256 canvas queries over all 768 keys (the attention_block
+sequence of forward.rs:312-343).  Inputs (16 distinct canvas sets, f32
+N(0,1), seeded) are resident in HBM before the timed region.
 
-value = algorithmic attention FLOPs of K steps / wall time of the K steps
-(graph replays of 16 steps each), FLOPs = 4 * h * hd * sum_q |visible keys| =
-3.221 GFLOP per step (softmax, masking and the store excluded).  roofline =
-the attention kernel alone: the same FLOPs / its mean launch duration, timed
-with HIP events on the library's stream around graph replays of 16
-back-to-back attention calls, against 2516.6 TFLOP/s dense bf16 MFMA; its
-traffic is the HBM bytes per launch from the rocprofv3 FETCH_SIZE /
+value = algorithmic attention FLOPs of K steps / wall time of the K steps,
+all of them graph replays (a graph of 32 steps, and one of the remainder),
+FLOPs = 4 * h * hd * sum_q |visible keys| = 3.221 GFLOP per step (softmax,
+masking and the store excluded).  roofline = the attention kernel alone:
+the same FLOPs / its mean launch duration over a graph of 32 back-to-back
+calls, one per layer (so K/V come from HBM, as in a real step), timed with
+HIP events on the library's stream, against 2516.6 TFLOP/s dense bf16 MFMA;
+its traffic is the HBM bytes per launch from the rocprofv3 FETCH_SIZE /
 WRITE_SIZE record in profiles/.  other_configs_attention_only = the same
-attention-only timing for configs[2..4].  cpu_baseline = the C restatement of
-the reference's AVX2 attention (oracle/, "port") timed on this host's cores on
-a bounded sample of the same workload; its output also checks the GPU result.
+timing for configs[2..4] (C5 also as its 6-layer S,S,S,S,S,G set).
+cpu_baseline = the C restatement of the reference's AVX2 attention (oracle/,
+"port") timed on this host's cores on a bounded sample of the same workload;
+its output also checks the GPU result.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode eager|graph]
+       python bench.py --only CFG [--calls N]   (one config's attention, for profiling)
 """
 from __future__ import annotations
 
@@ -49,17 +53,15 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "attn_fwd_C2_traffic.txt"
-
-
-def measured_traffic():
-    """HBM bytes per attn_fwd_kernel launch at this workload, as measured by
-    the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded in
-    profiles/attn_fwd_C2_traffic.txt, or None if that record is absent."""
+def measured_traffic(cfg_name: str):
+    """HBM bytes per attention launch at a config, as measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded in
+    profiles/attn_<cfg>_traffic.txt, or (None, None) if that record is absent."""
+    path = ROOT / "profiles" / f"attn_{cfg_name}_traffic.txt"
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
+        for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch"):
-                return int(float(line.split("=")[1])), TRAFFIC_FILE.name
+                return int(float(line.split("=")[1])), path.name
     except (OSError, ValueError, IndexError):
         pass
     return None, None
@@ -89,46 +91,112 @@ def attention_only_ms(torch, stream, call, n_calls: int, reps: int):
     return e0.elapsed_time(e1) / (reps * n_calls), g
 
 
+def _config_cache(torch, dr, ctx, stream, cfg, gen, n_layer: int = 1, windows=None):
+    """A cache of n_layer layers of cfg's geometry with random K/V stored in
+    every layer and batch slot, and the attention items of its canvas rows."""
+    h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+    n_t, n_c = cfg.n_total, cfg.n_canvas
+    cache = dr.StepCache(ctx, n_t, [hkv] * n_layer, [hd] * n_layer, n_batch=cfg.batch)
+    p_all = dr.Pass(ctx, range(n_t))
+    p_can = dr.Pass(ctx, range(cfg.n_prompt, n_t))
+    qn = kn = None
+    with torch.cuda.stream(stream):
+        if cfg.qk_norm:
+            qn = torch.rand(hd, device="cuda", generator=gen) + 0.5
+            kn = torch.rand(hd, device="cuda", generator=gen) + 0.5
+        Q = [torch.randn(n_c, h * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
+        O = [torch.empty(n_c * h * hd, device="cuda") for _ in range(cfg.batch)]
+    for layer in range(n_layer):
+        for b in range(cfg.batch):
+            with torch.cuda.stream(stream):
+                K = torch.randn(n_t, hkv * hd, device="cuda", generator=gen)
+                V = torch.randn(n_t, hkv * hd, device="cuda", generator=gen)
+            cache.store(layer, p_all, K, V, k_norm_w=kn, batch=b)
+    stream.synchronize()
+    items = [(Q[b], O[b], p_can) for b in range(cfg.batch)]
+    return cache, items, qn, (p_all, p_can)
+
+
 def other_configs(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
-    """Attention-only TFLOP/s of the other BASELINE.json configs and of a
-    real DiffusionGemma global layer at head dim 512 (synthetic N(0,1)
-    inputs, same graph-burst timing as the roofline)."""
+    """Attention-only TFLOP/s of the other BASELINE.json configs, of C5 as
+    the 6-layer set it states (5 sliding + 1 global layer), and of a real
+    DiffusionGemma global layer at head dim 512 (synthetic N(0,1) inputs;
+    graph bursts of 4 calls on one layer's cache, as the roofline's warm
+    figure; the C5 set is one graph of its 6 layers)."""
     res = {}
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
     from helpers import EXTRA_CONFIGS
     for name in ("C3", "C4", "C5S", "C5G", "G512"):
         cfg = CONFIGS[name] if name in CONFIGS else EXTRA_CONFIGS[name]
-        h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
-        n_t, n_c = cfg.n_total, cfg.n_canvas
-        with torch.cuda.stream(stream):
-            K = [torch.randn(n_t, hkv * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
-            V = [torch.randn(n_t, hkv * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
-            Q = [torch.randn(n_c, h * hd, device="cuda", generator=gen) for _ in range(cfg.batch)]
-            O = [torch.empty(n_c * h * hd, device="cuda") for _ in range(cfg.batch)]
-            qn = kn = None
-            if cfg.qk_norm:
-                qn = torch.rand(hd, device="cuda", generator=gen) + 0.5
-                kn = torch.rand(hd, device="cuda", generator=gen) + 0.5
-        cache = dr.StepCache(ctx, n_t, [hkv], [hd], n_batch=cfg.batch)
-        p_all = dr.Pass(ctx, range(n_t))
-        p_can = dr.Pass(ctx, range(cfg.n_prompt, n_t))
-        for b in range(cfg.batch):
-            cache.store(0, p_all, K[b], V[b], k_norm_w=kn, batch=b)
-        items = [(Q[b], O[b], p_can) for b in range(cfg.batch)]
+        cache, items, qn, _ = _config_cache(torch, dr, ctx, stream, cfg, gen)
 
         def call(i):
-            cache.attention(0, items, h, sliding_window=cfg.window, scale=cfg.attn_scale,
+            cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=cfg.attn_scale,
                             q_norm_w=qn)
         ms, _ = attention_only_ms(torch, stream, call, 4, reps)
         fl = cfg.flops()
+        traffic, src = measured_traffic(name)
         res[name] = {"workload": cfg.name, "us_per_call": round(ms * 1e3, 3),
                      "tflops": round(fl / (ms / 1e3) / 1e12, 2),
                      "pct_of_peak": round(100 * fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                     "traffic": traffic, "traffic_source": src,
                      "launch": ctx.last_launch()}
         log(f"{name}: {res[name]}")
         stream.synchronize()
         del cache
+    # C5 as stated: layers S,S,S,S,S,G of one cache, one call each
+    cs, cg = CONFIGS["C5S"], CONFIGS["C5G"]
+    cache, items, _, _ = _config_cache(torch, dr, ctx, stream, cs, gen, n_layer=6)
+
+    def six(i):
+        layer = i % 6
+        cache.attention(layer, items, cs.n_head, sliding_window=cs.window if layer < 5 else None,
+                        scale=cs.attn_scale)
+    ms6, _ = attention_only_ms(torch, stream, six, 6, max(2, reps // 2))
+    fl6 = 5 * cs.flops() + cg.flops()
+    t6 = ms6 * 6 / 1e3  # seconds per 6-layer set
+    res["C5_6layer"] = {"workload": "C5: 6 layers S,S,S,S,S,G (window 1024 / global), 16/8 heads, "
+                                    "hd 256, 4096 cached + 256 canvas",
+                        "us_per_6_layers": round(t6 * 1e6, 3), "tflops": round(fl6 / t6 / 1e12, 2),
+                        "pct_of_peak": round(100 * fl6 / t6 / 1e12 / PEAK_BF16_TFLOPS, 2),
+                        "gflop": round(fl6 / 1e9, 3)}
+    log(f"C5_6layer: {res['C5_6layer']}")
+    stream.synchronize()
+    del cache
+    return res
+
+
+def dropin_timing(torch, dr, CONFIGS) -> dict:
+    """The literal drop-in, dr_attention() (attention.rs:106): host f32 Q/K/V
+    in, host f32 out, synchronous (upload, pack K/V to bf16, attend,
+    download), at C1 and C2 (C2 with all 768 keys passed as rows, the
+    reference's [cached | active] assembly).  Host wall time per call."""
+    import numpy as np
+    res = {}
+    for name in ("C1", "C2"):
+        cfg = CONFIGS[name]
+        h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+        nq, nk = cfg.n_canvas, cfg.n_total
+        rng = np.random.default_rng(5)
+        q = rng.standard_normal(nq * h * hd, dtype=np.float32)
+        k = rng.standard_normal(nk * hkv * hd, dtype=np.float32)
+        v = rng.standard_normal(nk * hkv * hd, dtype=np.float32)
+        out = np.zeros(nq * h * hd, np.float32)
+        s = dr.AttnShape(nq, nk, h, hkv, hd, scale=cfg.attn_scale)
+        qr, kr = dr.Rows(list(range(cfg.n_prompt, nk))), dr.idpos(nk)
+        for _ in range(3):
+            dr.attention(out, q, k, v, s, qr, kr)
+        reps = 20
+        t = time.perf_counter()
+        for _ in range(reps):
+            dr.attention(out, q, k, v, s, qr, kr)
+        us = (time.perf_counter() - t) / reps * 1e6
+        fl = cfg.flops()
+        res[name] = {"us_per_call": round(us, 1), "tflops": round(fl / (us / 1e6) / 1e12, 3),
+                     "bytes_host_to_device": int(4 * (q.size + k.size + v.size)),
+                     "bytes_device_to_host": int(4 * out.size)}
+    log(f"drop-in dr_attention: {res}")
     return res
 
 
@@ -270,6 +338,29 @@ def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
     return res_d, (w.reshape(-1), rows, cols, x, n, res)
 
 
+N_LAYERS = 32  # LLaDA-8B
+
+
+def profile_only(args, torch, dr, CONFIGS) -> int:
+    """--only CFG: `calls` eager attention calls of one config (for rocprofv3
+    runs: kernel trace and counters of that config's launches)."""
+    from helpers import EXTRA_CONFIGS
+    cfg = CONFIGS[args.only] if args.only in CONFIGS else EXTRA_CONFIGS[args.only]
+    stream = torch.cuda.Stream()
+    ctx = dr.Context(0)
+    ctx.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(99)
+    cache, items, qn, _ = _config_cache(torch, dr, ctx, stream, cfg, gen)
+    with torch.cuda.stream(stream):
+        for _ in range(args.calls):
+            cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=cfg.attn_scale,
+                            q_norm_w=qn)
+    stream.synchronize()
+    print(json.dumps({"only": args.only, "calls": args.calls, "launch": ctx.last_launch()}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -281,6 +372,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true",
                     help="skip the attention-only timing of the other configs")
+    ap.add_argument("--only", default="", help="profile one config's attention and exit")
+    ap.add_argument("--calls", type=int, default=64, help="calls of --only")
     ap.add_argument("--calib-mib", type=int, default=0,
                     help="also run a plain streaming kernel (out = -in) over this many MiB, "
                          "three times: the calibration for rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -296,6 +389,10 @@ def main() -> int:
     import dr_attn as dr
     from helpers import CONFIGS, config_seed
 
+    torch.cuda.init()
+    if args.only:
+        return profile_only(args, torch, dr, CONFIGS)
+
     cfg = CONFIGS["C2"]
     h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
     n_p, n_c, n_t = cfg.n_prompt, cfg.n_canvas, cfg.n_total
@@ -303,7 +400,6 @@ def main() -> int:
     kvs = hkv * hd
     n_sets = 16
 
-    torch.cuda.init()
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()
     ctx = dr.Context(0)
@@ -324,16 +420,18 @@ def main() -> int:
         dKp, dVp = torch.from_numpy(Kp).to(dev), torch.from_numpy(Vp).to(dev)
         dsets = [tuple(torch.from_numpy(x).to(dev) for x in st) for st in sets]
         out = torch.empty(n_c * h * hd, dtype=torch.float32, device=dev)
-    cache = dr.StepCache(ctx, n_t, [hkv], [hd])
+    cache = dr.StepCache(ctx, n_t, [hkv] * N_LAYERS, [hd] * N_LAYERS)
     p_prompt = dr.Pass(ctx, range(n_p))
     p_canvas = dr.Pass(ctx, range(n_p, n_t))
-    cache.store(0, p_prompt, dKp, dVp)
+    for layer in range(N_LAYERS):
+        cache.store(layer, p_prompt, dKp, dVp)
     scale = cfg.attn_scale
 
     def step(i: int) -> None:
         Kc, Vc, Q = dsets[i % n_sets]
-        cache.store(0, p_canvas, Kc, Vc)
-        cache.attention(0, [(Q, out, p_canvas)], h, scale=scale)
+        layer = i % N_LAYERS
+        cache.store(layer, p_canvas, Kc, Vc)
+        cache.attention(layer, [(Q, out, p_canvas)], h, scale=scale)
 
     with torch.cuda.stream(stream):
         step(0)
@@ -352,46 +450,64 @@ def main() -> int:
         log(f"calibration: 3 x neg over {args.calib_mib} MiB (reads and writes that much)")
         del src, dst
 
-    # ---- roofline: the attention call alone.  16 calls (the 16 query sets)
-    # are captured in one graph and replayed back to back between two HIP
-    # events recorded on the library's stream; the mean launch duration is
-    # the elapsed time over the number of calls.
-    attn_mean_ms, attn_graph = attention_only_ms(
+    # ---- roofline: the attention call alone.  32 calls, one per layer (the
+    # K/V of a real denoise step, 384 MiB, more than the Infinity Cache), are
+    # captured in one graph and replayed back to back between two HIP events
+    # on the library's stream; the mean launch duration is the elapsed time
+    # over the number of calls.  The warm figure replays 16 calls on one
+    # layer's cache (its 12 MiB stay in the Infinity Cache).
+    reps = max(2, min(64, args.steps // N_LAYERS))
+    attn_mean_ms, _ = attention_only_ms(
+        torch, stream,
+        lambda i: cache.attention(i % N_LAYERS, [(dsets[i % n_sets][2], out, p_canvas)], h, scale=scale),
+        N_LAYERS, reps)
+    warm_mean_ms, _ = attention_only_ms(
         torch, stream, lambda i: cache.attention(0, [(dsets[i][2], out, p_canvas)], h, scale=scale),
-        n_sets, max(4, min(128, args.steps // n_sets)))
-    log(f"attention call (graph bursts): mean {attn_mean_ms * 1e3:.2f} us")
+        n_sets, reps)
+    log(f"attention call: {attn_mean_ms * 1e3:.2f} us over 32 layers, {warm_mean_ms * 1e3:.2f} us on one layer")
 
-    # ---- timed region: K whole steps
-    graph = None
-    if args.mode == "graph":
+    # ---- timed region: K whole steps, every one a graph replay (a graph of
+    # 32 steps, one per layer, and a graph of the remainder)
+    graphs = {}
+    mode = args.mode
+
+    def capture(n: int):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            for i in range(n):
+                step(i)
+        stream.synchronize()
+        return g
+
+    if mode == "graph":
         try:
-            steps_per_graph = n_sets
             with torch.cuda.stream(stream):
                 for i in range(3):
                     step(i)
             stream.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream, capture_error_mode="thread_local"):
-                for i in range(steps_per_graph):
-                    step(i)
-            stream.synchronize()
+            graphs["full"] = capture(N_LAYERS)
+            for n in {args.steps % N_LAYERS, args.warmup % N_LAYERS} - {0}:
+                graphs[n] = capture(n)
         except Exception as e:  # graph capture unavailable: measure eagerly
             log(f"graph capture failed ({e}); timing eagerly")
-            graph = None
-    mode = "graph" if graph is not None else "eager"
+            graphs = {}
+            mode = "eager"
 
     def run(n: int) -> None:
         with torch.cuda.stream(stream):
-            if graph is not None:
-                for _ in range(n // n_sets):
-                    graph.replay()
-                for i in range(n % n_sets):
-                    step(i)
+            if graphs:
+                for _ in range(n // N_LAYERS):
+                    graphs["full"].replay()
+                if n % N_LAYERS:
+                    graphs[n % N_LAYERS].replay()
             else:
                 for i in range(n):
                     step(i)
 
     run(args.warmup)
+    with torch.cuda.stream(stream):
+        for g in graphs.values():  # (a graph's first replay is slower than the next ones)
+            g.replay()
     torch.cuda.synchronize()
     stream.synchronize()
     t0 = time.perf_counter()
@@ -408,35 +524,42 @@ def main() -> int:
     value = flops * args.steps / total_s / 1e12
 
     achieved = flops / (attn_mean_ms / 1e3) / 1e12
-    traffic, traffic_src = measured_traffic()
+    traffic, traffic_src = measured_traffic("C2")
     algo_bytes = (n_c * h * hd * 4) * 2 + 2 * n_t * kvs * 2  # Q f32 + O f32 + K,V bf16
+    kernel_name = ("attn_ring_kernel" if launch.get("kernel") == dr.KERNEL_STREAMS else "attn_fwd_kernel")
     roofline = {
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
         "traffic_source": traffic_src,
-        "kernel": "attn_fwd_kernel (one launch per attention call)",
+        "kernel": f"{kernel_name} (one launch per attention call)",
         "flops_per_launch": flops, "launch_us_mean": round(attn_mean_ms * 1e3, 3),
-        "launch_timing": "HIP events around graph replays of 16 back-to-back calls",
+        "launch_timing": "HIP events around graph replays of 32 back-to-back calls, one per layer "
+                         "(K/V from HBM)",
+        "achieved_one_layer_warm": round(flops / (warm_mean_ms / 1e3) / 1e12, 2),
+        "launch_us_one_layer_warm": round(warm_mean_ms * 1e3, 3),
         "algorithmic_bytes_per_launch": algo_bytes,
         "hbm_ceiling_frac": round(min(1.0, flops / algo_bytes * PEAK_HBM_GBS * 1e9 / 1e12
                                       / PEAK_BF16_TFLOPS), 4),
     }
 
-    # ---- CPU baseline: the C restatement of the reference's attention on this
-    # host's cores, on the first step's inputs; its output also checks the
-    # GPU result of that step (the measured configuration).
-    others = epi = split = qmm = qmm_inputs = None
+    others = epi = split = qmm = qmm_inputs = dropin = None
     if not args.no_others:
-        others = other_configs(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
-        epi = qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, max(4, min(64, args.steps // 32)))
+        r2 = max(4, min(64, args.steps // 32))
+        others = other_configs(torch, dr, ctx, stream, CONFIGS, r2)
+        epi = qkv_epilogue_timing(torch, dr, ctx, stream, CONFIGS, r2)
         split = split_active_timing(torch, dr, ctx, stream)
-        qmm, qmm_inputs = qmatmul_timing(torch, dr, ctx, stream, max(4, min(64, args.steps // 32)))
+        qmm, qmm_inputs = qmatmul_timing(torch, dr, ctx, stream, r2)
+        dropin = dropin_timing(torch, dr, CONFIGS)
 
+    # ---- CPU baseline: the C restatement of the reference's attention on this
+    # host's cores, on step 0's inputs (layer 0); its output also checks the
+    # GPU result of that step.
     cpu, parity = None, None
     if not args.no_cpu:
         import oracle as orc
         from helpers import RowsSpec, Shape
-        step(0)
+        with torch.cuda.stream(stream):
+            step(0)
         stream.synchronize()
         got = out.cpu().numpy()
         Kc, Vc, Q = sets[0]
@@ -484,15 +607,17 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "C2: LLaDA-8B denoise step, 32/32 heads, hd 128, 512 cached + "
-                               "256 canvas, batch 1 (store canvas K/V + attention)",
+                               "256 canvas, batch 1 (store canvas K/V + attention; step i on "
+                               "layer i mod 32 of a 32-layer cache)",
                    "global_batch": 1, "seq_len": n_t, "parallelism": "none (1 GPU)",
                    "timing": mode, "accumulate": "fp32", "q_out_dtype": "f32",
-                   "kv_cache_dtype": "bf16"},
+                   "kv_cache_dtype": "bf16", "layers": N_LAYERS},
         "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 3),
         "attention_call_pct_of_peak": round(100 * achieved / PEAK_BF16_TFLOPS, 3),
         "gpu_event_ms": round(gpu_ms, 4), "wall_s": round(wall, 4),
         "launch": launch, "parity": parity, "roofline": roofline, "cpu_baseline": cpu,
         "other_configs_attention_only": others,
+        "dropin_dr_attention": dropin,
         "qkv_epilogue": epi,
         "split_active": split,
         "wo_qmatmul": qmm,
