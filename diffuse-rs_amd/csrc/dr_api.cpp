@@ -785,11 +785,11 @@ int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, 
     if (wtype == DR_WTYPE_Q4K && ((uintptr_t)w & 15))
         return fail(DR_ERR_INVALID, "dr_qmatmul: Q4_K blocks must start 16-byte aligned (16-byte loads)");
     const size_t nb = cols / 256;
-    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || n * nb > (size_t)INT32_MAX ||
-        n > (size_t)INT32_MAX / 32)
+    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX / 2 || n > (size_t)INT32_MAX / 2 ||
+        (size_t)dr::qmm_rows_padded((int)n) * nb > (size_t)INT32_MAX)
         return fail(DR_ERR_INVALID, "dr_qmatmul: %zu x %zu x %zu too large", n, rows, cols);
     DR_CHECK(use_device(ctx));
-    DR_CHECK(grow(ctx->q8k, n * nb * sizeof(dr::Q8KBlock), ctx->retired));
+    DR_CHECK(grow(ctx->q8k, dr::qmm_workspace_bytes((int)n, (int)cols), ctx->retired));
     dr::QmmArgs a{};
     a.wtype = wtype;
     a.w = w;
@@ -797,11 +797,45 @@ int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, 
     a.cols = (int)cols;
     a.act = act;
     a.n = (int)n;
-    a.q8 = static_cast<dr::Q8KBlock*>(ctx->q8k.p);
+    a.n_pad = dr::qmm_rows_padded((int)n);
+    a.ws = ctx->q8k.p;
     a.out = out;
     a.residual = residual;
     hipError_t e = dr::launch_qmatmul(a, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "qmatmul launch");
+    return DR_OK;
+}
+
+int dr_qmatmul_expert(dr_ctx* ctx, int wtype, const void* w, size_t n_expert, size_t expert, size_t rows,
+                      size_t cols, const float* act, size_t n, float* out, const float* residual) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_qmatmul_expert: ctx is NULL");
+    if (expert >= n_expert)
+        return fail(DR_ERR_INVALID, "dr_qmatmul_expert: expert index %zu out of range (%zu experts)", expert,
+                    n_expert);
+    if (wtype != DR_WTYPE_Q4K && wtype != DR_WTYPE_Q6K)
+        return fail(DR_ERR_UNSUPPORTED, "dr_qmatmul_expert: weight type %d not built (Q4_K = 12, Q6_K = 14)",
+                    wtype);
+    if (cols == 0 || cols % 256 != 0)
+        return fail(DR_ERR_INVALID, "dr_qmatmul_expert: cols %zu is not a positive multiple of 256", cols);
+    if (!w) return fail(DR_ERR_INVALID, "dr_qmatmul_expert: w is NULL");
+    const size_t bb = wtype == DR_WTYPE_Q4K ? 144 : 210;
+    const size_t expert_bytes = rows * (cols / 256) * bb;
+    return dr_qmatmul(ctx, wtype, static_cast<const uint8_t*>(w) + expert * expert_bytes, rows, cols, act, n, out,
+                      residual);
+}
+
+int dr_quantize_q8k(dr_ctx* ctx, const float* act, size_t n, size_t cols, void* out) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_quantize_q8k: ctx is NULL");
+    if (cols == 0 || cols % 256 != 0)
+        return fail(DR_ERR_INVALID, "dr_quantize_q8k: cols %zu is not a positive multiple of 256", cols);
+    if (n == 0) return DR_OK;
+    if (!act || !out) return fail(DR_ERR_INVALID, "dr_quantize_q8k: NULL act / out");
+    if ((uintptr_t)out & 3) return fail(DR_ERR_INVALID, "dr_quantize_q8k: out must be 4-byte aligned");
+    if (cols > (size_t)INT32_MAX || n * (cols / 256) > (size_t)INT32_MAX)
+        return fail(DR_ERR_INVALID, "dr_quantize_q8k: %zu x %zu too large", n, cols);
+    DR_CHECK(use_device(ctx));
+    hipError_t e = dr::launch_quantize_q8k(act, (int)n, (int)cols, static_cast<dr::Q8KBlock*>(out), ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize_q8k launch");
     return DR_OK;
 }
 

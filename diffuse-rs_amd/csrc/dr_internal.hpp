@@ -165,6 +165,28 @@ struct Q8KBlock {
 };
 static_assert(sizeof(Q8KBlock) == 292, "Q8_K block layout");
 
+// Activation rows of dr_qmatmul's workspace: a multiple of the 128 rows of a
+// qmm workgroup (the pad rows are quantized as zeros).
+__host__ __device__ inline int qmm_rows_padded(int n) { return (n + 127) / 128 * 128; }
+
+// dr_qmatmul's workspace: the Q8_K activations in the matrix-core layout.
+//   qs    int8 [n_pad][cols]  (each 256-value block permuted: value 32 s +
+//         16 g + j at byte 128 g + 16 s + j)
+//   bmin  bf16 [n_pad][nb][16]  (per block: bsum_s & 63 for s = 0..7, then
+//         bsum_s - (bsum_s & 63); bsum_s = sum of values 32 s .. 32 s + 31)
+//   xd    f32 [nb][n_pad]  (the Q8_K d of block b of row t at b * n_pad + t)
+struct QmmLayout {
+    int8_t* qs;
+    uint16_t* bmin;
+    float* xd;
+    __host__ __device__ QmmLayout(void* ws, int n_pad, int cols) {
+        const size_t nb = (size_t)cols / 256;
+        qs = static_cast<int8_t*>(ws);
+        bmin = reinterpret_cast<uint16_t*>(qs + (size_t)n_pad * cols);
+        xd = reinterpret_cast<float*>(bmin + (size_t)n_pad * nb * 16);
+    }
+};
+
 // native_matmul (src/model/matmul.rs:120-148) + residual_add (ops.rs:365-370):
 // out[t * rows + r] = vec_dot(w row r, q8k(act row t)) (+ residual).
 struct QmmArgs {
@@ -173,7 +195,8 @@ struct QmmArgs {
     int rows, cols;          // cols a multiple of 256
     const float* act;        // [n][cols]
     int n;
-    Q8KBlock* q8;            // workspace: n * cols/256 blocks
+    int n_pad;               // qmm_rows_padded(n)
+    void* ws;                // workspace of qmm_workspace_bytes(n, cols) bytes (QmmLayout)
     float* out;              // [n][rows]
     const float* residual;   // [n][rows] or nullptr (may alias out)
 };
@@ -249,6 +272,9 @@ hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
 hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);
 hipError_t launch_split_active(const SplitArgs& a, hipStream_t st);
+size_t qmm_workspace_bytes(int n, int cols);
 hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st);
+// quantize_rows_q8_k into the reference's BlockQ8K layout
+hipError_t launch_quantize_q8k(const float* act, int n, int cols, Q8KBlock* out, hipStream_t st);
 
 }  // namespace dr

@@ -4,11 +4,23 @@
 // takes, for every (activation row t, weight row r), the Q4_K or Q6_K x Q8_K
 // block dot product; residual_add (ops.rs:365-370) follows.
 //
-// Every output runs the reference's scalar dot in its own order (the test
-// module's vec_dot of src/kernels.rs:228-347): the integer parts are exact
-// whatever the grouping, and the f32 operations are the same ones in the same
-// sequence, without fused multiply-adds.  So each output matches that
-// restatement bit for bit.
+// The integer part of every block dot runs on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8).  A block dot is
+//   Q4_K:  d_x * (d_w * sum_s sc_s sum_{i in s} q_i x_i  -  dmin_w * sum_s mn_s bsum_s)
+//   Q6_K:  d_x *  d_w * sum_s sc_s sum_{i in s} (q_i - 32) x_i
+// with 6-bit (Q4_K, sub-blocks of 32) or int8 (Q6_K, sub-blocks of 16)
+// scales sc_s.  The scale is folded into the weight operand: sc_s * q_i does
+// not fit in int8, so it is split as hi * 2^k + lo with both parts in int8 and
+// run as two MFMA chains over the whole 256-value block, aux = (acc_hi << k)
+// + acc_lo, exact in int32.  The Q4_K min term is one exact bf16 MFMA per
+// block (mn_s <= 63 and the 32-value sums bsum_s split as lo + 64 hi are bf16
+// integers; every partial sum stays below 2^24).  Per block and output the f32
+// combine is fma(fma(aux, d_w, -dmin_w * mins), d_x, sum).
+//
+// Numerics: every integer is exact; each output differs from the reference's
+// scalar vec_dot (src/kernels.rs:228-347) only in the rounding of the f32
+// combine: both are within (nb + 12) * 2^-24 of sum_b (|d aux_b| +
+// |dmin sumi_b|) of the exact value, nb = cols / 256.
 #include "dr_internal.hpp"
 
 namespace dr {
@@ -16,6 +28,15 @@ namespace {
 
 constexpr int QK = 256;
 constexpr int Q4K_BYTES = 144, Q6K_BYTES = 210;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
 
 // f16_to_f32 of src/kernels.rs:46-69 (bit for bit, NaN payload included).
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -36,18 +57,69 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return __uint_as_float(bits);
 }
 
-// quantize_rows_q8_k (src/kernels.rs:79-122): one workgroup per 256-value
-// block, thread i owns value i.  The first value of largest magnitude gives
-// iscale = -128 / max; q = round(iscale x) capped at 127; d = 1 / iscale;
-// bsums = sums of 16.  NaN values never win the scan (amax < |x| is false).
-__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, int cols,
-                                                           int nb, Q8KBlock* __restrict__ out) {
+template <typename T>
+__device__ __forceinline__ T gld(const void* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+// 16 bytes from a 2-byte-aligned address (Q6_K blocks are 210 bytes)
+__device__ __forceinline__ u32x4 gld16_a2(const uint8_t* p) {
+    const uint8_t* q = static_cast<const uint8_t*>(__builtin_assume_aligned(p, 2));
+    u32x4 v;
+    __builtin_memcpy(&v, q, 16);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
+}
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+__device__ __forceinline__ uint32_t pk_ashr_i16(uint32_t a, int s) {
+    const i16x2 v = __builtin_bit_cast(i16x2, a);
+    return __builtin_bit_cast(uint32_t, v >> (short)s);
+}
+// bytes b0 b1 b2 b3 -> the two u16 lanes {b_lo, b_lo + 1} of the pair
+__device__ __forceinline__ uint32_t bytes01_u16(uint32_t x) { return __builtin_amdgcn_perm(x, x, 0x0c010c00u); }
+__device__ __forceinline__ uint32_t bytes23_u16(uint32_t x) { return __builtin_amdgcn_perm(x, x, 0x0c030c02u); }
+// low bytes of the four u16 lanes of (lo, hi) -> one dword
+__device__ __forceinline__ uint32_t pack_lo_bytes(uint32_t lo, uint32_t hi) {
+    return __builtin_amdgcn_perm(hi, lo, 0x06040200u);
+}
+// byte j of x in both u16 lanes
+__device__ __forceinline__ uint32_t rep_byte_u16(uint32_t x, int j) {
+    const uint32_t b = (x >> (8 * j)) & 0xFFu;
+    return b | (b << 16);
+}
+// bf16 of the small non-negative integers in bytes 0..3 of x, as two dwords
+__device__ __forceinline__ void bytes_to_bf16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+    const uint32_t f0 = __float_as_uint((float)(x & 0xFFu)), f1 = __float_as_uint((float)((x >> 8) & 0xFFu));
+    const uint32_t f2 = __float_as_uint((float)((x >> 16) & 0xFFu)), f3 = __float_as_uint((float)(x >> 24));
+    lo = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+    hi = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_K quantization (quantize_rows_q8_k, src/kernels.rs:79-122): one
+// workgroup per 256-value block, thread i owns value i.  The first value of
+// largest magnitude gives iscale = -128 / max; q = round(iscale x) capped at
+// 127; d = 1 / iscale.  NaN values never win the scan (amax < |x| is false).
+//
+// REF = true writes the reference's BlockQ8K (d, qs[256], bsums[16]); REF =
+// false writes the matrix-core layout of the workspace (QmmLayout): qs with
+// value 32 s + 16 g + j of a block at byte 128 g + 16 s + j, so the 16-value
+// operand of lane group g for sub-block s is one 16-byte run and a lane's
+// eight runs are one 128-byte line; the 32-value sums as bf16 lo / 64 hi;
+// d as [block][row].  Rows n .. n_pad - 1 are written as zeros.
+template <bool REF>
+__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, int cols, int nb,
+                                                           int n, int n_pad, void* __restrict__ out) {
     __shared__ float s_a[4];
     __shared__ int s_i[4];
     __shared__ float s_mx;
     const int blk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t = blk / nb, b = blk - t * nb;
-    const float v = x[(size_t)t * cols + (size_t)b * QK + tid];
+    const float v = t < n ? x[(size_t)t * cols + (size_t)b * QK + tid] : 0.0f;
     float a = v != v ? -1.0f : fabsf(v);
     int idx = tid;
 #pragma unroll
@@ -74,282 +146,263 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restri
         }
     if (tid == imax) s_mx = v;
     __syncthreads();
-    Q8KBlock* o = out + blk;
     int q = 0;
+    float d = 0.0f;
     if (amax > 0.0f) {
 #pragma clang fp contract(off)
         const float iscale = -128.0f / s_mx;
         const float r = fminf(roundf(iscale * v), 127.0f);
         q = (int)r;
-        if (tid == 0) o->d = 1.0f / iscale;
-    } else if (tid == 0) {
-        o->d = 0.0f;
+        d = 1.0f / iscale;
     }
-    o->qs[tid] = (int8_t)q;
-    int s = q;
+    if constexpr (REF) {
+        Q8KBlock* o = static_cast<Q8KBlock*>(out) + blk;
+        if (tid == 0) o->d = d;
+        o->qs[tid] = (int8_t)q;
+        int s = q;
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
-    if ((tid & 15) == 0) o->bsums[tid >> 4] = (int16_t)s;
+        for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+        if ((tid & 15) == 0) o->bsums[tid >> 4] = (int16_t)s;
+    } else {
+        const QmmLayout L(out, n_pad, cols);
+        // four neighbouring values land in one dword of the permuted block
+        const uint32_t q0 = q & 0xFF, q1 = __shfl_down(q, 1) & 0xFF, q2 = __shfl_down(q, 2) & 0xFF,
+                       q3 = __shfl_down(q, 3) & 0xFF;
+        if ((tid & 3) == 0) {
+            const int pos = 128 * ((tid >> 4) & 1) + 16 * (tid >> 5) + (tid & 15);
+            *reinterpret_cast<uint32_t*>(L.qs + (size_t)t * cols + (size_t)b * QK + pos) =
+                q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+        }
+        int s = q;
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) s += __shfl_xor(s, off);
+        if ((tid & 31) == 0) {
+            const int lo = s & 63, hi = s - lo;  // |s| <= 4096: both exact in bf16
+            uint16_t* bm = L.bmin + ((size_t)t * nb + b) * 16;
+            bm[tid >> 5] = (uint16_t)(__float_as_uint((float)lo) >> 16);
+            bm[8 + (tid >> 5)] = (uint16_t)(__float_as_uint((float)hi) >> 16);
+        }
+        if (tid == 0) L.xd[(size_t)b * n_pad + t] = d;
+    }
 }
 
-// Tile of one workgroup: TR weight rows x TT activation rows; thread (rg, tg)
-// owns weight rows 2 rg, 2 rg + 1 and activation rows 4 tg .. 4 tg + 3.
-constexpr int TR = 64, TT = 32;
-
-// Q4_K: the 6-bit scales and mins of a block (src/kernels.rs:193-201).
-__device__ __forceinline__ void q4k_unpack_scales(const uint8_t* p, uint8_t sc[8], uint8_t mn[8]) {
-    uint32_t u[4];
-    u[0] = p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);
-    u[1] = p[4] | (p[5] << 8) | (p[6] << 16) | ((uint32_t)p[7] << 24);
-    u[2] = p[8] | (p[9] << 8) | (p[10] << 16) | ((uint32_t)p[11] << 24);
-    const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
-    u[3] = ((u[2] >> 4) & k2) | (((u[1] >> 6) & k3) << 4);
-    const uint32_t aux = u[1] & k1;
-    u[1] = (u[2] & k2) | (((u[0] >> 6) & k3) << 4);
-    u[2] = aux;
-    u[0] &= k1;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        sc[i] = (u[i / 4] >> (8 * (i % 4))) & 0xFF;
-        mn[i] = (u[2 + i / 4] >> (8 * (i % 4))) & 0xFF;
-    }
-}
-
-// WT: 12 = Q4_K, 14 = Q6_K (GGML type ids).
+// ---------------------------------------------------------------------------
+// The block dots.  A workgroup owns 32 weight rows x 128 activation rows (four
+// 32 x 32 MFMA tiles); its four waves split the 256-value blocks of a row into
+// four contiguous ranges and their partial sums meet in LDS in wave order, so
+// every output is summed in the same order on every call.
 //
-// LDS per 256-value block: the weight values as int8 and the activation
-// values, both as 64 dwords per row.  For Q4_K dword 8 j + l holds the four
-// values 32 j + 8 g + l (g = 0..3) of sub-block j: the reference's eight
-// lanes gather element i into lane i % 8, so one sdot4 per (j, l) gives
-// exactly lane l's share of sub-block j.  For Q6_K the 16-value groups are
-// summed whole, so the values stay in order.
+// MFMA operands (A = activations: row t; B = weights: column r): lane (c, g),
+// c = lane % 32, g = lane / 32, holds values 32 s + 16 g .. + 15 of sub-block
+// slab s of row c; accumulator slot i of that lane is output (t = 8 (i / 4) +
+// 4 g + i % 4, r = c).
+//
+// Weight operand of a Q4_K block: slab s = sub-block s.  sc_s = 8 sh + sl with
+// sh, sl <= 7, so sh * q and sl * q (q <= 15) are bytes and a 16-bit packed
+// multiply scales two nibble bytes at once without carries.  Q6_K: slab s is
+// sub-blocks 2 s (g = 0) and 2 s + 1 (g = 1); w = sc * (q - 32) in
+// [-4064, 4096] is formed in 16-bit lanes and split as 64 hi + lo.
+template <int WT>
+struct WeightOps {
+    i32x4 hi[8], lo[8];
+    bf16x8 mn;        // Q4_K: the eight 6-bit mins
+    float wd, wdmin;  // f16 d (and dmin) of the block
+};
+
+__device__ __forceinline__ void prep_q4k(const uint8_t* blk, int g, WeightOps<12>& o) {
+    const u32x4 h = gld<u32x4>(blk);  // d, dmin, scales[12]
+    o.wd = f16_bits_to_f32(h.x & 0xFFFF);
+    o.wdmin = f16_bits_to_f32(h.x >> 16);
+    // the 12 packed bytes (src/kernels.rs:193-201): sc 0..3, sc 4..7, mn 0..3, mn 4..7
+    const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+    const uint32_t sc03 = h.y & k1, mn03 = h.z & k1;
+    const uint32_t sc47 = (h.w & k2) | (((h.y >> 6) & k3) << 4);
+    const uint32_t mn47 = ((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4);
+    const uint32_t sh[2] = {(sc03 >> 3) & 0x07070707u, (sc47 >> 3) & 0x07070707u};
+    const uint32_t sl[2] = {sc03 & 0x07070707u, sc47 & 0x07070707u};
+    uint32_t m0, m1, m2, m3;
+    bytes_to_bf16(mn03, m0, m1);
+    bytes_to_bf16(mn47, m2, m3);
+    o.mn = __builtin_bit_cast(bf16x8, u32x4{m0, m1, m2, m3});
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // qs bytes 32 j + 16 g ..: sub-blocks 2 j (low), 2 j + 1 (high)
+        const u32x4 raw = gld<u32x4>(blk + 16 + 32 * j + 16 * g);
+#pragma unroll
+        for (int hn = 0; hn < 2; ++hn) {
+            const int s = 2 * j + hn;
+            const uint32_t fh = rep_byte_u16(sh[s >> 2], s & 3), fl = rep_byte_u16(sl[s >> 2], s & 3);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t nib = hn ? (raw[c] >> 4) & 0x0F0F0F0Fu : raw[c] & 0x0F0F0F0Fu;
+                o.hi[s][c] = (int)pk_mul_u16(nib, fh);
+                o.lo[s][c] = (int)pk_mul_u16(nib, fl);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void prep_q6k(const uint8_t* blk, int g, WeightOps<14>& o) {
+    o.wd = f16_bits_to_f32(blk[208] | (blk[209] << 8));
+    o.wdmin = 0.0f;
+    const u32x4 scv = gld16_a2(blk + 192);  // int8 scales of the 16 sub-blocks
+    u32x4 ql[2][2], qh[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        qh[h] = gld16_a2(blk + 128 + 32 * h + 16 * g);
+#pragma unroll
+        for (int a = 0; a < 2; ++a) ql[h][a] = gld16_a2(blk + 64 * h + 32 * a + 16 * g);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        // values 128 h + 32 quarter + 16 g + j (src/kernels.rs:135-147)
+        const int h = s >> 2, quarter = s & 3, a = quarter & 1;
+        const int sb = 2 * s + g;  // sub-block of 16
+        const int scb = (int)(int8_t)((scv[sb >> 2] >> (8 * (sb & 3))) & 0xFF);
+        const uint32_t f = ((uint32_t)scb & 0xFFFFu) * 0x10001u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t nib = (quarter >> 1) ? (ql[h][a][c] >> 4) & 0x0F0F0F0Fu : ql[h][a][c] & 0x0F0F0F0Fu;
+            const uint32_t q6 = nib | (((qh[h][c] >> (2 * quarter)) & 0x03030303u) << 4);
+            const uint32_t w01 = pk_mul_u16(pk_sub_u16(bytes01_u16(q6), 0x00200020u), f);
+            const uint32_t w23 = pk_mul_u16(pk_sub_u16(bytes23_u16(q6), 0x00200020u), f);
+            o.hi[s][c] = (int)pack_lo_bytes(pk_ashr_i16(w01, 6), pk_ashr_i16(w23, 6));
+            o.lo[s][c] = (int)pack_lo_bytes(w01 & 0x003F003Fu, w23 & 0x003F003Fu);
+        }
+    }
+}
+
 template <int WT>
 __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
-#pragma clang fp contract(off)
     constexpr bool Q4 = WT == 12;
     constexpr int WB = Q4 ? Q4K_BYTES : Q6K_BYTES;
-    // (weight-row arrays padded by one word: a wave's 32 lanes read 32
-    // different rows at the same column, which would otherwise share a bank)
-    __shared__ uint32_t s_w[TR][65];
-    __shared__ uint32_t s_x[TT][64];
-    __shared__ int s_sc[TR][17];    // Q4_K: sc[0..7], mn[8..15]; Q6_K: scales[16]
-    __shared__ float s_wd[TR][3];   // f16 d (and dmin) of the weight block
-    __shared__ float s_xd[TT];      // Q8_K d
-    __shared__ int s_bs[TT][16];    // Q8_K bsums
+    constexpr int SHIFT = Q4 ? 3 : 6;
+    // partial sums of the three other waves for each wave's tile:
+    // [tile][source wave, own skipped][slot][lane]
+    __shared__ float s_part[4][3][16][64];
 
-    const int tid = threadIdx.x;
-    const int r0 = blockIdx.x * TR, t0 = blockIdx.y * TT;
-    const int rg = tid & 31, tg = tid >> 5;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 31, g = lane >> 5;
     const int nb = a.cols / QK;
-    const uint8_t* W = static_cast<const uint8_t*>(a.w);
+    const int n_rt = (a.rows + 31) / 32, n_tt = a.n_pad / 128;
+    const int nwg = n_rt * n_tt, hw = blockIdx.x;
+    // the 128-row tiles of one weight tile on one XCD: the weights (the larger
+    // operand) are read into each XCD's L2 once
+    const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
+    const int rt = lid / n_tt, tt = lid - rt * n_tt;
+    const int r = min(rt * 32 + col, a.rows - 1);
+    const int t0 = tt * 128;
+    const QmmLayout L(a.ws, a.n_pad, a.cols);
+    const uint8_t* wrow = static_cast<const uint8_t*>(a.w) + (size_t)r * nb * WB;
 
-    float sums[8][8];  // [output][lane] (Q4_K); Q6_K uses sumf only
-    float sumf[8];
+    f32x16 sum[4];
 #pragma unroll
-    for (int o = 0; o < 8; ++o) {
-        sumf[o] = 0.0f;
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int l = 0; l < 8; ++l) sums[o][l] = 0.0f;
-    }
+        for (int i = 0; i < 16; ++i) sum[c][i] = 0.0f;
 
-    for (int b = 0; b < nb; ++b) {
-        __syncthreads();  // the previous block's tiles are consumed
-        // ---- stage the weight rows: 4 threads per row, each 1/4 of the block
-        {
-            const int rr = tid >> 2, part = tid & 3, r = r0 + rr;
-            const uint8_t* blk = W + ((size_t)min(r, a.rows - 1) * nb + b) * WB;
+    const int b_begin = wave * nb / 4, b_end = (wave + 1) * nb / 4;
+    for (int b = b_begin; b < b_end; ++b) {
+        WeightOps<WT> wo;
+        if constexpr (Q4)
+            prep_q4k(wrow + (size_t)b * WB, g, wo);
+        else
+            prep_q6k(wrow + (size_t)b * WB, g, wo);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int tr = t0 + 32 * c + col;  // this lane's A row
+            const int8_t* ap = L.qs + (size_t)tr * a.cols + (size_t)b * QK + 128 * g;
+            i32x4 av[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) av[s] = gld<i32x4>(ap + 16 * s);
+            f32x4 xd[4];
+            const float* xp = L.xd + (size_t)b * a.n_pad + t0 + 32 * c + 4 * g;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xd[k] = gld<f32x4>(xp + 8 * k);
+            i32x16 ah = {}, al = {};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                ah = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], wo.hi[s], ah, 0, 0, 0);
+                al = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], wo.lo[s], al, 0, 0, 0);
+            }
+            f32x16 mins = {};
             if constexpr (Q4) {
-                // qs bytes 32 part .. 32 part + 31 (two 16-byte loads: blocks
-                // are 144 bytes, so 16-byte aligned): sub-blocks 2 part (low
-                // nibbles) and 2 part + 1 (high nibbles); byte 8 g + l goes to
-                // byte g of dword l
-                const uint4* q = reinterpret_cast<const uint4*>(blk + 16 + 32 * part);
-                const uint4 v0 = q[0], v1 = q[1];
-                const uint32_t qd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                const bf16x8 bm = gld<bf16x8>(L.bmin + ((size_t)tr * nb + b) * 16 + 8 * g);
+                f32x16 z;
 #pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    uint32_t lo = 0, hi = 0;
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int k = 8 * g + l;
-                        const uint32_t byte = (qd[k >> 2] >> (8 * (k & 3))) & 0xFF;
-                        lo |= (byte & 0xF) << (8 * g);
-                        hi |= (byte >> 4) << (8 * g);
-                    }
-                    s_w[rr][8 * (2 * part) + l] = lo;
-                    s_w[rr][8 * (2 * part + 1) + l] = hi;
-                }
-                if (part == 0) {
-                    const uint4 h = *reinterpret_cast<const uint4*>(blk);  // d, dmin, scales[12]
-                    uint8_t hb[16];
-                    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) hb[i] = (hw[i >> 2] >> (8 * (i & 3))) & 0xFF;
-                    uint8_t sc[8], mn[8];
-                    q4k_unpack_scales(hb + 4, sc, mn);
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        s_sc[rr][i] = sc[i];
-                        s_sc[rr][8 + i] = mn[i];
-                    }
-                    s_wd[rr][0] = f16_bits_to_f32(h.x & 0xFFFF);
-                    s_wd[rr][1] = f16_bits_to_f32(h.x >> 16);
-                }
-            } else {
-                // values 64 part .. 64 part + 63 (src/kernels.rs:135-147):
-                // half h = part / 2, quarter q = part % 2 of 32 ql bytes
-                const uint8_t* ql = blk + 64 * (part >> 1);
-                const uint8_t* qh = blk + 128 + 32 * (part >> 1);
-                const int qq = part & 1;  // values 128 h + 64 qq + [0, 64)
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {  // dword k of the 64 values
-                    uint32_t wv = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int i = 4 * k + e;           // 0..63 within the quarter
-                        const int sub = i >> 5, l = i & 31;  // 32-value run, index in it
-                        const int run = 2 * qq + sub;        // aux8[l + 32 run] of the half
-                        int val;
-                        if (run == 0) val = (ql[l] & 0xF) | ((qh[l] & 3) << 4);
-                        else if (run == 1) val = (ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4);
-                        else if (run == 2) val = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
-                        else val = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4);
-                        wv |= (uint32_t)((val - 32) & 0xFF) << (8 * e);
-                    }
-                    s_w[rr][16 * part + k] = wv;
-                }
-                if (part == 0) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) s_sc[rr][i] = (int8_t)blk[192 + i];
-                    s_wd[rr][0] = f16_bits_to_f32(blk[208] | (blk[209] << 8));
-                }
-            }
-        }
-        // ---- stage the activation rows: 8 threads per row, one sub-block each
-        {
-            const int tt = tid >> 3, j = tid & 7, t = t0 + tt;
-            const Q8KBlock* xb = a.q8 + (size_t)min(t, a.n - 1) * nb + b;
-            // sub-block j's 32 values as 8 dword loads (Q8_K blocks are 292
-            // bytes: 4-byte aligned)
-            const uint32_t* qw = reinterpret_cast<const uint32_t*>(xb->qs + 32 * j);
-            uint32_t qd[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qd[i] = qw[i];
-#pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                uint32_t v = 0;
-                if constexpr (Q4) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int k = 8 * g + l;
-                        v |= ((qd[k >> 2] >> (8 * (k & 3))) & 0xFF) << (8 * g);
-                    }
-                } else {
-                    v = qd[l];
-                }
-                s_x[tt][8 * j + l] = v;
-            }
-            const uint32_t bs = *reinterpret_cast<const uint32_t*>(xb->bsums + 2 * j);
-            s_bs[tt][2 * j] = (int16_t)(bs & 0xFFFF);
-            s_bs[tt][2 * j + 1] = (int16_t)(bs >> 16);
-            if (j == 0) s_xd[tt] = xb->d;
-        }
-        __syncthreads();
-
-        // ---- this block's contribution to the thread's 8 outputs
-        if constexpr (Q4) {
-            int aux[8][8];
-#pragma unroll
-            for (int o = 0; o < 8; ++o)
-#pragma unroll
-                for (int l = 0; l < 8; ++l) aux[o][l] = 0;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int sc0 = s_sc[2 * rg][j], sc1 = s_sc[2 * rg + 1][j];
-                // the sub-block's 64 independent dot4s first, then their
-                // scaling (a scaled product right behind its dot4 stalls)
-                int p[8][8];
-#pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    const int w0 = s_w[2 * rg][8 * j + l], w1 = s_w[2 * rg + 1][8 * j + l];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int xv = s_x[4 * tg + k][8 * j + l];
-                        p[k][l] = __builtin_amdgcn_sdot4(w0, xv, 0, false);
-                        p[4 + k][l] = __builtin_amdgcn_sdot4(w1, xv, 0, false);
-                    }
-                }
-                // (scales <= 63 and |dot4| <= 4 * 15 * 128: exact in the
-                // full-rate 24-bit multiply)
-#pragma unroll
-                for (int o = 0; o < 8; ++o)
-#pragma unroll
-                    for (int l = 0; l < 8; ++l) aux[o][l] += __mul24(o < 4 ? sc0 : sc1, p[o][l]);
+                for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+                mins = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bm, wo.mn, z, 0, 0, 0);
             }
 #pragma unroll
-            for (int o = 0; o < 8; ++o) {
-                const int rr = 2 * rg + (o >> 2), tt = 4 * tg + (o & 3);
-                int sumi = 0;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) sumi += s_bs[tt][j] * s_sc[rr][8 + j / 2];
-                const float d = s_wd[rr][0] * s_xd[tt];
-#pragma unroll
-                for (int l = 0; l < 8; ++l) sums[o][l] += d * (float)aux[o][l];
-                const float dmin = s_wd[rr][1] * s_xd[tt];
-                sumf[o] -= dmin * (float)sumi;
-            }
-        } else {
-#pragma unroll
-            for (int o = 0; o < 8; ++o) {
-                const int rr = 2 * rg + (o >> 2), tt = 4 * tg + (o & 3);
-                int sumi = 0;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    int p = 0;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) p = __builtin_amdgcn_sdot4(s_w[rr][4 * j + k], s_x[tt][4 * j + k], p, false);
-                    sumi += __mul24(s_sc[rr][j], p);  // |scale| <= 128, |p| <= 4 * 32 * 128
-                }
-                const float d = s_wd[rr][0] * s_xd[tt];
-                sumf[o] += d * (float)sumi;
+            for (int i = 0; i < 16; ++i) {
+                const float f = (float)(ah[i] * (1 << SHIFT) + al[i]);
+                const float inner = Q4 ? __builtin_fmaf(f, wo.wd, -(mins[i] * wo.wdmin)) : f * wo.wd;
+                sum[c][i] = __builtin_fmaf(inner, xd[i >> 2][i & 3], sum[c][i]);
             }
         }
     }
 
-    // ---- write: sumf + (sums[0] + ... + sums[7]) (+ residual)
+    // ---- the four partial sums of each tile, in wave order; wave w writes tile w
 #pragma unroll
-    for (int o = 0; o < 8; ++o) {
-        const int r = r0 + 2 * rg + (o >> 2), t = t0 + 4 * tg + (o & 3);
-        if (r >= a.rows || t >= a.n) continue;
-        float v = sumf[o];
-        if constexpr (Q4) {
-            float tot = 0.0f;
+    for (int c = 0; c < 4; ++c) {
+        if (c == wave) continue;
+        const int src = wave < c ? wave : wave - 1;
 #pragma unroll
-            for (int l = 0; l < 8; ++l) tot += sums[o][l];
-            v = v + tot;
+        for (int i = 0; i < 16; ++i) s_part[c][src][i][lane] = sum[c][i];
+    }
+    __syncthreads();
+    const int c = wave;
+    f32x16 own;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+        if (cc == c) own = sum[cc];
+    const int rr = rt * 32 + col;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float p = w == c ? own[i] : s_part[c][w < c ? w : (w > c ? w - 1 : 0)][i][lane];
+            v = w == 0 ? p : v + p;
         }
-        const size_t idx = (size_t)t * a.rows + r;
-        if (a.residual) v += a.residual[idx];
-        a.out[idx] = v;
+        const int t = t0 + 32 * c + 8 * (i >> 2) + 4 * g + (i & 3);
+        if (t < a.n && rr < a.rows) {
+            const size_t idx = (size_t)t * a.rows + rr;
+            if (a.residual) v += a.residual[idx];
+            a.out[idx] = v;
+        }
     }
 }
 
 }  // namespace
 
+size_t qmm_workspace_bytes(int n, int cols) {
+    const size_t n_pad = (size_t)qmm_rows_padded(n), nb = (size_t)cols / QK;
+    return n_pad * nb * (QK + 16 * sizeof(uint16_t) + sizeof(float));
+}
+
 hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st) {
     if (a.n <= 0 || a.rows <= 0) return hipSuccess;
+    if (a.n_pad != qmm_rows_padded(a.n) || a.cols % QK != 0) return hipErrorInvalidValue;
     const int nb = a.cols / QK;
-    hipLaunchKernelGGL(q8k_quantize_kernel, dim3((unsigned)(a.n * nb)), dim3(256), 0, st, a.act, a.cols, nb,
-                       a.q8);
+    hipLaunchKernelGGL(q8k_quantize_kernel<false>, dim3((unsigned)(a.n_pad * nb)), dim3(256), 0, st, a.act,
+                       a.cols, nb, a.n, a.n_pad, a.ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)((a.rows + TR - 1) / TR), (unsigned)((a.n + TT - 1) / TT));
+    const unsigned nwg = (unsigned)(((a.rows + 31) / 32) * (a.n_pad / 128));
     if (a.wtype == 12)
-        hipLaunchKernelGGL(qmm_kernel<12>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(qmm_kernel<12>, dim3(nwg), dim3(256), 0, st, a);
     else if (a.wtype == 14)
-        hipLaunchKernelGGL(qmm_kernel<14>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(qmm_kernel<14>, dim3(nwg), dim3(256), 0, st, a);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8k(const float* act, int n, int cols, Q8KBlock* out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int nb = cols / QK;
+    hipLaunchKernelGGL(q8k_quantize_kernel<true>, dim3((unsigned)(n * nb)), dim3(256), 0, st, act, cols, nb, n,
+                       n, static_cast<void*>(out));
     return hipGetLastError();
 }
 

@@ -140,6 +140,8 @@ _SIGS = {
     "dr_pass_len": (_SZ, [_VP]),
     "dr_pass_positions": (_I, [_VP, c_size_p, _SZ]),
     "dr_qmatmul": (_I, [_VP, _I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP]),
+    "dr_qmatmul_expert": (_I, [_VP, _I, _VP, _SZ, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP]),
+    "dr_quantize_q8k": (_I, [_VP, _VP, _SZ, _SZ, _VP]),
     "dr_pass_destroy": (None, [_VP]),
     "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_cache_destroy": (None, [_VP]),
@@ -559,3 +561,17 @@ def qmatmul(ctx: Context, wtype: int, w, rows: int, cols: int, act, n: int, out,
     device tensors; w holds rows * cols/256 GGUF blocks."""
     _check(ctx.lib.dr_qmatmul(ctx.h, wtype, _ptr(w), rows, cols, _ptr(act), n, _ptr(out),
                               _ptr(residual) or None))
+
+
+def qmatmul_expert(ctx: Context, wtype: int, w, n_expert: int, expert: int, rows: int, cols: int,
+                   act, n: int, out, residual=None) -> None:
+    """ExpertMat::forward_expert (matmul.rs:176-213): qmatmul on one expert's
+    slice of a [n_expert][rows][cols] block stack."""
+    _check(ctx.lib.dr_qmatmul_expert(ctx.h, wtype, _ptr(w), n_expert, expert, rows, cols, _ptr(act), n,
+                                     _ptr(out), _ptr(residual) or None))
+
+
+def quantize_q8k(ctx: Context, act, n: int, cols: int, out) -> None:
+    """quantize_rows_q8_k (kernels.rs:79-122) into n * cols/256 BlockQ8K
+    (292 bytes each) at device pointer / tensor out."""
+    _check(ctx.lib.dr_quantize_q8k(ctx.h, _ptr(act), n, cols, _ptr(out)))

@@ -330,10 +330,26 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
  * [n][cols], out and residual [n][rows] f32, all device pointers on the
  * context's stream; residual may equal out.  cols must be a multiple of 256,
  * and Q4_K blocks must start 16-byte aligned.
- * Each output is the reference's scalar block dot (src/kernels.rs:228-347),
- * operation for operation. */
+ * The integer part of each block dot (src/kernels.rs:228-347) is exact; the
+ * f32 combine of the per-block integers with the block scales rounds in its
+ * own order, so each output is within (nb + 12) * 2^-24 * S of the exact dot
+ * (nb = cols / 256, S the sum over blocks of |d * scaled dot| + |dmin *
+ * mins dot|), as the reference's scalar dot is. */
 int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
                size_t n, float* out, const float* residual);
+
+/* ExpertMat::forward_expert (src/model/matmul.rs:176-213): dr_qmatmul on
+ * expert `expert`'s slice of a [n_expert][rows][cols] stack of Q4_K / Q6_K
+ * blocks (expert_matmul, matmul.rs:201-213).  expert >= n_expert is
+ * DR_ERR_INVALID ("expert index out of range", matmul.rs:208). */
+int dr_qmatmul_expert(dr_ctx* ctx, int wtype, const void* w, size_t n_expert, size_t expert, size_t rows,
+                      size_t cols, const float* act, size_t n, float* out, const float* residual);
+
+/* quantize_rows_q8_k (src/kernels.rs:79-122), the quantization dr_qmatmul
+ * applies to its activations: act [n][cols] f32 (cols a multiple of 256) ->
+ * out, n * cols / 256 blocks of the reference's BlockQ8K (292 bytes: f32 d,
+ * int8 qs[256], int16 bsums[16]; kernels.rs:37-41), 4-byte aligned. */
+int dr_quantize_q8k(dr_ctx* ctx, const float* act, size_t n, size_t cols, void* out);
 
 /* Launch configuration of the last attention kernel this context enqueued
  * (for measurement): key splits across workgroups, workgroups, waves per

@@ -237,3 +237,65 @@ EXTRA_CONFIGS = {
 
 def config_seed(cfg_id: int, step: int = 0) -> int:
     return 0xD1FF0000 + cfg_id + 1000 * step
+
+
+# ---- k-quant Wo (native_matmul, matmul.rs:120-148) test inputs and bound
+
+def kquant_weights(rng: np.random.Generator, wtype: int, rows: int, cols: int) -> np.ndarray:
+    """rows * cols/256 random GGUF blocks (Q4_K = 12: 144 bytes, Q6_K = 14: 210)
+    with sane positive f16 d (and dmin); the quant bytes are arbitrary."""
+    nb = cols // 256
+    bb = 144 if wtype == 12 else 210
+    w = rng.integers(0, 256, (rows * nb, bb), dtype=np.uint8)
+    dpos = 0 if wtype == 12 else 208
+    w[:, dpos:dpos + 2] = np.float16(rng.uniform(1e-4, 0.02, rows * nb)).view(np.uint8).reshape(-1, 2)
+    if wtype == 12:
+        w[:, 2:4] = np.float16(rng.uniform(1e-4, 0.02, rows * nb)).view(np.uint8).reshape(-1, 2)
+    return w.reshape(-1)
+
+
+def kquant_acts(rng: np.random.Generator, n: int, cols: int) -> np.ndarray:
+    """Activations with an all-zero block (d = 0; n > 1), a negative extreme
+    and tied largest magnitudes (the first one sets the scale; n > 2)."""
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    if n > 1:
+        x[0, :256] = 0.0
+    if n > 2:
+        x[2, 300 % cols] = -40.0
+        x[1, 7] = x[1, 9] = 9.0
+        x[1, 8] = -9.0
+    return x
+
+
+def kquant_dequant_f64(orc, wtype: int, w: np.ndarray, rows: int, cols: int, magnitude: bool = False):
+    """[rows][cols] float64 of dequantize_q4k/q6k_row (kernels.rs:129-215).
+    magnitude=True: |d sc q| + |dmin mn| per value instead (Q4_K: the same
+    blocks with dmin negated, d and dmin > 0; Q6_K: |value|)."""
+    nb = cols // 256
+    wb = np.array(w, np.uint8).reshape(rows * nb, -1)
+    if magnitude and wtype == 12:
+        wb = wb.copy()
+        wb[:, 3] ^= 0x80  # sign bit of the f16 dmin
+    deq = orc.dequant(wtype, wb.reshape(-1), rows * nb).astype(np.float64).reshape(rows, cols)
+    return np.abs(deq) if magnitude else deq
+
+
+def kquant_acts_f64(orc, x: np.ndarray, n: int, cols: int) -> np.ndarray:
+    """[n][cols] float64 of the Q8_K activations d * qs (quantize_rows_q8_k,
+    kernels.rs:79-122)."""
+    q = orc.quantize_q8k(x, n, cols)
+    nb = cols // 256
+    return (q["qs"].astype(np.float64) * q["d"].astype(np.float64)[:, None]).reshape(n, nb * 256)
+
+
+def kquant_bound(orc, wtype: int, w, rows: int, cols: int, x: np.ndarray, n: int, res=None) -> np.ndarray:
+    """[n][rows] bound on |a k-quant Wo output - another one|.  Every integer
+    of a block dot is exact; the f32 combine of the per-block integers with d
+    and dmin, however ordered, is within (nb + 12) * 2^-24 * S of the exact
+    value, S = sum over blocks of |d dot| + |dmin mins dot| <= T = sum_i (|d sc
+    q_i| + |dmin mn|) |d_x qs_i|.  Two such computations differ by at most
+    twice that; the residual add rounds once on each side (|res| counted in)."""
+    nb = cols // 256
+    T = np.abs(kquant_acts_f64(orc, x, n, cols)) @ kquant_dequant_f64(orc, wtype, w, rows, cols, True).T
+    r = 0.0 if res is None else np.abs(np.asarray(res, np.float64).reshape(n, rows))
+    return 2.0 * (nb + 12) * 2.0 ** -24 * (T + r)

@@ -551,3 +551,69 @@ def test_q4k_scales_and_mins_closed_form():
     for j in range(8):
         q = 3 if j % 2 == 0 else 5
         assert np.all(w[32 * j:32 * j + 32] == np.float32(sc[j] * q - mn[j])), j
+
+
+@pytest.mark.parametrize("wtype", [orc.WTYPE_Q4K, orc.WTYPE_Q6K])
+def test_qmatmul_composition_vs_f64_dequant(wtype):
+    """or_qmatmul (native_matmul, matmul.rs:120-148, over Q8_K activations,
+    matmul.rs:64-71) against an independent float64 composition: out[t, r] =
+    sum_i dequant(W)[r, i] * d_t,b * qs_t,i + residual, with three blocks per
+    row and rows != n, within the stated f32 bound.  Negative controls: the
+    same composition with the output transposed (out[r * n + t]), with two
+    weight rows swapped, with two activation rows swapped, or without the
+    last block, each breaks the bound."""
+    from helpers import kquant_acts, kquant_acts_f64, kquant_bound, kquant_dequant_f64, kquant_weights
+    rng = np.random.default_rng(7 + wtype)
+    rows, cols, n = 7, 768, 4
+    w = kquant_weights(rng, wtype, rows, cols)
+    x = kquant_acts(rng, n, cols)
+    res = rng.standard_normal((n, rows)).astype(np.float32)
+    got = orc.qmatmul(wtype, w, rows, cols, x, n, res).reshape(n, rows).astype(np.float64)
+    W = kquant_dequant_f64(orc, wtype, w, rows, cols)
+    X = kquant_acts_f64(orc, x, n, cols)
+    want = X @ W.T + res
+    # dequant's own f32 rounding (d * sc * q - dmin * mn: 3 roundings) on top
+    tol = kquant_bound(orc, wtype, w, rows, cols, x, n, res) + \
+        3 * 2.0 ** -24 * (np.abs(X) @ kquant_dequant_f64(orc, wtype, w, rows, cols, True).T)
+    err = np.abs(got - want)
+    assert np.all(err <= tol), float(np.max(err / tol))
+    assert np.max(np.abs(want)) > 1.0  # not a vacuous comparison
+    bad_t = (X @ W.T + res).reshape(-1)[np.arange(n * rows).reshape(rows, n).T.reshape(-1)].reshape(n, rows)
+    W_sw = W[[1, 0] + list(range(2, rows))]
+    X_sw = X[[1, 0] + list(range(2, n))]
+    X_drop = X.copy()
+    X_drop[:, 512:] = 0.0
+    for name, wrong in (("transposed", bad_t), ("weight rows swapped", X @ W_sw.T + res),
+                        ("activation rows swapped", X_sw @ W.T + res), ("last block dropped", X_drop @ W.T + res)):
+        assert np.any(np.abs(got - wrong) > tol), name
+
+
+def test_q6k_values_bijective_and_scale_per_16():
+    """Q6_K (dequantize_q6k_row, kernels.rs:129-163): every one of the 256
+    6-bit fields (a 4-bit ql nibble + a 2-bit qh pair) feeds exactly one value,
+    and sub-block j (values 16 j .. 16 j + 15) takes scale j: with all fields
+    zero each value is d * sc_j * -32; raising one field's low bit moves
+    exactly one value by d * sc_j."""
+    b = np.zeros(210, np.uint8)
+    sc = np.arange(1, 17, dtype=np.int8)
+    b[192:208] = sc.view(np.uint8)
+    b[208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    base = orc.dequant(orc.WTYPE_Q6K, b, 1)
+    assert np.array_equal(base, np.repeat(sc.astype(np.float32) * -32.0, 16))
+    hit = np.zeros(256, int)
+    for byte in range(128):  # ql: two nibbles per byte
+        for shift in (0, 4):
+            bb = b.copy()
+            bb[byte] = 1 << shift
+            d = orc.dequant(orc.WTYPE_Q6K, bb, 1) - base
+            (idx,) = np.nonzero(d)
+            assert len(idx) == 1 and d[idx[0]] == sc[idx[0] // 16], (byte, shift)
+            hit[idx[0]] += 1
+    for byte in range(128, 192):  # qh: four 2-bit pairs per byte; +16 per pair
+        for pair in range(4):
+            bb = b.copy()
+            bb[byte] = 1 << (2 * pair)
+            d = orc.dequant(orc.WTYPE_Q6K, bb, 1) - base
+            (idx,) = np.nonzero(d)
+            assert len(idx) == 1 and d[idx[0]] == 16 * int(sc[idx[0] // 16]), (byte, pair)
+    assert np.all(hit == 1)
