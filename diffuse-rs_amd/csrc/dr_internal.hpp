@@ -169,22 +169,28 @@ static_assert(sizeof(Q8KBlock) == 292, "Q8_K block layout");
 // qmm workgroup (the pad rows are quantized as zeros).
 __host__ __device__ inline int qmm_rows_padded(int n) { return (n + 127) / 128 * 128; }
 
-// dr_qmatmul's workspace: the Q8_K activations in the matrix-core layout.
-//   qs    int8 [n_pad][cols]  (each 256-value block permuted: value 32 s +
-//         16 g + j at byte 128 g + 16 s + j)
-//   bmin  bf16 [n_pad][nb][16]  (per block: bsum_s & 63 for s = 0..7, then
-//         bsum_s - (bsum_s & 63); bsum_s = sum of values 32 s .. 32 s + 31)
-//   xd    f32 [nb][n_pad]  (the Q8_K d of block b of row t at b * n_pad + t)
+// dr_qmatmul's workspace: the Q8_K activations in the order the int8 MFMA
+// reads them, so every operand load of a wave is one contiguous run.  Rows
+// are grouped in 32-row tiles; lane (c, g) of a tile's operands (c = row % 32,
+// g = 0, 1) holds values 32 s + 16 g .. + 15 of sub-block slab s:
+//   qs    int8 [n_pad/32][nb][8 slabs][64 lanes][16]
+//   bmin  bf16 [n_pad/32][nb][64 lanes][8]  lane (c, 0): bsum_s & 63, lane
+//         (c, 1): bsum_s - (bsum_s & 63), s = 0..7 (bsum_s = sum of values
+//         32 s .. 32 s + 31 of row c)
+//   xd    f32  [n_pad/32][nb][32]  the Q8_K d of each row
 struct QmmLayout {
     int8_t* qs;
     uint16_t* bmin;
     float* xd;
+    int nb;
     __host__ __device__ QmmLayout(void* ws, int n_pad, int cols) {
-        const size_t nb = (size_t)cols / 256;
+        nb = cols / 256;
         qs = static_cast<int8_t*>(ws);
         bmin = reinterpret_cast<uint16_t*>(qs + (size_t)n_pad * cols);
         xd = reinterpret_cast<float*>(bmin + (size_t)n_pad * nb * 16);
     }
+    // (tile, block) index of row-tile t32 = t / 32 and block b
+    __host__ __device__ size_t tb(int t32, int b) const { return (size_t)t32 * nb + b; }
 };
 
 // native_matmul (src/model/matmul.rs:120-148) + residual_add (ops.rs:365-370):

@@ -14,8 +14,10 @@
 // run as two MFMA chains over the whole 256-value block, aux = (acc_hi << k)
 // + acc_lo, exact in int32.  The Q4_K min term is one exact bf16 MFMA per
 // block (mn_s <= 63 and the 32-value sums bsum_s split as lo + 64 hi are bf16
-// integers; every partial sum stays below 2^24).  Per block and output the f32
-// combine is fma(fma(aux, d_w, -dmin_w * mins), d_x, sum).
+// integers; every partial sum stays below 2^24).  The block scales d = d_x d_w
+// and dmin = d_x dmin_w of every output come out of a K = 2 f32 MFMA in the
+// accumulator layout, each one rounded product as in the reference; per
+// block and output the combine is sum = fma(-dmin, mins, fma(d, aux, sum)).
 //
 // Numerics: every integer is exact; each output differs from the reference's
 // scalar vec_dot (src/kernels.rs:228-347) only in the rounding of the f32
@@ -38,25 +40,6 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef short i16x2 __attribute__((ext_vector_type(2)));
 
-// f16_to_f32 of src/kernels.rs:46-69 (bit for bit, NaN payload included).
-__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-    const uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1Fu, mant = h & 0x3FFu;
-    uint32_t bits;
-    if (ex == 0) {
-        if (mant == 0) {
-            bits = sign << 31;
-        } else {
-            const uint32_t lz = __builtin_clz(mant) - 21;  // shifts until bit 10 is set
-            bits = (sign << 31) | ((113u - lz) << 23) | (((mant << lz) & 0x3FFu) << 13);
-        }
-    } else if (ex == 31) {
-        bits = (sign << 31) | (0xFFu << 23) | (mant ? 0x7FFFFFu : 0u);
-    } else {
-        bits = (sign << 31) | ((ex + 112u) << 23) | (mant << 13);
-    }
-    return __uint_as_float(bits);
-}
-
 template <typename T>
 __device__ __forceinline__ T gld(const void* p) {
     return *(const __attribute__((address_space(1))) T*)p;
@@ -68,6 +51,10 @@ __device__ __forceinline__ u32x4 gld16_a2(const uint8_t* p) {
     __builtin_memcpy(&v, q, 16);
     return v;
 }
+
+// A workgroup barrier that waits only for this wave's LDS operations (the
+// global loads in flight stay in flight).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
@@ -100,97 +87,145 @@ __device__ __forceinline__ void bytes_to_bf16(uint32_t x, uint32_t& lo, uint32_t
 }
 
 // ---------------------------------------------------------------------------
-// Q8_K quantization (quantize_rows_q8_k, src/kernels.rs:79-122): one
-// workgroup per 256-value block, thread i owns value i.  The first value of
-// largest magnitude gives iscale = -128 / max; q = round(iscale x) capped at
-// 127; d = 1 / iscale.  NaN values never win the scan (amax < |x| is false).
+// Q8_K quantization (quantize_rows_q8_k, src/kernels.rs:79-122): one wave per
+// 256-value block (four per workgroup), lane l owns values 4 l .. 4 l + 3.
+// The first value of largest magnitude gives iscale = -128 / max; q =
+// round(iscale x) capped at 127; d = 1 / iscale.  NaN values never win the
+// scan (amax < |x| is false).  Only max's sign needs the first index: the
+// magnitude is a wave maximum, the first holder a ballot.
 //
 // REF = true writes the reference's BlockQ8K (d, qs[256], bsums[16]); REF =
-// false writes the matrix-core layout of the workspace (QmmLayout): qs with
-// value 32 s + 16 g + j of a block at byte 128 g + 16 s + j, so the 16-value
-// operand of lane group g for sub-block s is one 16-byte run and a lane's
-// eight runs are one 128-byte line; the 32-value sums as bf16 lo / 64 hi;
-// d as [block][row].  Rows n .. n_pad - 1 are written as zeros.
-template <bool REF>
-__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, int cols, int nb,
-                                                           int n, int n_pad, void* __restrict__ out) {
-    __shared__ float s_a[4];
-    __shared__ int s_i[4];
-    __shared__ float s_mx;
-    const int blk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = blk / nb, b = blk - t * nb;
-    const float v = t < n ? x[(size_t)t * cols + (size_t)b * QK + tid] : 0.0f;
-    float a = v != v ? -1.0f : fabsf(v);
-    int idx = tid;
+// false writes the matrix-core operand order of the workspace (QmmLayout).
+// Rows n .. n_pad - 1 are written as zeros.
+// DPP steps of the wave reductions below (gfx9 row / quad patterns).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+// Maximum over the wave, in lane 63 and broadcast through a scalar.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));        // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_f<0x4E>(v));        // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_f<0x141>(v));       // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));       // row_mirror: every lane holds its row's maximum
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v));  // row_bcast:15 into rows 1 and 3
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v));  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Quantizes the 256 values of one row-block held by a wave (lane l: values
+// 4 l .. 4 l + 3): q (four values), d, and the lane's share of the sums.
+struct RowQ {
+    uint32_t packed;  // the lane's four q as bytes
+    int sum4;         // their sum
+    float d;
+};
+__device__ __forceinline__ RowQ quantize_row_block(const f32x4 v) {
+    // the largest |x| (a NaN never wins: it counts as -1), then the first
+    // value that has it: the lowest lane holding one, its first element
+    float ae[4];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(a, off);
-        const int oi = __shfl_xor(idx, off);
-        if (oa > a || (oa == a && oi < idx)) {
-            a = oa;
-            idx = oi;
-        }
-    }
-    if (lane == 0) {
-        s_a[wave] = a;
-        s_i[wave] = idx;
-    }
-    __syncthreads();
-    float amax = s_a[0];
-    int imax = s_i[0];
-#pragma unroll
-    for (int w = 1; w < 4; ++w)
-        if (s_a[w] > amax) {  // waves in index order: a tie keeps the earlier one
-            amax = s_a[w];
-            imax = s_i[w];
-        }
-    if (tid == imax) s_mx = v;
-    __syncthreads();
-    int q = 0;
-    float d = 0.0f;
+    for (int e = 0; e < 4; ++e) ae[e] = v[e] != v[e] ? -1.0f : fabsf(v[e]);
+    const float amax = wave_max(fmaxf(fmaxf(ae[0], ae[1]), fmaxf(ae[2], ae[3])));
+    const float mine = ae[0] == amax ? v[0] : ae[1] == amax ? v[1] : ae[2] == amax ? v[2] : v[3];
+    const unsigned long long hit = __ballot(ae[0] == amax || ae[1] == amax || ae[2] == amax || ae[3] == amax);
+    const int first = hit ? (int)__builtin_ctzll(hit) : 0;
+    const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
+    int q[4] = {0, 0, 0, 0};
+    RowQ o;
+    o.d = 0.0f;
     if (amax > 0.0f) {
 #pragma clang fp contract(off)
-        const float iscale = -128.0f / s_mx;
-        const float r = fminf(roundf(iscale * v), 127.0f);
-        q = (int)r;
-        d = 1.0f / iscale;
+        const float iscale = -128.0f / mx;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = (int)fminf(roundf(iscale * v[e]), 127.0f);
+        o.d = 1.0f / iscale;
     }
-    if constexpr (REF) {
-        Q8KBlock* o = static_cast<Q8KBlock*>(out) + blk;
-        if (tid == 0) o->d = d;
-        o->qs[tid] = (int8_t)q;
-        int s = q;
+    o.packed = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((uint32_t)q[3] << 24);
+    o.sum4 = q[0] + q[1] + q[2] + q[3];
+    return o;
+}
+
+// The reference's BlockQ8K (d, qs[256], bsums[16]): one wave per block, four
+// per workgroup.
+__global__ __launch_bounds__(256) void q8k_quantize_ref_kernel(const float* __restrict__ x, int cols, int nb, int n,
+                                                               Q8KBlock* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= n * nb) return;  // (no barriers below: a whole wave leaves)
+    const int t = blk / nb, b = blk - t * nb;
+    const RowQ rq = quantize_row_block(gld<f32x4>(x + (size_t)t * cols + (size_t)b * QK + 4 * lane));
+    Q8KBlock* o = out + blk;
+    if (lane == 0) o->d = rq.d;
+    *reinterpret_cast<uint32_t*>(o->qs + 4 * lane) = rq.packed;
+    int s = rq.sum4;
+    s += dpp_i<0xB1>(s);  // the quad: 16 values
+    s += dpp_i<0x4E>(s);
+    if ((lane & 3) == 0) o->bsums[lane >> 2] = (int16_t)s;
+}
+
+// The matrix-core operand order of the workspace (QmmLayout): one workgroup
+// (8 waves) per 32-row tile and block, wave w quantizes rows 4 w .. 4 w + 3.
+// The tile's operands are assembled in LDS and leave as whole 16-byte runs
+// (8 KB of qs, 1 KB of min operands, 128 bytes of d).  Rows n .. n_pad - 1
+// are written as zeros.
+__global__ __launch_bounds__(512) void q8k_quantize_tiles_kernel(const float* __restrict__ x, int cols, int nb,
+                                                                 int n, int n_pad, void* __restrict__ ws) {
+    // qs chunks [slab * 2 + g][33, one pad][16 bytes]: the 16 lane quads of a
+    // row write distinct banks
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[16 * 33 * 4];
+    __shared__ __attribute__((aligned(16))) uint16_t s_bm[64 * 8];
+    __shared__ __attribute__((aligned(16))) float s_xd[32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t32 = blockIdx.x / nb, b = blockIdx.x - t32 * nb;
+    f32x4 v[4];
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
-        if ((tid & 15) == 0) o->bsums[tid >> 4] = (int16_t)s;
-    } else {
-        const QmmLayout L(out, n_pad, cols);
-        // four neighbouring values land in one dword of the permuted block
-        const uint32_t q0 = q & 0xFF, q1 = __shfl_down(q, 1) & 0xFF, q2 = __shfl_down(q, 2) & 0xFF,
-                       q3 = __shfl_down(q, 3) & 0xFF;
-        if ((tid & 3) == 0) {
-            const int pos = 128 * ((tid >> 4) & 1) + 16 * (tid >> 5) + (tid & 15);
-            *reinterpret_cast<uint32_t*>(L.qs + (size_t)t * cols + (size_t)b * QK + pos) =
-                q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
-        }
-        int s = q;
+    for (int k = 0; k < 4; ++k) {
+        const int t = t32 * 32 + 4 * wave + k;
+        v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < n) v[k] = gld<f32x4>(x + (size_t)t * cols + (size_t)b * QK + 4 * lane);
+    }
 #pragma unroll
-        for (int off = 1; off < 32; off <<= 1) s += __shfl_xor(s, off);
-        if ((tid & 31) == 0) {
+    for (int k = 0; k < 4; ++k) {
+        const int c = 4 * wave + k;
+        const RowQ rq = quantize_row_block(v[k]);
+        // values 4 lane .. + 3: slab lane / 8, lane group (lane / 4) % 2
+        s_q[((lane >> 2) * 33 + c) * 4 + (lane & 3)] = rq.packed;
+        int s = rq.sum4;
+        s += dpp_i<0xB1>(s);   // the quad
+        s += dpp_i<0x4E>(s);
+        s += dpp_i<0x141>(s);  // and its half row: 32 values
+        if ((lane & 7) == 0) {
             const int lo = s & 63, hi = s - lo;  // |s| <= 4096: both exact in bf16
-            uint16_t* bm = L.bmin + ((size_t)t * nb + b) * 16;
-            bm[tid >> 5] = (uint16_t)(__float_as_uint((float)lo) >> 16);
-            bm[8 + (tid >> 5)] = (uint16_t)(__float_as_uint((float)hi) >> 16);
+            s_bm[c * 8 + (lane >> 3)] = (uint16_t)(__float_as_uint((float)lo) >> 16);
+            s_bm[(32 + c) * 8 + (lane >> 3)] = (uint16_t)(__float_as_uint((float)hi) >> 16);
         }
-        if (tid == 0) L.xd[(size_t)b * n_pad + t] = d;
+        if (lane == 0) s_xd[c] = rq.d;
     }
+    __syncthreads();
+    const QmmLayout L(ws, n_pad, cols);
+    const size_t tb = L.tb(t32, b);
+    const int q = threadIdx.x;  // chunk (slab * 2 + g) * 32 + row of the tile's 8 KB
+    *reinterpret_cast<u32x4*>(L.qs + tb * 8192 + (size_t)q * 16) =
+        *reinterpret_cast<const u32x4*>(&s_q[((q >> 5) * 33 + (q & 31)) * 4]);
+    if (q < 64)
+        *reinterpret_cast<u32x4*>(L.bmin + (tb * 64 + q) * 8) = *reinterpret_cast<const u32x4*>(&s_bm[q * 8]);
+    else if (q < 72)
+        *reinterpret_cast<f32x4*>(L.xd + tb * 32 + 4 * (q - 64)) = *reinterpret_cast<const f32x4*>(&s_xd[4 * (q - 64)]);
 }
 
 // ---------------------------------------------------------------------------
-// The block dots.  A workgroup owns 32 weight rows x 128 activation rows (four
-// 32 x 32 MFMA tiles); its four waves split the 256-value blocks of a row into
-// four contiguous ranges and their partial sums meet in LDS in wave order, so
-// every output is summed in the same order on every call.
+// The block dots.  A workgroup (8 waves, two per SIMD) owns 32 weight rows x
+// 128 activation rows: wave w computes the 32 x 32 MFMA tile c = w % 4 over
+// half h = w / 4 of the 256-value blocks of a row (the two halves' partial
+// sums meet in LDS, so every output is summed in one fixed order).  The
+// weight operands of a block are formed once per workgroup: each wave of a
+// half converts two of the eight sub-block slabs of its half's block into
+// LDS, double-buffered, one block ahead of the MFMAs; one barrier per block.
 //
 // MFMA operands (A = activations: row t; B = weights: column r): lane (c, g),
 // c = lane % 32, g = lane / 32, holds values 32 s + 16 g .. + 15 of sub-block
@@ -199,89 +234,129 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restri
 //
 // Weight operand of a Q4_K block: slab s = sub-block s.  sc_s = 8 sh + sl with
 // sh, sl <= 7, so sh * q and sl * q (q <= 15) are bytes and a 16-bit packed
-// multiply scales two nibble bytes at once without carries.  Q6_K: slab s is
+// multiply scales two nibble bytes at once without carries; the two parts
+// run as one accumulator chain: acc = 8 * (A . hi) + A . lo.  Q6_K: slab s is
 // sub-blocks 2 s (g = 0) and 2 s + 1 (g = 1); w = sc * (q - 32) in
 // [-4064, 4096] is formed in 16-bit lanes and split as 64 hi + lo.
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    // exact for every finite and infinite f16 (src/kernels.rs:46-69); a NaN
+    // stays a NaN
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// The raw bytes a wave needs of one block: the 16-byte Q4_K header (d, dmin,
+// scales) and the 16 qs bytes of its two slabs; for Q6_K the scales, the ql
+// and qh runs of its two slabs, and d.
 template <int WT>
-struct WeightOps {
-    i32x4 hi[8], lo[8];
-    bf16x8 mn;        // Q4_K: the eight 6-bit mins
-    float wd, wdmin;  // f16 d (and dmin) of the block
+struct RawBlock;
+template <>
+struct RawBlock<12> {
+    u32x4 h, q;
+};
+template <>
+struct RawBlock<14> {
+    u32x4 sc, ql[2], qh;
+    uint32_t d;
 };
 
-__device__ __forceinline__ void prep_q4k(const uint8_t* blk, int g, WeightOps<12>& o) {
-    const u32x4 h = gld<u32x4>(blk);  // d, dmin, scales[12]
-    o.wd = f16_bits_to_f32(h.x & 0xFFFF);
-    o.wdmin = f16_bits_to_f32(h.x >> 16);
+// slabs 2 c and 2 c + 1 of a Q4_K block: qs bytes 32 c + 16 g .. + 15
+__device__ __forceinline__ void load_raw(const uint8_t* blk, int c, int g, RawBlock<12>& r) {
+    r.h = gld<u32x4>(blk);
+    r.q = gld<u32x4>(blk + 16 + 32 * c + 16 * g);
+}
+// slabs 2 c, 2 c + 1 of a Q6_K block: half c / 2, quarters 2 (c % 2), + 1
+// (src/kernels.rs:135-147): ql runs 64 h + 32 a + 16 g, qh run 32 h + 16 g
+__device__ __forceinline__ void load_raw(const uint8_t* blk, int c, int g, RawBlock<14>& r) {
+    const int h = c >> 1;
+    r.sc = gld16_a2(blk + 192);
+    r.ql[0] = gld16_a2(blk + 64 * h + 16 * g);
+    r.ql[1] = gld16_a2(blk + 64 * h + 32 + 16 * g);
+    r.qh = gld16_a2(blk + 128 + 32 * h + 16 * g);
+    r.d = gld<uint16_t>(blk + 208);
+}
+
+// What the combine of a block needs besides the MFMA results.
+struct BlockScale {
+    float wd, wdmin;
+    bf16x8 mn;  // Q4_K: the eight 6-bit mins (B operand of the min MFMA)
+};
+
+// Scales of a block, and this wave's two slabs of B operands into LDS
+// (dst[slab][hi / lo][lane]).
+__device__ __forceinline__ void prep(const RawBlock<12>& r, int c, int lane, u32x4* dst, BlockScale& o) {
+    const u32x4 h = r.h;
+    o.wd = f16_to_f32(h.x & 0xFFFF);
+    o.wdmin = f16_to_f32(h.x >> 16);
     // the 12 packed bytes (src/kernels.rs:193-201): sc 0..3, sc 4..7, mn 0..3, mn 4..7
     const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
     const uint32_t sc03 = h.y & k1, mn03 = h.z & k1;
     const uint32_t sc47 = (h.w & k2) | (((h.y >> 6) & k3) << 4);
     const uint32_t mn47 = ((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4);
-    const uint32_t sh[2] = {(sc03 >> 3) & 0x07070707u, (sc47 >> 3) & 0x07070707u};
-    const uint32_t sl[2] = {sc03 & 0x07070707u, sc47 & 0x07070707u};
     uint32_t m0, m1, m2, m3;
     bytes_to_bf16(mn03, m0, m1);
     bytes_to_bf16(mn47, m2, m3);
     o.mn = __builtin_bit_cast(bf16x8, u32x4{m0, m1, m2, m3});
+    const uint32_t sc = c < 2 ? sc03 : sc47;  // bytes 2 c % 4, 2 c % 4 + 1
+    const uint32_t sh = (sc >> 3) & 0x07070707u, sl = sc & 0x07070707u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // qs bytes 32 j + 16 g ..: sub-blocks 2 j (low), 2 j + 1 (high)
-        const u32x4 raw = gld<u32x4>(blk + 16 + 32 * j + 16 * g);
+    for (int hn = 0; hn < 2; ++hn) {  // low nibbles: slab 2 c; high: 2 c + 1
+        const int byte = 2 * (c & 1) + hn;
+        const uint32_t fh = rep_byte_u16(sh, byte), fl = rep_byte_u16(sl, byte);
+        u32x4 vh, vl;
 #pragma unroll
-        for (int hn = 0; hn < 2; ++hn) {
-            const int s = 2 * j + hn;
-            const uint32_t fh = rep_byte_u16(sh[s >> 2], s & 3), fl = rep_byte_u16(sl[s >> 2], s & 3);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t nib = hn ? (raw[c] >> 4) & 0x0F0F0F0Fu : raw[c] & 0x0F0F0F0Fu;
-                o.hi[s][c] = (int)pk_mul_u16(nib, fh);
-                o.lo[s][c] = (int)pk_mul_u16(nib, fl);
-            }
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t nib = hn ? (r.q[k] >> 4) & 0x0F0F0F0Fu : r.q[k] & 0x0F0F0F0Fu;
+            vh[k] = pk_mul_u16(nib, fh);
+            vl[k] = pk_mul_u16(nib, fl);
         }
+        dst[((2 * c + hn) * 2 + 0) * 64 + lane] = vh;
+        dst[((2 * c + hn) * 2 + 1) * 64 + lane] = vl;
     }
 }
 
-__device__ __forceinline__ void prep_q6k(const uint8_t* blk, int g, WeightOps<14>& o) {
-    o.wd = f16_bits_to_f32(blk[208] | (blk[209] << 8));
+__device__ __forceinline__ void prep(const RawBlock<14>& r, int c, int lane, u32x4* dst, BlockScale& o) {
+    o.wd = f16_to_f32(r.d);
     o.wdmin = 0.0f;
-    const u32x4 scv = gld16_a2(blk + 192);  // int8 scales of the 16 sub-blocks
-    u32x4 ql[2][2], qh[2];
+    const int g = lane >> 5;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        qh[h] = gld16_a2(blk + 128 + 32 * h + 16 * g);
-#pragma unroll
-        for (int a = 0; a < 2; ++a) ql[h][a] = gld16_a2(blk + 64 * h + 32 * a + 16 * g);
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        // values 128 h + 32 quarter + 16 g + j (src/kernels.rs:135-147)
-        const int h = s >> 2, quarter = s & 3, a = quarter & 1;
-        const int sb = 2 * s + g;  // sub-block of 16
-        const int scb = (int)(int8_t)((scv[sb >> 2] >> (8 * (sb & 3))) & 0xFF);
+    for (int k2 = 0; k2 < 2; ++k2) {
+        const int s = 2 * c + k2;
+        const int quarter = s & 3;        // ql run a = quarter & 1, nibble quarter >> 1
+        const int sb = 2 * s + g;         // sub-block of 16
+        // (selects, not indexing: the indices differ between waves)
+        const uint32_t scw = (sb >> 2) == 0 ? r.sc.x : (sb >> 2) == 1 ? r.sc.y : (sb >> 2) == 2 ? r.sc.z : r.sc.w;
+        const int scb = (int)(int8_t)((scw >> (8 * (sb & 3))) & 0xFF);
         const uint32_t f = ((uint32_t)scb & 0xFFFFu) * 0x10001u;
+        const u32x4 qrun = (quarter & 1) ? r.ql[1] : r.ql[0];
+        const int nshift = (quarter >> 1) * 4;
+        u32x4 vh, vl;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint32_t nib = (quarter >> 1) ? (ql[h][a][c] >> 4) & 0x0F0F0F0Fu : ql[h][a][c] & 0x0F0F0F0Fu;
-            const uint32_t q6 = nib | (((qh[h][c] >> (2 * quarter)) & 0x03030303u) << 4);
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t nib = (qrun[k] >> nshift) & 0x0F0F0F0Fu;
+            const uint32_t q6 = nib | (((r.qh[k] >> (2 * quarter)) & 0x03030303u) << 4);
             const uint32_t w01 = pk_mul_u16(pk_sub_u16(bytes01_u16(q6), 0x00200020u), f);
             const uint32_t w23 = pk_mul_u16(pk_sub_u16(bytes23_u16(q6), 0x00200020u), f);
-            o.hi[s][c] = (int)pack_lo_bytes(pk_ashr_i16(w01, 6), pk_ashr_i16(w23, 6));
-            o.lo[s][c] = (int)pack_lo_bytes(w01 & 0x003F003Fu, w23 & 0x003F003Fu);
+            vh[k] = pack_lo_bytes(pk_ashr_i16(w01, 6), pk_ashr_i16(w23, 6));
+            vl[k] = pack_lo_bytes(w01 & 0x003F003Fu, w23 & 0x003F003Fu);
         }
+        dst[(s * 2 + 0) * 64 + lane] = vh;
+        dst[(s * 2 + 1) * 64 + lane] = vl;
     }
 }
 
 template <int WT>
-__global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
+__global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     constexpr bool Q4 = WT == 12;
     constexpr int WB = Q4 ? Q4K_BYTES : Q6K_BYTES;
     constexpr int SHIFT = Q4 ? 3 : 6;
-    // partial sums of the three other waves for each wave's tile:
-    // [tile][source wave, own skipped][slot][lane]
-    __shared__ float s_part[4][3][16][64];
+    // B operands [buffer][half][slab][hi / lo][lane] (64 KB); after the loop
+    // the first 16 KB carry half 1's partial sums [tile][slot][lane]
+    __shared__ u32x4 s_b[2][2][8][2][64];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int col = lane & 31, g = lane >> 5;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // (uniform: scalar branches)
+    const int c = wave & 3, kh = wave >> 2;
     const int nb = a.cols / QK;
     const int n_rt = (a.rows + 31) / 32, n_tt = a.n_pad / 128;
     const int nwg = n_rt * n_tt, hw = blockIdx.x;
@@ -289,86 +364,134 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
     // operand) are read into each XCD's L2 once
     const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
     const int rt = lid / n_tt, tt = lid - rt * n_tt;
+    const int col = lane & 31, g = lane >> 5;
     const int r = min(rt * 32 + col, a.rows - 1);
-    const int t0 = tt * 128;
+    const int tc = tt * 128 + 32 * c;  // first row of this wave's tile
     const QmmLayout L(a.ws, a.n_pad, a.cols);
     const uint8_t* wrow = static_cast<const uint8_t*>(a.w) + (size_t)r * nb * WB;
 
-    f32x16 sum[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sum[c][i] = 0.0f;
+    const int nh = (nb + 1) / 2;                 // iterations (blocks of half 0)
+    const int kb0 = kh ? nh : 0, kcnt = kh ? nb - nh : nh;
+    const int8_t* abase = L.qs + (size_t)(tc >> 5) * nb * 8 * 1024 + lane * 16;
+    const float* xbase = L.xd + (size_t)(tc >> 5) * nb * 32 + col;
+    const uint16_t* mbase = L.bmin + ((size_t)(tc >> 5) * nb * 64 + lane) * 8;
 
-    const int b_begin = wave * nb / 4, b_end = (wave + 1) * nb / 4;
-    for (int b = b_begin; b < b_end; ++b) {
-        WeightOps<WT> wo;
-        if constexpr (Q4)
-            prep_q4k(wrow + (size_t)b * WB, g, wo);
-        else
-            prep_q6k(wrow + (size_t)b * WB, g, wo);
+    f32x16 sum;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int tr = t0 + 32 * c + col;  // this lane's A row
-            const int8_t* ap = L.qs + (size_t)tr * a.cols + (size_t)b * QK + 128 * g;
-            i32x4 av[8];
-#pragma unroll
-            for (int s = 0; s < 8; ++s) av[s] = gld<i32x4>(ap + 16 * s);
-            f32x4 xd[4];
-            const float* xp = L.xd + (size_t)b * a.n_pad + t0 + 32 * c + 4 * g;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) xd[k] = gld<f32x4>(xp + 8 * k);
-            i32x16 ah = {}, al = {};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                ah = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], wo.hi[s], ah, 0, 0, 0);
-                al = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], wo.lo[s], al, 0, 0, 0);
-            }
-            f32x16 mins = {};
-            if constexpr (Q4) {
-                const bf16x8 bm = gld<bf16x8>(L.bmin + ((size_t)tr * nb + b) * 16 + 8 * g);
-                f32x16 z;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) z[i] = 0.0f;
-                mins = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bm, wo.mn, z, 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float f = (float)(ah[i] * (1 << SHIFT) + al[i]);
-                const float inner = Q4 ? __builtin_fmaf(f, wo.wd, -(mins[i] * wo.wdmin)) : f * wo.wd;
-                sum[c][i] = __builtin_fmaf(inner, xd[i >> 2][i & 3], sum[c][i]);
-            }
-        }
-    }
+    for (int i = 0; i < 16; ++i) sum[i] = 0.0f;
 
-    // ---- the four partial sums of each tile, in wave order; wave w writes tile w
+    // Per block: the A operands, the rows' Q8_K d and the min operand.  Two
+    // sets (the block being multiplied, the next one) and two raw weight sets
+    // (the block being formed into LDS, the one after), used alternately by
+    // an unrolled pair of iterations, so nothing is copied between registers.
+    // Prefetches past the wave's last block reload that block (in bounds,
+    // unused): no load sits behind a branch.
+    struct Stage {
+        i32x4 av[8];
+        float xd;  // lane (c, 0): the Q8_K d of row c (A operand of the scale MFMAs)
+        bf16x8 bm;
+    };
+    Stage S[2];
+    RawBlock<WT> R[2];
+    BlockScale bsc;
+    const int blast = kb0 + (kcnt > 0 ? kcnt - 1 : 0);
+    auto load_stage = [&](int b, Stage& st) __attribute__((always_inline)) {
+        // (in order of need: loads complete in issue order)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        if (c == wave) continue;
-        const int src = wave < c ? wave : wave - 1;
+        for (int s = 0; s < 8; ++s) st.av[s] = gld<i32x4>(abase + ((size_t)b * 8 + s) * 1024);
+        st.xd = gld<float>(xbase + (size_t)b * 32);
+        if constexpr (Q4) st.bm = gld<bf16x8>(mbase + (size_t)b * 64 * 8);
+    };
+    // The combine of a block runs in the next iteration, under that block's
+    // MFMA chains: the products of the previous block wait in registers.
+    struct Products {
+        i32x16 acc;
+        f32x16 mins, dd, dm;
+    };
+    Products P;
+    bool pending = false;  // P holds a block not yet added into sum (uniform)
+    auto combine = [&](const Products& pr) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s_part[c][src][i][lane] = sum[c][i];
-    }
-    __syncthreads();
-    const int c = wave;
-    f32x16 own;
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-        if (cc == c) own = sum[cc];
-    const int rr = rt * 32 + col;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float p = w == c ? own[i] : s_part[c][w < c ? w : (w > c ? w - 1 : 0)][i][lane];
-            v = w == 0 ? p : v + p;
+        for (int i = 0; i < 16; ++i) {
+            sum[i] = __builtin_fmaf(pr.dd[i], (float)pr.acc[i], sum[i]);
+            if constexpr (Q4) sum[i] = __builtin_fmaf(-pr.dm[i], pr.mins[i], sum[i]);
         }
-        const int t = t0 + 32 * c + 8 * (i >> 2) + 4 * g + (i & 3);
-        if (t < a.n && rr < a.rows) {
-            const size_t idx = (size_t)t * a.rows + rr;
-            if (a.residual) v += a.residual[idx];
-            a.out[idx] = v;
+    };
+    auto body = [&](int it, Stage& cur, Stage& nxt, RawBlock<WT>& rprep, RawBlock<WT>& rload, int buf)
+        __attribute__((always_inline)) {
+        if (it < kcnt) {
+            load_stage(min(kb0 + it + 1, blast), nxt);
+            load_raw(wrow + (size_t)min(kb0 + it + 2, blast) * WB, c, g, rload);
+            // (the scheduler would otherwise sink the prefetches to their use)
+            __builtin_amdgcn_sched_barrier(0);
+            // ---- MFMAs of this block: acc = 2^SHIFT (A . hi) + A . lo
+            const u32x4* bsrc = &s_b[buf][kh][0][0][lane];
+            Products np;
+            i32x16 acc = {};
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.av[s], __builtin_bit_cast(i32x4, bsrc[(s * 2) * 64]),
+                                                            acc, 0, 0, 0);
+            // ---- under the first chain: the previous block's combine
+            if (pending) combine(P);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] *= (1 << SHIFT);
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                    cur.av[s], __builtin_bit_cast(i32x4, bsrc[(s * 2 + 1) * 64]), acc, 0, 0, 0);
+            np.acc = acc;
+            np.mins = f32x16{};
+            if constexpr (Q4) np.mins = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.bm, bsc.mn, np.mins, 0, 0, 0);
+            // the block scales d_x d_w (and d_x dmin_w) of every slot, each one
+            // f32 product, on a K = 2 f32 MFMA with the second K row zero
+            const float xa = g == 0 ? cur.xd : 0.0f;
+            const f32x16 z = {};
+            np.dd = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, g == 0 ? bsc.wd : 0.0f, z, 0, 0, 0);
+            np.dm = f32x16{};
+            if constexpr (Q4) np.dm = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, g == 0 ? bsc.wdmin : 0.0f, z, 0, 0, 0);
+            // ---- under the second chain: the next block's B operands into the
+            // other buffer (past the last block: a repeat nobody reads)
+            prep(rprep, c, lane, &s_b[buf ^ 1][kh][0][0][0], bsc);
+            P = np;
+            pending = true;
+        }
+        lds_barrier();
+    };
+    if (kcnt > 0) {
+        RawBlock<WT> raw0;
+        load_raw(wrow + (size_t)kb0 * WB, c, g, raw0);
+        load_stage(kb0, S[0]);
+        load_raw(wrow + (size_t)min(kb0 + 1, blast) * WB, c, g, R[1]);
+        prep(raw0, c, lane, &s_b[0][kh][0][0][0], bsc);
+    }
+    lds_barrier();
+    int it = 0;
+    for (; it + 1 < nh; it += 2) {
+        body(it, S[0], S[1], R[1], R[0], 0);
+        body(it + 1, S[1], S[0], R[0], R[1], 1);
+    }
+    if (it < nh) body(it, S[0], S[1], R[1], R[0], 0);
+    if (pending) combine(P);
+
+    // ---- half 1's partial sums to LDS; half 0 adds them (and the residual)
+    float* red = reinterpret_cast<float*>(&s_b[0][0][0][0][0]);
+    if (kh == 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[(c * 16 + i) * 64 + lane] = sum[i];
+    }
+    lds_barrier();
+    if (kh == 0) {
+        const int rr = rt * 32 + col;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float v = sum[i] + red[(c * 16 + i) * 64 + lane];
+            const int t = tc + 8 * (i >> 2) + 4 * g + (i & 3);
+            if (t < a.n && rr < a.rows) {
+                const size_t idx = (size_t)t * a.rows + rr;
+                if (a.residual) v += a.residual[idx];
+                a.out[idx] = v;
+            }
         }
     }
 }
@@ -384,15 +507,15 @@ hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st) {
     if (a.n <= 0 || a.rows <= 0) return hipSuccess;
     if (a.n_pad != qmm_rows_padded(a.n) || a.cols % QK != 0) return hipErrorInvalidValue;
     const int nb = a.cols / QK;
-    hipLaunchKernelGGL(q8k_quantize_kernel<false>, dim3((unsigned)(a.n_pad * nb)), dim3(256), 0, st, a.act,
+    hipLaunchKernelGGL(q8k_quantize_tiles_kernel, dim3((unsigned)(a.n_pad / 32 * nb)), dim3(512), 0, st, a.act,
                        a.cols, nb, a.n, a.n_pad, a.ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const unsigned nwg = (unsigned)(((a.rows + 31) / 32) * (a.n_pad / 128));
     if (a.wtype == 12)
-        hipLaunchKernelGGL(qmm_kernel<12>, dim3(nwg), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(qmm_kernel<12>, dim3(nwg), dim3(512), 0, st, a);
     else if (a.wtype == 14)
-        hipLaunchKernelGGL(qmm_kernel<14>, dim3(nwg), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(qmm_kernel<14>, dim3(nwg), dim3(512), 0, st, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -401,8 +524,8 @@ hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st) {
 hipError_t launch_quantize_q8k(const float* act, int n, int cols, Q8KBlock* out, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     const int nb = cols / QK;
-    hipLaunchKernelGGL(q8k_quantize_kernel<true>, dim3((unsigned)(n * nb)), dim3(256), 0, st, act, cols, nb, n,
-                       n, static_cast<void*>(out));
+    hipLaunchKernelGGL(q8k_quantize_ref_kernel, dim3((unsigned)((n * nb + 3) / 4)), dim3(256), 0, st, act, cols, nb,
+                       n, out);
     return hipGetLastError();
 }
 
