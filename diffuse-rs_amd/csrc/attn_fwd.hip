@@ -1823,7 +1823,9 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.mg_rowgroups = div_magic(a.rowgroups, p.n_workgroups);
     a.mg_hkv = div_magic(a.n_head_kv, p.n_workgroups);
     a.part_rows = p.rowgroups * p.rb * 32;
-    hipError_t e = p.kernel == KERNEL_STREAMS ? launch_ring(p, a, st) : launch_shape(p, a, st);
+    hipError_t e = p.kernel == KERNEL_STREAMS ? launch_ring(p, a, st)
+                   : p.kernel == KERNEL_HILO  ? launch_hilo(p, a, st)
+                                              : launch_shape(p, a, st);
     if (e != hipSuccess || p.n_split <= 1) return e;
     const size_t items = (size_t)a.n_batch * a.n_head_kv * a.part_rows * (p.hd_tile / 4);
     const dim3 grid((unsigned)((items + 255) / 256));

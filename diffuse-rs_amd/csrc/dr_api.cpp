@@ -118,6 +118,7 @@ struct dr_ctx {
     DevBuf part;                         // key-split partials (grow() only)
     DevBuf q, k, v, kc, vtc, meta, out;  // dr_attention() staging
     DevBuf q8k;                          // dr_qmatmul's Q8_K activations (grow() only)
+    DevBuf qpre;                         // hi/lo attention: Q after its epilogue (grow() only)
     std::vector<void*> retired;          // workspaces replaced by larger ones
     // dr_ctx_destroy's reference plus one per pass, cache and RoPE table made
     // on the context: it is freed when the last of them is destroyed, so the
@@ -155,6 +156,7 @@ struct dr_step_cache {
     size_t n_total = 0, cap = 0, n_layer = 0, n_batch = 0;
     std::vector<int> hkv, hd, hd_tile;
     std::vector<uint16_t*> k, vt;  // [layer * n_batch + batch]
+    std::vector<uint16_t*> klo, vlo;  // lo halves of K and V^T (DR_PRECISION_HILO layers), else nullptr
     std::vector<Slot> slot;
     int32_t* d_meta = nullptr;     // [6] device-side split results
     int32_t* h_meta = nullptr;     // [6] pinned host copy
@@ -281,7 +283,7 @@ void ctx_free(dr_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (DevBuf* b : {&ctx->part, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc,
-                      &ctx->meta, &ctx->out, &ctx->q8k})
+                      &ctx->meta, &ctx->out, &ctx->q8k, &ctx->qpre})
         release(*b);
     for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
@@ -332,8 +334,8 @@ int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows) {
 
 int dr_ctx_set_kernel(dr_ctx* ctx, int kernel) {
     if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_kernel: ctx is NULL");
-    if (kernel < DR_KERNEL_AUTO || kernel > DR_KERNEL_STREAMS)
-        return fail(DR_ERR_INVALID, "kernel %d not DR_KERNEL_AUTO, _STAGED or _STREAMS", kernel);
+    if (kernel < DR_KERNEL_AUTO || kernel > DR_KERNEL_HILO)
+        return fail(DR_ERR_INVALID, "kernel %d not DR_KERNEL_AUTO, _STAGED, _STREAMS or _HILO", kernel);
     ctx->force_kernel = kernel;
     return DR_OK;
 }
@@ -433,6 +435,8 @@ int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n
     c->n_batch = n_batch;
     c->k.assign(n_layer * n_batch, nullptr);
     c->vt.assign(n_layer * n_batch, nullptr);
+    c->klo.assign(n_layer * n_batch, nullptr);
+    c->vlo.assign(n_layer * n_batch, nullptr);
     c->slot.resize(n_batch);
     for (auto& s : c->slot) {
         s.prev_seq.assign(n_total, -1);
@@ -466,6 +470,10 @@ void dr_cache_destroy(dr_step_cache* cache) {
         if (p) (void)hipFree(p);
     for (uint16_t* p : cache->vt)
         if (p) (void)hipFree(p);
+    for (uint16_t* p : cache->klo)
+        if (p) (void)hipFree(p);
+    for (uint16_t* p : cache->vlo)
+        if (p) (void)hipFree(p);
     for (auto& s : cache->slot) {
         if (s.d_prev) (void)hipFree(s.d_prev);
         if (s.d_lc) (void)hipFree(s.d_lc);
@@ -475,6 +483,37 @@ void dr_cache_destroy(dr_step_cache* cache) {
     dr_ctx* ctx = cache->ctx;
     delete cache;
     ctx_release(ctx);
+}
+
+int dr_cache_set_precision(dr_step_cache* cache, size_t layer, int precision) {
+    if (!cache) return fail(DR_ERR_INVALID, "dr_cache_set_precision: cache is NULL");
+    if (layer >= cache->n_layer)
+        return fail(DR_ERR_INVALID, "dr_cache_set_precision: layer %zu >= %zu", layer, cache->n_layer);
+    if (precision != DR_PRECISION_BF16 && precision != DR_PRECISION_HILO)
+        return fail(DR_ERR_INVALID, "dr_cache_set_precision: precision %d is not DR_PRECISION_BF16 (0) or "
+                    "DR_PRECISION_HILO (1)", precision);
+    DR_CHECK(use_device(cache->ctx));
+    const size_t bytes = (size_t)cache->hkv[layer] * cache->cap * cache->hd_tile[layer] * sizeof(uint16_t);
+    for (size_t b = 0; b < cache->n_batch; ++b) {
+        for (uint16_t** plo : {&cache->klo[layer * cache->n_batch + b], &cache->vlo[layer * cache->n_batch + b]}) {
+            uint16_t*& lo = *plo;
+            if (precision == DR_PRECISION_HILO && !lo) {
+                // (zero: rows stored before this call carry no lo half)
+                hipError_t e = hipMalloc(reinterpret_cast<void**>(&lo), bytes);
+                if (e == hipSuccess) e = hipMemset(lo, 0, bytes);
+                if (e != hipSuccess) {
+                    if (lo) (void)hipFree(lo);
+                    lo = nullptr;
+                    return hip_fail(e, "lo plane allocation");
+                }
+            } else if (precision == DR_PRECISION_BF16 && lo) {
+                (void)hipStreamSynchronize(cache->ctx->stream);
+                (void)hipFree(lo);
+                lo = nullptr;
+            }
+        }
+    }
+    return DR_OK;
 }
 
 // ---------------------------------------------------------------- Q/K/V epilogue
@@ -618,6 +657,8 @@ static int store_rows(dr_step_cache* cache, size_t layer, size_t batch, const dr
     a.cap = (int)cache->cap;
     a.kc = cache->k[layer * cache->n_batch + batch];
     a.vtc = cache->vt[layer * cache->n_batch + batch];
+    a.klo = cache->klo[layer * cache->n_batch + batch];
+    a.vlo = cache->vlo[layer * cache->n_batch + batch];
     a.kn_w = k_norm_w;
     a.kn_eps = eps;
     a.vec = a.hd == cache->hd_tile[layer] && (((uintptr_t)k | (uintptr_t)v) & 15) == 0;
@@ -653,6 +694,8 @@ int dr_cache_gather(dr_step_cache* cache, size_t layer, size_t batch, const size
     dr::GatherArgs a{};
     a.kc = cache->k[layer * cache->n_batch + batch];
     a.vtc = cache->vt[layer * cache->n_batch + batch];
+    a.klo = cache->klo[layer * cache->n_batch + batch];
+    a.vlo = cache->vlo[layer * cache->n_batch + batch];
     a.pos = static_cast<const int*>(ctx->meta.p);
     a.n = (int)n;
     a.n_head_kv = cache->hkv[layer];
@@ -917,17 +960,94 @@ int dr_cache_initialized(const dr_step_cache* cache, size_t batch) {
 
 // ---------------------------------------------------------------- attention
 
+// The hi/lo kernel's plan: 64 query rows per workgroup, the keys split
+// across workgroups when there are too few of them to fill the chip.
+static dr::LaunchPlan plan_hilo(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int max_nq, int max_nk,
+                                int mask) {
+    dr::LaunchPlan p{};
+    p.hd_tile = hd_tile_for((size_t)hd);
+    p.block_n = 32;
+    p.rb = dr::hilo_rows() / 32;
+    p.kq = 1;
+    p.waves = p.hd_tile > 256 ? 8 : 4;
+    p.stages = 1;
+    p.rowgroups = (a.group * max_nq + dr::hilo_rows() - 1) / dr::hilo_rows();
+    p.mask = mask;
+    p.w16 = true;
+    p.kernel = dr::KERNEL_HILO;
+    const int base = a.n_batch * a.n_head_kv * p.rowgroups;
+    const int ntiles = std::max(1, (max_nk + 31) / 32);
+    int split = 1;
+    if (ctx->force_split > 0)
+        split = ctx->force_split;
+    else if (2 * base <= ctx->n_cu)
+        split = std::min(ctx->n_cu / std::max(base, 1), ntiles);
+    p.n_split = std::max(1, split);
+    p.n_workgroups = base * p.n_split;
+    return p;
+}
+
 static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int max_nq,
                                int max_nk, int mask, int qepi) {
+    // a layer that keeps K's lo half gets f32-accurate scores, unless another
+    // kernel family is forced (then the lo half is not read)
+    const bool hilo_asked = ctx->force_kernel == dr::KERNEL_AUTO || ctx->force_kernel == dr::KERNEL_HILO;
+    if (a.slot[0].klo && hilo_asked && mask != dr::MASK_KEYS)
+        return plan_hilo(ctx, a, hd, max_nq, max_nk, mask);
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
                               ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
-                              ctx->force_rows, ctx->force_kernel);
+                              ctx->force_rows, ctx->force_kernel == dr::KERNEL_HILO ? dr::KERNEL_AUTO
+                                                                                    : ctx->force_kernel);
+}
+
+// The hi/lo kernel reads plain Q: with a Q epilogue (bias, QK-norm, RoPE),
+// each batch slot's Q is copied into the context's workspace and the
+// epilogue (qkv_epilogue.hip, Q heads only) runs there first.
+static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, bool fixed_ws) {
+    if (!a.qn_w && !a.qb && !a.rope) return DR_OK;
+    if (fixed_ws)
+        return fail(DR_ERR_UNSUPPORTED,
+                    "dr_attention_cached_noalloc: a hi/lo-precision layer with a Q epilogue needs a Q "
+                    "workspace (normalize Q first, or use dr_attention_cached)");
+    size_t total = 0;
+    for (int b = 0; b < a.n_batch; ++b) total += (size_t)a.slot[b].nq * a.q_rstride;
+    DR_CHECK(grow(ctx->qpre, total * sizeof(float), ctx->retired));
+    float* base = static_cast<float*>(ctx->qpre.p);
+    for (int b = 0; b < a.n_batch; ++b) {
+        dr::AttnSlot& s = a.slot[b];
+        const size_t n = (size_t)s.nq * a.q_rstride;
+        if (n == 0) continue;
+        DR_HIP(hipMemcpyAsync(base, s.q, n * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+        dr::EpiArgs e{};
+        e.q = base;
+        e.pos = s.qpos;
+        e.n = s.nq;
+        e.n_head = a.n_head;
+        e.n_head_kv = 0;  // Q heads only
+        e.hd = a.hd;
+        e.bq = a.qb;
+        e.qn_w = a.qn_w;
+        e.eps = a.qn_eps;
+        e.rope = a.rope;
+        e.rot = a.rot;
+        e.vec = a.hd % 4 == 0;
+        hipError_t err = dr::launch_epilogue(e, ctx->stream);
+        if (err != hipSuccess) return hip_fail(err, "hi/lo attention: Q epilogue launch");
+        s.q = base;
+        base += n;
+    }
+    a.qn_w = nullptr;
+    a.qb = nullptr;
+    a.rope = nullptr;
+    a.rot = 0;
+    return DR_OK;
 }
 
 // Launches plan p.  The key-split partials go to the context's workspace,
 // or with fixed_ws to the library's fixed device scratch (no allocation: a
 // plan that needs more than it holds is an error).
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws = false) {
+    if (p.kernel == dr::KERNEL_HILO) DR_CHECK(hilo_prepare_q(ctx, a, fixed_ws));
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
         if (fixed_ws) {
@@ -1011,6 +1131,8 @@ static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* 
         s.qpos = it.pass->d_pos;
         s.k = cache->k[layer * cache->n_batch + b];
         s.vt = cache->vt[layer * cache->n_batch + b];
+        s.klo = cache->klo[layer * cache->n_batch + b];
+        s.vlo = cache->vlo[layer * cache->n_batch + b];
         s.nq = (int)it.pass->n;
         s.nk = (int)cache->n_total;
         s.qpos_sorted = 1;  // dr_pass positions are strictly ascending
@@ -1097,7 +1219,7 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
     // stages tiles per key group, and no sliding window narrows a
     // workgroup's key range (each active tile is stored by one workgroup of
     // its kv head, which must visit it).
-    bool fused = cache->ctx->fused_step && a.hd == cache->hd_tile[layer] &&
+    bool fused = cache->ctx->fused_step && a.hd == cache->hd_tile[layer] && p.kernel != dr::KERNEL_HILO &&
                  dr::plan_supports_act(pf) && !sliding_window.present;
     for (size_t b = 0; b < n_items && fused; ++b) {
         const dr_pass* ps = items[b].pass;

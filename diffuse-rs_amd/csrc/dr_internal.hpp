@@ -31,6 +31,8 @@ struct AttnSlot {
     const int* qprefix;   // [nq] per-row causal prefix or nullptr
     const uint16_t* k;    // bf16 bits
     const uint16_t* vt;   // bf16 bits
+    const uint16_t* klo;  // K's lo half, bf16(k - bf16(k)), K's layout (the hi/lo kernel) or nullptr
+    const uint16_t* vlo;  // V's lo half in V^T's layout (with klo) or nullptr
     const int* kpos;      // [nk] or nullptr
     const int* kseq;      // [nk] or nullptr
     int nq;
@@ -96,6 +98,8 @@ struct StoreArgs {
     int cap;
     uint16_t* kc;        // [n_head_kv][cap][HD] bf16 bits
     uint16_t* vtc;       // [n_head_kv][cap / VT_KEYS][HD][VT_KEYS] bf16 bits
+    uint16_t* klo;       // nullptr, or K's lo half bf16(k - bf16(k)) in K's layout
+    uint16_t* vlo;       // with klo: V's lo half in V^T's layout
     const float* kn_w;   // K-norm gain or nullptr
     float kn_eps;
     int vec;             // rows may be read as 16-byte pieces (hd == HD tile, aligned)
@@ -114,6 +118,8 @@ struct StoreArgs {
 struct GatherArgs {
     const uint16_t* kc;
     const uint16_t* vtc;
+    const uint16_t* klo;  // nullptr, or K's lo half (added back)
+    const uint16_t* vlo;  // with klo: V's lo half (added back)
     const int* pos;      // [n] device
     int n;
     int n_head_kv;
@@ -228,17 +234,21 @@ struct LaunchPlan {
     bool qepi;       // Q epilogue compiled in: bias, QK-norm, RoPE, each where its operand is given
     bool act;        // fused step: active keys read from f32 rows and stored (see AttnSlot)
     bool w16;        // two 16-row compute waves per (row block, key group)
-    int kernel;      // KERNEL_STAGED (attn_fwd_kernel) or KERNEL_STREAMS (attn_ring_kernel)
+    int kernel;      // KernelKind
 };
 
 // Attention kernel families.  STAGED: attn_fwd_kernel, the workgroup's waves
 // share super-tiles of K/V staged in LDS (every head dim, mask mode, the Q
 // epilogue and the fused step).  STREAMS: attn_ring_kernel, head dim 128,
 // each wave streams its own key tiles (no mask or MASK_POS, Q norm only).
+// HILO: attn_hilo_kernel, f32-accurate scores and values from bf16 hi/lo
+// halves of Q, K and V (layers whose cache holds the lo halves; no mask or
+// MASK_POS, plain Q).
 enum KernelKind : int {
     KERNEL_AUTO = 0,
     KERNEL_STAGED = 1,
     KERNEL_STREAMS = 2,
+    KERNEL_HILO = 3,
 };
 
 // What of the Q/K/V epilogue the attention prologue applies to Q: nothing,
@@ -274,6 +284,8 @@ size_t scratch_bytes();
 hipError_t scratch_init(int device);
 void* scratch_ptr(int device);
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
+hipError_t launch_hilo(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
+int hilo_rows();  // query rows per workgroup of attn_hilo_kernel
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);
 hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
 hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);

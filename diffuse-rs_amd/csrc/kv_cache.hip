@@ -14,9 +14,12 @@
 // store:  StepCache::store (cache.rs:62-71) -- f32 rows -> bf16 at their
 //         positions, optionally after per-head RMSNorm of K (norm_heads,
 //         ops.rs:384-389, applied before the store in forward.rs:300-302).
+//         A layer kept at hi/lo precision also gets the lo halves,
+//         bf16(x - bf16(x)), of K and V in planes laid out like K and V^T.
 //         One launch, one workgroup per (64-row block, 64-wide head-dim
 //         chunk, kv head): K converted in registers, V transposed through LDS.
-// gather: StepCache::gather (cache.rs:73-82) -- bf16 back to f32 rows.
+// gather: StepCache::gather (cache.rs:73-82) -- bf16 back to f32 rows (hi +
+//         lo where the layer keeps the lo halves).
 #include <algorithm>
 
 #include "dr_internal.hpp"
@@ -64,6 +67,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
     constexpr int NDC = HD / SD;
     constexpr int V4 = SPT / 4;
     __shared__ __align__(16) uint16_t tile[SD][SR + 8];
+    __shared__ __align__(16) uint16_t tile_lo[SD][SR + 8];  // V's lo half, when kept
 
     // Workgroup -> (kv head g, chunk dc, row block).  The hardware deals
     // workgroups round-robin over the 8 XCDs (XCD = blockIdx & 7); each XCD in
@@ -254,11 +258,35 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
             }
             *reinterpret_cast<u32x4*>(dst + 4 * i) = w;
         }
+        if (a.klo) {
+            // the lo half: bf16 of what bf16 rounding dropped
+            uint16_t* dlo = a.klo + ((size_t)g * a.cap + pos) * HD + d0;
+#pragma unroll
+            for (int i = 0; i < V4; i += 2) {
+                u32x4 w;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    uint16_t lo[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) lo[e] = f2bf(xk[i + j][e] - bf2f(f2bf(xk[i + j][e])));
+                    w[2 * j] = (uint32_t)lo[0] | ((uint32_t)lo[1] << 16);
+                    w[2 * j + 1] = (uint32_t)lo[2] | ((uint32_t)lo[3] << 16);
+                }
+                *reinterpret_cast<u32x4*>(dlo + 4 * i) = w;
+            }
+        }
     }
 #pragma unroll
     for (int i = 0; i < V4; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) tile[part * SPT + 4 * i + e][rl] = f2bf(xv[i][e]);
+    if (a.vlo) {
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                tile_lo[part * SPT + 4 * i + e][rl] = f2bf(xv[i][e] - bf2f(f2bf(xv[i][e])));
+    }
     __syncthreads();
 
     // V^T: thread -> (d-row dl, positions p0 + [0,16)).
@@ -268,10 +296,11 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
     const int cnt = min(SPT, a.n - rfirst);
     const int dv = dc * SD + dl;  // this thread's d-row
     // V^T element (g, dv, p): tile p / VT_KEYS, offset p % VT_KEYS in its d-row
-    uint16_t* vplane = a.vtc + (size_t)g * HD * a.cap + (size_t)dv * VT_KEYS;
-    auto vt_at = [&](int p) __attribute__((always_inline)) {
-        return vplane + (size_t)(p / VT_KEYS) * (HD * VT_KEYS) + p % VT_KEYS;
+    const size_t vrow = (size_t)g * HD * a.cap + (size_t)dv * VT_KEYS;
+    auto vt_in = [&](uint16_t* plane, int p) __attribute__((always_inline)) {
+        return plane + vrow + (size_t)(p / VT_KEYS) * (HD * VT_KEYS) + p % VT_KEYS;
     };
+    auto vt_at = [&](int p) __attribute__((always_inline)) { return vt_in(a.vtc, p); };
     const int q0 = a.pos ? a.pos[rfirst] : rfirst;
     // pos is strictly ascending, so equal endpoint distance means contiguous.
     const bool contiguous = cnt == SPT && (q0 & 7) == 0 &&
@@ -284,6 +313,17 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
             *reinterpret_cast<u32x4*>(vt_at(q0 + 8 * h)) = *reinterpret_cast<const u32x4*>(t + 8 * h);
     } else {
         for (int e = 0; e < cnt; ++e) *vt_at(a.pos ? a.pos[rfirst + e] : rfirst + e) = t[e];
+    }
+    if (a.vlo) {
+        // the same positions of the lo plane (V^T's layout)
+        const uint16_t* tl = &tile_lo[dl][p0];
+        if (contiguous) {
+#pragma unroll
+            for (int h = 0; h < SPT / 8; ++h)
+                *reinterpret_cast<u32x4*>(vt_in(a.vlo, q0 + 8 * h)) = *reinterpret_cast<const u32x4*>(tl + 8 * h);
+        } else {
+            for (int e = 0; e < cnt; ++e) *vt_in(a.vlo, a.pos ? a.pos[rfirst + e] : rfirst + e) = tl[e];
+        }
     }
 }
 
@@ -298,9 +338,11 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
         const int g = (int)(rg % a.n_head_kv);
         const int r = (int)(rg / a.n_head_kv);
         const int pos = a.pos[r];
-        a.out_k[idx] = bf2f(a.kc[((size_t)g * a.cap + pos) * HD + d]);
-        a.out_v[idx] = bf2f(a.vtc[((size_t)g * a.cap + (size_t)(pos / VT_KEYS) * VT_KEYS) * HD +
-                                  (size_t)d * VT_KEYS + pos % VT_KEYS]);
+        const size_t ki = ((size_t)g * a.cap + pos) * HD + d;
+        a.out_k[idx] = a.klo ? bf2f(a.kc[ki]) + bf2f(a.klo[ki]) : bf2f(a.kc[ki]);
+        const size_t vi = ((size_t)g * a.cap + (size_t)(pos / VT_KEYS) * VT_KEYS) * HD + (size_t)d * VT_KEYS +
+                          pos % VT_KEYS;
+        a.out_v[idx] = a.vlo ? bf2f(a.vtc[vi]) + bf2f(a.vlo[vi]) : bf2f(a.vtc[vi]);
     }
 }
 

@@ -27,7 +27,8 @@ LIB_PATH = HERE / "lib" / "libdr_attn.so"
 HEADER_PATH = HERE.parent / "include" / "dr_attn.h"
 
 DR_OK, DR_ERR_INVALID, DR_ERR_NO_DEVICE, DR_ERR_OOM, DR_ERR_HIP, DR_ERR_UNSUPPORTED = range(6)
-KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS = range(3)
+KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS, KERNEL_HILO = range(4)
+PRECISION_BF16, PRECISION_HILO = 0, 1  # dr_cache_set_precision
 STATUS_NAMES = {
     DR_OK: "DR_OK",
     DR_ERR_INVALID: "DR_ERR_INVALID",
@@ -145,6 +146,7 @@ _SIGS = {
     "dr_pass_destroy": (None, [_VP]),
     "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_cache_destroy": (None, [_VP]),
+    "dr_cache_set_precision": (_I, [_VP, _SZ, _I]),
     "dr_cache_store": (_I, [_VP, _SZ, _SZ, _VP, _VP, _VP, _VP, _F]),
     "dr_cache_gather": (_I, [_VP, _SZ, _SZ, c_size_p, _SZ, _VP, _VP]),
     "dr_cache_update_seq": (_I, [_VP, _SZ, _VP, _SZ]),
@@ -326,7 +328,7 @@ class Context:
         _check(self.lib.dr_ctx_set_wave_rows(self.h, rows))
 
     def set_kernel(self, kernel: int) -> None:
-        """KERNEL_AUTO, KERNEL_STAGED or KERNEL_STREAMS (dr_ctx_set_kernel)."""
+        """KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS or KERNEL_HILO (dr_ctx_set_kernel)."""
         _check(self.lib.dr_ctx_set_kernel(self.h, kernel))
 
     def set_fused_step(self, enable: bool) -> None:
@@ -448,6 +450,11 @@ class StepCache:
         self.h = h
         self.n_total = n_total
         self.n_batch = n_batch
+
+    def set_precision(self, layer: int, precision: int) -> None:
+        """PRECISION_BF16 or PRECISION_HILO for one layer (dr_cache_set_precision):
+        HILO keeps K's lo half and gives the layer f32-accurate scores."""
+        _check(self.ctx.lib.dr_cache_set_precision(self.h, layer, precision))
 
     def store(self, layer: int, p: Pass, k, v, k_norm_w=None, eps: float = 1e-6, batch: int = 0):
         _check(self.ctx.lib.dr_cache_store(self.h, layer, batch, p.h, _ptr(k), _ptr(v),

@@ -148,6 +148,25 @@ int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n
                     const size_t* head_dim, size_t n_batch, dr_step_cache** out);
 void dr_cache_destroy(dr_step_cache* cache);
 
+/* Score precision of one cache layer; no counterpart in the reference, whose
+ * StepCache holds f32 K (cache.rs:25-54) and whose attention forms f32 scores
+ * (attention.rs:289-331).  DR_PRECISION_BF16 (the default): K is kept as
+ * bf16 and the scores come from bf16 Q and K, within 1e-2 of the reference
+ * at the usual 1/sqrt(head_dim) scale.  DR_PRECISION_HILO: the layer also
+ * keeps the lo halves bf16(x - bf16(x)) of K and V in two more planes (twice
+ * the layer's cache memory, written by every later store), and its attention
+ * forms S = Qh.Kh + Qh.Kl + Ql.Kh from the bf16 hi/lo halves of Q and K and
+ * P.(Vh + Vl): scores accurate to ~2^-16 and values to ~2^-17, for layers
+ * whose scale makes bf16 too coarse -- Gemma's kq_scale 1.0
+ * (forward.rs:338-341), where the softmax is nearly one-hot and bf16 moves
+ * outputs by ~0.15.  Set it before storing the layer's rows (rows stored
+ * earlier have zero lo halves); DR_PRECISION_BF16 frees the planes.  Hi/lo
+ * layers run without masks or with position masks (window, causal prefix,
+ * query sequence ids), not the fused dr_attention_step kernel. */
+#define DR_PRECISION_BF16 0
+#define DR_PRECISION_HILO 1
+int dr_cache_set_precision(dr_step_cache* cache, size_t layer, int precision);
+
 /* StepCache::store (cache.rs:62-71) for the pass's active positions: row r of
  * k/v ([n_active][n_head_kv][head_dim] f32, device) goes to position
  * active[r].  If k_norm_w (device, head_dim f32) is non-NULL each K head is
@@ -365,7 +384,7 @@ typedef struct {
     int key_groups;
     int fused_step; /* 1 when the launch also stored the step's active rows */
     int rows_per_wave; /* query rows per compute wave: 32, or 16 (two waves per row block) */
-    int kernel; /* DR_KERNEL_STAGED or DR_KERNEL_STREAMS: which attention kernel ran */
+    int kernel; /* DR_KERNEL_STAGED, DR_KERNEL_STREAMS or DR_KERNEL_HILO: which attention kernel ran */
 } dr_launch_info;
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 
@@ -382,10 +401,14 @@ int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
 #define DR_KERNEL_AUTO 0
 #define DR_KERNEL_STAGED 1
 #define DR_KERNEL_STREAMS 2
+/* HILO: layers kept at DR_PRECISION_HILO (f32-accurate scores from bf16
+ * hi/lo halves of Q and K; see dr_cache_set_precision). */
+#define DR_KERNEL_HILO 3
 /* Pick the kernel family for later calls on ctx: DR_KERNEL_AUTO (the
- * planner: STREAMS wherever it applies), or force STAGED / STREAMS (STREAMS
- * falls back to STAGED where it does not apply).  A tuning knob, for
- * measurement and tests. */
+ * planner: HILO on hi/lo layers, else STREAMS wherever it applies), or force
+ * STAGED / STREAMS (STREAMS falls back to STAGED where it does not apply; on
+ * a hi/lo layer both ignore the lo half).  A tuning knob, for measurement
+ * and tests. */
 int dr_ctx_set_kernel(dr_ctx* ctx, int kernel);
 /* Let dr_attention_step run its single fused kernel (1) or always the cache
  * store followed by the attention (0, the default: on the MI355X the fused

@@ -151,10 +151,11 @@ def test_hd512_step_epi_k_as_v_vs_oracle(dev):
         assert bad <= 2 and np.max(np.abs(g_ - w_)) <= 2.0**-7 * np.max(np.abs(w_)), (name, bad)
 
 
-def test_hd512_scale_one_reported(dev):
-    """Gemma's real kq_scale is 1.0 (forward.rs:338-341).  With N(0,1)
-    inputs at hd 512 the score std is ~23, the softmax is nearly one-hot and
-    bf16 rounding of Q and K moves scores by ~0.1: reported, bounded loosely."""
+def test_hd512_scale_one_hilo_layer(dev):
+    """Gemma's real kq_scale is 1.0 (forward.rs:338-341).  With N(0,1) inputs
+    at hd 512 the score std is ~23 and the softmax is nearly one-hot: bf16
+    Q/K err by ~0.25.  A layer kept at DR_PRECISION_HILO (f32-accurate scores
+    and values) meets the north-star tolerance."""
     rng = np.random.default_rng(5122)
     h, hkv, hd, n_t, n_c = 16, 2, 512, 512, 128
     n_p = n_t - n_c
@@ -162,12 +163,12 @@ def test_hd512_scale_one_reported(dev):
     V = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
     Q = rng.standard_normal((n_c, h * hd), dtype=np.float32)
     cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.set_precision(0, dr.PRECISION_HILO)
     cache.store(0, dr.Pass(dev.ctx, range(n_t)), dev.put(K), dev.put(V))
     out = dev.empty(n_c * h * hd)
     cache.attention(0, [(dev.put(Q), out, dr.Pass(dev.ctx, range(n_p, n_t)))], h, scale=1.0)
+    assert dev.ctx.last_launch()["kernel"] == dr.KERNEL_HILO
     s = Shape(n_c, n_t, h, hkv, hd, scale=1.0)
     want = oracle_run(s, RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t))),
                       Q.reshape(-1).copy(), K.reshape(-1).copy(), V.reshape(-1).copy())
-    mx, mean = err_stats(dev.get(out), want)
-    say(f"  hd 512 scale 1.0 (N(0,1)): max-abs {mx:.3e} mean-abs {mean:.3e}")
-    assert np.isfinite(mx) and mx < 1.5
+    check(dev.get(out), want, "hd 512 scale 1.0 (N(0,1)), hi/lo layer")

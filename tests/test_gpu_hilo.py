@@ -1,0 +1,228 @@
+"""Cache layers kept at DR_PRECISION_HILO (dr_cache_set_precision): the
+attention's scores come from bf16 hi/lo halves of Q and K (attn_hilo.hip),
+S = Qh.Kh + Qh.Kl + Ql.Kh, f32-accurate to ~2^-16.
+
+DiffusionGemma runs every layer at kq_scale 1.0 after QK-norm
+(src/model/forward.rs:338-341, docs/diffusiongemma.md:11-14).  There the
+score standard deviation is ~sqrt(head_dim), the softmax is nearly one-hot,
+and bf16 rounding of Q and K alone moves outputs by ~0.15: the bf16 path
+cannot meet 1e-2.  These tests hold the hi/lo path to the north-star
+tolerance (max-abs 1e-2, mean-abs 1e-3) against the f32 oracle of
+attention() (src/model/attention.rs:101-186) at that operating point --
+QK-normed inputs with gains U(0.5, 1.5), head dim 256 with the 1024 window
+and head dim 512 global, C5's 4096 + 256 context -- and check that the
+bf16 path on the same inputs does not (so the bar tests something).
+Needs an MI355X.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import dr_attn as dr
+import oracle as orc
+from helpers import TOL_MAX, TOL_MEAN, RowsSpec, Shape, err_stats
+
+from test_gpu_parity import _epilogue_oracle, check, dev, oracle_run, say, torch  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(dev, h, hkv, hd, n_p, n_c, window, scale, precision, seed, qk_norm=True, batch=1,
+             prefix=None):
+    """K/V of all positions stored (K QK-normed), canvas queries attended;
+    returns (outputs, oracle outputs, launch info)."""
+    rng = np.random.default_rng(seed)
+    n_t = n_p + n_c
+    kvs = hkv * hd
+    qn = kn = None
+    if qk_norm:
+        qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd], n_batch=batch)
+    if precision is not None:
+        cache.set_precision(0, precision)
+    p_all = dr.Pass(dev.ctx, range(n_t))
+    canvas = list(range(n_p, n_t))
+    p_c = dr.Pass(dev.ctx, canvas)
+    items, outs, wants = [], [], []
+    for b in range(batch):
+        K = rng.standard_normal((n_t, kvs), dtype=np.float32)
+        V = rng.standard_normal((n_t, kvs), dtype=np.float32)
+        Q = rng.standard_normal((n_c, h * hd), dtype=np.float32)
+        cache.store(0, p_all, dev.put(K), dev.put(V), dev.put(kn) if qk_norm else None, 1e-6, batch=b)
+        out = dev.empty(n_c * h * hd)
+        items.append((dev.put(Q), out, p_c))
+        outs.append(out)
+        q, k = Q.reshape(-1).copy(), K.reshape(-1).copy()
+        if qk_norm:
+            orc.norm_heads(q, qn, 1e-6)
+            orc.norm_heads(k, kn, 1e-6)
+        s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, causal_prefix=prefix, scale=scale)
+        wants.append(oracle_run(s, RowsSpec(canvas), RowsSpec(list(range(n_t))), q, k, V.reshape(-1).copy()))
+    cache.attention(0, items, h, sliding_window=window, causal_prefix=prefix, scale=scale,
+                    q_norm_w=dev.put(qn) if qk_norm else None, q_norm_eps=1e-6)
+    info = dev.ctx.last_launch()
+    return [dev.get(o) for o in outs], wants, info, cache
+
+
+GEMMA = {
+    # DiffusionGemma sliding layer at C5's context: 16 / 8 heads, hd 256, window 1024
+    "hd256_sliding_w1024": (16, 8, 256, 4096, 256, 1024),
+    # DiffusionGemma global layer: 16 / 2 heads at hd 512, full attention
+    "hd512_global": (16, 2, 512, 4096, 256, None),
+}
+
+
+@pytest.mark.parametrize("name", list(GEMMA))
+def test_gemma_scale_one_hilo_meets_tolerance(dev, name):
+    h, hkv, hd, n_p, n_c, window = GEMMA[name]
+    got, wants, info, _ = _problem(dev, h, hkv, hd, n_p, n_c, window, 1.0, dr.PRECISION_HILO,
+                                   sum(map(ord, name)))
+    say(f"{name} scale 1.0 hi/lo: launch {info}")
+    assert info["kernel"] == dr.KERNEL_HILO
+    check(got[0], wants[0], f"{name} hi/lo at scale 1.0")
+
+
+@pytest.mark.parametrize("name", list(GEMMA))
+def test_gemma_scale_one_bf16_misses_tolerance(dev, name):
+    """The bf16 path on the same inputs: reported, and far outside the bar
+    (which is why hi/lo layers exist)."""
+    h, hkv, hd, n_p, n_c, window = GEMMA[name]
+    got, wants, info, _ = _problem(dev, h, hkv, hd, n_p, n_c, window, 1.0, None, sum(map(ord, name)))
+    assert info["kernel"] != dr.KERNEL_HILO
+    mx, mean = err_stats(got[0], wants[0])
+    say(f"  {name} bf16 at scale 1.0: max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert np.isfinite(mx) and mx > TOL_MAX
+
+
+# (h, hkv, hd, n_prompt, n_canvas, window, prefix, batch, n_split, qk_norm)
+CASES = {
+    "hd64_mha_ragged": (4, 4, 64, 203, 77, None, None, 1, 0, False),
+    "hd128_gqa_window": (8, 2, 128, 700, 160, 150, None, 1, 0, True),
+    "hd128_prefix_batch2": (8, 4, 128, 300, 130, None, 360, 2, 0, False),
+    "hd256_gqa_split3": (8, 4, 256, 1500, 64, None, None, 1, 3, True),
+    "hd256_window_prefix": (6, 3, 256, 500, 111, 90, 540, 2, 0, True),
+    "hd512_ragged_window": (16, 2, 512, 600, 100, 300, None, 1, 0, True),
+    "hd512_split2_batch2": (8, 2, 512, 900, 64, None, None, 2, 2, False),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("scale_kind", ["rsqrt", "one"])
+def test_hilo_kernel_vs_oracle(dev, name, scale_kind):
+    """The hi/lo kernel at the usual 1/sqrt(hd) scale and at 1.0, over head
+    dims, GQA, ragged rows and keys, windows, causal prefixes, batch slots
+    and forced key splits."""
+    h, hkv, hd, n_p, n_c, window, prefix, batch, n_split, qk = CASES[name]
+    scale = 1 / math.sqrt(hd) if scale_kind == "rsqrt" else 1.0
+    dev.ctx.set_split(n_split)
+    try:
+        got, wants, info, _ = _problem(dev, h, hkv, hd, n_p, n_c, window, scale, dr.PRECISION_HILO,
+                                       sum(map(ord, name)) + hd, qk_norm=qk, batch=batch, prefix=prefix)
+    finally:
+        dev.ctx.set_split(0)
+    say(f"{name} {scale_kind}: launch {info}")
+    assert info["kernel"] == dr.KERNEL_HILO
+    if n_split:
+        assert info["n_split"] == n_split
+    for b in range(batch):
+        check(got[b], wants[b], f"{name} {scale_kind} batch {b}")
+
+
+def test_hilo_repeat_calls_bit_identical(dev):
+    """Each wave sums its keys in tile order: repeated calls give the same bits."""
+    args = (8, 4, 256, 700, 100, 200, 1.0, dr.PRECISION_HILO, 77)
+    first, _, _, _ = _problem(dev, *args)
+    again, _, _, _ = _problem(dev, *args)
+    assert np.array_equal(first[0], again[0])
+
+
+def test_hilo_gather_returns_hi_plus_lo(dev):
+    """gather on a hi/lo layer returns bf16 hi + bf16 lo of each stored K and
+    V (within 2^-16 of the f32 value)."""
+    rng = np.random.default_rng(3)
+    n_t, hkv, hd = 96, 2, 128
+    K = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    V = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.set_precision(0, dr.PRECISION_HILO)
+    cache.store(0, dr.Pass(dev.ctx, range(n_t)), dev.put(K), dev.put(V))
+    ok, ov = dev.empty(n_t * hkv * hd), dev.empty(n_t * hkv * hd)
+    cache.gather(0, list(range(n_t)), ok, ov)
+    for got, x in ((dev.get(ok).reshape(K.shape), K), (dev.get(ov).reshape(V.shape), V)):
+        assert np.max(np.abs(got - x) / np.maximum(np.abs(x), 1e-30)) <= 2.0**-16
+        assert np.max(np.abs(got - x)) > 0  # (hi + lo is not x itself for random x)
+
+
+def test_hilo_step_epi_vs_oracle(dev):
+    """dr_attention_step_epi on a hi/lo layer: the Q epilogue (bias, QK-norm,
+    RoPE) runs on a copy of Q before the hi/lo kernel; K's lo half is taken
+    after the K epilogue.  Gemma-like: V-norm, window, scale 1.0."""
+    h, hkv, hd, rot, n_p, n_c, window = 8, 4, 256, 256, 300, 120, 128
+    rng = np.random.default_rng(2561)
+    eps = 1e-6
+    n_t = n_p + n_c
+    kvs = hkv * hd
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    bq = (0.1 * rng.standard_normal(h * hd)).astype(np.float32)
+    bk = (0.1 * rng.standard_normal(kvs)).astype(np.float32)
+    bv = (0.1 * rng.standard_normal(kvs)).astype(np.float32)
+    table = orc.rope_table(n_t, rot, 10000.0)
+    rope = dr.Rope(dev.ctx, n_t, rot, 10000.0)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.set_precision(0, dr.PRECISION_HILO)
+    put = dev.put
+    K = rng.standard_normal(n_t * kvs).astype(np.float32)
+    V = rng.standard_normal(n_t * kvs).astype(np.float32)
+    Q = rng.standard_normal(n_c * h * hd).astype(np.float32)
+    canvas = list(range(n_p, n_t))
+    # every position stored through the step (prompt rows as one step, then the canvas)
+    qd = np.zeros(n_p * h * hd, np.float32)
+    p_pr = dr.Pass(dev.ctx, range(n_p))
+    cache.step_epi(0, [(put(qd), dev.empty(n_p * h * hd), p_pr, put(K[:n_p * kvs].copy()),
+                        put(V[:n_p * kvs].copy()))], h, sliding_window=window, scale=1.0, bq=put(bq),
+                   bk=put(bk), bv=put(bv), q_norm_w=put(qn), k_norm_w=put(kn), v_norm=True, eps=eps,
+                   rope=rope)
+    dq = put(Q)
+    out = dev.empty(n_c * h * hd)
+    cache.step_epi(0, [(dq, out, dr.Pass(dev.ctx, canvas), put(K[n_p * kvs:].copy()),
+                        put(V[n_p * kvs:].copy()))], h, sliding_window=window, scale=1.0,
+                   bq=put(bq), bk=put(bk), bv=put(bv), q_norm_w=put(qn), k_norm_w=put(kn), v_norm=True,
+                   eps=eps, rope=rope)
+    info = dev.ctx.last_launch()
+    assert info["kernel"] == dr.KERNEL_HILO
+    _, kp_o, vp_o = _epilogue_oracle(qd, K[:n_p * kvs].copy(), V[:n_p * kvs].copy(), list(range(n_p)), h,
+                                     hkv, hd, bq, bk, bv, qn, kn, True, eps, table, rot)
+    q_o, kc_o, vc_o = _epilogue_oracle(Q.copy(), K[n_p * kvs:].copy(), V[n_p * kvs:].copy(), canvas, h, hkv,
+                                       hd, bq, bk, bv, qn, kn, True, eps, table, rot)
+    s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, scale=1.0)
+    want = oracle_run(s, RowsSpec(canvas), RowsSpec(list(range(n_t))), q_o, np.concatenate([kp_o, kc_o]),
+                      np.concatenate([vp_o, vc_o]))
+    check(dev.get(out), want, "hi/lo step_epi at scale 1.0")
+    assert np.array_equal(dev.get(dq), Q)  # the caller's Q is only read
+
+
+def test_hilo_layer_with_forced_bf16_kernel(dev):
+    """Forcing the staged kernel on a hi/lo layer runs the bf16 scores (the
+    lo half unused): same answers as a bf16 layer at the usual scale."""
+    dev.ctx.set_kernel(dr.KERNEL_STAGED)
+    try:
+        got, wants, info, _ = _problem(dev, 8, 4, 256, 400, 96, None, 1 / 16, dr.PRECISION_HILO, 5, qk_norm=False)
+    finally:
+        dev.ctx.set_kernel(dr.KERNEL_AUTO)
+    assert info["kernel"] == dr.KERNEL_STAGED
+    check(got[0], wants[0], "hi/lo layer, staged kernel")
+
+
+def test_set_precision_rejects_bad_arguments(dev):
+    cache = dr.StepCache(dev.ctx, 64, [2], [128])
+    with pytest.raises(dr.DrError):
+        cache.set_precision(1, dr.PRECISION_HILO)  # no layer 1
+    with pytest.raises(dr.DrError):
+        cache.set_precision(0, 7)
+    cache.set_precision(0, dr.PRECISION_HILO)
+    cache.set_precision(0, dr.PRECISION_BF16)  # frees the plane again

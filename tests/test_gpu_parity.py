@@ -277,18 +277,31 @@ def test_config_cached_vs_oracle(dev, cid):
         check(got[b], want, f"{cid} batch {b}")
 
 
-def test_gemma_scale_one_error(dev):
-    # Gemma's real kq_scale is 1.0 (forward.rs:338-341): with N(0,1) inputs at
-    # hd 256 the score std is 16 and the softmax is close to one-hot, so bf16
-    # rounding of Q and K moves scores by ~0.05.  Reported, bounded loosely.
+def test_gemma_scale_one_hilo_layer(dev):
+    """Gemma's real kq_scale is 1.0 (forward.rs:338-341): with N(0,1) inputs
+    at hd 256 the score std is 16 and the softmax is close to one-hot, so a
+    bf16 Q/K path errs by ~0.15.  On a layer kept at DR_PRECISION_HILO the
+    scores and values are f32-accurate and C5S's shape at scale 1.0 meets the
+    north-star tolerance (tests/test_gpu_hilo.py covers QK-normed inputs,
+    hd 512 and the bf16 contrast)."""
     cfg = CONFIGS["C5S"]
-    cfg1 = type(cfg)(**{**cfg.__dict__, "scale": 1.0, "n_prompt": 1024})
-    got, ins, _, _ = _cached_problem(dev, cfg1, 4)
-    Q, K, V = ins[0]
-    want = _oracle_cfg(cfg1, Q, K, V)
-    mx, mean = err_stats(got[0], want)
-    say(f"  Gemma scale 1.0 (hd 256, N(0,1)): max-abs {mx:.3e} mean-abs {mean:.3e}")
-    assert np.isfinite(mx) and mx < 1.0
+    rng = np.random.default_rng(config_seed(4))
+    h, hkv, hd, n_p, n_c = cfg.n_head, cfg.n_head_kv, cfg.head_dim, 1024, cfg.n_canvas
+    n_t = n_p + n_c
+    K = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    V = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    Q = rng.standard_normal((n_c, h * hd), dtype=np.float32)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.set_precision(0, dr.PRECISION_HILO)
+    cache.store(0, dr.Pass(dev.ctx, range(n_t)), dev.put(K), dev.put(V))
+    out = dev.empty(n_c * h * hd)
+    cache.attention(0, [(dev.put(Q), out, dr.Pass(dev.ctx, range(n_p, n_t)))], h,
+                    sliding_window=cfg.window, scale=1.0)
+    assert dev.ctx.last_launch()["kernel"] == dr.KERNEL_HILO
+    s = Shape(n_c, n_t, h, hkv, hd, sliding_window=cfg.window, scale=1.0)
+    want = oracle_run(s, RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t))),
+                      Q.reshape(-1).copy(), K.reshape(-1).copy(), V.reshape(-1).copy())
+    check(dev.get(out), want, "Gemma scale 1.0 (hd 256, N(0,1)), hi/lo layer")
 
 
 @pytest.mark.parametrize("hd", [128, 256, 512])
