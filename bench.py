@@ -91,12 +91,15 @@ def attention_only_ms(torch, stream, call, n_calls: int, reps: int):
     return e0.elapsed_time(e1) / (reps * n_calls), g
 
 
-def _config_cache(torch, dr, ctx, stream, cfg, gen, n_layer: int = 1, windows=None):
+def _config_cache(torch, dr, ctx, stream, cfg, gen, n_layer: int = 1, windows=None, precision=None):
     """A cache of n_layer layers of cfg's geometry with random K/V stored in
     every layer and batch slot, and the attention items of its canvas rows."""
     h, hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
     n_t, n_c = cfg.n_total, cfg.n_canvas
     cache = dr.StepCache(ctx, n_t, [hkv] * n_layer, [hd] * n_layer, n_batch=cfg.batch)
+    if precision is not None:
+        for layer in range(n_layer):
+            cache.set_precision(layer, precision)
     p_all = dr.Pass(ctx, range(n_t))
     p_can = dr.Pass(ctx, range(cfg.n_prompt, n_t))
     qn = kn = None
@@ -164,6 +167,37 @@ def other_configs(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
     log(f"C5_6layer: {res['C5_6layer']}")
     stream.synchronize()
     del cache
+    return res
+
+
+def hilo_timing(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
+    """The cost of hi/lo-precision layers (dr_cache_set_precision), which
+    Gemma's kq_scale 1.0 needs: C5's sliding and global layers and the hd 512
+    global layer at scale 1.0 with QK-norm, each on a bf16 layer and on a
+    hi/lo layer (attention only, graph bursts as other_configs; the accuracy
+    of both is in tests/test_gpu_hilo.py)."""
+    import dataclasses
+    from helpers import EXTRA_CONFIGS
+    res = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4321)
+    for name in ("C5S", "C5G", "G512"):
+        base = CONFIGS[name] if name in CONFIGS else EXTRA_CONFIGS[name]
+        cfg = dataclasses.replace(base, scale=1.0, qk_norm=True)
+        entry = {"workload": cfg.name + ", scale 1.0, QK-norm"}
+        for label, prec in (("bf16", None), ("hilo", dr.PRECISION_HILO)):
+            cache, items, qn, _ = _config_cache(torch, dr, ctx, stream, cfg, gen, precision=prec)
+
+            def call(i):
+                cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=1.0, q_norm_w=qn)
+            ms, _ = attention_only_ms(torch, stream, call, 4, reps)
+            entry[f"{label}_us_per_call"] = round(ms * 1e3, 3)
+            entry[f"{label}_kernel"] = ctx.last_launch()["kernel"]
+            stream.synchronize()
+            del cache
+        entry["hilo_over_bf16"] = round(entry["hilo_us_per_call"] / entry["bf16_us_per_call"], 3)
+        res[name] = entry
+        log(f"hilo {name}: {entry}")
     return res
 
 
@@ -542,7 +576,7 @@ def main() -> int:
                                       / PEAK_BF16_TFLOPS), 4),
     }
 
-    others = epi = split = qmm = qmm_inputs = dropin = None
+    others = epi = split = qmm = qmm_inputs = dropin = hilo = None
     if not args.no_others:
         r2 = max(4, min(64, args.steps // 32))
         others = other_configs(torch, dr, ctx, stream, CONFIGS, r2)
@@ -550,6 +584,7 @@ def main() -> int:
         split = split_active_timing(torch, dr, ctx, stream)
         qmm, qmm_inputs = qmatmul_timing(torch, dr, ctx, stream, r2)
         dropin = dropin_timing(torch, dr, CONFIGS)
+        hilo = hilo_timing(torch, dr, ctx, stream, CONFIGS, r2)
 
     # ---- CPU baseline: the C restatement of the reference's attention on this
     # host's cores, on step 0's inputs (layer 0); its output also checks the
@@ -621,6 +656,7 @@ def main() -> int:
         "qkv_epilogue": epi,
         "split_active": split,
         "wo_qmatmul": qmm,
+        "precision_hilo": hilo,
     }
     print(json.dumps(line), flush=True)
     return 0
