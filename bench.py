@@ -338,12 +338,9 @@ def split_active_timing(torch, dr, ctx, stream, reps: int = 200) -> dict:
     return res
 
 
-def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
-    """Wo + residual on Q4_K weights (dr_qmatmul) at LLaDA-8B's shape for the
-    C2 step: 256 canvas rows x 4096 x 4096, synthetic blocks.  Ops = 2 * n *
-    rows * cols (the int8 products and their sums), against MI355X's dense
-    int8 MFMA peak; bytes = Q4_K weights + f32 activations in + residual in +
-    out.  The CPU baseline leg times the oracle on the same call."""
+def _wo_inputs(torch, stream):
+    """LLaDA-8B's Wo at the C2 step: synthetic Q4_K blocks (sane f16 scales)
+    for 4096 x 4096, 256 activation rows, a residual; host and device copies."""
     import numpy as np
     n, rows, cols = 256, 4096, 4096
     rng = np.random.default_rng(7)
@@ -358,6 +355,16 @@ def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
         dres = torch.from_numpy(res).cuda()
         out = torch.empty(n * rows, device="cuda")
     stream.synchronize()
+    return n, rows, cols, nb, w, x, res, dw, dx, dres, out
+
+
+def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
+    """Wo + residual on Q4_K weights (dr_qmatmul) at LLaDA-8B's shape for the
+    C2 step: 256 canvas rows x 4096 x 4096, synthetic blocks.  Ops = 2 * n *
+    rows * cols (the int8 products and their sums), against MI355X's dense
+    int8 MFMA peak; bytes = Q4_K weights + f32 activations in + residual in +
+    out.  The CPU baseline leg times the oracle on the same call."""
+    n, rows, cols, nb, w, x, res, dw, dx, dres, out = _wo_inputs(torch, stream)
 
     def call(i):
         dr.qmatmul(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dres)
@@ -377,15 +384,31 @@ N_LAYERS = 32  # LLaDA-8B
 
 def profile_only(args, torch, dr, CONFIGS) -> int:
     """--only CFG: `calls` eager attention calls of one config (for rocprofv3
-    runs: kernel trace and counters of that config's launches)."""
+    runs: kernel trace and counters of that config's launches).  --only wo:
+    `calls` dr_qmatmul calls at LLaDA-8B's Wo.  --precision hilo: the config
+    on a hi/lo-precision layer at scale 1.0 with QK-norm (Gemma's operating
+    point)."""
+    import dataclasses
     from helpers import EXTRA_CONFIGS
-    cfg = CONFIGS[args.only] if args.only in CONFIGS else EXTRA_CONFIGS[args.only]
     stream = torch.cuda.Stream()
     ctx = dr.Context(0)
     ctx.set_stream(stream.cuda_stream)
+    if args.only == "wo":
+        n, rows, cols, nb, w, x, res, dw, dx, dres, out = _wo_inputs(torch, stream)
+        with torch.cuda.stream(stream):
+            for _ in range(args.calls):
+                dr.qmatmul(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dres)
+        stream.synchronize()
+        print(json.dumps({"only": "wo", "calls": args.calls}), flush=True)
+        return 0
+    cfg = CONFIGS[args.only] if args.only in CONFIGS else EXTRA_CONFIGS[args.only]
+    prec = None
+    if args.precision == "hilo":
+        cfg = dataclasses.replace(cfg, scale=1.0, qk_norm=True)
+        prec = dr.PRECISION_HILO
     gen = torch.Generator(device="cuda")
     gen.manual_seed(99)
-    cache, items, qn, _ = _config_cache(torch, dr, ctx, stream, cfg, gen)
+    cache, items, qn, _ = _config_cache(torch, dr, ctx, stream, cfg, gen, precision=prec)
     with torch.cuda.stream(stream):
         for _ in range(args.calls):
             cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=cfg.attn_scale,
@@ -408,6 +431,8 @@ def main() -> int:
                     help="skip the attention-only timing of the other configs")
     ap.add_argument("--only", default="", help="profile one config's attention and exit")
     ap.add_argument("--calls", type=int, default=64, help="calls of --only")
+    ap.add_argument("--precision", choices=["bf16", "hilo"], default="bf16",
+                    help="--only: the layer's precision (hilo: at scale 1.0 with QK-norm)")
     ap.add_argument("--calib-mib", type=int, default=0,
                     help="also run a plain streaming kernel (out = -in) over this many MiB, "
                          "three times: the calibration for rocprofv3 FETCH_SIZE/WRITE_SIZE")
