@@ -1680,7 +1680,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 }  // namespace
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, int qepi, int n_cu, int force_rb, int force_kq,
+                          int mask, int qepi, int window, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows, int force_kernel) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
@@ -1691,25 +1691,31 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     const int cus = n_cu > 0 ? n_cu : 256;
     const int row_blocks = (group * max_nq + 31) / 32;  // per (batch, kv head)
     const int ntiles = (max_nk + BN - 1) / BN;
-    // Head dim exactly 128 without per-key metadata and without the Q bias /
-    // RoPE: the per-wave key streams of attn_ring_kernel (one 32-row block
-    // per workgroup, 8 key groups).  A 32-row workgroup pulls every K/V byte
-    // of its key range through its CU's L2 link (64 B/clk), so the call is
-    // bound by that stream; independent per-wave DMA keeps it nearer that
-    // rate than the staged kernel's shared super-tiles.  When one-block
-    // workgroups would take more than one round of the CUs (C3's GQA rows:
-    // 448 blocks on 256 CUs), the staged kernel's 64-row workgroups read
-    // each K/V tile once for twice the rows and win, so it keeps them.
+    // Head dim exactly 128 or 256 without per-key metadata and without the
+    // Q bias / RoPE: the per-wave key streams of attn_ring_kernel (one 32-row
+    // block per workgroup, 8 or 4 key groups).  A 32-row workgroup pulls
+    // every K/V byte of its key range through its CU, so the call is bound by
+    // that stream; independent per-wave DMA keeps it nearer the CU's rate
+    // than the staged kernel's shared super-tiles.  Picked when the one-block
+    // workgroups fit one round of the CUs, and at head dim 256 only for a
+    // sliding window of at most 1024 (each workgroup's band is then at most
+    // ~2k keys, and the staged kernel's 64-row blocks would need a key split:
+    // DiffusionGemma's sliding layers take 21.6 against 28.7 us; on its
+    // global layers the 64-row split blocks win, 34.3 against 37.4).  When
+    // one-block workgroups would take more than one round of the CUs (C3's
+    // GQA rows: 448 blocks on 256 CUs), the staged kernel's 64-row workgroups
+    // read each K/V tile once for twice the rows and keep them.
     const int ring_blocks = n_batch * n_head_kv * row_blocks;
-    const bool ring_ok = hd == 128 && mask != MASK_KEYS && qepi != QEPI_FULL;
-    const bool ring_auto = ring_blocks <= cus;
+    const int rw = ring_waves(hd);
+    const bool ring_ok = rw > 0 && mask != MASK_KEYS && qepi != QEPI_FULL;
+    const bool ring_auto = ring_blocks <= cus && (hd == 128 || (window >= 0 && window <= 1024));
     if (ring_ok && (force_kernel == KERNEL_STREAMS || (force_kernel == KERNEL_AUTO && ring_auto)) &&
         force_rb <= 0 && force_kq <= 0 && force_rows <= 0) {
         p.kernel = KERNEL_STREAMS;
         p.rb = 1;
-        p.kq = 8;
+        p.kq = rw;
         p.w16 = false;
-        p.waves = 8;
+        p.waves = rw;
         p.stages = 1;
         p.qepi = false;  // the Q norm is a runtime operand of the kernel
         p.rowgroups = row_blocks < 1 ? 1 : row_blocks;
@@ -1717,11 +1723,14 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
         int split = 1;
         if (force_split > 0) {
             split = force_split;
-        } else if (2 * base <= cus) {
+        } else if ((hd == 128 ? 2 : 4) * base <= cus) {
             // too few workgroups for the CUs: split the keys, keeping a tile
-            // for each of a split's waves
+            // for each of a split's waves.  (At head dim 256 a half-filled
+            // chip is not reason enough: the merge and the second round of
+            // partial traffic cost more than the idle CUs, 23.3 against
+            // 21.6 us on DiffusionGemma's sliding layers.)
             split = cus / base;
-            const int max_split = ntiles / 8 > 1 ? ntiles / 8 : 1;
+            const int max_split = ntiles / rw > 1 ? ntiles / rw : 1;
             if (split > max_split) split = max_split;
         }
         if (split < 1) split = 1;

@@ -38,21 +38,37 @@
 namespace dr {
 namespace {
 
-constexpr int RW = 8;             // waves (key groups) per workgroup
-constexpr int RHD = 128;          // head dim of the kernel
-constexpr int RT = BN * RHD;      // bf16 elements per K tile (and per V^T tile)
-constexpr int R_KCH = RHD / 8;    // 16-byte chunks per K row
-constexpr int R_VCH = BN / 8;     // 16-byte chunks per V^T row
-constexpr int RING_BYTES = RW * 2 * RT * 2;           // per wave: K tile + V^T tile
-constexpr int Q_BYTES = 32 * RHD * 2;                 // the block's Q rows, bf16
-constexpr int ML_OFF = RING_BYTES + Q_BYTES;          // [RW][32] max, then [RW][32] sum
-constexpr int RING_LDS = ML_OFF + 2 * RW * 32 * 4;
-static_assert(32 * RHD * 4 == 2 * RT * 2, "a wave's O^T partial fills its K + V^T buffers");
-static_assert(RING_LDS <= 160 * 1024, "LDS budget");
+// Geometry per head dim.  hd 128: 8 waves, two per SIMD.  hd 256: a wave's
+// O^T (128 registers) and Q^T fragments (64) fill most of a SIMD's register
+// file, and its K + V^T tiles take 32 KB of LDS, so the workgroup has 4
+// waves, one per SIMD; each still streams its own tiles.
+template <int HD>
+struct Ring {
+    static constexpr int RW = HD == 128 ? 8 : 4;  // waves (key groups) per workgroup
+    static constexpr int RT = BN * HD;            // bf16 elements per K tile (and per V^T tile)
+    static constexpr int KCH = HD / 8;            // 16-byte chunks per K row
+    static constexpr int VCH = BN / 8;            // 16-byte chunks per V^T row
+    static constexpr int NDMA = RT * 2 / 1024;    // 1 KB DMA instructions per tile
+    static constexpr int KS = HD / 16;            // contraction steps of QK^T
+    static constexpr int DB = HD / 32;            // 32-dim blocks of O^T
+    static constexpr int TPR = RW * 64 / 32;      // threads per query row (Q load, final pass)
+    static constexpr int QP = HD / 4 / TPR;       // f32x4 pieces per thread and row
+    static constexpr int RING_BYTES = RW * 2 * RT * 2;   // per wave: K tile + V^T tile
+    static constexpr int Q_BYTES = 32 * HD * 2;          // the block's Q rows, bf16
+    static constexpr int ML_OFF = RING_BYTES + Q_BYTES;  // [RW][32] max, then [RW][32] sum
+    static constexpr int LDS = ML_OFF + 2 * RW * 32 * 4;
+    static_assert(32 * HD * 4 == 2 * RT * 2, "a wave's O^T partial fills its K + V^T buffers");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(NDMA < 32, "two tiles of DMA fit the vmcnt counter");
+};
 
-template <int MODE>
-__global__ __launch_bounds__(RW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int HD, int MODE>
+__global__ __launch_bounds__(Ring<HD>::RW * 64) __attribute__((amdgpu_waves_per_eu(Ring<HD>::RW / 4, Ring<HD>::RW / 4)))
 void attn_ring_kernel(const AttnArgs a) {
+    using G = Ring<HD>;
+    constexpr int RW = G::RW, RT = G::RT, R_KCH = G::KCH, R_VCH = G::VCH, NDMA = G::NDMA;
+    constexpr int RHD = HD, TPR = G::TPR, QP = G::QP, KS = G::KS, DB = G::DB;
+    constexpr int RING_BYTES = G::RING_BYTES, ML_OFF = G::ML_OFF;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_red[3];
 
@@ -101,25 +117,26 @@ void attn_ring_kernel(const AttnArgs a) {
         }
     };
 
-    // ---- Q rows first: they gate the first MFMA.  Thread tid holds f32x4
-    // pieces d0 and d0 + 64 of workgroup row tid / 16 (rows past the block
-    // load row 0 and are zeroed later: no branch, so nothing issued below
-    // waits for these loads).
-    const int qlr = tid >> 4;
-    const int qd0 = (tid & 15) * 4;
+    // ---- Q rows first: they gate the first MFMA.  Thread tid holds the QP
+    // f32x4 pieces d0 + (HD / QP) p of workgroup row tid / TPR (rows past the
+    // block load row 0 and are zeroed later: no branch, so nothing issued
+    // below waits for these loads).
+    constexpr int QSTR = HD / QP;
+    const int qlr = tid / TPR;
+    const int qd0 = (tid % TPR) * 4;
     const int qr = wg_row0 + qlr;
     const bool qok = qr < rows_total;
-    f32x4 xq[2], wq[2];
+    f32x4 xq[QP], wq[QP];
     {
         int qhg, qqi;
         split_row(qok ? qr : 0, qhg, qqi);
         const float* qrow = static_cast<const float*>(S.q) + (size_t)qqi * a.q_rstride +
                             (size_t)(g * a.group + qhg) * RHD;
-        xq[0] = gload<f32x4>(qrow + qd0);
-        xq[1] = gload<f32x4>(qrow + qd0 + 64);
+#pragma unroll
+        for (int p = 0; p < QP; ++p) xq[p] = gload<f32x4>(qrow + qd0 + QSTR * p);
         if (qn_w) {  // the QK-norm gains of these dims
-            wq[0] = gload<f32x4>(qn_w + qd0);
-            wq[1] = gload<f32x4>(qn_w + qd0 + 64);
+#pragma unroll
+            for (int p = 0; p < QP; ++p) wq[p] = gload<f32x4>(qn_w + qd0 + QSTR * p);
         }
     }
 
@@ -200,9 +217,9 @@ void attn_ring_kernel(const AttnArgs a) {
     const uint32_t plane_bytes = (uint32_t)a.cap * RHD * 2;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k + (size_t)g * a.cap * RHD, plane_bytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vt + (size_t)g * RHD * a.cap, plane_bytes);
-    int kvo[8], vvo[8];
+    int kvo[NDMA], vvo[NDMA];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NDMA; ++j) {
         const int idx = j * 64 + lane;
         const int R = idx / R_KCH, pk = idx % R_KCH;
         kvo[j] = (sigma(R) * RHD + ((pk ^ swz<R_KCH>(R)) << 3)) * 2;
@@ -213,15 +230,15 @@ void attn_ring_kernel(const AttnArgs a) {
     uint16_t* const vbuf = kbuf + RT;
     auto issue_k = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16(rk, kbuf + j * 512, kvo[j], t * (BN * RHD * 2));
+        for (int j = 0; j < NDMA; ++j) dma16(rk, kbuf + j * 512, kvo[j], t * (BN * RHD * 2));
     };
     auto issue_v = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16(rv, vbuf + j * 512, vvo[j], t * (BN * RHD * 2));
+        for (int j = 0; j < NDMA; ++j) dma16(rv, vbuf + j * 512, vvo[j], t * (BN * RHD * 2));
     };
     auto issue_v_to_k = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16(rv, kbuf + j * 512, vvo[j], t * (BN * RHD * 2));
+        for (int j = 0; j < NDMA; ++j) dma16(rv, kbuf + j * 512, vvo[j], t * (BN * RHD * 2));
     };
     // Wave w takes tiles t0 + w, t0 + w + RW, ...: a fixed assignment, so
     // every call sums each row's keys in the same order (bit-identical
@@ -233,21 +250,21 @@ void attn_ring_kernel(const AttnArgs a) {
     issue_v(t0 + wave);
 
     // QK-norm (rms_norm_inplace, ops.rs:106-114): f32 squares summed in f64
-    // over the 16 lanes of the row, then x * scale * w.
+    // over the TPR lanes of the row, then x * scale * w.
     if (qn_w) {
         double ss = 0.0;
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < QP; ++p)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float sq = xq[p][e] * xq[p][e];
                 ss += (double)sq;
             }
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off);
+        for (int off = 1; off < TPR; off <<= 1) ss += __shfl_xor(ss, off);
         const float sc = 1.0f / (float)sqrt(ss / (double)RHD + (double)a.qn_eps);
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < QP; ++p)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
 #pragma clang fp contract(off)
@@ -256,8 +273,8 @@ void attn_ring_kernel(const AttnArgs a) {
     }
     uint16_t* const qs = smem + RING_BYTES / 2;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int d = qd0 + 64 * p;
+    for (int p = 0; p < QP; ++p) {
+        const int d = qd0 + QSTR * p;
         bf16x4 y;
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = (__bf16)(qok ? xq[p][e] * a.c : 0.0f);
@@ -266,14 +283,14 @@ void attn_ring_kernel(const AttnArgs a) {
     lds_barrier();  // (the first K/V tiles stay in flight)
     // Q^T fragments, held for the whole key loop: lane (col, hf) supplies
     // row col, dims 16 c + 8 hf .. + 8 of contraction step c
-    bf16x8 qf[8];
+    bf16x8 qf[KS];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < KS; ++c)
         qf[c] = *reinterpret_cast<const bf16x8*>(qs + col * RHD + (((2 * c + hf) ^ swz<R_KCH>(col)) << 3));
 
-    f32x16 o[4];
+    f32x16 o[DB];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+    for (int db = 0; db < DB; ++db) o[db] = f32x16{};
     float mu = 0.0f;        // running max m (log2 units), valid once m_set
     bool m_set = false;
     float thr = -INFINITY;  // a score above mu + thr moves m
@@ -282,9 +299,9 @@ void attn_ring_kernel(const AttnArgs a) {
 
     // V^T fragments of a tile: lane (col, hf) supplies row d = 32 db + col,
     // keys 16 hf + 8 sl .. + 8 of key slice sl (the P^T slice it holds)
-    auto read_v = [&](const uint16_t* vsrc, bf16x8 (&vf)[4][2]) __attribute__((always_inline)) {
+    auto read_v = [&](const uint16_t* vsrc, bf16x8 (&vf)[DB][2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < DB; ++db) {
             const int d = 32 * db + col;
             const uint16_t* vrow = vsrc + d * BN;
             const int sw = swz<R_VCH>(d);
@@ -292,9 +309,9 @@ void attn_ring_kernel(const AttnArgs a) {
             vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
         }
     };
-    auto pv = [&](const bf16x8 (&vf)[4][2], const bf16x8 (&pp)[2]) __attribute__((always_inline)) {
+    auto pv = [&](const bf16x8 (&vf)[DB][2], const bf16x8 (&pp)[2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < DB; ++db) {
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pp[0], o[db], 0, 0, 0);
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][1], pp[1], o[db], 0, 0, 0);
         }
@@ -319,7 +336,7 @@ void attn_ring_kernel(const AttnArgs a) {
         const int sw = swz<R_KCH>(col);
         f32x16 sacc = negm;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < KS / 4; ++h) {
             bf16x8 kf[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c)
@@ -404,7 +421,7 @@ void attn_ring_kernel(const AttnArgs a) {
     int t = wave < nt ? t0 + wave : -1;  // the current tile (uniform over the wave)
     if (t >= 0) {
         // step 0: K tile 0 has landed when only V^T tile 0 is outstanding
-        wait_vmcnt<8>();
+        wait_vmcnt<NDMA>();
         f32x16 sv = qk();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -416,12 +433,12 @@ void attn_ring_kernel(const AttnArgs a) {
         t = tn;
     }
     for (int i = 1; t >= 0; ++i) {
-        // K tile i has landed: outstanding after it is V^T tile i - 1 (8
+        // K tile i has landed: outstanding after it is V^T tile i - 1 (NDMA
         // instructions), except at i = 1, where V^T 0 was issued before K 1
         if (i == 1)
             wait_vmcnt<0>();
         else
-            wait_vmcnt<8>();
+            wait_vmcnt<NDMA>();
         f32x16 sv = qk();
         // every K fragment is in registers: the K buffer takes the next tile,
         // or this last tile's V^T
@@ -434,8 +451,8 @@ void attn_ring_kernel(const AttnArgs a) {
             issue_v_to_k(t);
         // V^T tile i - 1 (the pending PV product's operand) has landed: after
         // it only the DMA just issued is outstanding
-        wait_vmcnt<8>();
-        bf16x8 vf[4][2];
+        wait_vmcnt<NDMA>();
+        bf16x8 vf[DB][2];
         read_v(vbuf, vf);
         float alpha;
         const bool moved = mask_and_max(sv, t, alpha);
@@ -447,15 +464,15 @@ void attn_ring_kernel(const AttnArgs a) {
             pv(vf, pp);
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);  // four VALU / transcendental
+        for (int k = 0; k < 2 * DB; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, 16 / DB, 0);  // VALU / transcendental
         }
         pin(pcur);
         __builtin_amdgcn_sched_barrier(0);
         if (moved) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            for (int db = 0; db < DB; ++db) o[db] *= alpha;
         }
         pprev[0] = pcur[0];
         pprev[1] = pcur[1];
@@ -471,7 +488,7 @@ void attn_ring_kernel(const AttnArgs a) {
     // the last tile's PV product (a wave without tiles multiplies zeros)
     wait_vmcnt<0>();
     {
-        bf16x8 vf[4][2];
+        bf16x8 vf[DB][2];
         read_v(last_in_k ? kbuf : vbuf, vf);
         const bf16x8 pp[2] = {wave < nt ? __builtin_bit_cast(bf16x8, pprev[0]) : bf16x8{},
                               wave < nt ? __builtin_bit_cast(bf16x8, pprev[1]) : bf16x8{}};
@@ -480,12 +497,12 @@ void attn_ring_kernel(const AttnArgs a) {
 
     // ---- merge the RW key groups of each row.  A wave's K and V^T buffers
     // are its own and free once its last PV product has read them: its O^T
-    // (32 rows x 128 f32, 16 KB) goes there right away, while other waves
+    // (32 rows x HD f32) goes there right away, while other waves
     // may still be in their loops, with (m, l) beside the other rows'
     // statistics.  After one barrier every thread finishes a row: wave w's
     // partial is weighted by exp2(m_w - M), M the row's largest m, and
     // O = sum_w w_w O_w / sum_w w_w l_w.  16-byte chunk c of row q sits at
-    // chunk c ^ q of its 512-byte row, so both the writes (lanes spread over
+    // chunk c ^ q of its row, so both the writes (lanes spread over
     // rows) and the reads (lanes spread over chunks) hit distinct banks.
     float* const sm = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + ML_OFF);  // [RW][32]
     float* const sl = sm + RW * 32;                                                    // [RW][32]
@@ -500,16 +517,17 @@ void attn_ring_kernel(const AttnArgs a) {
         // 8 db + 2 (e / 4) + hf of row col
         float* myrow = reinterpret_cast<float*>(kbuf) + col * RHD;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 *reinterpret_cast<f32x4*>(myrow + 4 * ((8 * db + 2 * j + hf) ^ col)) =
                     f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
     }
     lds_barrier();
-    // thread tid: row rr = tid / 16, chunks ch and ch + 16
+    // thread tid: row rr = tid / TPR, chunks ch + TPR k, k < CPT
     {
-        const int rr = tid >> 4, ch = tid & 15;
+        constexpr int CPT = HD / 4 / TPR;
+        const int rr = tid / TPR, ch = tid % TPR;
         const int row = wg_row0 + rr;
         if (row < rows_total) {
             float mw[RW];
@@ -519,14 +537,17 @@ void attn_ring_kernel(const AttnArgs a) {
                 mw[w] = sm[w * 32 + rr];
                 M = __builtin_fmaxf(M, mw[w]);
             }
-            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+            f32x4 acc[CPT];
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             float L = 0.0f;
 #pragma unroll
             for (int w = 0; w < RW; ++w) {
                 const float wt = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
                 const float* prow = reinterpret_cast<const float*>(smem + w * 2 * RT) + rr * RHD;
-                acc0 += wt * *reinterpret_cast<const f32x4*>(prow + 4 * (ch ^ rr));
-                acc1 += wt * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + 16) ^ rr));
+#pragma unroll
+                for (int k = 0; k < CPT; ++k)
+                    acc[k] += wt * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + TPR * k) ^ rr));
                 L += wt * sl[w * 32 + rr];
             }
             if (a.n_split > 1) {
@@ -535,42 +556,55 @@ void attn_ring_kernel(const AttnArgs a) {
                 const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
                 const size_t prow =
                     (size_t)split * plane + (size_t)(b * a.n_head_kv + g) * a.part_rows + row;
-                gstore(a.part_o + prow * RHD + 4 * ch, acc0);
-                gstore(a.part_o + prow * RHD + 4 * (ch + 16), acc1);
+#pragma unroll
+                for (int k = 0; k < CPT; ++k) gstore(a.part_o + prow * RHD + 4 * (ch + TPR * k), acc[k]);
                 if (ch == 0) gstore(a.part_ml + prow * 2, make_float2(M, L));
             } else {
                 int ohg, oqi;
                 split_row(row, ohg, oqi);
                 float* orow = S.out + (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
                 const float il = __builtin_amdgcn_rcpf(L);
-                gstore(orow + 4 * ch, acc0 * il);
-                gstore(orow + 4 * (ch + 16), acc1 * il);
+#pragma unroll
+                for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), acc[k] * il);
             }
         }
     }
 }
 
-template <int MODE>
+template <int HD, int MODE>
 hipError_t launch_ring_mode(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     static bool attr_set = false;
-    auto fn = attn_ring_kernel<MODE>;
+    auto fn = attn_ring_kernel<HD, MODE>;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, RING_LDS);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, Ring<HD>::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(RW * 64), RING_LDS, st, a);
+    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(Ring<HD>::RW * 64), Ring<HD>::LDS, st, a);
     return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_ring_hd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    switch (p.mask) {
+        case MASK_NONE: return launch_ring_mode<HD, MASK_NONE>(p, a, st);
+        case MASK_POS: return launch_ring_mode<HD, MASK_POS>(p, a, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
 
+int ring_waves(int hd) {
+    return hd == 128 ? Ring<128>::RW : (hd == 256 ? Ring<256>::RW : 0);
+}
+
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    if (p.hd_tile != RHD || a.hd != RHD || p.act || a.qb || a.rope) return hipErrorInvalidValue;
-    switch (p.mask) {
-        case MASK_NONE: return launch_ring_mode<MASK_NONE>(p, a, st);
-        case MASK_POS: return launch_ring_mode<MASK_POS>(p, a, st);
+    if (p.act || a.qb || a.rope || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
+    switch (a.hd) {
+        case 128: return launch_ring_hd<128>(p, a, st);
+        case 256: return launch_ring_hd<256>(p, a, st);
         default: return hipErrorInvalidValue;
     }
 }

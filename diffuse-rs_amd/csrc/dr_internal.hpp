@@ -260,11 +260,12 @@ enum QEpilogue : int {
 };
 
 // Chooses tile sizes and the key split for a problem on a device with n_cu
-// compute units.  force_rb / force_kq / force_split > 0 override the
-// heuristic (tuning); force_rows 16 or 32 picks the query rows per compute
-// wave where both are built (0: automatic).
+// compute units (window: the sliding window, < 0 for none).  force_rb /
+// force_kq / force_split > 0 override the heuristic (tuning); force_rows 16
+// or 32 picks the query rows per compute wave where both are built (0:
+// automatic).
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, int qepi, int n_cu, int force_rb, int force_kq,
+                          int mask, int qepi, int window, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows, int force_kernel);
 
 // Whether a plan's shape can run the fused step (each DMA wave stages one
@@ -284,6 +285,7 @@ size_t scratch_bytes();
 hipError_t scratch_init(int device);
 void* scratch_ptr(int device);
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
+int ring_waves(int hd);  // waves per workgroup of attn_ring_kernel (0: head dim not built)
 hipError_t launch_hilo(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 int hilo_rows();  // query rows per workgroup of attn_hilo_kernel
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);

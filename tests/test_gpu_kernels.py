@@ -67,14 +67,25 @@ CASES = {
     "split2": (4, 4, 900, 64, 1, None, None, False, 2),
     "split3_window": (4, 2, 1500, 64, 1, 400, None, False, 3),
 }
+# head dim 256 (DiffusionGemma's sliding and global layers): the same kinds
+# of problem for the 4-wave build of the per-wave-stream kernel
+CASES_256 = {
+    "mha": (4, 4, 600, 200, 1, None, None, False, 0),
+    "ragged": (2, 2, 203, 77, 1, None, None, False, 0),
+    "gqa_batch2": (8, 4, 300, 100, 2, None, None, False, 0),
+    "window": (8, 4, 1100, 160, 1, 300, None, False, 0),
+    "window_prefix": (4, 2, 500, 111, 2, 90, 540, False, 0),
+    "qk_norm": (4, 4, 400, 96, 1, None, None, True, 0),
+    "split2": (4, 4, 900, 64, 1, None, None, False, 2),
+    "split3_window": (4, 2, 1500, 64, 1, 400, None, False, 3),
+}
 
 
-def _run(dev, name, kernel):
-    h, hkv, n_p, n_c, batch, window, prefix, qk_norm, n_split = CASES[name]
-    hd = 128
+def _run(dev, name, kernel, hd=128):
+    h, hkv, n_p, n_c, batch, window, prefix, qk_norm, n_split = (CASES if hd == 128 else CASES_256)[name]
     n_t = n_p + n_c
     kvs = hkv * hd
-    rng = np.random.default_rng(sum(map(ord, name)))
+    rng = np.random.default_rng(sum(map(ord, name)) + hd)
     qn = kn = None
     if qk_norm:
         qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
@@ -134,6 +145,22 @@ def test_kernel_family_vs_oracle(dev, name, kernel):
         assert mx <= TOL_MAX and mean <= TOL_MEAN, (name, b, mx, mean)
 
 
+@pytest.mark.parametrize("kernel", [dr.KERNEL_STAGED, dr.KERNEL_STREAMS], ids=["staged", "streams"])
+@pytest.mark.parametrize("name", list(CASES_256))
+def test_kernel_family_hd256_vs_oracle(dev, name, kernel):
+    got, wants, info = _run(dev, name, kernel, hd=256)
+    say(f"hd 256 {name} kernel {kernel}: launch {info}")
+    assert info["kernel"] == kernel
+    if kernel == dr.KERNEL_STREAMS:
+        assert info["waves_per_wg"] == 4
+    if CASES_256[name][8]:
+        assert info["n_split"] == CASES_256[name][8]
+    for b, (g, w) in enumerate(zip(got, wants)):
+        mx, mean = err_stats(g, w)
+        say(f"  batch {b}: max-abs {mx:.3e} mean-abs {mean:.3e}")
+        assert mx <= TOL_MAX and mean <= TOL_MEAN, (name, b, mx, mean)
+
+
 @pytest.mark.parametrize("name", ["mha", "gqa_batch2", "window_prefix", "qk_norm"])
 def test_kernel_families_agree(dev, name):
     """The two families compute the same function: they differ only in the
@@ -147,11 +174,12 @@ def test_kernel_families_agree(dev, name):
 def test_streams_kernel_is_deterministic(dev):
     """Each wave owns a fixed set of key tiles, so every call sums each
     row's keys in the same order: repeated calls are bit-identical."""
-    first, _, _ = _run(dev, "window_prefix", dr.KERNEL_STREAMS)
-    for _ in range(3):
-        again, _, _ = _run(dev, "window_prefix", dr.KERNEL_STREAMS)
-        for x, y in zip(first, again):
-            assert np.array_equal(x, y)
+    for hd in (128, 256):
+        first, _, _ = _run(dev, "window_prefix", dr.KERNEL_STREAMS, hd)
+        for _ in range(3):
+            again, _, _ = _run(dev, "window_prefix", dr.KERNEL_STREAMS, hd)
+            for x, y in zip(first, again):
+                assert np.array_equal(x, y)
 
 
 def test_planner_picks_streams_for_one_round(dev):

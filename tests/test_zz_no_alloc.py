@@ -54,7 +54,10 @@ def dev():
 # (h, hkv, hd, n_prompt, n_canvas first call, n_canvas second call, window, forced splits)
 SHAPES = {
     "hd128_split3": (8, 8, 128, 1400, 200, 70, None, 3),
-    "hd256_window_auto_split": (16, 8, 256, 2048, 256, 100, 700, 0),
+    # a window above 1024 keeps hd 256 on the staged kernel, which splits the keys by itself
+    "hd256_window_auto_split": (16, 8, 256, 2048, 256, 100, 1500, 0),
+    # the per-wave-stream kernel (hd 256, window <= 1024) with forced splits
+    "hd256_streams_split2": (16, 8, 256, 2048, 256, 100, 700, 2),
 }
 
 
@@ -82,6 +85,10 @@ def test_noalloc_matches_cached_twice(dev, name):
                 outs[noalloc] = dev.get(out)
             say(f"{name} call {call} (n_c {n_c}): launch {info}")
             assert info["n_split"] > 1, "the shape must use the split workspace"
+            if name == "hd256_window_auto_split":
+                assert info["kernel"] == dr.KERNEL_STAGED
+            if name == "hd256_streams_split2":
+                assert info["kernel"] == dr.KERNEL_STREAMS
             assert not np.any(np.isnan(outs[False]))
             assert np.array_equal(outs[False], outs[True]), name
     finally:
