@@ -15,7 +15,9 @@
 // V alone would move it by up to 2^-9 of that row.  P stays bf16: the
 // dominant key's p is exactly 1 and l sums the same rounded p.  The cache
 // holds the lo halves of K and V^T in planes of their own, written by the
-// store next to the hi halves (dr_cache_set_precision).
+// store next to the hi halves (dr_cache_set_precision).  The drop-in
+// dr_attention() runs every call here on its f32 inputs, with the per-key
+// positions and sequence ids of its arbitrary key order (MASK_KEYS).
 //
 // Work decomposition.  A workgroup owns 64 query rows of one (batch slot, kv
 // head) -- four 16-row blocks, GQA heads packed into rows as in attn_fwd.hip --
@@ -228,6 +230,20 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
         // K of tile t has landed (the V^T DMA issued after it may be in flight)
         wait_vmcnt<VDMA>();
         lds_barrier();
+        // per-key positions and sequence ids of this lane's 8 keys
+        // (MASK_KEYS; identity positions / one sequence where absent).  Loads
+        // issued here complete before the vmcnt(0) below, so the counted DMA
+        // waits stay exact or wait longer, never less.
+        int kp[8], kqs[8];
+        if constexpr (MODE == MASK_KEYS) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int kidx = t * BN + 8 * gq + i;
+                const int kc = min(kidx, S.nk - 1);
+                kp[i] = S.kpos ? gload<int>(S.kpos + kc) : kidx;
+                kqs[i] = S.kseq ? gload<int>(S.kseq + kc) : 0;
+            }
+        }
         // ---- S^T = K Q^T over this wave's head dims, hi/lo split
         f32x4 s[2];
 #pragma unroll
@@ -270,6 +286,7 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
             const int kidx = t * BN + 8 * gq + i;
             bool vis = rvalid && kidx < S.nk;
             if constexpr (MODE == MASK_POS) vis = vis && visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+            if constexpr (MODE == MASK_KEYS) vis = vis && visible(my_qpos, kp[i], my_qseq, kqs[i], a.window, my_pref);
             sv[i] = vis ? s[i >> 2][i & 3] : -INFINITY;
         }
         float mt = max3(sv[0], sv[1], sv[2]);
@@ -346,6 +363,11 @@ hipError_t launch_hilo_hd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st
         hipLaunchKernelGGL(k, dim3(p.n_workgroups), dim3(G::NT), lds, st, a);
     } else if (p.mask == MASK_POS) {
         auto k = attn_hilo_kernel<HD, MASK_POS>;
+        hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k, dim3(p.n_workgroups), dim3(G::NT), lds, st, a);
+    } else if (p.mask == MASK_KEYS) {
+        auto k = attn_hilo_kernel<HD, MASK_KEYS>;
         hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k, dim3(p.n_workgroups), dim3(G::NT), lds, st, a);

@@ -81,7 +81,11 @@ int dr_device_count(void);
  * at src/model/attention.rs:106 (caller: src/model/forward.rs:343).
  *
  * Host pointers, synchronous: uploads q/k/v and row metadata, runs the fused
- * bf16-MFMA kernel on device 0, downloads out.  Layouts as the reference:
+ * kernel on device 0, downloads out.  The kernel takes Q, K and V as bf16
+ * hi + lo halves (the hi/lo kernel of DR_PRECISION_HILO layers): scores and
+ * values are f32-accurate, so out matches the reference's f32 attention to
+ * the bar of the f32 computation under every mask, also where a row sees
+ * only a few keys.  The host copies dominate the call.  Layouts as the reference:
  * q [nq][n_head][head_dim], k and v [nk][n_head_kv][head_dim], out
  * [nq][n_head * head_dim], all f32 row-major; out is fully overwritten.
  * Lengths are checked as the reference's debug_asserts (:107-109) and

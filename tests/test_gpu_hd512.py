@@ -53,10 +53,9 @@ def test_hd512_dropin_random_masks_vs_oracle(torch, hd):
     say(f"hd {hd} drop-in, window {s.sliding_window} prefix {s.causal_prefix}")
     got = np.zeros(nq * h * hd, np.float32)
     dr.attention(got, q, k, v, dr.AttnShape(**s.__dict__), dr.Rows(qpos, seq_q), dr.Rows(kpos, seq_k))
-    check(got, oracle_run(s, qr, kr, *as_kernel_sees(q, k, v, sc)), f"hd {hd} masked (bf16 operands)")
-    # windows of 20..60 keys average few V rows: the f32 comparison is looser,
-    # as for the other head dims
-    check(got, oracle_run(s, qr, kr, q, k, v), f"hd {hd} masked (f32 inputs)", tol_max=3e-2)
+    # windows of 20..60 keys average few V rows; the drop-in's hi/lo scores
+    # and values hold the f32 comparison to the standard bar
+    check(got, oracle_run(s, qr, kr, q, k, v), f"hd {hd} masked (f32 inputs)")
 
 
 @pytest.mark.parametrize("n_split", [0, 1, 3])
