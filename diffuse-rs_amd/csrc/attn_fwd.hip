@@ -102,21 +102,17 @@ struct Geometry {
                   "head-dim split: head dim 512, one key group, no DMA waves");
 };
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool ACT, bool W16>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool W16>
 __attribute__((amdgpu_waves_per_eu(Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD,
                                    Geometry<HD, RB, KQ, NS, NP, W16>::WAVES_PER_SIMD))) __global__
 __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void attn_fwd_kernel(const AttnArgs a) {
     using G = Geometry<HD, RB, KQ, NS, NP, W16>;
-    static_assert(!(W16 && ACT), "the fused step runs 32-row waves");
     constexpr int NW = G::NW, NWT = G::NWT, NT = G::NT, NC = G::NC, ND = G::ND;
     constexpr int KCH = G::KCH, VCH = G::VCH, TILE = G::TILE, SLOT = G::SLOT;
     constexpr int CPT = G::CPT, NLDW = G::NLDW, ROWF = G::ROWF, QROWS = G::QROWS;
 
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_red[3][NWT];
-    // fused step: each DMA wave's own copy of the K-norm gain (written and
-    // read by that wave only, so no barrier orders it)
-    __shared__ __attribute__((aligned(16))) float s_kn[ACT ? NP : 1][ACT ? HD : 1];
 
     // Every scalar of the decode and the first loads, and batch slot 0, is
     // requested here at once (wide scalar loads, one wait) rather than by one
@@ -235,45 +231,9 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
     const int t1 = kt_lo + min((split + 1) * per, ntiles);
     const int nsup = (t1 - t0 + KQ - 1) / KQ;  // super-tiles
 
-    // Tile of slot u (super-tile u) of this wave's key group.  Without ACT,
-    // t0 + u*KQ + kq.  With ACT the fresh tiles (the suffix [ta, t1) of the
-    // range) are staged from f32 rows, which costs the staging wave far more
-    // than a DMA; the softmax does not depend on the key order, so each key
-    // group w takes the fresh tiles ta + j*KQ + w (j < m_w) spread evenly over
-    // its column of slots, phase-shifted by w so the groups stage in turn, and
-    // away from the first NS slots (staged before the loop can overlap them)
-    // when the column has room; the cached tiles fill the remaining slots, a
-    // contiguous block of them per key group.  Every tile of [t0, t1) lands in
-    // exactly one slot.
+    // Tile of slot u (super-tile u) of this wave's key group.
     const int kg = compute ? kq : dwave;  // this wave's key group
-    auto group_slots = [&](int cnt, int w) __attribute__((always_inline)) {
-        return cnt > w ? (cnt - w + KQ - 1) / KQ : 0;
-    };
-    const int ta = ACT ? min(max(S.act0 / BN, t0), t1) : t1;  // first fresh tile
-    const int sl_w = group_slots(t1 - t0, kg), m_w = group_slots(t1 - ta, kg);
-    int pc_w = 0;  // cached tiles of the key groups before this one
-#pragma unroll
-    for (int w = 0; w < KQ; ++w)
-        if (w < kg) pc_w += group_slots(t1 - t0, w) - group_slots(t1 - ta, w);
-    const int ulo_w = min(NS, sl_w - m_w), span_w = sl_w - ulo_w;
-    // fresh slots of this key group before slot U: the j whose slot
-    // ulo_w + floor((j*KQ + kg) * span_w / (m_w*KQ)) is below U
-    auto fresh_before = [&](int U) __attribute__((always_inline)) {
-        const int num = (U - ulo_w) * m_w * KQ - kg * span_w;
-        if (m_w == 0 || num <= 0) return 0;
-        return min(m_w, (num + KQ * span_w - 1) / (KQ * span_w));
-    };
-    auto tile_at = [&](int u) __attribute__((always_inline)) {
-        if constexpr (!ACT) {
-            return t0 + u * KQ + kg;
-        } else {
-            // (uniform over the wave: the divisions run on the vector unit,
-            // and the DMA takes the tile offset in a scalar register)
-            const int b0 = fresh_before(u);
-            return __builtin_amdgcn_readfirstlane(fresh_before(u + 1) > b0 ? ta + b0 * KQ + kg
-                                                                           : t0 + pc_w + (u - b0));
-        }
-    };
+    auto tile_at = [&](int u) __attribute__((always_inline)) { return t0 + u * KQ + kg; };
 
     // ---- DMA plan: instruction j of this wave fills 64 chunks of one tile
     // region (region 2*i is K tile i of the super-tile, 2*i+1 its V^T tile).
@@ -306,16 +266,10 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k + (size_t)g * a.cap * HD, plane_bytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vt + (size_t)g * HD * a.cap, plane_bytes);
 
-    // DMA instructions [j0, j1) of super-tile u into stage st (ACT: each DMA
-    // wave fills its own key group, whose tile in super-tile u is tt).
-    auto issue_range = [&](int u, int st, int j0, int j1, int tt) __attribute__((always_inline)) {
+    // DMA instructions [j0, j1) of super-tile u into stage st.
+    auto issue_range = [&](int u, int st, int j0, int j1) __attribute__((always_inline)) {
         const int cofs = WHOLE ? 0 : (dwave * NLDW * 64) % CPT;  // first chunk in the region
-        // (fused step: an opaque lane index, as for the staged tiles below)
-        int ln = lane;
-        if constexpr (ACT) {
-            asm volatile("" : "+v"(ln));
-            ln &= 63;
-        }
+        const int ln = lane;
 #pragma unroll
         for (int j = 0; j < NLDW; ++j) {
             if (j < j0 || j >= j1) continue;
@@ -324,7 +278,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             uint16_t* dst = smem + (kqr * NS + st) * SLOT + (reg & 1) * TILE +
                             ((WHOLE ? (j * 64) % CPT : cofs + j * 64) << 3);
             // slots past the range reload the last tile: in bounds, unused
-            const int t = ACT ? __builtin_amdgcn_readfirstlane(tt) : min(t0 + u * KQ + kqr, t1 - 1);
+            const int t = min(t0 + u * KQ + kqr, t1 - 1);
             const int vo = NP > 0 ? voff_of(j, ln) : voff[NP > 0 ? 0 : j];
             // (K tile t and V^T tile t both start at byte t * BN * HD * 2)
             if (reg & 1)
@@ -333,151 +287,11 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                 dma16(rk, dst, vo, t * (BN * HD * 2));
         }
     };
-    auto issue = [&](int u, int st, int tt = 0) __attribute__((always_inline)) {
-        issue_range(u, st, 0, NLDW, tt);
-    };
+    auto issue = [&](int u, int st) __attribute__((always_inline)) { issue_range(u, st, 0, NLDW); };
 
-    // Fused step (ACT): a tile whose keys are the step's fresh rows is staged
-    // by the DMA wave of its key group through registers instead of the DMA:
-    // f32 rows of ka / va, K-normalised when asked, rounded to bf16 and
-    // written as the same permuted, swizzled LDS image the DMA produces (V
-    // transposed on the way).  The workgroup whose row group matches the
-    // tile (one per kv head and key split) also writes the bf16 rows into the
-    // cache: StepCache::store (cache.rs:62-71) of those rows, positions the
-    // launch never reads from the cache.  Staging has two phases so that the
-    // load latency overlaps a super-tile of compute: act_load issues the f32
-    // loads into kx / vx one pipeline iteration ahead, act_write converts and
-    // writes them in the iteration the DMA would have been issued.
-    static_assert(!ACT || (NP > 0 && NP == KQ && NLDW * 64 == 2 * CPT),
-                  "fused step: each DMA wave stages one key group's K and V^T tiles");
-    constexpr int KJ = ACT ? CPT / 64 : 1;             // K chunks per lane
-    constexpr int VJ = ACT ? (HD / 4) * VCH / 64 : 1;  // (4 d x 8 keys) blocks per lane
-    // The lane index as a value the compiler cannot see through: offsets
-    // derived from it are recomputed per use instead of hoisted out of the
-    // producer loop (which holds a staged tile in registers) and spilled.
-    auto opaque_lane = [&]() __attribute__((always_inline)) {
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        return ln & 63;  // the range, for the compiler's arithmetic
-    };
-    using KRegs = f32x4[KJ][2];
-    using VRegs = f32x4[VJ][8];
-    // Buffer loads with 32-bit offsets from kv head g's first element; the
-    // range of the resources ends at the pass's last row, so rows past it
-    // read as zeros (the padding of the tile) and every load is issued
-    // without a branch, needing no wait until act_write.
-    auto act_load = [&](int t, KRegs& kx, VRegs& vx) __attribute__((always_inline)) {
-        const int key0 = t * BN - S.act0;
-        const int ln = opaque_lane();
-        const uint32_t nb = (uint32_t)(S.n_act * a.kv_rstride - g * HD) * 4u;
-        const __amdgpu_buffer_rsrc_t rka = make_rsrc(S.ka + (size_t)g * HD, nb);
-        const __amdgpu_buffer_rsrc_t rva = make_rsrc(S.va + (size_t)g * HD, nb);
-#pragma unroll
-        for (int j = 0; j < KJ; ++j) {
-            const int c = ln + 64 * j, R = c / KCH, lc = (c % KCH) ^ swz<KCH>(R);
-            const int off = ((key0 + sigma(R)) * a.kv_rstride + 8 * lc) * 4;
-            kx[j][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rka, off, 0, 0));
-            kx[j][1] =
-                __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rka, off + 16, 0, 0));
-        }
-#pragma unroll
-        for (int jj = 0; jj < VJ; ++jj) {
-            const int pp = ln + 64 * jj, d0 = 4 * (pp / VCH), lv = pp % VCH;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const int off = ((key0 + 8 * lv + kk) * a.kv_rstride + d0) * 4;
-                vx[jj][kk] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rva, off, 0, 0));
-            }
-        }
-    };
-    auto act_write = [&](int t, int st, const KRegs& kx, const VRegs& vx)
-        __attribute__((always_inline)) {
-        uint16_t* kdst = smem + (dwave * NS + st) * SLOT;
-        uint16_t* vdst = kdst + TILE;
-        const int key0 = t * BN;
-        const int ln = opaque_lane();
-        const bool own = ((t - S.act0 / BN) % a.rowgroups) == rg;
-        // cache planes of kv head g, written with 32-bit byte offsets (one
-        // register per address: 64-bit addresses of the 16 row pieces would
-        // not fit beside the staged data)
-        const __amdgpu_buffer_rsrc_t wk = make_rsrc(S.kst + (size_t)g * a.cap * HD, plane_bytes);
-        const __amdgpu_buffer_rsrc_t wv = make_rsrc(S.vst + (size_t)g * HD * a.cap, plane_bytes);
-#pragma unroll
-        for (int j = 0; j < KJ; ++j) {
-            const int c = ln + 64 * j, R = c / KCH, lc = (c % KCH) ^ swz<KCH>(R);
-            f32x4 x0 = kx[j][0], x1 = kx[j][1];
-            if (a.kn_w) {
-                // rms_norm_inplace (ops.rs:106-114) per head row: f32 squares
-                // summed in f64; the KCH lanes holding a row's chunks are
-                // consecutive.
-                double ss = 0.0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float sq0 = x0[e] * x0[e];
-                    ss += (double)sq0;
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float sq1 = x1[e] * x1[e];
-                    ss += (double)sq1;
-                }
-#pragma unroll
-                for (int off = 1; off < KCH; off <<= 1) ss += __shfl_xor(ss, off);
-                const float sc = 1.0f / (float)sqrt(ss / (double)HD + (double)a.kn_eps);
-                const f32x4 w0 = *reinterpret_cast<const f32x4*>(&s_kn[dwave][8 * lc]);
-                const f32x4 w1 = *reinterpret_cast<const f32x4*>(&s_kn[dwave][8 * lc + 4]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    x0[e] = x0[e] * sc * w0[e];
-                    x1[e] = x1[e] * sc * w1[e];
-                }
-            }
-            bf16x8 y;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                y[e] = (__bf16)x0[e];
-                y[4 + e] = (__bf16)x1[e];
-            }
-            *reinterpret_cast<bf16x8*>(kdst + c * 8) = y;
-            if (own && key0 + sigma(R) - S.act0 < S.n_act)
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(u32x4, y), wk, ((key0 + sigma(R)) * HD + 8 * lc) * 2, 0, 0);
-        }
-#pragma unroll
-        for (int jj = 0; jj < VJ; ++jj) {
-            const int pp = ln + 64 * jj, d0 = 4 * (pp / VCH), lv = pp % VCH;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = d0 + i;
-                bf16x8 y;
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk) y[kk] = (__bf16)vx[jj][kk][i];
-                *reinterpret_cast<bf16x8*>(vdst + (d * VCH + (lv ^ swz<VCH>(d))) * 8) = y;
-                if (own)
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), wv,
-                                                           (key0 * HD + d * BN + 8 * lv) * 2, 0, 0);
-            }
-        }
-    };
     // What a DMA wave does for super-tile u into stage st before the main
-    // loop: the DMA, or with ACT, both staging phases when its key group's
-    // tile is active (no work when the key group has no tile there).
-    auto fill = [&](int u, int st) __attribute__((always_inline)) {
-        if constexpr (ACT) {
-            if (u >= sl_w) return;
-            const int t = tile_at(u);
-            if (t >= ta) {
-                KRegs kx;
-                VRegs vx;
-                act_load(t, kx, vx);
-                act_write(t, st, kx, vx);
-            } else {
-                issue(u, st, t);
-            }
-            return;
-        }
-        issue(u, st);
-    };
+    // loop: the DMA.
+    auto fill = [&](int u, int st) __attribute__((always_inline)) { issue(u, st); };
 
     // ---- Q: the workgroup's rows, loaded once (coalesced f32x4 row pieces,
     // requested before the first K/V DMA: they gate the first MFMA),
@@ -568,10 +382,6 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
         }
 
         if (ib == 0 && dma) {  // (first batch only)
-            if constexpr (ACT) {
-                if (a.kn_w)
-                    for (int i = lane; i < HD; i += 64) s_kn[dwave][i] = a.kn_w[i];
-            }
 #pragma unroll
             for (int i = 0; i < NS - 1; ++i)
                 if (i < nsup) fill(i, i);
@@ -672,8 +482,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
 
     // Compute waves and DMA-only waves run separate loops with the same
     // number of barriers, so that none of the compute state (O, P, V^T and Q
-    // fragments) is live in the DMA waves' code, which needs registers of its
-    // own to stage fused-step tiles.
+    // fragments) is live in the DMA waves' code.
     if (W16 && compute) {
         if constexpr (W16) {
             // 16 query rows per wave on 16x16x32 MFMAs: two compute waves per
@@ -742,7 +551,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                     pout = bf16x8{};
                     return;
                 }
-                if (pf) issue_range(un, stn, 0, J1, 0);
+                if (pf) issue_range(un, stn, 0, J1);
                 const int t = t0 + u * KQ + kq;
                 const uint16_t* ks = smem + (kq * NS + st) * SLOT;
                 const uint16_t* vs = ks + TILE;
@@ -789,7 +598,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if (pf) issue_range(un, stn, J1, J2, 0);
+                if (pf) issue_range(un, stn, J1, J2);
                 if constexpr (WDS) {
                     // both halves of every score through LDS; the pair adds
                     // them (IEEE addition commutes: both get the same sums)
@@ -880,7 +689,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
 #pragma unroll
                     for (int db = 0; db < NDW; ++db) o[db] *= alpha;
                 }
-                if (pf) issue_range(un, stn, J2, NLDW, 0);
+                if (pf) issue_range(un, stn, J2, NLDW);
                 // this tile's V^T fragments: rows 16*(db0 + db) + n16, keys 8*g16 ..
                 auto vfrag = [&](int db) __attribute__((always_inline)) {
                     const int d = 16 * (db0 + db) + n16;
@@ -992,7 +801,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                         kqs[i] = S.kseq ? S.kseq[kidx] : 0;
                     }
                 }
-                if (pf) issue_range(un, stn, 0, J1, 0);
+                if (pf) issue_range(un, stn, 0, J1);
                 __builtin_amdgcn_sched_barrier(0);
 
                 // this half of S^T = K Q^T; wave 0 of the pair starts from -m
@@ -1033,7 +842,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                     vf[db][0] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf) ^ sw) << 3));
                     vf[db][1] = *reinterpret_cast<const bf16x8*>(vrow + (((2 * hf + 1) ^ sw) << 3));
                 }
-                if (pf) issue_range(un, stn, J1, J2, 0);
+                if (pf) issue_range(un, stn, J1, J2);
                 __syncthreads();  // both halves of every score are in LDS
                 {
                     const f32x4* theirs = reinterpret_cast<const f32x4*>(xch) + partner * 256;
@@ -1107,7 +916,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                     pw[hh] = __builtin_bit_cast(bf16x8, w4);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if (pf) issue_range(un, stn, J2, NLDW, 0);
+                if (pf) issue_range(un, stn, J2, NLDW);
 #pragma unroll
                 for (int db = 0; db < NDH; ++db) {
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][0], pw[0], o[db], 0, 0, 0);
@@ -1189,15 +998,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             auto step = [&](int u, bf16x8 (&vf)[ND][2], const bf16x8 (&pin)[2], bf16x8 (&pout)[2])
                 __attribute__((always_inline)) {
                 const int st = u % NS;
-                if (dma) {
-                    // a fused-step super-tile may issue no DMA (staged) or extra
-                    // cache stores, so the per-super-tile vmcnt accounting does not
-                    // hold: wait for everything
-                    if constexpr (ACT)
-                        wait_vmcnt<0>();
-                    else
-                        wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
-                }
+                if (dma) wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
                 __syncthreads();  // super-tile u visible to all waves; u-1 (and Q) fully consumed
                 const int un = u + NS - 1, stn = (u + NS - 1) % NS;
                 const bool pf = NP == 0 && un < nsup;
@@ -1223,7 +1024,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                         kqs[i] = S.kseq ? S.kseq[kidx] : 0;
                     }
                 }
-                if (pf) issue_range(un, stn, 0, J1, 0);
+                if (pf) issue_range(un, stn, 0, J1);
                 __builtin_amdgcn_sched_barrier(0);
 
                 // S^T = K Q^T - m: -m enters as the accumulator init, so the scores
@@ -1263,7 +1064,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                     }
                 };
                 if constexpr (!PIPE) read_v();
-                if (pf) issue_range(un, stn, J1, J2, 0);
+                if (pf) issue_range(un, stn, J1, J2);
 
                 // Masking: s[i] is the score of key t*BN + 16*hf + i.
                 bool full = kbase_t + BN <= S.nk;
@@ -1346,7 +1147,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                     for (int db = 0; db < ND; ++db) o[db] *= alpha;
                 }
                 if constexpr (PIPE) read_v();
-                if (pf) issue_range(un, stn, J2, NLDW, 0);
+                if (pf) issue_range(un, stn, J2, NLDW);
                 if constexpr (!PIPE) pv(vf, pout);
             };
 
@@ -1394,48 +1195,6 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                 if (hf == 0) sl[wave * 32 + col] = l_tot * sc;
             }
         }
-    } else if constexpr (ACT) {
-        // A DMA fill is waited for before the next barrier; a staged one is
-        // not (its LDS writes complete before the barrier, and its cache
-        // stores need no wait).  pre: kx / vx hold super-tile un's tile; when
-        // its NLA loads were issued after the DMA, the wait leaves them in
-        // flight (vector memory instructions complete in issue order for
-        // vmcnt; every load of act_load is issued, none is predicated).
-        constexpr int NLA = 2 * KJ + 8 * VJ;
-        static_assert(NLA < 64, "vmcnt range");
-        bool wait_dma = true, pre = false;
-        KRegs kx;
-        VRegs vx;
-        int tnext = NS - 1 < sl_w ? tile_at(NS - 1) : -1;  // tile of slot un
-        for (int u = 0; u < nsup; ++u) {
-            if (wait_dma) {
-                if (pre)
-                    wait_vmcnt<NLA>();
-                else
-                    wait_vmcnt<0>();
-            }
-            __syncthreads();
-            const int un = u + NS - 1;
-            wait_dma = false;
-            if (un < sl_w) {
-                const int tn = tnext;
-                tnext = un + 1 < sl_w ? tile_at(un + 1) : -1;
-                if (tn >= ta) {
-                    if (!pre) act_load(tn, kx, vx);
-                    act_write(tn, un % NS, kx, vx);
-                } else {
-                    issue(un, un % NS, tn);
-                    wait_dma = true;
-                }
-                pre = tnext >= ta;
-                // the next tile's loads go after this tile's conversion (not
-                // interleaved with it: both register sets would be live)
-                __builtin_amdgcn_sched_barrier(0);
-                if (pre) act_load(tnext, kx, vx);
-            }
-        }
-        __syncthreads();  // the two barriers of the compute waves' merge
-        __syncthreads();
     } else {
         for (int u = 0; u < nsup; ++u) {
             wait_tiles<NLDW, NS>(min(NS - 2, nsup - 1 - u));
@@ -1569,12 +1328,12 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     }
 }
 
-template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool ACT, bool W16 = false>
+template <int HD, int RB, int KQ, int NS, int NP, int MODE, bool QEPI, bool W16 = false>
 hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     using G = Geometry<HD, RB, KQ, NS, NP, W16>;
     constexpr size_t lds = G::LDS_BYTES;
     static bool attr_set = false;
-    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QEPI, ACT, W16>;
+    auto fn = attn_fwd_kernel<HD, RB, KQ, NS, NP, MODE, QEPI, W16>;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1585,51 +1344,34 @@ hipError_t launch_fwd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// The 16-row-wave builds (no fused step).
+// The 16-row-wave builds.
 template <int HD, int RB, int KQ, int NS, int NP>
 hipError_t launch_modes16(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    if (p.act) return hipErrorInvalidValue;
     switch (p.mask) {
         case MASK_NONE:
-            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false, true>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, false, true>(p, a, st);
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, true>(p, a, st);
         case MASK_POS:
-            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false, true>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false, true>(p, a, st);
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, true>(p, a, st);
         default:
             if (p.qepi) return hipErrorInvalidValue;
-            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false, true>(p, a, st);
+            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, true>(p, a, st);
     }
 }
 
 template <int HD, int RB, int KQ, int NS, int NP>
 hipError_t launch_modes(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    // Fused-step instances exist for the shapes whose DMA waves each own one
-    // key group (plan_supports_act), in the cached modes.
-    constexpr bool CAN_ACT = NP > 0 && NP == KQ && RB == 1;
-    if (p.act) {
-        if constexpr (CAN_ACT) {
-            // The fused step runs the position-masked kernel also without a
-            // mask: with no window, prefix or sequence ids its full tiles take
-            // the unmasked path, and the register budget of that build holds
-            // a staged tile across the producer loop.
-            if (p.mask == MASK_KEYS) return hipErrorInvalidValue;
-            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, true>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, true>(p, a, st);
-        } else {
-            return hipErrorInvalidValue;
-        }
-    }
     switch (p.mask) {
         case MASK_NONE:
-            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true, false>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false, false>(p, a, st);
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_NONE, false>(p, a, st);
         case MASK_POS:
-            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true, false>(p, a, st)
-                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false, false>(p, a, st);
+            return p.qepi ? launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, true>(p, a, st)
+                           : launch_fwd<HD, RB, KQ, NS, NP, MASK_POS, false>(p, a, st);
         default:
             if (p.qepi) return hipErrorInvalidValue;
-            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false, false>(p, a, st);
+            return launch_fwd<HD, RB, KQ, NS, NP, MASK_KEYS, false>(p, a, st);
     }
 }
 
@@ -1801,11 +1543,6 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     p.n_split = split;
     p.n_workgroups = base * split;
     return p;
-}
-
-bool plan_supports_act(const LaunchPlan& p) {
-    const Shape* sh = find_shape(p.hd_tile, p.rb, p.kq, p.w16);
-    return sh && !sh->w16 && sh->np > 0 && sh->np == sh->kq && sh->rb == 1 && p.mask != MASK_KEYS;
 }
 
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv) {

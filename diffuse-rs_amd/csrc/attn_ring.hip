@@ -601,7 +601,7 @@ int ring_waves(int hd) {
 }
 
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    if (p.act || a.qb || a.rope || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
+    if (a.qb || a.rope || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
     switch (a.hd) {
         case 128: return launch_ring_hd<128>(p, a, st);
         case 256: return launch_ring_hd<256>(p, a, st);

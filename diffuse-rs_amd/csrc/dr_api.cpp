@@ -110,7 +110,6 @@ struct dr_ctx {
     int force_split = 0;
     int force_rb = 0;
     int force_kq = 0;
-    int fused_step = 0;  // dr_attention_step may run the fused kernel
     int force_rows = 0;  // query rows per compute wave (0: automatic)
     int force_kernel = 0;  // dr::KernelKind (0: automatic)
     dr::LaunchPlan last{};
@@ -313,7 +312,6 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
     info->head_dim_tile = ctx->last.hd_tile;
     info->row_blocks = ctx->last.rb;
     info->key_groups = ctx->last.kq;
-    info->fused_step = ctx->last.act ? 1 : 0;
     info->rows_per_wave = ctx->last.w16 ? 16 : 32;
     info->kernel = ctx->last.kernel;
     return DR_OK;
@@ -338,12 +336,6 @@ int dr_ctx_set_kernel(dr_ctx* ctx, int kernel) {
     if (kernel < DR_KERNEL_AUTO || kernel > DR_KERNEL_HILO)
         return fail(DR_ERR_INVALID, "kernel %d not DR_KERNEL_AUTO, _STAGED, _STREAMS or _HILO", kernel);
     ctx->force_kernel = kernel;
-    return DR_OK;
-}
-
-int dr_ctx_set_fused_step(dr_ctx* ctx, int enable) {
-    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_fused_step: ctx is NULL");
-    ctx->fused_step = enable ? 1 : 0;
     return DR_OK;
 }
 
@@ -1196,58 +1188,13 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
             return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
     if (max_nq == 0) return DR_OK;
     DR_CHECK(use_device(cache->ctx));
+    // StepCache::store of each item's active rows, then the attention over
+    // the cache (two launches on the context's stream)
+    for (size_t b = 0; b < n_items; ++b)
+        DR_CHECK(dr_cache_store(cache, layer, b, items[b].pass, items[b].k, items[b].v, k_norm_w, k_norm_eps));
     const int mask = mask_of(sliding_window, causal_prefix);
-    dr_ctx* ctx = cache->ctx;
     const int qepi = q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE;
-    dr::LaunchPlan p = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
-    // The fused kernel is built for one row block of 32-row waves and four
-    // key groups with their DMA waves; when asked for, plan that shape too
-    // (p stays the plan of the unfused store + attention).
-    dr::LaunchPlan pf = p;
-    if (ctx->fused_step && !dr::plan_supports_act(p) && ctx->force_rb == 0 && ctx->force_kq == 0) {
-        const int rows_saved = ctx->force_rows;
-        ctx->force_rb = 1;
-        ctx->force_kq = 4;
-        if (rows_saved == 0) ctx->force_rows = 32;
-        pf = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
-        ctx->force_rb = ctx->force_kq = 0;
-        ctx->force_rows = rows_saved;
-    }
-    // One kernel when every pass is the block [n_total - n, n_total) starting
-    // on a 32-key tile, its K/V rows take 32-bit byte offsets (with the last
-    // tile's padding rows), rows are whole tiles of the head dim, the shape
-    // stages tiles per key group, and no sliding window narrows a
-    // workgroup's key range (each active tile is stored by one workgroup of
-    // its kv head, which must visit it).
-    bool fused = cache->ctx->fused_step && a.hd == cache->hd_tile[layer] && p.kernel != dr::KERNEL_HILO &&
-                 dr::plan_supports_act(pf) && !sliding_window.present;
-    for (size_t b = 0; b < n_items && fused; ++b) {
-        const dr_pass* ps = items[b].pass;
-        fused = ps->n > 0 && ps->max_pos + 1 == cache->n_total && ps->max_pos + 1 - ps->min_pos == ps->n &&
-                ps->min_pos % 32 == 0 && (((uintptr_t)items[b].k | (uintptr_t)items[b].v) & 15) == 0 &&
-                (ps->n + 32) * (size_t)a.n_head_kv * a.hd * sizeof(float) < ((size_t)1 << 31);
-    }
-    if (!fused) {
-        for (size_t b = 0; b < n_items; ++b)
-            DR_CHECK(dr_cache_store(cache, layer, b, items[b].pass, items[b].k, items[b].v,
-                                    k_norm_w, k_norm_eps));
-        return launch_plan(cache->ctx, a, p);
-    }
-    p = pf;
-    p.act = true;
-    a.kv_rstride = a.n_head_kv * a.hd;
-    a.kn_w = k_norm_w;
-    a.kn_eps = k_norm_eps;
-    for (size_t b = 0; b < n_items; ++b) {
-        dr::AttnSlot& s = a.slot[b];
-        s.ka = items[b].k;
-        s.va = items[b].v;
-        s.kst = cache->k[layer * cache->n_batch + b];
-        s.vst = cache->vt[layer * cache->n_batch + b];
-        s.act0 = (int)items[b].pass->min_pos;
-        s.n_act = (int)items[b].pass->n;
-    }
-    return launch_plan(cache->ctx, a, p);
+    return launch_plan(cache->ctx, a, plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi));
 }
 
 int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item* items,

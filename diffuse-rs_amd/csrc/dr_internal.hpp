@@ -39,17 +39,6 @@ struct AttnSlot {
     int nk;
     int qpos_sorted;      // qpos strictly ascending (a dr_pass): key ranges from endpoints
     int qpos0;            // >= 0: qpos[i] == qpos0 + i (contiguous), read without a load
-    // Fused step (LaunchPlan::act): keys at positions [act0, act0 + n_act)
-    // are the step's fresh rows, read as f32 from ka / va ([n_act][kv_rstride],
-    // head g at g*hd) instead of from the cache, and written into the cache
-    // (kst / vst, the same buffers as k / vt) on the way.  act0 is a multiple
-    // of 32 and act0 + n_act == nk.
-    const float* ka;
-    const float* va;
-    uint16_t* kst;
-    uint16_t* vst;
-    int act0;
-    int n_act;
 };
 
 struct AttnArgs {
@@ -76,9 +65,6 @@ struct AttnArgs {
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
     int part_rows;                 // rows per (batch, kv head) in a split plane
-    int kv_rstride;                // fused step: elements between active K/V rows
-    const float* kn_w;             // fused step: K-norm gain for the active rows or nullptr
-    float kn_eps;
     // the Q/K/V epilogue's Q part (forward.rs:291-310): bias before the
     // QK-norm, RoPE after it, at the query rows' positions (qpos)
     const float* qb;               // [n_head*hd] or nullptr
@@ -232,18 +218,17 @@ struct LaunchPlan {
     int n_workgroups;
     int mask;        // MaskMode
     bool qepi;       // Q epilogue compiled in: bias, QK-norm, RoPE, each where its operand is given
-    bool act;        // fused step: active keys read from f32 rows and stored (see AttnSlot)
     bool w16;        // two 16-row compute waves per (row block, key group)
     int kernel;      // KernelKind
 };
 
 // Attention kernel families.  STAGED: attn_fwd_kernel, the workgroup's waves
-// share super-tiles of K/V staged in LDS (every head dim, mask mode, the Q
-// epilogue and the fused step).  STREAMS: attn_ring_kernel, head dim 128,
-// each wave streams its own key tiles (no mask or MASK_POS, Q norm only).
-// HILO: attn_hilo_kernel, f32-accurate scores and values from bf16 hi/lo
-// halves of Q, K and V (layers whose cache holds the lo halves; no mask or
-// MASK_POS, plain Q).
+// share super-tiles of K/V staged in LDS (every head dim, mask mode and the
+// Q epilogue).  STREAMS: attn_ring_kernel, head dims 128 and 256, each wave
+// streams its own key tiles (no mask or MASK_POS, Q norm only).  HILO:
+// attn_hilo_kernel, f32-accurate scores and values from bf16 hi/lo halves of
+// Q, K and V (layers whose cache holds the lo halves, and the drop-in; every
+// mask mode, plain Q).
 enum KernelKind : int {
     KERNEL_AUTO = 0,
     KERNEL_STAGED = 1,
@@ -267,10 +252,6 @@ enum QEpilogue : int {
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, int qepi, int window, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows, int force_kernel);
-
-// Whether a plan's shape can run the fused step (each DMA wave stages one
-// key group's K and V^T tiles).
-bool plan_supports_act(const LaunchPlan& p);
 
 // Bytes of split workspace a plan needs (part_o + part_ml).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);

@@ -93,7 +93,6 @@ class CLaunchInfo(ctypes.Structure):
         ("head_dim_tile", ctypes.c_int),
         ("row_blocks", ctypes.c_int),
         ("key_groups", ctypes.c_int),
-        ("fused_step", ctypes.c_int),
         ("rows_per_wave", ctypes.c_int),
         ("kernel", ctypes.c_int),
     ]
@@ -124,7 +123,6 @@ _SIGS = {
     "dr_ctx_destroy": (None, [_VP]),
     "dr_ctx_last_launch": (_I, [_VP, ctypes.POINTER(CLaunchInfo)]),
     "dr_ctx_set_split": (_I, [_VP, _I]),
-    "dr_ctx_set_fused_step": (_I, [_VP, _I]),
     "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
     "dr_ctx_set_kernel": (_I, [_VP, _I]),
     "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
@@ -330,9 +328,6 @@ class Context:
     def set_kernel(self, kernel: int) -> None:
         """KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS or KERNEL_HILO (dr_ctx_set_kernel)."""
         _check(self.lib.dr_ctx_set_kernel(self.h, kernel))
-
-    def set_fused_step(self, enable: bool) -> None:
-        _check(self.lib.dr_ctx_set_fused_step(self.h, 1 if enable else 0))
 
     def set_tuning(self, row_blocks: int = 0, key_groups: int = 0, n_split: int = 0) -> None:
         _check(self.lib.dr_ctx_set_tuning(self.h, row_blocks, key_groups, n_split))

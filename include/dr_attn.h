@@ -166,7 +166,7 @@ void dr_cache_destroy(dr_step_cache* cache);
  * outputs by ~0.15.  Set it before storing the layer's rows (rows stored
  * earlier have zero lo halves); DR_PRECISION_BF16 frees the planes.  Hi/lo
  * layers run without masks or with position masks (window, causal prefix,
- * query sequence ids), not the fused dr_attention_step kernel. */
+ * query sequence ids). */
 #define DR_PRECISION_BF16 0
 #define DR_PRECISION_HILO 1
 int dr_cache_set_precision(dr_step_cache* cache, size_t layer, int precision);
@@ -281,11 +281,7 @@ typedef struct {
  * k_norm_w when it is non-NULL (K only), stored into the cache at the
  * pass's positions, and the queries attend over every position 0..n_total,
  * the active ones with the rows just given.  This is dr_cache_store per item
- * followed by dr_attention_cached, or, when dr_ctx_set_fused_step enabled it
- * and every pass is one block of consecutive positions that starts at a
- * multiple of 32 and ends at n_total (the canvas of a prompt + canvas
- * sequence), one kernel that does both.  Other arguments as
- * dr_attention_cached.
+ * followed by dr_attention_cached.  Other arguments as dr_attention_cached.
  */
 int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* items,
                       size_t n_items, size_t n_head, dr_opt_usize sliding_window,
@@ -386,7 +382,6 @@ typedef struct {
     int head_dim_tile;
     int row_blocks;
     int key_groups;
-    int fused_step; /* 1 when the launch also stored the step's active rows */
     int rows_per_wave; /* query rows per compute wave: 32, or 16 (two waves per row block) */
     int kernel; /* DR_KERNEL_STAGED, DR_KERNEL_STREAMS or DR_KERNEL_HILO: which attention kernel ran */
 } dr_launch_info;
@@ -399,14 +394,15 @@ int dr_ctx_set_split(dr_ctx* ctx, int n_split);
 int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
 /* Attention kernel families, for dr_ctx_set_kernel and dr_launch_info.kernel.
  * STAGED: the workgroup's waves share K/V super-tiles staged in LDS (every
- * head dim and mask, the Q bias / RoPE epilogue, the fused step).  STREAMS:
- * head dim 128 only; each wave streams its own key tiles into LDS with no
- * workgroup barrier in the key loop (no mask or position masks, Q norm). */
+ * head dim and mask, the Q bias / RoPE epilogue).  STREAMS: head dims 128
+ * and 256; each wave streams its own key tiles into LDS with no workgroup
+ * barrier in the key loop (no mask or position masks, Q norm). */
 #define DR_KERNEL_AUTO 0
 #define DR_KERNEL_STAGED 1
 #define DR_KERNEL_STREAMS 2
-/* HILO: layers kept at DR_PRECISION_HILO (f32-accurate scores from bf16
- * hi/lo halves of Q and K; see dr_cache_set_precision). */
+/* HILO: layers kept at DR_PRECISION_HILO and the drop-in dr_attention
+ * (f32-accurate scores and values from bf16 hi/lo halves of Q, K and V; see
+ * dr_cache_set_precision). */
 #define DR_KERNEL_HILO 3
 /* Pick the kernel family for later calls on ctx: DR_KERNEL_AUTO (the
  * planner: HILO on hi/lo layers, else STREAMS wherever it applies), or force
@@ -414,10 +410,6 @@ int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
  * a hi/lo layer both ignore the lo half).  A tuning knob, for measurement
  * and tests. */
 int dr_ctx_set_kernel(dr_ctx* ctx, int kernel);
-/* Let dr_attention_step run its single fused kernel (1) or always the cache
- * store followed by the attention (0, the default: on the MI355X the fused
- * kernel is the slower of the two at the shapes measured so far). */
-int dr_ctx_set_fused_step(dr_ctx* ctx, int enable);
 /* Override the workgroup shape (32-row query blocks x key groups) and the
  * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
  * to the automatic one. */

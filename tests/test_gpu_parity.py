@@ -380,7 +380,7 @@ def test_c2_sixteen_denoise_steps(dev):
             check(got, want, f"C2 step {step}")
 
 
-# Ragged shapes of the fused step (not BASELINE configs).
+# Ragged shapes of the step (not BASELINE configs).
 STEP_RAGGED = {
     "R1": Config("ragged_gqa_qknorm_96c+77q_b2", 8, 2, 128, 96, 77, batch=2, qk_norm=True),
     "R2": Config("hd64_all_fresh_0c+50q", 4, 4, 64, 0, 50),
@@ -388,7 +388,7 @@ STEP_RAGGED = {
 }
 
 
-def _step_problem(dev, cfg, cfg_id, n_split=0, fused=True):
+def _step_problem(dev, cfg, cfg_id, n_split=0):
     """Prompt K/V stored once, then one denoise-step layer through
     StepCache.step (store of the canvas rows + attention).  Returns outputs,
     inputs, norms, the cache and the launch info."""
@@ -418,7 +418,6 @@ def _step_problem(dev, cfg, cfg_id, n_split=0, fused=True):
         outs.append(out)
         ins.append((Q, K, V))
     dev.ctx.set_split(n_split)
-    dev.ctx.set_fused_step(fused)
     try:
         cache.step(0, items, cfg.n_head, sliding_window=cfg.window, scale=cfg.attn_scale,
                    q_norm_w=dev.put(qn) if qn is not None else None, q_norm_eps=1e-6,
@@ -426,7 +425,6 @@ def _step_problem(dev, cfg, cfg_id, n_split=0, fused=True):
         launch = dev.ctx.last_launch()
     finally:
         dev.ctx.set_split(0)
-        dev.ctx.set_fused_step(False)
     got = [dev.get(o) for o in outs]
     return got, ins, (qn, kn), cache, launch
 
@@ -439,27 +437,21 @@ def _normed_bf16(dev, x, w):
     return t.from_numpy(x).to(t.bfloat16).to(t.float32).numpy()
 
 
-@pytest.mark.parametrize("cid,n_split,fused", [
-    ("C2", 0, True), ("C2", 2, True), ("C3", 0, True), ("C4", 0, True), ("C5S", 0, True),
-    ("C5G", 0, True), ("R1", 0, True), ("R1", 3, True), ("R2", 0, True), ("R3", 0, True),
-    ("C2", 0, False), ("C4", 0, False), ("R1", 0, False)])
-def test_step_vs_oracle_and_cache(dev, cid, n_split, fused):
+@pytest.mark.parametrize("cid,n_split", [
+    ("C2", 0), ("C2", 2), ("C3", 0), ("C4", 0), ("C5S", 0), ("C5G", 0), ("R1", 0), ("R1", 3),
+    ("R2", 0), ("R3", 0)])
+def test_step_vs_oracle_and_cache(dev, cid, n_split):
     """StepCache.step = norm_heads(k) + cache.store(canvas) + attention over
     [prompt | canvas] (forward.rs:296-343): the outputs meet the parity bar
     against the oracle, and afterwards the cache holds bf16 of the (K-normed)
-    canvas rows and still the prompt rows, bit for bit.  With fusion on, C2-C4
-    take the fused kernel (also with a key split: each active tile is stored
-    once); C5 (hd 256, window) and every case with fusion off take the store
-    + attention path.  R1-R3 are ragged
-    fused cases: a partial last tile (rows past the pass staged as zeros and
-    not stored), every key fresh (head dim 64, no prompt), and a first fresh
-    tile right after the pipeline prologue."""
+    canvas rows and still the prompt rows, bit for bit.  R1-R3 are ragged
+    cases: a partial last tile (rows past the pass stored as zeros), every
+    key fresh (head dim 64, no prompt), and a prompt of 128 rows."""
     cfg = CONFIGS.get(cid) or STEP_RAGGED[cid]
     cfg_id = list(CONFIGS).index(cid) if cid in CONFIGS else 100 + list(STEP_RAGGED).index(cid)
-    say(f"step {cid} split {n_split} fused {fused} ({cfg.name})")
-    got, ins, (qn, kn), cache, launch = _step_problem(dev, cfg, cfg_id, n_split, fused)
+    say(f"step {cid} split {n_split} ({cfg.name})")
+    got, ins, (qn, kn), cache, launch = _step_problem(dev, cfg, cfg_id, n_split)
     say(f"  launch {launch}")
-    assert launch["fused_step"] == (1 if fused and cid not in ("C5S", "C5G") else 0)
     if n_split:
         assert launch["n_split"] == n_split
     kvs = cfg.n_head_kv * cfg.head_dim
@@ -485,31 +477,26 @@ def test_step_sixteen_denoise_steps(dev):
     cache.store(0, dr.Pass(dev.ctx, range(cfg.n_prompt)), dev.put(Kp), dev.put(Vp))
     p_can = dr.Pass(dev.ctx, range(cfg.n_prompt, cfg.n_total))
     out = dev.empty(cfg.n_canvas * cfg.n_head * cfg.head_dim)
-    dev.ctx.set_fused_step(True)
-    try:
-        for step in range(16):
-            r = np.random.default_rng(config_seed(1, step + 1))
-            Kc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
-            Vc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
-            Q = r.standard_normal((cfg.n_canvas, cfg.n_head * cfg.head_dim), dtype=np.float32)
-            cache.step(0, [(dev.put(Q), out, p_can, dev.put(Kc), dev.put(Vc))], cfg.n_head,
-                       scale=cfg.attn_scale)
-            assert dev.ctx.last_launch()["fused_step"] == 1
-            if step in (0, 7, 15):
-                want = _oracle_cfg(cfg, Q, np.concatenate([Kp, Kc]), np.concatenate([Vp, Vc]))
-                check(dev.get(out), want, f"C2 fused step {step}")
-    finally:
-        dev.ctx.set_fused_step(False)
+    for step in range(16):
+        r = np.random.default_rng(config_seed(1, step + 1))
+        Kc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
+        Vc = r.standard_normal((cfg.n_canvas, kvs), dtype=np.float32)
+        Q = r.standard_normal((cfg.n_canvas, cfg.n_head * cfg.head_dim), dtype=np.float32)
+        cache.step(0, [(dev.put(Q), out, p_can, dev.put(Kc), dev.put(Vc))], cfg.n_head,
+                   scale=cfg.attn_scale)
+        if step in (0, 7, 15):
+            want = _oracle_cfg(cfg, Q, np.concatenate([Kp, Kc]), np.concatenate([Vp, Vc]))
+            check(dev.get(out), want, f"C2 step {step}")
     ok, ov = dev.empty(cfg.n_total * kvs), dev.empty(cfg.n_total * kvs)
     cache.gather(0, list(range(cfg.n_total)), ok, ov)
     assert np.array_equal(dev.get(ok), _normed_bf16(dev, np.concatenate([Kp, Kc]), None))
     assert np.array_equal(dev.get(ov), _normed_bf16(dev, np.concatenate([Vp, Vc]), None))
 
 
-def test_step_scattered_pass_falls_back(dev):
+def test_step_scattered_pass(dev):
     """A pass that is not one block ending at n_total (the ActiveSplit of a
-    later step) runs as store + attention; the result is the reference's
-    [cached | active] concatenation (forward.rs:312-343)."""
+    later step): the result is the reference's [cached | active]
+    concatenation (forward.rs:312-343)."""
     rng = np.random.default_rng(43)
     n_tot, h, hkv, hd = 300, 8, 4, 128
     kvs = hkv * hd
@@ -524,12 +511,7 @@ def test_step_scattered_pass_falls_back(dev):
     Q = rng.standard_normal((len(active), h * hd), dtype=np.float32)
     pa = dr.Pass(dev.ctx, active)
     out = dev.empty(len(active) * h * hd)
-    dev.ctx.set_fused_step(True)
-    try:
-        cache.step(0, [(dev.put(Q), out, pa, dev.put(Ka), dev.put(Va))], h, scale=0.1)
-    finally:
-        dev.ctx.set_fused_step(False)
-    assert dev.ctx.last_launch()["fused_step"] == 0
+    cache.step(0, [(dev.put(Q), out, pa, dev.put(Ka), dev.put(Va))], h, scale=0.1)
     Kf = np.concatenate([K[cached], Ka]).reshape(-1).copy()
     Vf = np.concatenate([V[cached], Va]).reshape(-1).copy()
     s = Shape(len(active), n_tot, h, hkv, hd, scale=0.1)
