@@ -1422,7 +1422,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 }  // namespace
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, int qepi, int window, int n_cu, int force_rb, int force_kq,
+                          int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows, int force_kernel) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
@@ -1433,8 +1433,9 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     const int cus = n_cu > 0 ? n_cu : 256;
     const int row_blocks = (group * max_nq + 31) / 32;  // per (batch, kv head)
     const int ntiles = (max_nk + BN - 1) / BN;
-    // Head dim exactly 128 or 256 without per-key metadata and without the
-    // Q bias / RoPE: the per-wave key streams of attn_ring_kernel (one 32-row
+    // Head dim exactly 128 or 256 without per-key metadata, with a Q
+    // epilogue of at most the bias, the QK-norm and a full-rotary RoPE: the
+    // per-wave key streams of attn_ring_kernel (one 32-row
     // block per workgroup, 8 or 4 key groups).  A 32-row workgroup pulls
     // every K/V byte of its key range through its CU, so the call is bound by
     // that stream; independent per-wave DMA keeps it nearer the CU's rate
@@ -1449,7 +1450,7 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     // read each K/V tile once for twice the rows and keep them.
     const int ring_blocks = n_batch * n_head_kv * row_blocks;
     const int rw = ring_waves(hd);
-    const bool ring_ok = rw > 0 && mask != MASK_KEYS && qepi != QEPI_FULL;
+    const bool ring_ok = rw > 0 && mask != MASK_KEYS && (qepi != QEPI_FULL || rot == 0 || rot == hd);
     const bool ring_auto = ring_blocks <= cus && (hd == 128 || (window >= 0 && window <= 1024));
     if (ring_ok && (force_kernel == KERNEL_STREAMS || (force_kernel == KERNEL_AUTO && ring_auto)) &&
         force_rb <= 0 && force_kq <= 0 && force_rows <= 0) {
@@ -1459,7 +1460,7 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
         p.w16 = false;
         p.waves = rw;
         p.stages = 1;
-        p.qepi = false;  // the Q norm is a runtime operand of the kernel
+        p.qepi = false;  // the Q bias, norm and RoPE are runtime operands of the kernel
         p.rowgroups = row_blocks < 1 ? 1 : row_blocks;
         const int base = n_batch * n_head_kv * p.rowgroups;
         int split = 1;

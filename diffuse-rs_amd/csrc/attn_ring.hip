@@ -126,7 +126,14 @@ void attn_ring_kernel(const AttnArgs a) {
     const int qd0 = (tid % TPR) * 4;
     const int qr = wg_row0 + qlr;
     const bool qok = qr < rows_total;
-    f32x4 xq[QP], wq[QP];
+    // The Q part of the Q/K/V epilogue (forward.rs:291-310) when the caller
+    // folds it in: the bias (add_bias, ops.rs:373-382) before the QK-norm,
+    // RoPE (rotate_rows, ops.rs:433-452) after it.  Full rotary only (rot ==
+    // HD, checked at launch): dim d < HD/2 and its partner d + HD/2 are then
+    // pieces p and p + QP/2 of the same thread, and the (sin, cos) pairs of
+    // the row's position are those of the thread's first QP/2 pieces.
+    f32x4 xq[QP], wq[QP], bq4[QP];
+    f32x4 tab[QP / 2][2];
     {
         int qhg, qqi;
         split_row(qok ? qr : 0, qhg, qqi);
@@ -137,6 +144,22 @@ void attn_ring_kernel(const AttnArgs a) {
         if (qn_w) {  // the QK-norm gains of these dims
 #pragma unroll
             for (int p = 0; p < QP; ++p) wq[p] = gload<f32x4>(qn_w + qd0 + QSTR * p);
+        }
+        if (a.qb) {
+            const float* bq = a.qb + (size_t)(g * a.group + qhg) * RHD;
+#pragma unroll
+            for (int p = 0; p < QP; ++p) bq4[p] = gload<f32x4>(bq + qd0 + QSTR * p);
+        }
+        if (a.rope) {
+            // the row's position (contiguous passes need no load), then the
+            // table row: pairs j = qd0 + QSTR p, 2 floats each
+            const int pos = S.qpos0 >= 0 ? S.qpos0 + qqi : gload<int>(S.qpos + qqi);
+            const float* trow = a.rope + ((size_t)pos * (RHD / 2) + qd0) * 2;
+#pragma unroll
+            for (int p = 0; p < QP / 2; ++p) {
+                tab[p][0] = gload<f32x4>(trow + 2 * QSTR * p);
+                tab[p][1] = gload<f32x4>(trow + 2 * QSTR * p + 4);
+            }
         }
     }
 
@@ -249,6 +272,10 @@ void attn_ring_kernel(const AttnArgs a) {
     issue_k(t0 + wave);
     issue_v(t0 + wave);
 
+    if (a.qb) {
+#pragma unroll
+        for (int p = 0; p < QP; ++p) xq[p] += bq4[p];
+    }
     // QK-norm (rms_norm_inplace, ops.rs:106-114): f32 squares summed in f64
     // over the TPR lanes of the row, then x * scale * w.
     if (qn_w) {
@@ -269,6 +296,17 @@ void attn_ring_kernel(const AttnArgs a) {
             for (int e = 0; e < 4; ++e) {
 #pragma clang fp contract(off)
                 xq[p][e] = xq[p][e] * sc * wq[p][e];
+            }
+    }
+    if (a.rope) {
+#pragma unroll
+        for (int p = 0; p < QP / 2; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sn = tab[p][e >> 1][2 * (e & 1)], cs = tab[p][e >> 1][2 * (e & 1) + 1];
+                const float lo = xq[p][e], hi = xq[p + QP / 2][e];
+                xq[p][e] = rope_lo(lo, hi, sn, cs);
+                xq[p + QP / 2][e] = rope_hi(lo, hi, sn, cs);
             }
     }
     uint16_t* const qs = smem + RING_BYTES / 2;
@@ -601,7 +639,8 @@ int ring_waves(int hd) {
 }
 
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
-    if (a.qb || a.rope || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
+    // (RoPE on Q only at full rotary: see the Q load)
+    if ((a.rope && a.rot != a.hd) || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
     switch (a.hd) {
         case 128: return launch_ring_hd<128>(p, a, st);
         case 256: return launch_ring_hd<256>(p, a, st);

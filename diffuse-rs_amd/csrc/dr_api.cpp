@@ -987,7 +987,7 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
     const bool hilo_asked = ctx->force_kernel == dr::KERNEL_AUTO || ctx->force_kernel == dr::KERNEL_HILO;
     if (a.slot[0].klo && hilo_asked) return plan_hilo(ctx, a, hd, max_nq, max_nk, mask);
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
-                              mask == dr::MASK_POS ? a.window : -1, ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
+                              mask == dr::MASK_POS ? a.window : -1, a.rope ? a.rot : 0, ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
                               ctx->force_rows, ctx->force_kernel == dr::KERNEL_HILO ? dr::KERNEL_AUTO
                                                                                     : ctx->force_kernel);
 }

@@ -245,12 +245,13 @@ enum QEpilogue : int {
 };
 
 // Chooses tile sizes and the key split for a problem on a device with n_cu
-// compute units (window: the sliding window, < 0 for none).  force_rb /
+// compute units (window: the sliding window, < 0 for none; rot: the rotary
+// dims of a RoPE in the Q epilogue, 0 for none).  force_rb /
 // force_kq / force_split > 0 override the heuristic (tuning); force_rows 16
 // or 32 picks the query rows per compute wave where both are built (0:
 // automatic).
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
-                          int mask, int qepi, int window, int n_cu, int force_rb, int force_kq,
+                          int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows, int force_kernel);
 
 // Bytes of split workspace a plan needs (part_o + part_ml).

@@ -795,6 +795,11 @@ def test_step_epi_vs_oracle(dev, h, hkv, hd, rot, n_p, n_c, batch, norm, v_norm,
     cache.step_epi(0, items, h, sliding_window=window, scale=scale, bq=put(bq), bk=put(bk),
                    bv=put(bv), q_norm_w=put(qn), k_norm_w=put(kn), v_norm=v_norm, eps=eps,
                    rope=rope)
+    # full rotary folds into the per-wave-stream kernel's Q load; partial
+    # rotary (a dim's partner in another lane) runs on the staged kernel
+    launch = dev.ctx.last_launch()
+    say(f"  launch {launch}")
+    assert launch["kernel"] == (dr.KERNEL_STREAMS if rot == hd else dr.KERNEL_STAGED)
     for b in range(batch):
         want, Kf, Vf = wants[b]
         check(dev.get(outs[b]), want, f"batch {b} vs oracle")
