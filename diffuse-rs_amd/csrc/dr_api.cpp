@@ -158,8 +158,8 @@ struct dr_step_cache {
     std::vector<uint16_t*> k, vt;  // [layer * n_batch + batch]
     std::vector<uint16_t*> klo, vlo;  // lo halves of K and V^T (DR_PRECISION_HILO layers), else nullptr
     std::vector<Slot> slot;
-    int32_t* d_meta = nullptr;     // [6] device-side split results
-    int32_t* h_meta = nullptr;     // [6] pinned host copy
+    int32_t* h_meta = nullptr;     // [6] split results, pinned host memory the kernel writes
+    int32_t* h_meta_dev = nullptr; // its device address
 };
 
 namespace {
@@ -471,7 +471,6 @@ void dr_cache_destroy(dr_step_cache* cache) {
         if (s.d_prev) (void)hipFree(s.d_prev);
         if (s.d_lc) (void)hipFree(s.d_lc);
     }
-    if (cache->d_meta) (void)hipFree(cache->d_meta);
     if (cache->h_meta) (void)hipHostFree(cache->h_meta);
     dr_ctx* ctx = cache->ctx;
     delete cache;
@@ -590,6 +589,7 @@ int dr_qkv_epilogue(dr_ctx* ctx, const dr_pass* pass, float* q, float* k, float*
     a.k = k;
     a.v = v;
     a.pos = pass->d_pos;
+    a.pos0 = pass->n > 0 && pass->max_pos - pass->min_pos + 1 == pass->n ? (int)pass->min_pos : -1;
     a.n = (int)pass->n;
     a.n_head = (int)n_head;
     a.n_head_kv = (int)n_head_kv;
@@ -779,8 +779,12 @@ int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t*
     DR_CHECK(state_to_device(cache, s));
     DR_CHECK(reserve_pass(active, std::max(n, (size_t)1)));
     DR_CHECK(reserve_pass(cached, std::max(n, (size_t)1)));
-    if (!cache->d_meta) DR_HIP(hipMalloc(&cache->d_meta, 6 * sizeof(int32_t)));
-    if (!cache->h_meta) DR_HIP(hipHostMalloc(&cache->h_meta, 6 * sizeof(int32_t)));
+    if (!cache->h_meta) {
+        // the six results go straight to pinned host memory (no copy call
+        // between the kernel and the synchronisation the caller waits on)
+        DR_HIP(hipHostMalloc(&cache->h_meta, 6 * sizeof(int32_t)));
+        DR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&cache->h_meta_dev), cache->h_meta, 0));
+    }
     dr::SplitArgs a{};
     a.seq = seq;
     a.is_masked = is_masked;
@@ -788,14 +792,13 @@ int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t*
     a.last_changed = s.d_lc;
     a.active = active->d_pos;
     a.cached = cached->d_pos;
-    a.meta = cache->d_meta;
+    a.meta = cache->h_meta_dev;
     a.n = (int)n;
     a.step = (int)step;
     a.vicinity = (int)s.vicinity;
     hipStream_t st = cache->ctx->stream;
     hipError_t e = dr::launch_split_active(a, st);
     if (e != hipSuccess) return hip_fail(e, "split_active launch");
-    DR_HIP(hipMemcpyAsync(cache->h_meta, cache->d_meta, 6 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
     DR_HIP(hipStreamSynchronize(st));
     const int32_t* m = cache->h_meta;
     active->n = (size_t)m[0];
@@ -1013,6 +1016,7 @@ static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, bool fixed_ws) {
         dr::EpiArgs e{};
         e.q = base;
         e.pos = s.qpos;
+        e.pos0 = s.qpos0;
         e.n = s.nq;
         e.n_head = a.n_head;
         e.n_head_kv = 0;  // Q heads only

@@ -122,6 +122,7 @@ struct EpiArgs {
     float* k;
     float* v;
     const int* pos;       // [n] sequence positions of the rows (device)
+    int pos0;             // >= 0: pos[r] == pos0 + r (contiguous rows), read without a load
     int n, n_head, n_head_kv, hd;
     const float* bq;      // [n_head*hd] or nullptr (add_bias)
     const float* bk;      // [n_head_kv*hd] or nullptr

@@ -83,7 +83,9 @@ __global__ __launch_bounds__(EPI_WAVES * 64) void qkv_epilogue_kernel(const EpiA
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
         sg[i] = seg_of(a, s0 + i);
-        pos[i] = (sg[i].valid && sg[i].kind < 2 && a.rope) ? a.pos[sg[i].r] : 0;
+        // (contiguous rows: the table row follows from the row index, so the
+        // table loads need not wait for a position load)
+        pos[i] = (sg[i].valid && sg[i].kind < 2 && a.rope) ? (a.pos0 >= 0 ? a.pos0 + sg[i].r : a.pos[sg[i].r]) : 0;
         if (sg[i].valid && whole && EPL % 4 == 0) {
 #pragma unroll
             for (int e = 0; e < EPL; e += 4) {
