@@ -137,10 +137,21 @@ void attn_ring_kernel(const AttnArgs a) {
     {
         int qhg, qqi;
         split_row(qok ? qr : 0, qhg, qqi);
-        const float* qrow = static_cast<const float*>(S.q) + (size_t)qqi * a.q_rstride +
-                            (size_t)(g * a.group + qhg) * RHD;
+        const size_t qoff = (size_t)qqi * a.q_rstride + (size_t)(g * a.group + qhg) * RHD + qd0;
+        if (a.q_bf16) {
+            // bf16 rows: 8-byte pieces, widened exactly to f32
+            const uint16_t* qrow = static_cast<const uint16_t*>(S.q) + qoff;
 #pragma unroll
-        for (int p = 0; p < QP; ++p) xq[p] = gload<f32x4>(qrow + qd0 + QSTR * p);
+            for (int p = 0; p < QP; ++p) {
+                const uint2 w = gload<uint2>(qrow + QSTR * p);
+                xq[p] = f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                              __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+            }
+        } else {
+            const float* qrow = static_cast<const float*>(S.q) + qoff;
+#pragma unroll
+            for (int p = 0; p < QP; ++p) xq[p] = gload<f32x4>(qrow + QSTR * p);
+        }
         if (qn_w) {  // the QK-norm gains of these dims
 #pragma unroll
             for (int p = 0; p < QP; ++p) wq[p] = gload<f32x4>(qn_w + qd0 + QSTR * p);

@@ -112,6 +112,7 @@ struct dr_ctx {
     int force_kq = 0;
     int force_rows = 0;  // query rows per compute wave (0: automatic)
     int force_kernel = 0;  // dr::KernelKind (0: automatic)
+    int q_bf16 = 0;        // the cached entry points' Q rows are bf16
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials (grow() only)
@@ -336,6 +337,14 @@ int dr_ctx_set_kernel(dr_ctx* ctx, int kernel) {
     if (kernel < DR_KERNEL_AUTO || kernel > DR_KERNEL_HILO)
         return fail(DR_ERR_INVALID, "kernel %d not DR_KERNEL_AUTO, _STAGED, _STREAMS or _HILO", kernel);
     ctx->force_kernel = kernel;
+    return DR_OK;
+}
+
+int dr_ctx_set_q_dtype(dr_ctx* ctx, int dtype) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_q_dtype: ctx is NULL");
+    if (dtype != DR_DTYPE_F32 && dtype != DR_DTYPE_BF16)
+        return fail(DR_ERR_INVALID, "dtype %d not DR_DTYPE_F32 or DR_DTYPE_BF16", dtype);
+    ctx->q_bf16 = dtype == DR_DTYPE_BF16 ? 1 : 0;
     return DR_OK;
 }
 
@@ -988,11 +997,13 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
     // a layer that keeps K's lo half gets f32-accurate scores, unless another
     // kernel family is forced (then the lo half is not read)
     const bool hilo_asked = ctx->force_kernel == dr::KERNEL_AUTO || ctx->force_kernel == dr::KERNEL_HILO;
-    if (a.slot[0].klo && hilo_asked) return plan_hilo(ctx, a, hd, max_nq, max_nk, mask);
+    if (a.slot[0].klo && hilo_asked && !a.q_bf16) return plan_hilo(ctx, a, hd, max_nq, max_nk, mask);
+    // bf16 Q rows: only the per-wave-stream kernel reads them
+    const int kernel = a.q_bf16 ? dr::KERNEL_STREAMS
+                                : (ctx->force_kernel == dr::KERNEL_HILO ? dr::KERNEL_AUTO : ctx->force_kernel);
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
-                              mask == dr::MASK_POS ? a.window : -1, a.rope ? a.rot : 0, ctx->n_cu, ctx->force_rb, ctx->force_kq, ctx->force_split,
-                              ctx->force_rows, ctx->force_kernel == dr::KERNEL_HILO ? dr::KERNEL_AUTO
-                                                                                    : ctx->force_kernel);
+                              mask == dr::MASK_POS ? a.window : -1, a.rope ? a.rot : 0, ctx->n_cu,
+                              ctx->force_rb, ctx->force_kq, ctx->force_split, ctx->force_rows, kernel);
 }
 
 // The hi/lo kernel reads plain Q: with a Q epilogue (bias, QK-norm, RoPE),
@@ -1042,7 +1053,18 @@ static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, bool fixed_ws) {
 // Launches plan p.  The key-split partials go to the context's workspace,
 // or with fixed_ws to the library's fixed device scratch (no allocation: a
 // plan that needs more than it holds is an error).
+// bf16 Q rows are read by the per-wave-stream kernel only.
+static int check_q_dtype(const dr::AttnArgs& a, const dr::LaunchPlan& p, const char* who) {
+    if (!a.q_bf16 || p.kernel == dr::KERNEL_STREAMS) return DR_OK;
+    return fail(DR_ERR_UNSUPPORTED,
+                "%s: bf16 Q rows (dr_ctx_set_q_dtype) are read by the per-wave-stream kernel only: head dim "
+                "128 or 256, no per-key masks, a Q epilogue of at most bias, QK-norm and full-rotary RoPE, "
+                "no forced tile shape and no hi/lo layer",
+                who);
+}
+
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws = false) {
+    DR_CHECK(check_q_dtype(a, p, "attention"));
     if (p.kernel == dr::KERNEL_HILO) DR_CHECK(hilo_prepare_q(ctx, a, fixed_ws));
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
@@ -1107,8 +1129,14 @@ static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* 
     a.prefix = opt_to_int(causal_prefix);
     a.qn_w = q_norm_w;
     a.qn_eps = q_norm_eps;
+    a.q_bf16 = ctx->q_bf16;
     max_nq = 0;
     const int tile = cache->hd_tile[layer];
+    if (a.q_bf16 && ((hd != 128 && hd != 256) || cache->klo[layer * cache->n_batch]))
+        return fail(DR_ERR_UNSUPPORTED,
+                    "%s: bf16 Q rows (dr_ctx_set_q_dtype) need head dim 128 or 256 and a bf16 layer (head "
+                    "dim %zu%s)",
+                    who, hd, cache->klo[layer * cache->n_batch] ? ", hi/lo layer" : "");
     for (size_t b = 0; b < n_items; ++b) {
         const dr_batch_item& it = items[b];
         if (!it.pass) return fail(DR_ERR_INVALID, "item %zu: pass is NULL", b);
@@ -1192,13 +1220,15 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
             return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
     if (max_nq == 0) return DR_OK;
     DR_CHECK(use_device(cache->ctx));
+    const int mask = mask_of(sliding_window, causal_prefix);
+    const int qepi = q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE;
+    const dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
+    DR_CHECK(check_q_dtype(a, p, "dr_attention_step"));  // (before any store)
     // StepCache::store of each item's active rows, then the attention over
     // the cache (two launches on the context's stream)
     for (size_t b = 0; b < n_items; ++b)
         DR_CHECK(dr_cache_store(cache, layer, b, items[b].pass, items[b].k, items[b].v, k_norm_w, k_norm_eps));
-    const int mask = mask_of(sliding_window, causal_prefix);
-    const int qepi = q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE;
-    return launch_plan(cache->ctx, a, plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi));
+    return launch_plan(cache->ctx, a, p);
 }
 
 int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item* items,
@@ -1228,19 +1258,20 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
     int max_nq = 0;
     DR_CHECK(cached_args(cache, layer, bi, n_items, n_head, sliding_window, causal_prefix, scale,
                          epi->q_norm_w, epi->eps, "dr_attention_step_epi", a, max_nq));
-    for (size_t b = 0; b < n_items; ++b) {
+    for (size_t b = 0; b < n_items; ++b)
         if (items[b].pass->n > 0 && (!items[b].k || !items[b].v))
             return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
-        DR_CHECK(store_rows(cache, layer, b, items[b].pass, items[b].k, items[b].v, epi->k_norm_w,
-                            epi->eps, epi->bk, epi->bv, epi->v_norm, rope));
-    }
-    if (max_nq == 0) return DR_OK;
     a.qb = epi->bq;
     a.rope = rope ? rope->d_table : nullptr;
     a.rot = rope ? (int)rope->rope_dim : 0;
     const int mask = mask_of(sliding_window, causal_prefix);
     const int qepi = (epi->bq || rope) ? dr::QEPI_FULL : (epi->q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
-    dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
+    const dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
+    if (max_nq > 0) DR_CHECK(check_q_dtype(a, p, "dr_attention_step_epi"));  // (before any store)
+    for (size_t b = 0; b < n_items; ++b)
+        DR_CHECK(store_rows(cache, layer, b, items[b].pass, items[b].k, items[b].v, epi->k_norm_w,
+                            epi->eps, epi->bk, epi->bv, epi->v_norm, rope));
+    if (max_nq == 0) return DR_OK;
     return launch_plan(cache->ctx, a, p);
 }
 

@@ -24,7 +24,7 @@ constexpr int VT_KEYS = 32;
 // Key index j has sequence position kpos[j] (kpos == nullptr: position j)
 // and sequence id kseq[j] (nullptr: 0).
 struct AttnSlot {
-    const void* q;        // [nq][q_rstride] f32, head h at h*hd
+    const void* q;        // [nq][q_rstride] f32 (bf16 with AttnArgs::q_bf16), head h at h*hd
     float* out;           // [nq][o_rstride] f32
     const int* qpos;      // [nq] sequence positions of the queries (device)
     const int* qseq;      // [nq] or nullptr
@@ -65,6 +65,7 @@ struct AttnArgs {
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
     int part_rows;                 // rows per (batch, kv head) in a split plane
+    int q_bf16;                    // Q rows are bf16 (the per-wave-stream kernel reads them)
     // the Q/K/V epilogue's Q part (forward.rs:291-310): bias before the
     // QK-norm, RoPE after it, at the query rows' positions (qpos)
     const float* qb;               // [n_head*hd] or nullptr

@@ -28,6 +28,7 @@ HEADER_PATH = HERE.parent / "include" / "dr_attn.h"
 
 DR_OK, DR_ERR_INVALID, DR_ERR_NO_DEVICE, DR_ERR_OOM, DR_ERR_HIP, DR_ERR_UNSUPPORTED = range(6)
 KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS, KERNEL_HILO = range(4)
+DTYPE_F32, DTYPE_BF16 = 0, 1
 PRECISION_BF16, PRECISION_HILO = 0, 1  # dr_cache_set_precision
 STATUS_NAMES = {
     DR_OK: "DR_OK",
@@ -125,6 +126,7 @@ _SIGS = {
     "dr_ctx_set_split": (_I, [_VP, _I]),
     "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
     "dr_ctx_set_kernel": (_I, [_VP, _I]),
+    "dr_ctx_set_q_dtype": (_I, [_VP, _I]),
     "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
                             ctypes.POINTER(ctypes.c_void_p)]),
     "dr_rope_destroy": (None, [_VP]),
@@ -328,6 +330,11 @@ class Context:
     def set_kernel(self, kernel: int) -> None:
         """KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS or KERNEL_HILO (dr_ctx_set_kernel)."""
         _check(self.lib.dr_ctx_set_kernel(self.h, kernel))
+
+    def set_q_dtype(self, dtype: int) -> None:
+        """DTYPE_F32 or DTYPE_BF16: the element type of the Q rows of later
+        cached attention calls (dr_ctx_set_q_dtype)."""
+        _check(self.lib.dr_ctx_set_q_dtype(self.h, dtype))
 
     def set_tuning(self, row_blocks: int = 0, key_groups: int = 0, n_split: int = 0) -> None:
         _check(self.lib.dr_ctx_set_tuning(self.h, row_blocks, key_groups, n_split))

@@ -410,6 +410,19 @@ int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
  * a hi/lo layer both ignore the lo half).  A tuning knob, for measurement
  * and tests. */
 int dr_ctx_set_kernel(dr_ctx* ctx, int kernel);
+/* The element type of the Q rows that later dr_attention_cached /
+ * _cached_noalloc / _step / _step_epi calls on ctx read (no counterpart in
+ * the reference, whose attention() takes f32; for callers whose projections
+ * produce bf16).  DR_DTYPE_F32 (the default): q points at float rows.
+ * DR_DTYPE_BF16: q points at bf16 rows of the same shape (uint16 bit
+ * patterns), read by the per-wave-stream kernel, which applies the Q
+ * epilogue and the scale to them as to f32 rows.  Calls that that kernel
+ * cannot run (head dims other than 128 / 256, hi/lo layers, RoPE below full
+ * rotary, forced tile shapes) fail with DR_ERR_UNSUPPORTED before any
+ * store. */
+#define DR_DTYPE_F32 0
+#define DR_DTYPE_BF16 1
+int dr_ctx_set_q_dtype(dr_ctx* ctx, int dtype);
 /* Override the workgroup shape (32-row query blocks x key groups) and the
  * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
  * to the automatic one. */
