@@ -525,6 +525,36 @@ def main() -> int:
         n_sets, reps)
     log(f"attention call: {attn_mean_ms * 1e3:.2f} us over 32 layers, {warm_mean_ms * 1e3:.2f} us on one layer")
 
+    # ---- the same attention call with Q rows in bf16 (dr_ctx_set_q_dtype):
+    # the kernel-only figure for a caller whose projections emit bf16
+    # (Q 2 bytes per element instead of 4; cache on the device either way).
+    bf16_q = None
+    if launch.get("kernel") == dr.KERNEL_STREAMS:
+        with torch.cuda.stream(stream):
+            qb = [st[2].to(torch.bfloat16) for st in dsets]
+        stream.synchronize()
+        ctx.set_q_dtype(dr.DTYPE_BF16)
+        try:
+            b_mean_ms, _ = attention_only_ms(
+                torch, stream,
+                lambda i: cache.attention(i % N_LAYERS, [(qb[i % n_sets], out, p_canvas)], h, scale=scale),
+                N_LAYERS, reps)
+            b_warm_ms, _ = attention_only_ms(
+                torch, stream, lambda i: cache.attention(0, [(qb[i], out, p_canvas)], h, scale=scale),
+                n_sets, reps)
+            b_launch = ctx.last_launch()
+        finally:
+            ctx.set_q_dtype(dr.DTYPE_F32)
+        bf16_q = {"launch_us_mean": round(b_mean_ms * 1e3, 3),
+                  "tflops": round(flops / (b_mean_ms / 1e3) / 1e12, 2),
+                  "launch_us_one_layer_warm": round(b_warm_ms * 1e3, 3),
+                  "tflops_one_layer_warm": round(flops / (b_warm_ms / 1e3) / 1e12, 2),
+                  "kernel": b_launch.get("kernel"),
+                  "timing": "as the roofline's launch timing, Q rows bf16 (values of the f32 sets "
+                            "rounded to bf16), out f32"}
+        del qb
+        log(f"attention call, bf16 Q: {bf16_q}")
+
     # ---- timed region: K whole steps, every one a graph replay (a graph of
     # 32 steps, one per layer, and a graph of the remainder)
     graphs = {}
@@ -676,6 +706,7 @@ def main() -> int:
         "attention_call_pct_of_peak": round(100 * achieved / PEAK_BF16_TFLOPS, 3),
         "gpu_event_ms": round(gpu_ms, 4), "wall_s": round(wall, 4),
         "launch": launch, "parity": parity, "roofline": roofline, "cpu_baseline": cpu,
+        "attention_bf16_q": bf16_q,
         "other_configs_attention_only": others,
         "dropin_dr_attention": dropin,
         "qkv_epilogue": epi,

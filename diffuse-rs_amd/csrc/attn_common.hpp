@@ -187,5 +187,57 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
     return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
 }
 
+// Folds SG key-split softmax states (m_j, l_j, o_j: row max in log2 units,
+// weight sum, C 4-float chunks of the unnormalised row) into the running
+// state (Mx, Ls, acc) as softmax states merge: weights exp2(m_j - max), a
+// state with m_j = -inf weighs 0.  Every kernel that merges splits calls this,
+// with the operations spelled out (no contraction), so they agree bit for bit.
+template <int SG, int C>
+__device__ __forceinline__ void merge_split_states(float& Mx, float& Ls, f32x4 (&acc)[C],
+                                                   const float (&m)[SG], const float (&l)[SG],
+                                                   const f32x4 (&o)[SG][C]) {
+#pragma clang fp contract(off)
+    float nm = Mx;
+#pragma unroll
+    for (int j = 0; j < SG; ++j) nm = __builtin_fmaxf(nm, m[j]);
+    if (nm == -INFINITY) return;  // no visible key in these splits
+    const float f = Mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mx - nm);
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = acc[c] * f;
+    Ls = Ls * f;
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+        const float w = m[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[j] - nm);
+        Ls = __builtin_fmaf(w, l[j], Ls);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[c][e] = __builtin_fmaf(w, o[j][c][e], acc[c][e]);
+    }
+    Mx = nm;
+}
+
+// Agent-scope (sc1) accesses: coherent across the XCDs' separate L2s without
+// a cache-wide writeback or invalidate.  The key-split partials that a
+// workgroup merges in-kernel (the last split of a row block to finish, by an
+// atomic ticket) are written and read only through these; the 16-byte forms
+// are buffer instructions with the sc1 cache-policy bit.
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t r, int voff, const f32x4& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, 0, CPOL_SC1);
+}
+__device__ __forceinline__ f32x4 load_sc1(__amdgpu_buffer_rsrc_t r, int voff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, CPOL_SC1));
+}
+__device__ __forceinline__ void store2_sc1(__amdgpu_buffer_rsrc_t r, int voff, float x, float y) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) uint32_t,
+                                                             (float __attribute__((ext_vector_type(2)))){x, y}),
+                                          r, voff, 0, CPOL_SC1);
+}
+__device__ __forceinline__ float2 load2_sc1(__amdgpu_buffer_rsrc_t r, int voff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, CPOL_SC1);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
 }  // namespace
 }  // namespace dr

@@ -1286,38 +1286,25 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     const AttnSlot& S = a.slot[b];
     if (r >= a.group * S.nq) return;
     float Mx = -INFINITY, Ls = 0.0f;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
     for (int s0 = 0; s0 < a.n_split; s0 += SG) {
         float m[SG], l[SG];
-        f32x4 o[SG];
+        f32x4 o[SG][1];
 #pragma unroll
         for (int j = 0; j < SG; ++j) {
             const int sp = min(s0 + j, a.n_split - 1);
             const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + ((size_t)sp * plane + prow) * 2);
-            o[j] = *reinterpret_cast<const f32x4*>(a.part_o + ((size_t)sp * plane + prow) * HD + ch * 4);
+            o[j][0] = *reinterpret_cast<const f32x4*>(a.part_o + ((size_t)sp * plane + prow) * HD + ch * 4);
             const bool in = s0 + j < a.n_split;
             m[j] = in ? ml.x : -INFINITY;
             l[j] = ml.y;
         }
-        float nm = Mx;
-#pragma unroll
-        for (int j = 0; j < SG; ++j) nm = __builtin_fmaxf(nm, m[j]);
-        if (nm == -INFINITY) continue;  // no visible key in these splits
-        const float f = Mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mx - nm);
-        acc *= f;
-        Ls *= f;
-#pragma unroll
-        for (int j = 0; j < SG; ++j) {
-            const float w = m[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[j] - nm);
-            Ls += w * l[j];
-            acc += w * o[j];
-        }
-        Mx = nm;
+        merge_split_states<SG, 1>(Mx, Ls, acc, m, l, o);
     }
     int hg, qi;
     row_split(r, S.nq, __builtin_amdgcn_rcpf((float)S.nq), a.group, hg, qi);
     float* orow = S.out + (size_t)qi * a.o_rstride + (size_t)(g * a.group + hg) * a.hd;
-    const f32x4 val = acc * __builtin_amdgcn_rcpf(Ls);
+    const f32x4 val = acc[0] * __builtin_amdgcn_rcpf(Ls);
     const int c0 = ch * 4;
     if (a.hd == HD) {
         *reinterpret_cast<f32x4*>(orow + c0) = val;
@@ -1423,7 +1410,7 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
-                          int force_split, int force_rows, int force_kernel) {
+                          int force_split, int force_rows, int force_kernel, bool merge_in_kernel) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
     p.block_n = BN;
@@ -1466,12 +1453,14 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
         int split = 1;
         if (force_split > 0) {
             split = force_split;
+        } else if (hd == 256 && merge_in_kernel && 2 * base <= cus && ntiles >= 2 * rw) {
+            // A half-filled chip at head dim 256: two key splits merged
+            // in-kernel (DiffusionGemma's sliding layers: 18.1 against 21.8 us
+            // unsplit; with the separate merge kernel the split lost, 22.9).
+            split = 2;
         } else if ((hd == 128 ? 2 : 4) * base <= cus) {
             // too few workgroups for the CUs: split the keys, keeping a tile
-            // for each of a split's waves.  (At head dim 256 a half-filled
-            // chip is not reason enough: the merge and the second round of
-            // partial traffic cost more than the idle CUs, 23.3 against
-            // 21.6 us on DiffusionGemma's sliding layers.)
+            // for each of a split's waves
             split = cus / base;
             const int max_split = ntiles / rw > 1 ? ntiles / rw : 1;
             if (split > max_split) split = max_split;
@@ -1570,10 +1559,11 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.mg_rowgroups = div_magic(a.rowgroups, p.n_workgroups);
     a.mg_hkv = div_magic(a.n_head_kv, p.n_workgroups);
     a.part_rows = p.rowgroups * p.rb * 32;
+    if (p.kernel != KERNEL_STREAMS) a.ticket = nullptr;  // (the others always merge in a second kernel)
     hipError_t e = p.kernel == KERNEL_STREAMS ? launch_ring(p, a, st)
                    : p.kernel == KERNEL_HILO  ? launch_hilo(p, a, st)
                                               : launch_shape(p, a, st);
-    if (e != hipSuccess || p.n_split <= 1) return e;
+    if (e != hipSuccess || p.n_split <= 1 || a.ticket) return e;
     const size_t items = (size_t)a.n_batch * a.n_head_kv * a.part_rows * (p.hd_tile / 4);
     const dim3 grid((unsigned)((items + 255) / 256));
     switch (p.hd_tile) {

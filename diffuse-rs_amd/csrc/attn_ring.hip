@@ -57,6 +57,7 @@ struct Ring {
     static constexpr int Q_BYTES = 32 * HD * 2;          // the block's Q rows, bf16
     static constexpr int ML_OFF = RING_BYTES + Q_BYTES;  // [RW][32] max, then [RW][32] sum
     static constexpr int LDS = ML_OFF + 2 * RW * 32 * 4;
+    static constexpr int MS = HD == 128 ? 4 : 2;  // most key splits merged in-kernel (registers)
     static_assert(32 * HD * 4 == 2 * RT * 2, "a wave's O^T partial fills its K + V^T buffers");
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(NDMA < 32, "two tiles of DMA fit the vmcnt counter");
@@ -574,50 +575,109 @@ void attn_ring_kernel(const AttnArgs a) {
     }
     lds_barrier();
     // thread tid: row rr = tid / TPR, chunks ch + TPR k, k < CPT
-    {
-        constexpr int CPT = HD / 4 / TPR;
-        const int rr = tid / TPR, ch = tid % TPR;
-        const int row = wg_row0 + rr;
-        if (row < rows_total) {
-            float mw[RW];
-            float M = -INFINITY;
+    constexpr int CPT = HD / 4 / TPR;
+    const int rr = tid / TPR, ch = tid % TPR;
+    const int row = wg_row0 + rr;
+    const bool row_ok = row < rows_total;
+    f32x4 acc[CPT];
+    float M = -INFINITY, L = 0.0f;
+    if (row_ok) {
+        float mw[RW];
 #pragma unroll
-            for (int w = 0; w < RW; ++w) {
-                mw[w] = sm[w * 32 + rr];
-                M = __builtin_fmaxf(M, mw[w]);
-            }
-            f32x4 acc[CPT];
+        for (int w = 0; w < RW; ++w) {
+            mw[w] = sm[w * 32 + rr];
+            M = __builtin_fmaxf(M, mw[w]);
+        }
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            float L = 0.0f;
+        for (int k = 0; k < CPT; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int w = 0; w < RW; ++w) {
-                const float wt = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
-                const float* prow = reinterpret_cast<const float*>(smem + w * 2 * RT) + rr * RHD;
+        for (int w = 0; w < RW; ++w) {
+            const float wt = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+            const float* prow = reinterpret_cast<const float*>(smem + w * 2 * RT) + rr * RHD;
 #pragma unroll
-                for (int k = 0; k < CPT; ++k)
-                    acc[k] += wt * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + TPR * k) ^ rr));
-                L += wt * sl[w * 32 + rr];
-            }
-            if (a.n_split > 1) {
-                // this split's partial row, for split_merge_kernel: the sum
-                // relative to the row max M, and (M, L)
-                const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
-                const size_t prow =
-                    (size_t)split * plane + (size_t)(b * a.n_head_kv + g) * a.part_rows + row;
-#pragma unroll
-                for (int k = 0; k < CPT; ++k) gstore(a.part_o + prow * RHD + 4 * (ch + TPR * k), acc[k]);
-                if (ch == 0) gstore(a.part_ml + prow * 2, make_float2(M, L));
-            } else {
-                int ohg, oqi;
-                split_row(row, ohg, oqi);
-                float* orow = S.out + (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
-                const float il = __builtin_amdgcn_rcpf(L);
-#pragma unroll
-                for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), acc[k] * il);
-            }
+            for (int k = 0; k < CPT; ++k)
+                acc[k] += wt * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + TPR * k) ^ rr));
+            L += wt * sl[w * 32 + rr];
         }
     }
+    auto store_rows = [&](const f32x4 (&val)[CPT], float l) __attribute__((always_inline)) {
+        int ohg, oqi;
+        split_row(row, ohg, oqi);
+        float* orow = S.out + (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
+        const float il = __builtin_amdgcn_rcpf(l);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), val[k] * il);
+    };
+    if (a.n_split == 1) {
+        if (row_ok) store_rows(acc, L);
+        return;
+    }
+    // This split's partial row: the sum relative to the row max M, and (M, L).
+    const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
+    const size_t prow0 = (size_t)(b * a.n_head_kv + g) * a.part_rows + row;  // in split plane 0
+    if (!a.ticket) {
+        // for split_merge_kernel, launched next
+        if (row_ok) {
+            const size_t prow = (size_t)split * plane + prow0;
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) gstore(a.part_o + prow * RHD + 4 * (ch + TPR * k), acc[k]);
+            if (ch == 0) gstore(a.part_ml + prow * 2, make_float2(M, L));
+        }
+        return;
+    }
+    // In-kernel merge.  Each split stores its partial with agent-scope
+    // stores and waits until they are complete; one thread then takes the
+    // row block's ticket.  The split that draws n_split - 1 arrives last: the
+    // others' stores are complete, and its agent-scope loads see them.  It
+    // merges the splits in split order (the same bits whichever split
+    // arrives last, and those of split_merge_kernel) and resets the ticket
+    // for the next call.  No workgroup waits for another.
+    // (Byte offsets of a row plane fit 32 bits: the host checks the size.)
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o, 0xffffffffu);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.part_ml, 0xffffffffu);
+    if (row_ok) {
+        const int po = (int)(((size_t)split * plane + prow0) * RHD * 4);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) store_sc1(ro, po + 16 * (ch + TPR * k), acc[k]);
+        if (ch == 0) store2_sc1(rm, (int)(((size_t)split * plane + prow0) * 8), M, L);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int* const tk = a.ticket + (b * a.n_head_kv + g) * a.rowgroups + rg;
+    if (tid == 0) s_red[0] = __hip_atomic_fetch_add(tk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_red[0] != a.n_split - 1) return;
+    if (tid == 0) __hip_atomic_store(tk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!row_ok) return;
+    // one group of G::MS states (n_split <= MS, checked on the host), the
+    // own one from registers; past n_split, weight 0
+    constexpr int MS = G::MS;
+    float Mx = -INFINITY, Ls = 0.0f;
+    f32x4 macc[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) macc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[MS], l[MS];
+    f32x4 so[MS][CPT];
+#pragma unroll
+    for (int j = 0; j < MS; ++j) {
+        const int sp = min(j, a.n_split - 1);
+        if (sp == split) {
+            m[j] = M;
+            l[j] = L;
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) so[j][k] = acc[k];
+        } else {
+            const float2 ml = load2_sc1(rm, (int)(((size_t)sp * plane + prow0) * 8));
+            m[j] = ml.x;
+            l[j] = ml.y;
+            const int po = (int)(((size_t)sp * plane + prow0) * RHD * 4);
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) so[j][k] = load_sc1(ro, po + 16 * (ch + TPR * k));
+        }
+        if (j >= a.n_split) m[j] = -INFINITY;
+    }
+    merge_split_states<MS, CPT>(Mx, Ls, macc, m, l, so);
+    store_rows(macc, Ls);
 }
 
 template <int HD, int MODE>
@@ -649,9 +709,14 @@ int ring_waves(int hd) {
     return hd == 128 ? Ring<128>::RW : (hd == 256 ? Ring<256>::RW : 0);
 }
 
+int ring_merge_splits(int hd) {
+    return hd == 128 ? Ring<128>::MS : (hd == 256 ? Ring<256>::MS : 0);
+}
+
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     // (RoPE on Q only at full rotary: see the Q load)
     if ((a.rope && a.rot != a.hd) || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
+    if (a.ticket && a.n_split > ring_merge_splits(a.hd)) return hipErrorInvalidValue;
     switch (a.hd) {
         case 128: return launch_ring_hd<128>(p, a, st);
         case 256: return launch_ring_hd<256>(p, a, st);

@@ -54,6 +54,9 @@ int hip_fail(hipError_t e, const char* what) {
 // Largest sequence position / window the kernels accept (int32 arithmetic
 // on |qpos - kpos|).  The reference caps sequences at 32768 (model.rs:403-407).
 constexpr size_t MAX_POS = (size_t)1 << 30;
+// Row blocks (batch x kv head x 32-row group) whose key splits one call can
+// merge in-kernel: the size of each context's ticket buffer.
+constexpr size_t TICKETS = (size_t)1 << 16;
 
 struct DevBuf {
     void* p = nullptr;
@@ -113,6 +116,7 @@ struct dr_ctx {
     int force_rows = 0;  // query rows per compute wave (0: automatic)
     int force_kernel = 0;  // dr::KernelKind (0: automatic)
     int q_bf16 = 0;        // the cached entry points' Q rows are bf16
+    int merge_in_kernel = 1;  // key splits of the per-wave-stream kernel merge in-kernel
     dr::LaunchPlan last{};
     bool has_last = false;
     DevBuf part;                         // key-split partials (grow() only)
@@ -120,6 +124,7 @@ struct dr_ctx {
     DevBuf kclo, vtclo;                  // dr_attention(): lo halves of K and V^T
     DevBuf q8k;                          // dr_qmatmul's Q8_K activations (grow() only)
     DevBuf qpre;                         // hi/lo attention: Q after its epilogue (grow() only)
+    DevBuf tick;                         // in-kernel split merge: per-row-block tickets, zero at rest
     std::vector<void*> retired;          // workspaces replaced by larger ones
     // dr_ctx_destroy's reference plus one per pass, cache and RoPE table made
     // on the context: it is freed when the last of them is destroyed, so the
@@ -259,6 +264,20 @@ int dr_ctx_create(int device, dr_ctx** out) {
         delete c;
         return hip_fail(e, "hipDeviceGetAttribute");
     }
+    // the in-kernel split merge's tickets: allocated and zeroed here, once,
+    // so that no call allocates or clears them (each merge resets its own)
+    e = hipMalloc(&c->tick.p, TICKETS * sizeof(int));
+    if (e == hipSuccess) {
+        c->tick.cap = TICKETS * sizeof(int);
+        e = hipMemsetAsync(c->tick.p, 0, TICKETS * sizeof(int), c->own);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->own);
+    }
+    if (e != hipSuccess) {
+        release(c->tick);
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return hip_fail(e, "ticket buffer");
+    }
     *out = c;
     return DR_OK;
 }
@@ -284,7 +303,7 @@ void ctx_free(dr_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (DevBuf* b : {&ctx->part, &ctx->q, &ctx->k, &ctx->v, &ctx->kc, &ctx->vtc, &ctx->kclo, &ctx->vtclo,
-                      &ctx->meta, &ctx->out, &ctx->q8k, &ctx->qpre})
+                      &ctx->meta, &ctx->out, &ctx->q8k, &ctx->qpre, &ctx->tick})
         release(*b);
     for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
@@ -315,6 +334,7 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info) {
     info->key_groups = ctx->last.kq;
     info->rows_per_wave = ctx->last.w16 ? 16 : 32;
     info->kernel = ctx->last.kernel;
+    info->split_merge = ctx->last.merge;
     return DR_OK;
 }
 
@@ -345,6 +365,13 @@ int dr_ctx_set_q_dtype(dr_ctx* ctx, int dtype) {
     if (dtype != DR_DTYPE_F32 && dtype != DR_DTYPE_BF16)
         return fail(DR_ERR_INVALID, "dtype %d not DR_DTYPE_F32 or DR_DTYPE_BF16", dtype);
     ctx->q_bf16 = dtype == DR_DTYPE_BF16 ? 1 : 0;
+    return DR_OK;
+}
+
+int dr_ctx_set_split_merge(dr_ctx* ctx, int in_kernel) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_split_merge: ctx is NULL");
+    if (in_kernel != 0 && in_kernel != 1) return fail(DR_ERR_INVALID, "in_kernel %d not 0 or 1", in_kernel);
+    ctx->merge_in_kernel = in_kernel;
     return DR_OK;
 }
 
@@ -1003,7 +1030,8 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
                                 : (ctx->force_kernel == dr::KERNEL_HILO ? dr::KERNEL_AUTO : ctx->force_kernel);
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
                               mask == dr::MASK_POS ? a.window : -1, a.rope ? a.rot : 0, ctx->n_cu,
-                              ctx->force_rb, ctx->force_kq, ctx->force_split, ctx->force_rows, kernel);
+                              ctx->force_rb, ctx->force_kq, ctx->force_split, ctx->force_rows, kernel,
+                              ctx->merge_in_kernel != 0);
 }
 
 // The hi/lo kernel reads plain Q: with a Q epilogue (bias, QK-norm, RoPE),
@@ -1081,9 +1109,20 @@ static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bo
             a.part_o = static_cast<float*>(ctx->part.p);
         }
     }
+    // Key splits of the per-wave-stream kernel merge in-kernel when they are
+    // few enough for its registers, the context's tickets cover the row
+    // blocks and the partials' byte offsets fit the kernel's 32-bit buffer
+    // offsets; otherwise split_merge_kernel runs.
+    a.ticket = nullptr;
+    if (ctx->merge_in_kernel && p.kernel == dr::KERNEL_STREAMS && p.n_split > 1 &&
+        p.n_split <= dr::ring_merge_splits(p.hd_tile)) {
+        const size_t blocks = (size_t)a.n_batch * a.n_head_kv * p.rowgroups;
+        if (blocks <= TICKETS && ws < ((size_t)1 << 31)) a.ticket = static_cast<int*>(ctx->tick.p);
+    }
     hipError_t e = dr::launch_attention(p, a, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "attention launch");
     ctx->last = p;
+    ctx->last.merge = p.n_split <= 1 ? 0 : (a.ticket ? 2 : 1);
     ctx->has_last = true;
     return DR_OK;
 }

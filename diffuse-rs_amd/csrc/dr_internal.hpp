@@ -65,6 +65,11 @@ struct AttnArgs {
     float* part_o;                 // [split][batch*kv head][row][HD] partial accumulators
     float* part_ml;                // [split][batch*kv head][row][2] partial (max, sum)
     int part_rows;                 // rows per (batch, kv head) in a split plane
+    // Per-row-block arrival counters [batch*kv head][rowgroups], zero between
+    // calls, or nullptr.  Set: the last split of each row block to finish
+    // merges the partials in-kernel (agent-scope accesses) and resets its
+    // counter; no split_merge_kernel follows.  The per-wave-stream kernel only.
+    int* ticket;
     int q_bf16;                    // Q rows are bf16 (the per-wave-stream kernel reads them)
     // the Q/K/V epilogue's Q part (forward.rs:291-310): bias before the
     // QK-norm, RoPE after it, at the query rows' positions (qpos)
@@ -222,6 +227,7 @@ struct LaunchPlan {
     bool qepi;       // Q epilogue compiled in: bias, QK-norm, RoPE, each where its operand is given
     bool w16;        // two 16-row compute waves per (row block, key group)
     int kernel;      // KernelKind
+    int merge;       // set at launch: 0 no split, 1 split_merge_kernel, 2 in-kernel
 };
 
 // Attention kernel families.  STAGED: attn_fwd_kernel, the workgroup's waves
@@ -251,10 +257,11 @@ enum QEpilogue : int {
 // dims of a RoPE in the Q epilogue, 0 for none).  force_rb /
 // force_kq / force_split > 0 override the heuristic (tuning); force_rows 16
 // or 32 picks the query rows per compute wave where both are built (0:
-// automatic).
+// automatic).  merge_in_kernel: the per-wave-stream kernel's key splits (up
+// to ring_merge_splits) will be merged in-kernel, which makes them cheaper.
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
-                          int force_split, int force_rows, int force_kernel);
+                          int force_split, int force_rows, int force_kernel, bool merge_in_kernel);
 
 // Bytes of split workspace a plan needs (part_o + part_ml).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);
@@ -270,6 +277,7 @@ hipError_t scratch_init(int device);
 void* scratch_ptr(int device);
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 int ring_waves(int hd);  // waves per workgroup of attn_ring_kernel (0: head dim not built)
+int ring_merge_splits(int hd);  // most key splits attn_ring_kernel merges in-kernel
 hipError_t launch_hilo(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 int hilo_rows();  // query rows per workgroup of attn_hilo_kernel
 hipError_t launch_store(int hd_tile, const StoreArgs& a, hipStream_t st);

@@ -96,6 +96,7 @@ class CLaunchInfo(ctypes.Structure):
         ("key_groups", ctypes.c_int),
         ("rows_per_wave", ctypes.c_int),
         ("kernel", ctypes.c_int),
+        ("split_merge", ctypes.c_int),
     ]
 
 
@@ -127,6 +128,7 @@ _SIGS = {
     "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
     "dr_ctx_set_kernel": (_I, [_VP, _I]),
     "dr_ctx_set_q_dtype": (_I, [_VP, _I]),
+    "dr_ctx_set_split_merge": (_I, [_VP, _I]),
     "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
                             ctypes.POINTER(ctypes.c_void_p)]),
     "dr_rope_destroy": (None, [_VP]),
@@ -335,6 +337,11 @@ class Context:
         """DTYPE_F32 or DTYPE_BF16: the element type of the Q rows of later
         cached attention calls (dr_ctx_set_q_dtype)."""
         _check(self.lib.dr_ctx_set_q_dtype(self.h, dtype))
+
+    def set_split_merge(self, in_kernel: bool) -> None:
+        """Key splits of the STREAMS kernel merge in-kernel (True, the
+        default) or in a second kernel (dr_ctx_set_split_merge)."""
+        _check(self.lib.dr_ctx_set_split_merge(self.h, 1 if in_kernel else 0))
 
     def set_tuning(self, row_blocks: int = 0, key_groups: int = 0, n_split: int = 0) -> None:
         _check(self.lib.dr_ctx_set_tuning(self.h, row_blocks, key_groups, n_split))

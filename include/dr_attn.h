@@ -384,6 +384,7 @@ typedef struct {
     int key_groups;
     int rows_per_wave; /* query rows per compute wave: 32, or 16 (two waves per row block) */
     int kernel; /* DR_KERNEL_STAGED, DR_KERNEL_STREAMS or DR_KERNEL_HILO: which attention kernel ran */
+    int split_merge; /* key splits merged: 0 no split, 1 by a second kernel, 2 in-kernel */
 } dr_launch_info;
 int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 
@@ -423,6 +424,16 @@ int dr_ctx_set_kernel(dr_ctx* ctx, int kernel);
 #define DR_DTYPE_F32 0
 #define DR_DTYPE_BF16 1
 int dr_ctx_set_q_dtype(dr_ctx* ctx, int dtype);
+/* How key splits of the STREAMS kernel are merged on later calls on ctx (a
+ * tuning knob with no counterpart in the reference, for measurement and
+ * tests).  1 (the default): in-kernel; the last split of each 32-row block
+ * to finish merges the others' partials, which every split writes and reads
+ * with agent-scope (L2-coherent) accesses, counted by per-block tickets that
+ * dr_ctx_create allocates and zeroes and each merge resets.  0: a second
+ * kernel merges them, as for the other kernel families.  Both give the same
+ * bits.  Calls on one context that overlap on the device share its tickets
+ * and split workspace, and race. */
+int dr_ctx_set_split_merge(dr_ctx* ctx, int in_kernel);
 /* Override the workgroup shape (32-row query blocks x key groups) and the
  * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
  * to the automatic one. */
