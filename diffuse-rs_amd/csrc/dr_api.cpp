@@ -1009,11 +1009,16 @@ static dr::LaunchPlan plan_hilo(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int 
     p.kernel = dr::KERNEL_HILO;
     const int base = a.n_batch * a.n_head_kv * p.rowgroups;
     const int ntiles = std::max(1, (max_nk + 31) / 32);
+    // Workgroups that run at once: up to head dim 256 a workgroup takes 64 KB
+    // of LDS or less, so two share a CU, and key splits fill both (C5's
+    // global layer at scale 1.0: 74.8 us at 8 splits against 94.8 at 4; its
+    // sliding layer 46.5 against 49.0).  At 512 (144 KB) one per CU.
+    const int slots = ctx->n_cu * (p.hd_tile > 256 ? 1 : 2);
     int split = 1;
     if (ctx->force_split > 0)
         split = ctx->force_split;
-    else if (2 * base <= ctx->n_cu)
-        split = std::min(ctx->n_cu / std::max(base, 1), ntiles);
+    else if (2 * base <= slots)
+        split = std::min(slots / std::max(base, 1), ntiles);
     p.n_split = std::max(1, split);
     p.n_workgroups = base * p.n_split;
     return p;
