@@ -278,11 +278,21 @@ void attn_ring_kernel(const AttnArgs a) {
     // Wave w takes tiles t0 + w, t0 + w + RW, ...: a fixed assignment, so
     // every call sums each row's keys in the same order (bit-identical
     // results run to run; claiming tiles dynamically balanced the waves'
-    // finishing times but made the summation order depend on timing).
-    // (The first DMA is issued even when the wave has no tile: past the
-    // range the descriptor's bounds check returns zeros.)
-    issue_k(t0 + wave);
-    issue_v(t0 + wave);
+    // finishing times but made the summation order depend on timing).  Each
+    // row group walks its waves' lists from a different point (rotated by
+    // the row group), so the row groups of one kv head, which share an XCD,
+    // first request different tiles: the head's K/V comes from HBM in one
+    // round, and later tiles are L2 hits.
+    // (The first DMA is issued even when the wave has no tile: its data is
+    // never used, and past the cache the descriptor returns zeros.)
+    const int kw = wave < nt ? (nt - wave + RW - 1) / RW : 0;  // this wave's tiles
+    const int krot = kw > 1 ? rg % kw : 0;
+    auto tile_at = [&](int k) __attribute__((always_inline)) {
+        const int kk = k + krot;
+        return t0 + wave + RW * (kk >= kw ? kk - kw : kk);
+    };
+    issue_k(kw > 0 ? tile_at(0) : t0 + wave);
+    issue_v(kw > 0 ? tile_at(0) : t0 + wave);
 
     if (a.qb) {
 #pragma unroll
@@ -468,14 +478,14 @@ void attn_ring_kernel(const AttnArgs a) {
 
     u32x4 pprev[2];
     bool last_in_k = false;  // the last tile's V^T is in the K buffer
-    int t = wave < nt ? t0 + wave : -1;  // the current tile (uniform over the wave)
+    int t = kw > 0 ? tile_at(0) : -1;  // the current tile (uniform over the wave)
     if (t >= 0) {
         // step 0: K tile 0 has landed when only V^T tile 0 is outstanding
         wait_vmcnt<NDMA>();
         f32x16 sv = qk();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        const int tn = t + RW < t1 ? t + RW : -1;
+        const int tn = kw > 1 ? tile_at(1) : -1;
         if (tn >= 0) issue_k(tn);
         float alpha;
         mask_and_max(sv, t, alpha);  // (O is still zero: no rescale)
@@ -494,7 +504,7 @@ void attn_ring_kernel(const AttnArgs a) {
         // or this last tile's V^T
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        const int tn = t + RW < t1 ? t + RW : -1;
+        const int tn = i + 1 < kw ? tile_at(i + 1) : -1;
         if (tn >= 0)
             issue_k(tn);
         else
