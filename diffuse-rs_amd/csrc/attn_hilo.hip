@@ -152,29 +152,61 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
     {
         const float* qrow = static_cast<const float*>(S.q) + (size_t)qi * a.q_rstride +
                             (size_t)(g * a.group + hg) * a.hd;
+        float x[NST][8];
 #pragma unroll
         for (int st = 0; st < NST; ++st) {
             const int d0 = dh * HDW + 32 * st + 8 * gq;
-            float x[8];
             if (rvalid && a.hd == HD) {
                 const f32x4 u = gload<f32x4>(qrow + d0), w = gload<f32x4>(qrow + d0 + 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    x[e] = u[e];
-                    x[4 + e] = w[e];
+                    x[st][e] = u[e];
+                    x[st][4 + e] = w[e];
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = (rvalid && d0 + e < a.hd) ? gload<float>(qrow + d0 + e) : 0.0f;
+                for (int e = 0; e < 8; ++e)
+                    x[st][e] = (rvalid && d0 + e < a.hd) ? gload<float>(qrow + d0 + e) : 0.0f;
             }
+        }
+        if constexpr (G::DSPLIT == 1) {
+            // QK-norm of the row (rms_norm_inplace, ops.rs:106-114), when the
+            // host leaves it to this kernel (no bias or RoPE, hd == HD): f32
+            // squares summed in f64 over the row's four lanes (slot groups gq),
+            // then x * scale * w
+            if (a.qn_w) {
+                double ss = 0.0;
+#pragma unroll
+                for (int st = 0; st < NST; ++st)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float sq = x[st][e] * x[st][e];
+                        ss += (double)sq;
+                    }
+                ss += __shfl_xor(ss, 16);
+                ss += __shfl_xor(ss, 32);
+                const float sc = 1.0f / (float)sqrt(ss / (double)HD + (double)a.qn_eps);
+#pragma unroll
+                for (int st = 0; st < NST; ++st) {
+                    const int d0 = 32 * st + 8 * gq;
+                    const f32x4 w0 = gload<f32x4>(a.qn_w + d0), w1 = gload<f32x4>(a.qn_w + d0 + 4);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+#pragma clang fp contract(off)
+                        x[st][e] = x[st][e] * sc * (e < 4 ? w0[e] : w1[e - 4]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < NST; ++st)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float xs = x[e] * a.c;
+                const float xs = x[st][e] * a.c;
                 const __bf16 h = (__bf16)xs;
                 qh[st][e] = h;
                 ql[st][e] = (__bf16)(xs - (float)h);
             }
-        }
     }
 
     // ---- DMA: instruction j of this wave moves 64 chunks (1 KB) of a tile

@@ -1042,8 +1042,11 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
 // The hi/lo kernel reads plain Q: with a Q epilogue (bias, QK-norm, RoPE),
 // each batch slot's Q is copied into the context's workspace and the
 // epilogue (qkv_epilogue.hip, Q heads only) runs there first.
-static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, bool fixed_ws) {
+static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws) {
     if (!a.qn_w && !a.qb && !a.rope) return DR_OK;
+    // the QK-norm alone, at a full head-dim tile up to 256: the kernel
+    // applies it as it loads Q (a row's dims sit in four lanes of one wave)
+    if (!a.qb && !a.rope && p.hd_tile <= 256 && a.hd == p.hd_tile) return DR_OK;
     if (fixed_ws)
         return fail(DR_ERR_UNSUPPORTED,
                     "dr_attention_cached_noalloc: a hi/lo-precision layer with a Q epilogue needs a Q "
@@ -1098,7 +1101,7 @@ static int check_q_dtype(const dr::AttnArgs& a, const dr::LaunchPlan& p, const c
 
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws = false) {
     DR_CHECK(check_q_dtype(a, p, "attention"));
-    if (p.kernel == dr::KERNEL_HILO) DR_CHECK(hilo_prepare_q(ctx, a, fixed_ws));
+    if (p.kernel == dr::KERNEL_HILO) DR_CHECK(hilo_prepare_q(ctx, a, p, fixed_ws));
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
     if (ws > 0) {
         if (fixed_ws) {
