@@ -169,26 +169,34 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
                     x[st][e] = (rvalid && d0 + e < a.hd) ? gload<float>(qrow + d0 + e) : 0.0f;
             }
         }
-        if constexpr (G::DSPLIT == 1) {
-            // QK-norm of the row (rms_norm_inplace, ops.rs:106-114), when the
-            // host leaves it to this kernel (no bias or RoPE, hd == HD): f32
-            // squares summed in f64 over the row's four lanes (slot groups gq),
-            // then x * scale * w
-            if (a.qn_w) {
-                double ss = 0.0;
+        // QK-norm of the row (rms_norm_inplace, ops.rs:106-114), when the
+        // host leaves it to this kernel (no bias or RoPE, hd == HD): f32
+        // squares summed in f64 over the row's four lanes (slot groups gq)
+        // and, at hd 512, over the two waves of the row block (half 0's sum
+        // first on both), then x * scale * w
+        if (a.qn_w) {
+            double ss = 0.0;
 #pragma unroll
-                for (int st = 0; st < NST; ++st)
+            for (int st = 0; st < NST; ++st)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float sq = x[st][e] * x[st][e];
-                        ss += (double)sq;
-                    }
-                ss += __shfl_xor(ss, 16);
-                ss += __shfl_xor(ss, 32);
+                for (int e = 0; e < 8; ++e) {
+                    const float sq = x[st][e] * x[st][e];
+                    ss += (double)sq;
+                }
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if constexpr (G::DSPLIT > 1) {
+                __shared__ double s_ss[NW][16];
+                if (gq == 0) s_ss[wave][qc] = ss;
+                __syncthreads();
+                const double other = s_ss[wave ^ RBW][qc];
+                ss = dh == 0 ? ss + other : other + ss;
+            }
+            {
                 const float sc = 1.0f / (float)sqrt(ss / (double)HD + (double)a.qn_eps);
 #pragma unroll
                 for (int st = 0; st < NST; ++st) {
-                    const int d0 = 32 * st + 8 * gq;
+                    const int d0 = dh * HDW + 32 * st + 8 * gq;
                     const f32x4 w0 = gload<f32x4>(a.qn_w + d0), w1 = gload<f32x4>(a.qn_w + d0 + 4);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {

@@ -1044,9 +1044,10 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
 // epilogue (qkv_epilogue.hip, Q heads only) runs there first.
 static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws) {
     if (!a.qn_w && !a.qb && !a.rope) return DR_OK;
-    // the QK-norm alone, at a full head-dim tile up to 256: the kernel
-    // applies it as it loads Q (a row's dims sit in four lanes of one wave)
-    if (!a.qb && !a.rope && p.hd_tile <= 256 && a.hd == p.hd_tile) return DR_OK;
+    // the QK-norm alone, at a full head-dim tile: the kernel applies it as it
+    // loads Q (a row's sum of squares over four lanes of one wave, or of the
+    // row block's two waves at hd 512)
+    if (!a.qb && !a.rope && a.hd == p.hd_tile) return DR_OK;
     if (fixed_ws)
         return fail(DR_ERR_UNSUPPORTED,
                     "dr_attention_cached_noalloc: a hi/lo-precision layer with a Q epilogue needs a Q "
