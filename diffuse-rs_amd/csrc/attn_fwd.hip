@@ -320,6 +320,26 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
     const bool qbias = QEPI && a.qb != nullptr;
     const bool qrope = QEPI && a.rope != nullptr;
     uint16_t* const qs = smem + (NS - 1) * SLOT;
+    // The QK-norm gains of this lane's dims, the same for every row it
+    // normalises: loaded once, through the global address space (a generic
+    // load inside the row loop may alias the LDS stores of the rows before
+    // it, so each one waited for the previous row's store and its own
+    // round trip).
+    f32x4 wqv[PPL];
+    if constexpr (QEPI) {
+        if (a.qn_w) {
+#pragma unroll
+            for (int pc = 0; pc < PPL; ++pc) {
+                const int dp = d0 + pc * HW;
+                if (a.hd == HD) {
+                    wqv[pc] = gload<f32x4>(a.qn_w + dp);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) wqv[pc][e] = dp + e < a.hd ? gload<float>(a.qn_w + dp + e) : 0.0f;
+                }
+            }
+        }
+    }
     auto q_batch = [&](const int ib) __attribute__((always_inline)) {
         f32x4 xq[QB][PPL];
         f32x4 bq4[QB][PPL];
@@ -413,7 +433,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                 for (int pc = 0; pc < PPL; ++pc)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (d0 + pc * HW + e < a.hd) x[pc][e] = x[pc][e] * sc * a.qn_w[d0 + pc * HW + e];
+                        if (d0 + pc * HW + e < a.hd) x[pc][e] = x[pc][e] * sc * wqv[pc][e];
             }
             if (qrope) {
                 // rotate_rows (ops.rs:433-452): dim d < rot pairs with d +- rot/2,
