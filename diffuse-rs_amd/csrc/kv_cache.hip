@@ -104,6 +104,21 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
                 xv[i][e] = in ? a.v[row + d] : 0.0f;
             }
     }
+    // The K-norm gains of this thread's dims and, with RoPE, of their
+    // partners (d +- rot/2), requested with the rows: read where they are
+    // used, after the row's norm, they cost a dependent round trip.
+    f32x4 kw[V4], kwp[V4];
+    if (a.kn_w) {
+        const int hr = a.rot / 2;
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = d0 + 4 * i + e;
+                kw[i][e] = d < a.hd ? a.kn_w[d] : 0.0f;
+                kwp[i][e] = (a.rope && d < a.rot) ? a.kn_w[d < hr ? d + hr : d - hr] : 0.0f;
+            }
+    }
     const int pos = ok ? (a.pos0 >= 0 ? a.pos0 + r : (a.pos ? a.pos[r] : r)) : 0;
     // RoPE's (sin, cos) pairs of this thread's 16 dims, requested with the
     // rows: when rot/2 is a multiple of 16 they lie on one side of it, 32
@@ -195,7 +210,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d = d0 + 4 * i + e;
-                if (d < a.hd) xk[i][e] = xk[i][e] * ksc * a.kn_w[d];
+                if (d < a.hd) xk[i][e] = xk[i][e] * ksc * kw[i][e];
             }
     }
     if (a.v_norm) {
@@ -232,7 +247,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
                     xp = a.k[row + pd];
                     if (kb) xp += kb[pd];
                 }
-                if (a.kn_w) xp = xp * ksc * a.kn_w[pd];
+                if (a.kn_w) xp = xp * ksc * kwp[i][e];
                 const int j = d < half ? d : pd;
                 float2 t;
                 if (tab_vec) {
