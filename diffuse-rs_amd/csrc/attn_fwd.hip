@@ -169,7 +169,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
     int qmin = 0, qmax = 0;
     bool tiles_can_be_full = MODE == MASK_NONE;
     if constexpr (MODE != MASK_NONE) {
-        my_qpos = rvalid ? S.qpos[qi] : 0;
+        my_qpos = rvalid ? (S.qpos0 >= 0 ? S.qpos0 + qi : S.qpos[qi]) : 0;  // (contiguous: no load)
         my_qseq = (rvalid && S.qseq) ? S.qseq[qi] : 0;
         my_pref = S.qprefix ? (rvalid ? S.qprefix[qi] : -1) : a.prefix;
     }
@@ -182,8 +182,8 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             const int h0 = wg_row0 / S.nq, h1 = r1 / S.nq;
             const int lo = h0 == h1 ? wg_row0 - h0 * S.nq : 0;
             const int hi = h0 == h1 ? r1 - h0 * S.nq : S.nq - 1;
-            qmin = S.qpos[lo];
-            qmax = S.qpos[hi];
+            qmin = S.qpos0 >= 0 ? S.qpos0 + lo : S.qpos[lo];
+            qmax = S.qpos0 >= 0 ? S.qpos0 + hi : S.qpos[hi];
             prefix_free = a.prefix < 0 || qmin >= a.prefix;
         } else {
             int vmin = rvalid ? my_qpos : INT_MAX;

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
     int kt_lo = 0, kt_hi = (S.nk + BN - 1) / BN;
     int my_qpos = 0, my_qseq = 0, my_pref = -1;
     if constexpr (MODE != MASK_NONE) {
-        my_qpos = rvalid ? gload<int>(S.qpos + qi) : 0;
+        my_qpos = rvalid ? (S.qpos0 >= 0 ? S.qpos0 + qi : gload<int>(S.qpos + qi)) : 0;  // (contiguous: no load)
         my_qseq = (rvalid && S.qseq) ? gload<int>(S.qseq + qi) : 0;
         my_pref = S.qprefix ? (rvalid ? gload<int>(S.qprefix + qi) : -1) : a.prefix;
     }

@@ -186,7 +186,9 @@ void attn_ring_kernel(const AttnArgs a) {
     int qmin = 0, qmax = 0;
     bool tiles_can_be_full = MODE == MASK_NONE;
     if constexpr (MODE == MASK_POS) {
-        my_qpos = gload<int>(S.qpos + (rvalid ? qi : 0));
+        // (contiguous passes: positions without a load, so the key range,
+        // and the first K/V DMA behind it, wait for nothing)
+        my_qpos = S.qpos0 >= 0 ? S.qpos0 + (rvalid ? qi : 0) : gload<int>(S.qpos + (rvalid ? qi : 0));
         if (S.qseq) my_qseq = gload<int>(S.qseq + (rvalid ? qi : 0));
         my_pref = S.qprefix ? (rvalid ? gload<int>(S.qprefix + qi) : -1) : a.prefix;
         bool prefix_free;
@@ -197,8 +199,13 @@ void attn_ring_kernel(const AttnArgs a) {
             const int h0 = wg_row0 / S.nq, h1 = r1 / S.nq;
             const int lo = h0 == h1 ? wg_row0 - h0 * S.nq : 0;
             const int hi = h0 == h1 ? r1 - h0 * S.nq : S.nq - 1;
-            qmin = *(const __attribute__((address_space(4))) int*)(S.qpos + lo);
-            qmax = *(const __attribute__((address_space(4))) int*)(S.qpos + hi);
+            if (S.qpos0 >= 0) {
+                qmin = S.qpos0 + lo;
+                qmax = S.qpos0 + hi;
+            } else {
+                qmin = *(const __attribute__((address_space(4))) int*)(S.qpos + lo);
+                qmax = *(const __attribute__((address_space(4))) int*)(S.qpos + hi);
+            }
             prefix_free = a.prefix < 0 || qmin >= a.prefix;
         } else {
             int vmin = rvalid ? my_qpos : INT_MAX;
