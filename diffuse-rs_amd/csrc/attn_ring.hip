@@ -75,8 +75,14 @@ void attn_ring_kernel(const AttnArgs a) {
 
     AttnSlot S = a.slot[0];
     const float* qn_w = a.qn_w;
+    // (every argument the Q load depends on is fetched in this first batch:
+    // fetched where first used, each cost a dependent scalar round trip)
+    int q_bf16 = a.q_bf16;
+    const float* qb = a.qb;
+    const float* rope = a.rope;
     asm volatile("" : "+s"(S.q), "+s"(S.out), "+s"(S.qpos), "+s"(S.qseq), "+s"(S.qprefix),
-                 "+s"(S.k), "+s"(S.vt), "+s"(S.nq), "+s"(S.nk), "+s"(S.qpos_sorted), "+s"(qn_w)
+                 "+s"(S.k), "+s"(S.vt), "+s"(S.nq), "+s"(S.nk), "+s"(S.qpos_sorted), "+s"(qn_w),
+                 "+s"(S.qpos0), "+s"(q_bf16), "+s"(qb), "+s"(rope)
                  : "s"(a.n_batch), "s"(a.n_head_kv), "s"(a.group), "s"(a.cap),
                    "s"(a.q_rstride), "s"(a.rowgroups), "s"(a.n_split), "s"(a.mg_split),
                    "s"(a.mg_rowgroups), "s"(a.mg_hkv), "s"(a.c), "s"(a.n_wg), "s"(a.window),
@@ -134,20 +140,28 @@ void attn_ring_kernel(const AttnArgs a) {
     // pieces p and p + QP/2 of the same thread, and the (sin, cos) pairs of
     // the row's position are those of the thread's first QP/2 pieces.
     f32x4 xq[QP], wq[QP], bq4[QP];
+    u32x2 xq16[QP];  // bf16 rows: the raw pieces, widened after the first DMA is issued
     f32x4 tab[QP / 2][2];
+    int tab_pos = 0;  // RoPE on a pass with scattered positions: the row's position
+    auto load_tab = [&](int pos) __attribute__((always_inline)) {
+        const float* trow = rope + ((size_t)pos * (RHD / 2) + qd0) * 2;
+#pragma unroll
+        for (int p = 0; p < QP / 2; ++p) {
+            tab[p][0] = gload<f32x4>(trow + 2 * QSTR * p);
+            tab[p][1] = gload<f32x4>(trow + 2 * QSTR * p + 4);
+        }
+    };
     {
         int qhg, qqi;
         split_row(qok ? qr : 0, qhg, qqi);
         const size_t qoff = (size_t)qqi * a.q_rstride + (size_t)(g * a.group + qhg) * RHD + qd0;
-        if (a.q_bf16) {
-            // bf16 rows: 8-byte pieces, widened exactly to f32
+        if (q_bf16) {
+            // bf16 rows: 8-byte pieces, kept raw here (a vector type, not
+            // HIP's uint2 struct, whose copy made a flat load; widening them
+            // here made the wave wait for them before any K/V DMA)
             const uint16_t* qrow = static_cast<const uint16_t*>(S.q) + qoff;
 #pragma unroll
-            for (int p = 0; p < QP; ++p) {
-                const uint2 w = gload<uint2>(qrow + QSTR * p);
-                xq[p] = f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
-                              __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
-            }
+            for (int p = 0; p < QP; ++p) xq16[p] = gload<u32x2>(qrow + QSTR * p);
         } else {
             const float* qrow = static_cast<const float*>(S.q) + qoff;
 #pragma unroll
@@ -157,21 +171,22 @@ void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
             for (int p = 0; p < QP; ++p) wq[p] = gload<f32x4>(qn_w + qd0 + QSTR * p);
         }
-        if (a.qb) {
-            const float* bq = a.qb + (size_t)(g * a.group + qhg) * RHD;
+        if (qb) {
+            const float* bq = qb + (size_t)(g * a.group + qhg) * RHD;
 #pragma unroll
             for (int p = 0; p < QP; ++p) bq4[p] = gload<f32x4>(bq + qd0 + QSTR * p);
         }
-        if (a.rope) {
-            // the row's position (contiguous passes need no load), then the
-            // table row: pairs j = qd0 + QSTR p, 2 floats each
-            const int pos = S.qpos0 >= 0 ? S.qpos0 + qqi : gload<int>(S.qpos + qqi);
-            const float* trow = a.rope + ((size_t)pos * (RHD / 2) + qd0) * 2;
-#pragma unroll
-            for (int p = 0; p < QP / 2; ++p) {
-                tab[p][0] = gload<f32x4>(trow + 2 * QSTR * p);
-                tab[p][1] = gload<f32x4>(trow + 2 * QSTR * p + 4);
-            }
+        if (rope) {
+            // the row's position, then the table row (pairs j = qd0 + QSTR p,
+            // 2 floats each).  Contiguous passes know the position and load
+            // the row here.  Other passes load the position here and the row
+            // after the first K/V DMA: a table address that depends on a load
+            // made the compiler wait for every load so far (the Q rows too)
+            // before the first DMA.
+            if (S.qpos0 >= 0)
+                load_tab(S.qpos0 + qqi);
+            else
+                tab_pos = gload<int>(S.qpos + qqi);
         }
     }
 
@@ -301,7 +316,17 @@ void attn_ring_kernel(const AttnArgs a) {
     issue_k(kw > 0 ? tile_at(0) : t0 + wave);
     issue_v(kw > 0 ? tile_at(0) : t0 + wave);
 
-    if (a.qb) {
+    if (rope && S.qpos0 < 0) load_tab(tab_pos);
+    if (q_bf16) {  // widened exactly to f32
+#pragma unroll
+        for (int p = 0; p < QP; ++p) {
+            const u32x2 w = xq16[p];
+            xq[p] = f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                          __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+        }
+    }
+
+    if (qb) {
 #pragma unroll
         for (int p = 0; p < QP; ++p) xq[p] += bq4[p];
     }
@@ -327,7 +352,7 @@ void attn_ring_kernel(const AttnArgs a) {
                 xq[p][e] = xq[p][e] * sc * wq[p][e];
             }
     }
-    if (a.rope) {
+    if (rope) {
 #pragma unroll
         for (int p = 0; p < QP / 2; ++p)
 #pragma unroll
