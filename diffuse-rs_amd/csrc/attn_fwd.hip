@@ -341,9 +341,15 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
         }
     }
     auto q_batch = [&](const int ib) __attribute__((always_inline)) {
+        // Loads first, all of them unconditional and unmasked (rows past the
+        // block read row 0, dims past the head a clamped in-row piece, both
+        // zeroed after the first K/V DMA is issued): a load on some lanes, or
+        // a select of a loaded value before the DMA, made each row wait for
+        // the previous row's loads (the branches write the same registers).
         f32x4 xq[QB][PPL];
         f32x4 bq4[QB][PPL];
-        float2 rq[QB][PPL][4];
+        f32x4 tq[QB][PPL][2];  // RoPE: the (sin, cos) pairs of a piece's four dims, raw
+        bool okq[QB];
         int qp[QB];  // the rows' positions, requested before the rows (RoPE's table index)
 #pragma unroll
         for (int ii = 0; ii < QB; ++ii) {
@@ -354,14 +360,20 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                 const bool ok = it < QIT && q_lrow(it) < QROWS && rr < rows_total;
                 int hgq = 0, qiq = 0;
                 if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
-                qp[ii] = (qrope && ok) ? (S.qpos0 >= 0 ? S.qpos0 + qiq : S.qpos[qiq]) : 0;
+                if (qrope) qp[ii] = S.qpos0 >= 0 ? S.qpos0 + qiq : gload<int>(S.qpos + qiq);
             }
         }
+        // (two copies of the loop, picked once: a head dim that is a multiple
+        // of 4 loads whole pieces, any other one element by element; one
+        // loop holding both kept a wait between them on every row)
+        auto load_rows = [&](auto vec_tag) __attribute__((always_inline)) {
+            constexpr bool VEC = decltype(vec_tag)::value;
 #pragma unroll
         for (int ii = 0; ii < QB; ++ii) {
             const int it = ib + ii;
             const int rr = wg_row0 + q_lrow(it);
             const bool ok = it < QIT && q_lrow(it) < QROWS && rr < rows_total;
+            okq[ii] = ok;
             int hgq = 0, qiq = 0;
             if (ok) row_split(rr, S.nq, inv_nq, a.group, hgq, qiq);
             const int qh = g * a.group + hgq;
@@ -370,36 +382,36 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
 #pragma unroll
             for (int pc = 0; pc < PPL; ++pc) {
                 const int dp = d0 + pc * HW;
-                if (ok && a.hd == HD) {
-                    xq[ii][pc] = *reinterpret_cast<const f32x4*>(qrow + dp);
+                if constexpr (VEC) {
+                    const int dpc = min(dp, a.hd - 4);
+                    xq[ii][pc] = gload<f32x4>(qrow + dpc);
+                    if (qbias) bq4[ii][pc] = gload<f32x4>(a.qb + (size_t)qh * a.hd + dpc);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) xq[ii][pc][e] = (ok && dp + e < a.hd) ? qrow[dp + e] : 0.0f;
-                }
-                if (qbias) {
+                    if (qbias) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        bq4[ii][pc][e] = (ok && dp + e < a.hd) ? a.qb[(size_t)qh * a.hd + dp + e] : 0.0f;
+                        for (int e = 0; e < 4; ++e)
+                            bq4[ii][pc][e] = (ok && dp + e < a.hd) ? a.qb[(size_t)qh * a.hd + dp + e] : 0.0f;
+                    }
                 }
                 if (qrope) {
                     // dims dp .. dp+3 lie on one side of rot/2 (a multiple of 4):
-                    // their four (sin, cos) pairs are 32 contiguous bytes of the table
-                    const int j0 = dp < rhalf ? dp : dp - rhalf;
-                    if (ok && dp < a.rot) {
-                        const f32x4* t =
-                            reinterpret_cast<const f32x4*>(a.rope + ((size_t)qp[ii] * rhalf + j0) * 2);
-                        const f32x4 t0 = t[0], t1 = t[1];
-                        rq[ii][pc][0] = make_float2(t0[0], t0[1]);
-                        rq[ii][pc][1] = make_float2(t0[2], t0[3]);
-                        rq[ii][pc][2] = make_float2(t1[0], t1[1]);
-                        rq[ii][pc][3] = make_float2(t1[2], t1[3]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) rq[ii][pc][e] = make_float2(0.0f, 1.0f);
-                    }
+                    // their four (sin, cos) pairs are 32 contiguous bytes of the
+                    // table (a piece past rot reads the last in-range one, unused)
+                    const int dr = min(dp, a.rot - 4);
+                    const int j0 = dr < rhalf ? dr : dr - rhalf;
+                    const float* t = a.rope + ((size_t)qp[ii] * rhalf + j0) * 2;
+                    tq[ii][pc][0] = gload<f32x4>(t);
+                    tq[ii][pc][1] = gload<f32x4>(t + 4);
                 }
             }
         }
+        };
+        if (a.hd % 4 == 0)
+            load_rows(std::true_type{});
+        else
+            load_rows(std::false_type{});
 
         if (ib == 0 && dma) {  // (first batch only)
 #pragma unroll
@@ -413,8 +425,9 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             f32x4 x[PPL];
 #pragma unroll
             for (int pc = 0; pc < PPL; ++pc) {
-                x[pc] = xq[ii][pc];
-                if (qbias) x[pc] += bq4[ii][pc];  // add_bias (ops.rs:373-382)
+                const bool in = okq[ii] && d0 + pc * HW < a.hd;
+                x[pc] = in ? xq[ii][pc] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (qbias && in) x[pc] += bq4[ii][pc];  // add_bias (ops.rs:373-382)
             }
             if (QEPI && a.qn_w) {
                 // rms_norm_inplace (ops.rs:106-114): f32 squares summed in f64.
@@ -463,8 +476,10 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             x[pc][e] = dp < rhalf
-                                           ? rope_lo(x[pc][e], xp[pc][e], rq[ii][pc][e].x, rq[ii][pc][e].y)
-                                           : rope_hi(xp[pc][e], x[pc][e], rq[ii][pc][e].x, rq[ii][pc][e].y);
+                                           ? rope_lo(x[pc][e], xp[pc][e], tq[ii][pc][e >> 1][2 * (e & 1)],
+                                                     tq[ii][pc][e >> 1][2 * (e & 1) + 1])
+                                           : rope_hi(xp[pc][e], x[pc][e], tq[ii][pc][e >> 1][2 * (e & 1)],
+                                                     tq[ii][pc][e >> 1][2 * (e & 1) + 1]);
                     }
                 }
             }
