@@ -314,7 +314,6 @@ void attn_ring_kernel(const AttnArgs a) {
         return t0 + wave + RW * (kk >= kw ? kk - kw : kk);
     };
     issue_k(kw > 0 ? tile_at(0) : t0 + wave);
-    issue_v(kw > 0 ? tile_at(0) : t0 + wave);
 
     if (rope && S.qpos0 < 0) load_tab(tab_pos);
     if (q_bf16) {  // widened exactly to f32
@@ -372,7 +371,12 @@ void attn_ring_kernel(const AttnArgs a) {
         for (int e = 0; e < 4; ++e) y[e] = (__bf16)(qok ? xq[p][e] * a.c : 0.0f);
         *reinterpret_cast<bf16x4*>(qs + qlr * RHD + (((d >> 3) ^ swz<R_KCH>(qlr)) << 3) + (d & 7)) = y;
     }
-    lds_barrier();  // (the first K/V tiles stay in flight)
+    lds_barrier();  // (the first K tile stays in flight)
+    // The first V^T tile, first needed by the PV product of step 1, is
+    // requested only now: at kernel start every CU asks for its Q rows and
+    // first tiles at once, and the smaller that burst, the sooner Q and the
+    // first K tile land.  (DMA order stays K0, V0, K1, ...)
+    issue_v(kw > 0 ? tile_at(0) : t0 + wave);
     // Q^T fragments, held for the whole key loop: lane (col, hf) supplies
     // row col, dims 16 c + 8 hf .. + 8 of contraction step c
     bf16x8 qf[KS];
