@@ -316,10 +316,15 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
         return plane + vrow + (size_t)(p / VT_KEYS) * (HD * VT_KEYS) + p % VT_KEYS;
     };
     auto vt_at = [&](int p) __attribute__((always_inline)) { return vt_in(a.vtc, p); };
-    const int q0 = a.pos ? a.pos[rfirst] : rfirst;
+    // (contiguous rows, pos0 >= 0: positions without a load -- a load here,
+    // after the barrier, was a dependent round trip before the V^T stores)
+    const bool known = a.pos0 >= 0 || a.pos == nullptr;
+    const int pbase = a.pos0 >= 0 ? a.pos0 : 0;
+    const int q0 = known ? pbase + rfirst : a.pos[rfirst];
     // pos is strictly ascending, so equal endpoint distance means contiguous.
     const bool contiguous = cnt == SPT && (q0 & 7) == 0 &&
-                            (a.pos == nullptr || a.pos[rfirst + SPT - 1] - q0 == SPT - 1);
+                            (known || a.pos[rfirst + SPT - 1] - q0 == SPT - 1);
+    auto pos_of = [&](int rr) __attribute__((always_inline)) { return known ? pbase + rr : a.pos[rr]; };
     const uint16_t* t = &tile[dl][p0];
     if (contiguous) {
         // 8 positions from a multiple of 8 never cross a 32-key tile
@@ -327,7 +332,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
         for (int h = 0; h < SPT / 8; ++h)
             *reinterpret_cast<u32x4*>(vt_at(q0 + 8 * h)) = *reinterpret_cast<const u32x4*>(t + 8 * h);
     } else {
-        for (int e = 0; e < cnt; ++e) *vt_at(a.pos ? a.pos[rfirst + e] : rfirst + e) = t[e];
+        for (int e = 0; e < cnt; ++e) *vt_at(pos_of(rfirst + e)) = t[e];
     }
     if (a.vlo) {
         // the same positions of the lo plane (V^T's layout)
@@ -337,7 +342,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
             for (int h = 0; h < SPT / 8; ++h)
                 *reinterpret_cast<u32x4*>(vt_in(a.vlo, q0 + 8 * h)) = *reinterpret_cast<const u32x4*>(tl + 8 * h);
         } else {
-            for (int e = 0; e < cnt; ++e) *vt_in(a.vlo, a.pos ? a.pos[rfirst + e] : rfirst + e) = tl[e];
+            for (int e = 0; e < cnt; ++e) *vt_in(a.vlo, pos_of(rfirst + e)) = tl[e];
         }
     }
 }
