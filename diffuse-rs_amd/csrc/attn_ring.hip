@@ -581,13 +581,14 @@ void attn_ring_kernel(const AttnArgs a) {
         last_in_k = true;
         t = tn;
     }
-    // the last tile's PV product (a wave without tiles multiplies zeros)
+    // the last tile's PV product (a wave without tiles has none: its buffer
+    // holds a tile past its range, whose values it must not multiply, even
+    // by zero)
     wait_vmcnt<0>();
-    {
+    if (kw > 0) {
         bf16x8 vf[DB][2];
         read_v(last_in_k ? kbuf : vbuf, vf);
-        const bf16x8 pp[2] = {wave < nt ? __builtin_bit_cast(bf16x8, pprev[0]) : bf16x8{},
-                              wave < nt ? __builtin_bit_cast(bf16x8, pprev[1]) : bf16x8{}};
+        const bf16x8 pp[2] = {__builtin_bit_cast(bf16x8, pprev[0]), __builtin_bit_cast(bf16x8, pprev[1])};
         pv(vf, pp);
     }
 
