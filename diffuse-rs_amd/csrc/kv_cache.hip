@@ -18,6 +18,9 @@
 //         bf16(x - bf16(x)), of K and V in planes laid out like K and V^T.
 //         One launch, one workgroup per (64-row block, 64-wide head-dim
 //         chunk, kv head): K converted in registers, V transposed through LDS.
+//         Rows that fill whole 32-key tiles at contiguous positions, with no
+//         epilogue (the denoise step's canvas rows), take a second kernel:
+//         one workgroup per (kv head, tile), whole-line loads and stores.
 // gather: StepCache::gather (cache.rs:73-82) -- bf16 back to f32 rows (hi +
 //         lo where the layer keeps the lo halves).
 #include <algorithm>
@@ -347,6 +350,70 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
     }
 }
 
+// The store of rows that fill whole 32-key V^T tiles at contiguous positions
+// (pos0 and n multiples of 32), head dim == HD (64, 128 or 256), with no
+// epilogue and no lo halves: the canvas rows of every denoise step.  One
+// workgroup per (kv head, tile); thread (rg, dc), rg fastest, holds the 4
+// dims 4 dc .. 4 dc + 3 of the tile's rows RPG rg .. RPG rg + RPG - 1.
+// - Loads: per instruction the wave reads whole 128-byte lines (hd 128: 8
+//   rows x 128 B), against 64-byte pieces at a 64-byte lane stride in
+//   kv_store_kernel.
+// - K: bf16 of the 4 dims, 8 bytes per row.
+// - V^T: at step e the thread writes the RPG keys of its rows in d-row
+//   4 dc + e of the tile; the NRG lanes of one dc together write that
+//   d-row's 64 bytes whole, so no LDS transpose and no barrier is needed.
+// Same values as kv_store_kernel: bf16 (round to nearest even) of each f32.
+template <int HD>
+__global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) {
+    constexpr int CPR = HD / 4;     // 4-dim pieces per row
+    constexpr int NRG = 256 / CPR;  // row groups
+    constexpr int RPG = VT_KEYS / NRG;  // rows per row group
+    static_assert(NRG * RPG == VT_KEYS && RPG >= 2 && RPG <= 8, "tile geometry");
+
+    const int x = blockIdx.x & 7;  // (XCD placement as kv_store_kernel)
+    if (x < a.xcd_lo || x >= a.xcd_lo + a.xcd_n) return;
+    const int lid = (x - a.xcd_lo) * a.per_xcd + (int)(blockIdx.x >> 3);
+    const int ntl = a.n / VT_KEYS;
+    if (lid >= a.n_head_kv * ntl) return;
+    const int g = lid / ntl, tb = lid - g * ntl;
+    const int tid = threadIdx.x;
+    const int rg = tid % NRG, dc = tid / NRG;
+    const int r0 = tb * VT_KEYS + rg * RPG;  // first row of this thread
+    const size_t rstride = (size_t)a.n_head_kv * HD;
+    const size_t src = ((size_t)r0 * a.n_head_kv + g) * HD + 4 * dc;
+    f32x4 xk[RPG], xv[RPG];
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+        xk[j] = *reinterpret_cast<const f32x4*>(a.k + src + j * rstride);
+        xv[j] = *reinterpret_cast<const f32x4*>(a.v + src + j * rstride);
+    }
+    const int p0 = a.pos0 >= 0 ? a.pos0 : 0;  // (host: pos0 >= 0, or no position list)
+    uint16_t* kdst = a.kc + ((size_t)g * a.cap + p0 + r0) * HD + 4 * dc;
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+        uint32_t w0 = (uint32_t)f2bf(xk[j][0]) | ((uint32_t)f2bf(xk[j][1]) << 16);
+        uint32_t w1 = (uint32_t)f2bf(xk[j][2]) | ((uint32_t)f2bf(xk[j][3]) << 16);
+        *reinterpret_cast<uint2*>(kdst + (size_t)j * HD) = make_uint2(w0, w1);
+    }
+    uint16_t* vdst = a.vtc + (size_t)g * HD * a.cap + (size_t)(p0 / VT_KEYS + tb) * (HD * VT_KEYS) +
+                     (size_t)(4 * dc) * VT_KEYS + rg * RPG;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t w[RPG / 2];
+#pragma unroll
+        for (int j = 0; j < RPG / 2; ++j)
+            w[j] = (uint32_t)f2bf(xv[2 * j][e]) | ((uint32_t)f2bf(xv[2 * j + 1][e]) << 16);
+        uint16_t* row = vdst + e * VT_KEYS;
+        if constexpr (RPG == 2) {
+            *reinterpret_cast<uint32_t*>(row) = w[0];
+        } else if constexpr (RPG == 4) {
+            *reinterpret_cast<uint2*>(row) = make_uint2(w[0], w[1]);
+        } else {
+            *reinterpret_cast<u32x4*>(row) = u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
 // One thread per (row, kv head, d).
 template <int HD>
 __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
@@ -377,6 +444,23 @@ hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
     const int nb = a.n_batch > 0 ? a.n_batch : 1;
     a.xcd_lo = 8 * a.batch / nb;
     a.xcd_n = std::max(1, 8 * (a.batch + 1) / nb - a.xcd_lo);
+    // whole tiles at contiguous positions, no epilogue: the tile kernel
+    const int p0 = a.pos0 >= 0 ? a.pos0 : (a.pos == nullptr ? 0 : -1);
+    const bool tiles = a.vec && a.hd == hd_tile && hd_tile <= 256 && p0 >= 0 && p0 % VT_KEYS == 0 &&
+                       a.n % VT_KEYS == 0 && !a.kn_w && !a.rope && !a.kb && !a.vb && !a.v_norm && !a.klo &&
+                       !a.vlo;
+    if (tiles) {
+        a.pos0 = p0;
+        const int work = a.n_head_kv * (a.n / VT_KEYS);
+        a.per_xcd = (work + a.xcd_n - 1) / a.xcd_n;
+        const dim3 grid((unsigned)(8 * a.per_xcd));
+        switch (hd_tile) {
+            case 64: hipLaunchKernelGGL(kv_store_tiles_kernel<64>, grid, dim3(256), 0, st, a); break;
+            case 128: hipLaunchKernelGGL(kv_store_tiles_kernel<128>, grid, dim3(256), 0, st, a); break;
+            default: hipLaunchKernelGGL(kv_store_tiles_kernel<256>, grid, dim3(256), 0, st, a); break;
+        }
+        return hipGetLastError();
+    }
     a.n_rb = (a.n + SR - 1) / SR;
     const int work = a.n_head_kv * (hd_tile / SD) * a.n_rb;
     a.per_xcd = (work + a.xcd_n - 1) / a.xcd_n;

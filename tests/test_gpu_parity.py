@@ -548,6 +548,36 @@ def test_cache_gather_is_bf16_of_store(dev):
     assert np.array_equal(dev.get(ov), bf(V))
 
 
+@pytest.mark.parametrize("hd,hkv,p0,n,n_batch", [(128, 32, 512, 256, 1), (128, 3, 0, 96, 2), (64, 5, 32, 64, 1),
+                                                 (256, 8, 4096, 256, 1), (256, 2, 64, 32, 2), (96, 2, 32, 64, 1)])
+def test_cache_store_whole_tiles_is_bf16(dev, hd, hkv, p0, n, n_batch):
+    """Rows that fill whole 32-key tiles at contiguous positions (the canvas
+    rows of a denoise step; their own store kernel at head dim 64/128/256,
+    the general one at 96): gather returns bf16 of every stored row bit for
+    bit (cache.rs:62-82), in the last layer of a three-layer cache and in
+    every batch slot, and the rows stored before, around the tiles, keep
+    their values."""
+    rng = np.random.default_rng(hd + p0 + n)
+    n_tot = p0 + n + 40
+    cache = dr.StepCache(dev.ctx, n_tot, [hkv] * 3, [hd] * 3, n_batch=n_batch)
+    t = dev.t
+    bf = lambda a: t.from_numpy(a).to(t.bfloat16).to(t.float32).numpy().reshape(-1)  # noqa: E731
+    every = list(range(n_tot))
+    for b in range(n_batch):
+        K0 = rng.standard_normal((n_tot, hkv * hd), dtype=np.float32)
+        V0 = rng.standard_normal((n_tot, hkv * hd), dtype=np.float32)
+        cache.store(2, dr.Pass(dev.ctx, every), dev.put(K0), dev.put(V0), batch=b)  # ragged: the general kernel
+        K = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+        V = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+        cache.store(2, dr.Pass(dev.ctx, range(p0, p0 + n)), dev.put(K), dev.put(V), batch=b)
+        wk, wv = K0.copy(), V0.copy()
+        wk[p0:p0 + n], wv[p0:p0 + n] = K, V
+        ok, ov = dev.empty(n_tot * hkv * hd), dev.empty(n_tot * hkv * hd)
+        cache.gather(2, every, ok, ov, batch=b)
+        assert np.array_equal(dev.get(ok), bf(wk)), b
+        assert np.array_equal(dev.get(ov), bf(wv)), b
+
+
 @pytest.mark.parametrize("hd,n,n_tot", [(64, 70, 200), (96, 129, 150), (128, 64, 64),
                                         (256, 33, 90), (512, 70, 100), (320, 17, 40)])
 def test_cache_store_k_norm_is_bf16_of_oracle(dev, hd, n, n_tot):
