@@ -18,9 +18,10 @@
 //         bf16(x - bf16(x)), of K and V in planes laid out like K and V^T.
 //         One launch, one workgroup per (64-row block, 64-wide head-dim
 //         chunk, kv head): K converted in registers, V transposed through LDS.
-//         Rows that fill whole 32-key tiles at contiguous positions, with no
-//         epilogue (the denoise step's canvas rows), take a second kernel:
-//         one workgroup per (kv head, tile), whole-line loads and stores.
+//         Rows that fill whole 32-key tiles at contiguous positions, without
+//         RoPE or lo halves (the denoise step's canvas rows), take a second
+//         kernel: one workgroup per (kv head, tile), whole-line loads and
+//         stores.
 // gather: StepCache::gather (cache.rs:73-82) -- bf16 back to f32 rows (hi +
 //         lo where the layer keeps the lo halves).
 #include <algorithm>
@@ -351,19 +352,25 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
 }
 
 // The store of rows that fill whole 32-key V^T tiles at contiguous positions
-// (pos0 and n multiples of 32), head dim == HD (64, 128 or 256), with no
-// epilogue and no lo halves: the canvas rows of every denoise step.  One
+// (pos0 and n multiples of 32), head dim == HD (64, 128 or 256), without RoPE
+// and lo halves: the canvas rows of every denoise step.  One
 // workgroup per (kv head, tile); thread (rg, dc), rg fastest, holds the 4
 // dims 4 dc .. 4 dc + 3 of the tile's rows RPG rg .. RPG rg + RPG - 1.
 // - Loads: per instruction the wave reads whole 128-byte lines (hd 128: 8
 //   rows x 128 B), against 64-byte pieces at a 64-byte lane stride in
 //   kv_store_kernel.
+// - The K / V biases, the K norm and Gemma's V norm of the epilogue, as in
+//   kv_store_kernel: a row's f32 squares summed in f64, over the 4 dims of
+//   each thread, then across the lanes of the row in the wave (shuffles),
+//   then across the 4 waves in wave order (LDS).
 // - K: bf16 of the 4 dims, 8 bytes per row.
 // - V^T: at step e the thread writes the RPG keys of its rows in d-row
 //   4 dc + e of the tile; the NRG lanes of one dc together write that
 //   d-row's 64 bytes whole, so no LDS transpose and no barrier is needed.
 // Same values as kv_store_kernel: bf16 (round to nearest even) of each f32.
-template <int HD>
+// EPI: the biases and norms are compiled in (without them, the conditional
+// updates of the loaded rows made the K stores wait for every load).
+template <int HD, bool EPI>
 __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) {
     constexpr int CPR = HD / 4;     // 4-dim pieces per row
     constexpr int NRG = 256 / CPR;  // row groups
@@ -386,6 +393,70 @@ __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) 
     for (int j = 0; j < RPG; ++j) {
         xk[j] = *reinterpret_cast<const f32x4*>(a.k + src + j * rstride);
         xv[j] = *reinterpret_cast<const f32x4*>(a.v + src + j * rstride);
+    }
+    if constexpr (EPI) {
+    f32x4 kw4 = {}, kb4 = {}, vb4 = {};
+    if (a.kn_w) kw4 = *reinterpret_cast<const f32x4*>(a.kn_w + 4 * dc);
+    if (a.kb) kb4 = *reinterpret_cast<const f32x4*>(a.kb + (size_t)g * HD + 4 * dc);
+    if (a.vb) vb4 = *reinterpret_cast<const f32x4*>(a.vb + (size_t)g * HD + 4 * dc);
+    if (a.kb || a.vb) {
+#pragma unroll
+        for (int j = 0; j < RPG; ++j) {
+            xk[j] += kb4;
+            xv[j] += vb4;
+        }
+    }
+    if (a.kn_w || a.v_norm) {
+        // rms_norm_inplace (ops.rs:106-114) / rms_norm_noscale: sum of the
+        // row's f32 squares in f64; the row's lanes in this wave are lanes
+        // rg + NRG i, the other CPR / (64 / NRG) - 1 shares are in the
+        // other waves
+        __shared__ double s_ss[2][4][VT_KEYS];  // [K, V][wave][row of the tile]
+        const int wave = tid >> 6;
+        auto row_ss = [&](const f32x4 (&x)[RPG], double (&ss)[RPG]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < RPG; ++j) {
+                double t = 0.0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sq = x[j][e] * x[j][e];
+                    t += (double)sq;
+                }
+#pragma unroll
+                for (int off = NRG; off < 64; off <<= 1) t += __shfl_xor(t, off);
+                ss[j] = t;
+            }
+        };
+        double ssk[RPG], ssv[RPG];
+        if (a.kn_w) row_ss(xk, ssk);
+        if (a.v_norm) row_ss(xv, ssv);
+        if ((tid & 63) < NRG) {
+#pragma unroll
+            for (int j = 0; j < RPG; ++j) {
+                if (a.kn_w) s_ss[0][wave][rg * RPG + j] = ssk[j];
+                if (a.v_norm) s_ss[1][wave][rg * RPG + j] = ssv[j];
+            }
+        }
+        __syncthreads();
+        auto scale_of = [&](int kv, int j) __attribute__((always_inline)) {
+            const double t = ((s_ss[kv][0][rg * RPG + j] + s_ss[kv][1][rg * RPG + j]) + s_ss[kv][2][rg * RPG + j]) +
+                             s_ss[kv][3][rg * RPG + j];
+            return 1.0f / (float)sqrt(t / (double)HD + (double)a.kn_eps);
+        };
+#pragma unroll
+        for (int j = 0; j < RPG; ++j) {
+            if (a.kn_w) {
+                const float sc = scale_of(0, j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xk[j][e] = xk[j][e] * sc * kw4[e];
+            }
+            if (a.v_norm) {
+                const float sc = scale_of(1, j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[j][e] *= sc;
+            }
+        }
+    }
     }
     const int p0 = a.pos0 >= 0 ? a.pos0 : 0;  // (host: pos0 >= 0, or no position list)
     uint16_t* kdst = a.kc + ((size_t)g * a.cap + p0 + r0) * HD + 4 * dc;
@@ -447,17 +518,21 @@ hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
     // whole tiles at contiguous positions, no epilogue: the tile kernel
     const int p0 = a.pos0 >= 0 ? a.pos0 : (a.pos == nullptr ? 0 : -1);
     const bool tiles = a.vec && a.hd == hd_tile && hd_tile <= 256 && p0 >= 0 && p0 % VT_KEYS == 0 &&
-                       a.n % VT_KEYS == 0 && !a.kn_w && !a.rope && !a.kb && !a.vb && !a.v_norm && !a.klo &&
-                       !a.vlo;
+                       a.n % VT_KEYS == 0 && !a.rope && !a.klo && !a.vlo &&
+                       (((uintptr_t)a.kn_w | (uintptr_t)a.kb | (uintptr_t)a.vb) & 15) == 0;
     if (tiles) {
         a.pos0 = p0;
         const int work = a.n_head_kv * (a.n / VT_KEYS);
         a.per_xcd = (work + a.xcd_n - 1) / a.xcd_n;
         const dim3 grid((unsigned)(8 * a.per_xcd));
-        switch (hd_tile) {
-            case 64: hipLaunchKernelGGL(kv_store_tiles_kernel<64>, grid, dim3(256), 0, st, a); break;
-            case 128: hipLaunchKernelGGL(kv_store_tiles_kernel<128>, grid, dim3(256), 0, st, a); break;
-            default: hipLaunchKernelGGL(kv_store_tiles_kernel<256>, grid, dim3(256), 0, st, a); break;
+        const bool epi = a.kn_w || a.kb || a.vb || a.v_norm;
+        switch (hd_tile * 2 + (epi ? 1 : 0)) {
+            case 128: hipLaunchKernelGGL((kv_store_tiles_kernel<64, false>), grid, dim3(256), 0, st, a); break;
+            case 129: hipLaunchKernelGGL((kv_store_tiles_kernel<64, true>), grid, dim3(256), 0, st, a); break;
+            case 256: hipLaunchKernelGGL((kv_store_tiles_kernel<128, false>), grid, dim3(256), 0, st, a); break;
+            case 257: hipLaunchKernelGGL((kv_store_tiles_kernel<128, true>), grid, dim3(256), 0, st, a); break;
+            case 512: hipLaunchKernelGGL((kv_store_tiles_kernel<256, false>), grid, dim3(256), 0, st, a); break;
+            default: hipLaunchKernelGGL((kv_store_tiles_kernel<256, true>), grid, dim3(256), 0, st, a); break;
         }
         return hipGetLastError();
     }

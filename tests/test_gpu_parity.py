@@ -578,6 +578,54 @@ def test_cache_store_whole_tiles_is_bf16(dev, hd, hkv, p0, n, n_batch):
         assert np.array_equal(dev.get(ov), bf(wv)), b
 
 
+@pytest.mark.parametrize("hd,hkv,h,n_p,n_c,bias,norm,v_norm", [
+    (128, 16, 16, 512, 256, False, True, False),  # C4-like QK-norm
+    (256, 8, 16, 256, 128, True, True, True),     # Gemma-like: biases, K norm, V norm
+    (64, 4, 8, 64, 96, True, False, False),       # biases only
+    (128, 2, 8, 96, 64, False, False, True),      # V norm only
+])
+def test_cache_store_whole_tiles_epilogue(dev, hd, hkv, h, n_p, n_c, bias, norm, v_norm):
+    """The Q/K/V epilogue's K and V part (forward.rs:291-310) on the whole-tile
+    store (canvas rows at contiguous positions, no RoPE), through
+    dr_attention_step_epi: add_bias (ops.rs:373-382), then K's RMSNorm with
+    its gain (ops.rs:106-114) and V's without one (ops.rs:116-124).  The
+    gathered rows equal bf16 of the oracle's rows bit for bit."""
+    rng = np.random.default_rng(hd + n_c + 10 * bias + 100 * norm + 1000 * v_norm)
+    eps = 1e-6
+    n_t, kvs = n_p + n_c, hkv * hd
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    K = (rng.standard_normal((n_c, kvs)) * 2).astype(np.float32)
+    V = rng.standard_normal((n_c, kvs)).astype(np.float32)
+    Q = rng.standard_normal((n_c, h * hd)).astype(np.float32)
+    bk = (0.1 * rng.standard_normal(kvs)).astype(np.float32) if bias else None
+    bv = (0.1 * rng.standard_normal(kvs)).astype(np.float32) if bias else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    put = lambda x: dev.put(x) if x is not None else None  # noqa: E731
+    out = dev.empty(n_c * h * hd)
+    p_c = dr.Pass(dev.ctx, range(n_p, n_t))
+    cache.step_epi(0, [(dev.put(Q), out, p_c, dev.put(K), dev.put(V))], h, scale=1 / math.sqrt(hd),
+                   bk=put(bk), bv=put(bv), k_norm_w=put(kn), v_norm=v_norm, eps=eps)
+    wk, wv = K.reshape(-1).copy(), V.reshape(-1).copy()
+    if bias:
+        orc.add_bias(wk, bk, n_c)
+        orc.add_bias(wv, bv, n_c)
+    for o in range(0, wk.size, hd):
+        if norm:
+            seg = wk[o:o + hd].copy()
+            orc.rms_norm_inplace(seg, kn, eps)
+            wk[o:o + hd] = seg
+        if v_norm:
+            seg = wv[o:o + hd].copy()
+            orc.rms_norm_noscale(seg, eps)
+            wv[o:o + hd] = seg
+    ok, ov = dev.empty(n_c * kvs), dev.empty(n_c * kvs)
+    cache.gather(0, list(range(n_p, n_t)), ok, ov)
+    t = dev.t
+    bf = lambda a: t.from_numpy(a).to(t.bfloat16).to(t.float32).numpy().reshape(-1)  # noqa: E731
+    assert np.array_equal(dev.get(ok), bf(wk))
+    assert np.array_equal(dev.get(ov), bf(wv))
+
+
 @pytest.mark.parametrize("hd,n,n_tot", [(64, 70, 200), (96, 129, 150), (128, 64, 64),
                                         (256, 33, 90), (512, 70, 100), (320, 17, 40)])
 def test_cache_store_k_norm_is_bf16_of_oracle(dev, hd, n, n_tot):
