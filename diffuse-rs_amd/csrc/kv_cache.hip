@@ -352,8 +352,8 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
 }
 
 // The store of rows that fill whole 32-key V^T tiles at contiguous positions
-// (pos0 and n multiples of 32), head dim == HD (64, 128 or 256), without RoPE
-// and lo halves: the canvas rows of every denoise step.  One
+// (pos0 and n multiples of 32), head dim == HD (64, 128 or 256), without lo
+// halves: the canvas rows of every denoise step.  One
 // workgroup per (kv head, tile); thread (rg, dc), rg fastest, holds the 4
 // dims 4 dc .. 4 dc + 3 of the tile's rows RPG rg .. RPG rg + RPG - 1.
 // - Loads: per instruction the wave reads whole 128-byte lines (hd 128: 8
@@ -362,7 +362,10 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
 // - The K / V biases, the K norm and Gemma's V norm of the epilogue, as in
 //   kv_store_kernel: a row's f32 squares summed in f64, over the 4 dims of
 //   each thread, then across the lanes of the row in the wave (shuffles),
-//   then across the 4 waves in wave order (LDS).
+//   then across the 4 waves in wave order (LDS).  RoPE on K (rotate_rows,
+//   ops.rs:433-452; rot a multiple of 8, so a thread's 4 dims lie on one side
+//   of rot / 2) reads the partner dim d +- rot / 2 of the normed row from LDS
+//   and the (sin, cos) pairs of the row's position, loaded with the rows.
 // - K: bf16 of the 4 dims, 8 bytes per row.
 // - V^T: at step e the thread writes the RPG keys of its rows in d-row
 //   4 dc + e of the tile; the NRG lanes of one dc together write that
@@ -395,6 +398,20 @@ __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) 
         xv[j] = *reinterpret_cast<const f32x4*>(a.v + src + j * rstride);
     }
     if constexpr (EPI) {
+    const int half = a.rot / 2;
+    const int d0 = 4 * dc;
+    const bool rot_me = a.rope && d0 < a.rot;
+    f32x4 tab[RPG][2];  // (sin, cos) of pairs jj .. jj + 3 at each row's position
+    if (rot_me) {
+        const int jj = d0 < half ? d0 : d0 - half;
+        const int pp = (a.pos0 >= 0 ? a.pos0 : 0) + r0;
+#pragma unroll
+        for (int j = 0; j < RPG; ++j) {
+            const float* t = a.rope + ((size_t)(pp + j) * half + jj) * 2;
+            tab[j][0] = *reinterpret_cast<const f32x4*>(t);
+            tab[j][1] = *reinterpret_cast<const f32x4*>(t + 4);
+        }
+    }
     f32x4 kw4 = {}, kb4 = {}, vb4 = {};
     if (a.kn_w) kw4 = *reinterpret_cast<const f32x4*>(a.kn_w + 4 * dc);
     if (a.kb) kb4 = *reinterpret_cast<const f32x4*>(a.kb + (size_t)g * HD + 4 * dc);
@@ -454,6 +471,24 @@ __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) 
                 const float sc = scale_of(1, j);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) xv[j][e] *= sc;
+            }
+        }
+    }
+    if (a.rope) {
+        __shared__ __align__(16) float s_k[VT_KEYS][HD + 4];  // the tile's normed K rows
+#pragma unroll
+        for (int j = 0; j < RPG; ++j) *reinterpret_cast<f32x4*>(&s_k[rg * RPG + j][d0]) = xk[j];
+        __syncthreads();
+        if (rot_me) {
+            const int pd0 = d0 < half ? d0 + half : d0 - half;
+#pragma unroll
+            for (int j = 0; j < RPG; ++j) {
+                const f32x4 xp = *reinterpret_cast<const f32x4*>(&s_k[rg * RPG + j][pd0]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sn = tab[j][e >> 1][2 * (e & 1)], cs = tab[j][e >> 1][2 * (e & 1) + 1];
+                    xk[j][e] = d0 < half ? rope_lo(xk[j][e], xp[e], sn, cs) : rope_hi(xp[e], xk[j][e], sn, cs);
+                }
             }
         }
     }
@@ -518,14 +553,14 @@ hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
     // whole tiles at contiguous positions, no epilogue: the tile kernel
     const int p0 = a.pos0 >= 0 ? a.pos0 : (a.pos == nullptr ? 0 : -1);
     const bool tiles = a.vec && a.hd == hd_tile && hd_tile <= 256 && p0 >= 0 && p0 % VT_KEYS == 0 &&
-                       a.n % VT_KEYS == 0 && !a.rope && !a.klo && !a.vlo &&
-                       (((uintptr_t)a.kn_w | (uintptr_t)a.kb | (uintptr_t)a.vb) & 15) == 0;
+                       a.n % VT_KEYS == 0 && !a.klo && !a.vlo && (!a.rope || (a.rot % 8 == 0 && a.rot <= a.hd)) &&
+                       (((uintptr_t)a.kn_w | (uintptr_t)a.kb | (uintptr_t)a.vb | (uintptr_t)a.rope) & 15) == 0;
     if (tiles) {
         a.pos0 = p0;
         const int work = a.n_head_kv * (a.n / VT_KEYS);
         a.per_xcd = (work + a.xcd_n - 1) / a.xcd_n;
         const dim3 grid((unsigned)(8 * a.per_xcd));
-        const bool epi = a.kn_w || a.kb || a.vb || a.v_norm;
+        const bool epi = a.kn_w || a.kb || a.vb || a.v_norm || a.rope;
         switch (hd_tile * 2 + (epi ? 1 : 0)) {
             case 128: hipLaunchKernelGGL((kv_store_tiles_kernel<64, false>), grid, dim3(256), 0, st, a); break;
             case 129: hipLaunchKernelGGL((kv_store_tiles_kernel<64, true>), grid, dim3(256), 0, st, a); break;

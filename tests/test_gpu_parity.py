@@ -578,19 +578,23 @@ def test_cache_store_whole_tiles_is_bf16(dev, hd, hkv, p0, n, n_batch):
         assert np.array_equal(dev.get(ov), bf(wv)), b
 
 
-@pytest.mark.parametrize("hd,hkv,h,n_p,n_c,bias,norm,v_norm", [
-    (128, 16, 16, 512, 256, False, True, False),  # C4-like QK-norm
-    (256, 8, 16, 256, 128, True, True, True),     # Gemma-like: biases, K norm, V norm
-    (64, 4, 8, 64, 96, True, False, False),       # biases only
-    (128, 2, 8, 96, 64, False, False, True),      # V norm only
+@pytest.mark.parametrize("hd,hkv,h,n_p,n_c,bias,norm,v_norm,rot", [
+    (128, 16, 16, 512, 256, False, True, False, 0),   # C4-like QK-norm
+    (128, 16, 16, 512, 256, True, True, False, 128),  # the same with the biases and RoPE
+    (256, 8, 16, 256, 128, True, True, True, 256),    # Gemma-like: biases, K norm, V norm, RoPE
+    (64, 4, 8, 64, 96, True, False, False, 0),        # biases only
+    (128, 2, 8, 96, 64, False, False, True, 0),       # V norm only
+    (128, 4, 8, 64, 64, True, True, False, 64),       # partial rotary
+    (64, 2, 4, 32, 32, False, False, False, 24),      # RoPE only, rot / 2 not a multiple of 8
 ])
-def test_cache_store_whole_tiles_epilogue(dev, hd, hkv, h, n_p, n_c, bias, norm, v_norm):
+def test_cache_store_whole_tiles_epilogue(dev, hd, hkv, h, n_p, n_c, bias, norm, v_norm, rot):
     """The Q/K/V epilogue's K and V part (forward.rs:291-310) on the whole-tile
-    store (canvas rows at contiguous positions, no RoPE), through
+    store (canvas rows at contiguous positions), through
     dr_attention_step_epi: add_bias (ops.rs:373-382), then K's RMSNorm with
-    its gain (ops.rs:106-114) and V's without one (ops.rs:116-124).  The
-    gathered rows equal bf16 of the oracle's rows bit for bit."""
-    rng = np.random.default_rng(hd + n_c + 10 * bias + 100 * norm + 1000 * v_norm)
+    its gain (ops.rs:106-114) and V's without one (ops.rs:116-124), then RoPE
+    on K (rotate_rows, ops.rs:433-452).  The gathered rows equal bf16 of the
+    oracle's rows bit for bit."""
+    rng = np.random.default_rng(hd + n_c + 10 * bias + 100 * norm + 1000 * v_norm + rot)
     eps = 1e-6
     n_t, kvs = n_p + n_c, hkv * hd
     cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
@@ -603,8 +607,9 @@ def test_cache_store_whole_tiles_epilogue(dev, hd, hkv, h, n_p, n_c, bias, norm,
     put = lambda x: dev.put(x) if x is not None else None  # noqa: E731
     out = dev.empty(n_c * h * hd)
     p_c = dr.Pass(dev.ctx, range(n_p, n_t))
+    rope = dr.Rope(dev.ctx, n_t, rot, 10000.0) if rot else None
     cache.step_epi(0, [(dev.put(Q), out, p_c, dev.put(K), dev.put(V))], h, scale=1 / math.sqrt(hd),
-                   bk=put(bk), bv=put(bv), k_norm_w=put(kn), v_norm=v_norm, eps=eps)
+                   bk=put(bk), bv=put(bv), k_norm_w=put(kn), v_norm=v_norm, eps=eps, rope=rope)
     wk, wv = K.reshape(-1).copy(), V.reshape(-1).copy()
     if bias:
         orc.add_bias(wk, bk, n_c)
@@ -618,6 +623,8 @@ def test_cache_store_whole_tiles_epilogue(dev, hd, hkv, h, n_p, n_c, bias, norm,
             seg = wv[o:o + hd].copy()
             orc.rms_norm_noscale(seg, eps)
             wv[o:o + hd] = seg
+    if rot:
+        orc.rotate_rows(wk, orc.rope_table(n_t, rot, 10000.0), list(range(n_p, n_t)), hkv, hd, rot)
     ok, ov = dev.empty(n_c * kvs), dev.empty(n_c * kvs)
     cache.gather(0, list(range(n_p, n_t)), ok, ov)
     t = dev.t
