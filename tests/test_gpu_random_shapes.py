@@ -5,7 +5,8 @@ Each case draws a shape and the options a caller can combine: head dims
 that fill their tile or not (multiples of 4 or not), GQA groups, sliding
 windows, causal prefixes, batch slots, QK-norm, contiguous or scattered
 query positions, a forced kernel family, forced key splits merged in-kernel
-or by the merge kernel, bf16 Q rows where the stream kernel runs, and
+or by the merge kernel, bf16 Q rows where the stream kernel runs, key
+counts that fill whole 32-key tiles (the cache store's tile kernel), and
 hi/lo-precision layers (checked against the oracle on the unrounded f32
 inputs, since that kernel is f32-accurate).  The seeds are fixed, so every
 run draws the same cases.  Needs an MI355X.
@@ -25,7 +26,7 @@ from test_gpu_kernels import dev, say  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 96
+N_CASES = 128
 
 
 def _draw(seed: int) -> dict:
@@ -48,6 +49,11 @@ def _draw(seed: int) -> dict:
     qk_norm = bool(rng.random() < 0.4)
     bf16_q = kernel == dr.KERNEL_STREAMS and rng.random() < 0.5
     hilo = kernel == dr.KERNEL_AUTO and rng.random() < 0.35
+    if seed % 4 == 0:
+        # whole 32-key tiles from position 0: the cache store's tile kernel
+        n_p = (n_p + n_c + 31) // 32 * 32 - n_c
+        if prefix is not None:
+            prefix = min(prefix, n_p + n_c - 1)
     return dict(kernel=kernel, hd=hd, hkv=hkv, h=hkv * group, n_p=n_p, n_c=n_c, batch=batch,
                 window=window, prefix=prefix, scattered=scattered, split=split, in_kernel=in_kernel,
                 qk_norm=qk_norm, bf16_q=bf16_q, hilo=hilo, seed=seed)
