@@ -353,9 +353,9 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
 
 // The store of rows that fill whole 32-key V^T tiles at contiguous positions
 // (pos0 and n multiples of 32), head dim == HD (64, 128 or 256), without lo
-// halves: the canvas rows of every denoise step.  One
-// workgroup per (kv head, tile); thread (rg, dc), rg fastest, holds the 4
-// dims 4 dc .. 4 dc + 3 of the tile's rows RPG rg .. RPG rg + RPG - 1.
+// halves: the canvas rows of every denoise step.  One workgroup per (kv
+// head, tile); thread (rg, dc), rg fastest, holds the 4 dims 4 dc .. 4 dc + 3
+// of the tile's rows RPG rg .. RPG rg + RPG - 1.
 // - Loads: per instruction the wave reads whole 128-byte lines (hd 128: 8
 //   rows x 128 B), against 64-byte pieces at a 64-byte lane stride in
 //   kv_store_kernel.
@@ -371,8 +371,9 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
 //   4 dc + e of the tile; the NRG lanes of one dc together write that
 //   d-row's 64 bytes whole, so no LDS transpose and no barrier is needed.
 // Same values as kv_store_kernel: bf16 (round to nearest even) of each f32.
-// EPI: the biases and norms are compiled in (without them, the conditional
-// updates of the loaded rows made the K stores wait for every load).
+// EPI: the epilogue (biases, norms, RoPE) is compiled in; the plain build
+// keeps it out, since its conditional updates of the loaded rows made the K
+// stores wait for every load.
 template <int HD, bool EPI>
 __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) {
     constexpr int CPR = HD / 4;     // 4-dim pieces per row
@@ -398,100 +399,102 @@ __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) 
         xv[j] = *reinterpret_cast<const f32x4*>(a.v + src + j * rstride);
     }
     if constexpr (EPI) {
-    const int half = a.rot / 2;
-    const int d0 = 4 * dc;
-    const bool rot_me = a.rope && d0 < a.rot;
-    f32x4 tab[RPG][2];  // (sin, cos) of pairs jj .. jj + 3 at each row's position
-    if (rot_me) {
-        const int jj = d0 < half ? d0 : d0 - half;
-        const int pp = (a.pos0 >= 0 ? a.pos0 : 0) + r0;
-#pragma unroll
-        for (int j = 0; j < RPG; ++j) {
-            const float* t = a.rope + ((size_t)(pp + j) * half + jj) * 2;
-            tab[j][0] = *reinterpret_cast<const f32x4*>(t);
-            tab[j][1] = *reinterpret_cast<const f32x4*>(t + 4);
-        }
-    }
-    f32x4 kw4 = {}, kb4 = {}, vb4 = {};
-    if (a.kn_w) kw4 = *reinterpret_cast<const f32x4*>(a.kn_w + 4 * dc);
-    if (a.kb) kb4 = *reinterpret_cast<const f32x4*>(a.kb + (size_t)g * HD + 4 * dc);
-    if (a.vb) vb4 = *reinterpret_cast<const f32x4*>(a.vb + (size_t)g * HD + 4 * dc);
-    if (a.kb || a.vb) {
-#pragma unroll
-        for (int j = 0; j < RPG; ++j) {
-            xk[j] += kb4;
-            xv[j] += vb4;
-        }
-    }
-    if (a.kn_w || a.v_norm) {
-        // rms_norm_inplace (ops.rs:106-114) / rms_norm_noscale: sum of the
-        // row's f32 squares in f64; the row's lanes in this wave are lanes
-        // rg + NRG i, the other CPR / (64 / NRG) - 1 shares are in the
-        // other waves
-        __shared__ double s_ss[2][4][VT_KEYS];  // [K, V][wave][row of the tile]
-        const int wave = tid >> 6;
-        auto row_ss = [&](const f32x4 (&x)[RPG], double (&ss)[RPG]) __attribute__((always_inline)) {
-#pragma unroll
-            for (int j = 0; j < RPG; ++j) {
-                double t = 0.0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float sq = x[j][e] * x[j][e];
-                    t += (double)sq;
-                }
-#pragma unroll
-                for (int off = NRG; off < 64; off <<= 1) t += __shfl_xor(t, off);
-                ss[j] = t;
-            }
-        };
-        double ssk[RPG], ssv[RPG];
-        if (a.kn_w) row_ss(xk, ssk);
-        if (a.v_norm) row_ss(xv, ssv);
-        if ((tid & 63) < NRG) {
-#pragma unroll
-            for (int j = 0; j < RPG; ++j) {
-                if (a.kn_w) s_ss[0][wave][rg * RPG + j] = ssk[j];
-                if (a.v_norm) s_ss[1][wave][rg * RPG + j] = ssv[j];
-            }
-        }
-        __syncthreads();
-        auto scale_of = [&](int kv, int j) __attribute__((always_inline)) {
-            const double t = ((s_ss[kv][0][rg * RPG + j] + s_ss[kv][1][rg * RPG + j]) + s_ss[kv][2][rg * RPG + j]) +
-                             s_ss[kv][3][rg * RPG + j];
-            return 1.0f / (float)sqrt(t / (double)HD + (double)a.kn_eps);
-        };
-#pragma unroll
-        for (int j = 0; j < RPG; ++j) {
-            if (a.kn_w) {
-                const float sc = scale_of(0, j);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) xk[j][e] = xk[j][e] * sc * kw4[e];
-            }
-            if (a.v_norm) {
-                const float sc = scale_of(1, j);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) xv[j][e] *= sc;
-            }
-        }
-    }
-    if (a.rope) {
-        __shared__ __align__(16) float s_k[VT_KEYS][HD + 4];  // the tile's normed K rows
-#pragma unroll
-        for (int j = 0; j < RPG; ++j) *reinterpret_cast<f32x4*>(&s_k[rg * RPG + j][d0]) = xk[j];
-        __syncthreads();
+        const int half = a.rot / 2;
+        const int d0 = 4 * dc;
+        const bool rot_me = a.rope && d0 < a.rot;
+        f32x4 tab[RPG][2];  // (sin, cos) of pairs jj .. jj + 3 at each row's position
         if (rot_me) {
-            const int pd0 = d0 < half ? d0 + half : d0 - half;
+            const int jj = d0 < half ? d0 : d0 - half;
+            const int pp = (a.pos0 >= 0 ? a.pos0 : 0) + r0;
 #pragma unroll
             for (int j = 0; j < RPG; ++j) {
-                const f32x4 xp = *reinterpret_cast<const f32x4*>(&s_k[rg * RPG + j][pd0]);
+                const float* t = a.rope + ((size_t)(pp + j) * half + jj) * 2;
+                tab[j][0] = *reinterpret_cast<const f32x4*>(t);
+                tab[j][1] = *reinterpret_cast<const f32x4*>(t + 4);
+            }
+        }
+        f32x4 kw4 = {}, kb4 = {}, vb4 = {};
+        if (a.kn_w) kw4 = *reinterpret_cast<const f32x4*>(a.kn_w + 4 * dc);
+        if (a.kb) kb4 = *reinterpret_cast<const f32x4*>(a.kb + (size_t)g * HD + 4 * dc);
+        if (a.vb) vb4 = *reinterpret_cast<const f32x4*>(a.vb + (size_t)g * HD + 4 * dc);
+        // (each bias only where given: adding a zero would turn -0.0 into +0.0)
+        if (a.kb) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float sn = tab[j][e >> 1][2 * (e & 1)], cs = tab[j][e >> 1][2 * (e & 1) + 1];
-                    xk[j][e] = d0 < half ? rope_lo(xk[j][e], xp[e], sn, cs) : rope_hi(xp[e], xk[j][e], sn, cs);
+            for (int j = 0; j < RPG; ++j) xk[j] += kb4;
+        }
+        if (a.vb) {
+#pragma unroll
+            for (int j = 0; j < RPG; ++j) xv[j] += vb4;
+        }
+        if (a.kn_w || a.v_norm) {
+            // rms_norm_inplace (ops.rs:106-114) / rms_norm_noscale: sum of the
+            // row's f32 squares in f64; the row's lanes in this wave are lanes
+            // rg + NRG i, the other CPR / (64 / NRG) - 1 shares are in the
+            // other waves
+            __shared__ double s_ss[2][4][VT_KEYS];  // [K, V][wave][row of the tile]
+            const int wave = tid >> 6;
+            auto row_ss = [&](const f32x4 (&x)[RPG], double (&ss)[RPG]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < RPG; ++j) {
+                    double t = 0.0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float sq = x[j][e] * x[j][e];
+                        t += (double)sq;
+                    }
+#pragma unroll
+                    for (int off = NRG; off < 64; off <<= 1) t += __shfl_xor(t, off);
+                    ss[j] = t;
+                }
+            };
+            double ssk[RPG], ssv[RPG];
+            if (a.kn_w) row_ss(xk, ssk);
+            if (a.v_norm) row_ss(xv, ssv);
+            if ((tid & 63) < NRG) {
+#pragma unroll
+                for (int j = 0; j < RPG; ++j) {
+                    if (a.kn_w) s_ss[0][wave][rg * RPG + j] = ssk[j];
+                    if (a.v_norm) s_ss[1][wave][rg * RPG + j] = ssv[j];
+                }
+            }
+            __syncthreads();
+            auto scale_of = [&](int kv, int j) __attribute__((always_inline)) {
+                const double t = ((s_ss[kv][0][rg * RPG + j] + s_ss[kv][1][rg * RPG + j]) + s_ss[kv][2][rg * RPG + j]) +
+                                 s_ss[kv][3][rg * RPG + j];
+                return 1.0f / (float)sqrt(t / (double)HD + (double)a.kn_eps);
+            };
+#pragma unroll
+            for (int j = 0; j < RPG; ++j) {
+                if (a.kn_w) {
+                    const float sc = scale_of(0, j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xk[j][e] = xk[j][e] * sc * kw4[e];
+                }
+                if (a.v_norm) {
+                    const float sc = scale_of(1, j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xv[j][e] *= sc;
                 }
             }
         }
-    }
+        if (a.rope) {
+            __shared__ __align__(16) float s_k[VT_KEYS][HD + 4];  // the tile's normed K rows
+#pragma unroll
+            for (int j = 0; j < RPG; ++j) *reinterpret_cast<f32x4*>(&s_k[rg * RPG + j][d0]) = xk[j];
+            __syncthreads();
+            if (rot_me) {
+                const int pd0 = d0 < half ? d0 + half : d0 - half;
+#pragma unroll
+                for (int j = 0; j < RPG; ++j) {
+                    const f32x4 xp = *reinterpret_cast<const f32x4*>(&s_k[rg * RPG + j][pd0]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float sn = tab[j][e >> 1][2 * (e & 1)], cs = tab[j][e >> 1][2 * (e & 1) + 1];
+                        xk[j][e] = d0 < half ? rope_lo(xk[j][e], xp[e], sn, cs) : rope_hi(xp[e], xk[j][e], sn, cs);
+                    }
+                }
+            }
+        }
     }
     const int p0 = a.pos0 >= 0 ? a.pos0 : 0;  // (host: pos0 >= 0, or no position list)
     uint16_t* kdst = a.kc + ((size_t)g * a.cap + p0 + r0) * HD + 4 * dc;
