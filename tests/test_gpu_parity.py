@@ -578,6 +578,34 @@ def test_cache_store_whole_tiles_is_bf16(dev, hd, hkv, p0, n, n_batch):
         assert np.array_equal(dev.get(ov), bf(wv)), b
 
 
+@pytest.mark.parametrize("hd,hkv,n,n_tot,n_batch", [(128, 32, 256, 768, 1), (128, 3, 173, 400, 2), (64, 5, 40, 90, 1),
+                                                 (256, 8, 100, 4352, 1), (256, 2, 7, 64, 2), (96, 2, 77, 200, 1)])
+def test_cache_store_position_list_is_bf16(dev, hd, hkv, n, n_tot, n_batch):
+    """Rows stored at sorted scattered positions (split_active's active rows,
+    on kv_store_kernel's position-list V^T path): gather returns bf16 of every
+    stored row bit for bit (cache.rs:62-82), and every other position keeps
+    its value."""
+    rng = np.random.default_rng(hd * 7 + n + n_tot)
+    cache = dr.StepCache(dev.ctx, n_tot, [hkv] * 2, [hd] * 2, n_batch=n_batch)
+    t = dev.t
+    bf = lambda a: t.from_numpy(a).to(t.bfloat16).to(t.float32).numpy().reshape(-1)  # noqa: E731
+    every = list(range(n_tot))
+    for b in range(n_batch):
+        K0 = rng.standard_normal((n_tot, hkv * hd), dtype=np.float32)
+        V0 = rng.standard_normal((n_tot, hkv * hd), dtype=np.float32)
+        cache.store(1, dr.Pass(dev.ctx, every), dev.put(K0), dev.put(V0), batch=b)
+        pos = sorted(rng.choice(n_tot, size=n, replace=False).tolist())
+        K = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+        V = rng.standard_normal((n, hkv * hd), dtype=np.float32)
+        cache.store(1, dr.Pass(dev.ctx, pos), dev.put(K), dev.put(V), batch=b)
+        wk, wv = K0.copy(), V0.copy()
+        wk[pos], wv[pos] = K, V
+        ok, ov = dev.empty(n_tot * hkv * hd), dev.empty(n_tot * hkv * hd)
+        cache.gather(1, every, ok, ov, batch=b)
+        assert np.array_equal(dev.get(ok), bf(wk)), b
+        assert np.array_equal(dev.get(ov), bf(wv)), b
+
+
 @pytest.mark.parametrize("hd,hkv,h,n_p,n_c,bias,norm,v_norm,rot", [
     (128, 16, 16, 512, 256, False, True, False, 0),   # C4-like QK-norm
     (128, 16, 16, 512, 256, True, True, False, 128),  # the same with the biases and RoPE
