@@ -244,24 +244,10 @@ void attn_ring_kernel(const AttnArgs a) {
             prefix_free = s_red[2] == 0;
         }
         tiles_can_be_full = prefix_free && S.qseq == nullptr;
-        if (a.window >= 0) {
-            const long lo = max(0L, (long)qmin - a.window + 1);
-            const long hi = min((long)S.nk, (long)qmax + a.window);
-            if (hi <= lo) {
-                kt_lo = kt_hi = 0;
-            } else {
-                kt_lo = (int)(lo / BN);
-                kt_hi = (int)((hi + BN - 1) / BN);
-            }
-        }
+        if (a.window >= 0) band_tile_range(S.nk, a.window, qmin, qmax, kt_lo, kt_hi);
     }
-    int t0 = kt_lo, t1 = kt_hi;
-    if (a.n_split > 1) {
-        const int ntiles = kt_hi - kt_lo;
-        const int per = (ntiles + a.n_split - 1) / a.n_split;
-        t0 = kt_lo + min(split * per, ntiles);
-        t1 = kt_lo + min((split + 1) * per, ntiles);
-    }
+    int t0, t1;
+    split_tile_range(kt_lo, kt_hi, a.n_split, split, t0, t1);
     const int nt = t1 - t0;  // tiles of this workgroup: t0 + j, j < nt
 
     // ---- the K / V^T planes of kv head g, and this wave's DMA offsets.
@@ -305,15 +291,14 @@ void attn_ring_kernel(const AttnArgs a) {
     // the row group), so the row groups of one kv head, which share an XCD,
     // first request different tiles: the head's K/V comes from HBM in one
     // round, and later tiles are L2 hits.
-    // (The first DMA is issued even when the wave has no tile: its data is
-    // never used, and past the cache the descriptor returns zeros.)
-    const int kw = wave < nt ? (nt - wave + RW - 1) / RW : 0;  // this wave's tiles
-    const int krot = kw > 1 ? rg % kw : 0;
-    auto tile_at = [&](int k) __attribute__((always_inline)) {
-        const int kk = k + krot;
-        return t0 + wave + RW * (kk >= kw ? kk - kw : kk);
-    };
-    issue_k(kw > 0 ? tile_at(0) : t0 + wave);
+    // (The first DMA is issued even when the wave has no tile, unconditional
+    // for the compiler's wait accounting; its data is never used, and it reads
+    // a tile clamped into the cache plane, since the tile base goes in the
+    // DMA's scalar offset, which the descriptor's range check excludes.)
+    const RingWaveTiles wt(t0, nt, wave, RW, rg, a.cap / BN);
+    const int kw = wt.kw;  // this wave's tiles
+    auto tile_at = [&](int k) __attribute__((always_inline)) { return wt.at(k); };
+    issue_k(wt.first_dma());
 
     if (rope && S.qpos0 < 0) load_tab(tab_pos);
     if (q_bf16) {  // widened exactly to f32
@@ -376,7 +361,7 @@ void attn_ring_kernel(const AttnArgs a) {
     // requested only now: at kernel start every CU asks for its Q rows and
     // first tiles at once, and the smaller that burst, the sooner Q and the
     // first K tile land.  (DMA order stays K0, V0, K1, ...)
-    issue_v(kw > 0 ? tile_at(0) : t0 + wave);
+    issue_v(wt.first_dma());
     // Q^T fragments, held for the whole key loop: lane (col, hf) supplies
     // row col, dims 16 c + 8 hf .. + 8 of contraction step c
     bf16x8 qf[KS];

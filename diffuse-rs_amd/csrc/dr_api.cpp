@@ -24,6 +24,20 @@ namespace {
 
 thread_local std::string g_err;
 
+// Every device and pinned host allocation the library makes goes through
+// these two, which count it (dr_debug_alloc_count).
+std::atomic<long> g_allocs{0};
+template <typename T>
+hipError_t dev_malloc(T** p, size_t bytes) {
+    g_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(reinterpret_cast<void**>(p), bytes);
+}
+template <typename T>
+hipError_t host_malloc(T** p, size_t bytes) {
+    g_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipHostMalloc(reinterpret_cast<void**>(p), bytes);
+}
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -72,7 +86,7 @@ int ensure(DevBuf& b, size_t bytes) {
         if (e != hipSuccess) return hip_fail(e, "hipFree");
     }
     size_t nb = std::max(bytes, (size_t)4096);
-    DR_HIP(hipMalloc(&b.p, nb));
+    DR_HIP(dev_malloc(&b.p, nb));
     b.cap = nb;
     return DR_OK;
 }
@@ -86,7 +100,7 @@ int grow(DevBuf& b, size_t bytes, std::vector<void*>& retired) {
     if (bytes <= b.cap) return DR_OK;
     const size_t nb = std::max({bytes, 2 * b.cap, (size_t)4096});
     void* p = nullptr;
-    DR_HIP(hipMalloc(&p, nb));
+    DR_HIP(dev_malloc(&p, nb));
     if (b.p) retired.push_back(b.p);
     b.p = p;
     b.cap = nb;
@@ -185,7 +199,7 @@ int reserve_pass(dr_pass* p, size_t n) {
         p->cap = 0;
         if (e != hipSuccess) return hip_fail(e, "hipFree");
     }
-    DR_HIP(hipMalloc(&p->d_pos, n * sizeof(int32_t)));
+    DR_HIP(dev_malloc(&p->d_pos, n * sizeof(int32_t)));
     p->cap = n;
     return DR_OK;
 }
@@ -266,7 +280,7 @@ int dr_ctx_create(int device, dr_ctx** out) {
     }
     // the in-kernel split merge's tickets: allocated and zeroed here, once,
     // so that no call allocates or clears them (each merge resets its own)
-    e = hipMalloc(&c->tick.p, TICKETS * sizeof(int));
+    e = dev_malloc(&c->tick.p, TICKETS * sizeof(int));
     if (e == hipSuccess) {
         c->tick.cap = TICKETS * sizeof(int);
         e = hipMemsetAsync(c->tick.p, 0, TICKETS * sizeof(int), c->own);
@@ -478,7 +492,7 @@ int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n
         const size_t bytes = (size_t)n_head_kv[l] * c->cap * c->hd_tile[l] * sizeof(uint16_t);
         for (size_t b = 0; b < n_batch; ++b) {
             for (uint16_t** dst : {&c->k[l * n_batch + b], &c->vt[l * n_batch + b]}) {
-                hipError_t e = hipMalloc(reinterpret_cast<void**>(dst), bytes);
+                hipError_t e = dev_malloc(reinterpret_cast<void**>(dst), bytes);
                 if (e == hipSuccess) e = hipMemset(*dst, 0, bytes);
                 if (e != hipSuccess) {
                     dr_cache_destroy(c);
@@ -527,7 +541,7 @@ int dr_cache_set_precision(dr_step_cache* cache, size_t layer, int precision) {
             uint16_t*& lo = *plo;
             if (precision == DR_PRECISION_HILO && !lo) {
                 // (zero: rows stored before this call carry no lo half)
-                hipError_t e = hipMalloc(reinterpret_cast<void**>(&lo), bytes);
+                hipError_t e = dev_malloc(reinterpret_cast<void**>(&lo), bytes);
                 if (e == hipSuccess) e = hipMemset(lo, 0, bytes);
                 if (e != hipSuccess) {
                     if (lo) (void)hipFree(lo);
@@ -575,7 +589,7 @@ int dr_rope_create(dr_ctx* ctx, size_t max_len, size_t rope_dim, float theta,
     ctx_retain(ctx);
     r->max_len = max_len;
     r->rope_dim = rope_dim;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&r->d_table), h.size() * sizeof(float));
+    hipError_t e = dev_malloc(reinterpret_cast<void**>(&r->d_table), h.size() * sizeof(float));
     if (e == hipSuccess)
         e = hipMemcpy(r->d_table, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -746,8 +760,8 @@ int state_to_device(dr_step_cache* c, dr_step_cache::Slot& s) {
     if (s.dev_state) return DR_OK;
     DR_CHECK(use_device(c->ctx));
     const size_t bytes = std::max(c->n_total, (size_t)1) * sizeof(int32_t);
-    if (!s.d_prev) DR_HIP(hipMalloc(&s.d_prev, bytes));
-    if (!s.d_lc) DR_HIP(hipMalloc(&s.d_lc, bytes));
+    if (!s.d_prev) DR_HIP(dev_malloc(&s.d_prev, bytes));
+    if (!s.d_lc) DR_HIP(dev_malloc(&s.d_lc, bytes));
     if (c->n_total > 0) {
         DR_HIP(hipMemcpyAsync(s.d_prev, s.prev_seq.data(), c->n_total * sizeof(int32_t),
                               hipMemcpyHostToDevice, c->ctx->stream));
@@ -818,7 +832,7 @@ int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t*
     if (!cache->h_meta) {
         // the six results go straight to pinned host memory (no copy call
         // between the kernel and the synchronisation the caller waits on)
-        DR_HIP(hipHostMalloc(&cache->h_meta, 6 * sizeof(int32_t)));
+        DR_HIP(host_malloc(&cache->h_meta, 6 * sizeof(int32_t)));
         DR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&cache->h_meta_dev), cache->h_meta, 0));
     }
     dr::SplitArgs a{};
@@ -1040,22 +1054,21 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
 }
 
 // The hi/lo kernel reads plain Q: with a Q epilogue (bias, QK-norm, RoPE),
-// each batch slot's Q is copied into the context's workspace and the
-// epilogue (qkv_epilogue.hip, Q heads only) runs there first.
-static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws) {
-    if (!a.qn_w && !a.qb && !a.rope) return DR_OK;
-    // the QK-norm alone, at a full head-dim tile: the kernel applies it as it
-    // loads Q (a row's sum of squares over four lanes of one wave, or of the
-    // row block's two waves at hd 512)
-    if (!a.qb && !a.rope && a.hd == p.hd_tile) return DR_OK;
-    if (fixed_ws)
-        return fail(DR_ERR_UNSUPPORTED,
-                    "dr_attention_cached_noalloc: a hi/lo-precision layer with a Q epilogue needs a Q "
-                    "workspace (normalize Q first, or use dr_attention_cached)");
+// each batch slot's Q is copied into a workspace and the epilogue
+// (qkv_epilogue.hip, Q heads only) runs there first.  Bytes of that
+// workspace (0: the kernel reads the caller's rows): the QK-norm alone at a
+// full head-dim tile needs none, the kernel applies it as it loads Q (a
+// row's sum of squares over four lanes of one wave, or of the row block's
+// two waves at hd 512).
+static size_t hilo_q_bytes(const dr::AttnArgs& a, const dr::LaunchPlan& p) {
+    if (p.kernel != dr::KERNEL_HILO || (!a.qn_w && !a.qb && !a.rope)) return 0;
+    if (!a.qb && !a.rope && a.hd == p.hd_tile) return 0;
     size_t total = 0;
     for (int b = 0; b < a.n_batch; ++b) total += (size_t)a.slot[b].nq * a.q_rstride;
-    DR_CHECK(grow(ctx->qpre, total * sizeof(float), ctx->retired));
-    float* base = static_cast<float*>(ctx->qpre.p);
+    return total * sizeof(float);
+}
+
+static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, float* base) {
     for (int b = 0; b < a.n_batch; ++b) {
         dr::AttnSlot& s = a.slot[b];
         const size_t n = (size_t)s.nq * a.q_rstride;
@@ -1102,22 +1115,34 @@ static int check_q_dtype(const dr::AttnArgs& a, const dr::LaunchPlan& p, const c
 
 static int launch_plan(dr_ctx* ctx, dr::AttnArgs& a, const dr::LaunchPlan& p, bool fixed_ws = false) {
     DR_CHECK(check_q_dtype(a, p, "attention"));
-    if (p.kernel == dr::KERNEL_HILO) DR_CHECK(hilo_prepare_q(ctx, a, p, fixed_ws));
+    // device memory beyond the inputs and outputs: the key-split partials,
+    // and the hi/lo kernel's copy of Q with its epilogue applied
     const size_t ws = dr::split_workspace_bytes(p, a.n_batch, a.n_head_kv);
-    if (ws > 0) {
-        if (fixed_ws) {
-            if (ws > dr::scratch_bytes())
-                return fail(DR_ERR_INVALID,
-                            "dr_attention_cached_noalloc: the plan's %d key splits need %zu bytes of "
-                            "workspace, more than the fixed %zu",
-                            p.n_split, ws, dr::scratch_bytes());
-            a.part_o = static_cast<float*>(dr::scratch_ptr(ctx->device));
-            if (!a.part_o) return fail(DR_ERR_HIP, "the device scratch of device %d is not set up", ctx->device);
-        } else {
+    const size_t qws = hilo_q_bytes(a, p);
+    float* qpre = nullptr;
+    if (fixed_ws) {
+        // both in the fixed scratch, Q after the partials (256-byte aligned)
+        const size_t qoff = round_up(ws, 256);
+        if (qoff + qws > dr::scratch_bytes())
+            return fail(DR_ERR_INVALID,
+                        "dr_attention_cached_noalloc: the plan (%d key splits%s) needs %zu bytes of "
+                        "workspace, more than the fixed %zu",
+                        p.n_split, qws ? ", hi/lo Q epilogue" : "", qoff + qws, dr::scratch_bytes());
+        char* base = static_cast<char*>(dr::scratch_ptr(ctx->device));
+        if (!base) return fail(DR_ERR_HIP, "the device scratch of device %d is not set up", ctx->device);
+        if (ws > 0) a.part_o = reinterpret_cast<float*>(base);
+        if (qws > 0) qpre = reinterpret_cast<float*>(base + qoff);
+    } else {
+        if (ws > 0) {
             DR_CHECK(grow(ctx->part, ws, ctx->retired));
             a.part_o = static_cast<float*>(ctx->part.p);
         }
+        if (qws > 0) {
+            DR_CHECK(grow(ctx->qpre, qws, ctx->retired));
+            qpre = static_cast<float*>(ctx->qpre.p);
+        }
     }
+    if (qpre) DR_CHECK(hilo_prepare_q(ctx, a, qpre));
     // Key splits of the per-wave-stream kernel merge in-kernel when they are
     // few enough for its registers, the context's tickets cover the row
     // blocks and the partials' byte offsets fit the kernel's 32-bit buffer
@@ -1479,6 +1504,63 @@ int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const
     DR_CHECK(launch_planned(ctx, a, (int)hd, (int)nq, (int)nk, mask, dr::QEPI_NONE));
     DR_HIP(hipMemcpyAsync(out, ctx->out.p, qb, hipMemcpyDeviceToHost, st));
     DR_HIP(hipStreamSynchronize(st));
+    return DR_OK;
+}
+
+long dr_debug_alloc_count(void) { return g_allocs.load(std::memory_order_relaxed); }
+
+int dr_debug_ring_tiles(size_t head_dim, size_t nk, size_t cap, long long window, long long qmin,
+                        long long qmax, size_t n_split, int* min_tile, int* max_tile, int* partition_ok) {
+    const int rw = dr::ring_waves((int)head_dim);
+    if (rw == 0) return fail(DR_ERR_UNSUPPORTED, "no stream kernel at head_dim %zu", head_dim);
+    if (!min_tile || !max_tile || !partition_ok || n_split < 1 || nk > cap || cap % dr::KEY_ALIGN != 0 ||
+        cap == 0 || cap >= MAX_POS)
+        return fail(DR_ERR_INVALID, "dr_debug_ring_tiles: bad arguments");
+    // the workgroup's key tile range, as the kernel derives it
+    int kt_lo = 0, kt_hi = (int)((nk + 31) / 32);
+    if (window >= 0) {
+        if (window >= (long long)MAX_POS || qmin < 0 || qmax < qmin || qmax >= (long long)MAX_POS)
+            return fail(DR_ERR_INVALID, "dr_debug_ring_tiles: bad window or query range");
+        dr::band_tile_range((int)nk, (int)window, (int)qmin, (int)qmax, kt_lo, kt_hi);
+    }
+    const int cap_tiles = (int)(cap / 32);
+    int lo = INT32_MAX, hi = INT32_MIN;
+    bool ok = true;
+    std::vector<int> mult(cap_tiles, 0);
+    for (int split = 0; split < (int)n_split; ++split) {
+        int t0, t1;
+        dr::split_tile_range(kt_lo, kt_hi, (int)n_split, split, t0, t1);
+        for (int rg = 0; rg < 24; ++rg) {  // (the row group only rotates each wave's order)
+            std::vector<int> seen(cap_tiles, 0);
+            for (int w = 0; w < rw; ++w) {
+                const dr::RingWaveTiles wt(t0, t1 - t0, w, rw, rg, cap_tiles);
+                const int f = wt.first_dma();
+                lo = std::min(lo, f);
+                hi = std::max(hi, f);
+                for (int k = 0; k < wt.kw; ++k) {
+                    const int t = wt.at(k);
+                    lo = std::min(lo, t);
+                    hi = std::max(hi, t);
+                    if (t < t0 || t >= t1 || t < 0 || t >= cap_tiles) {
+                        ok = false;
+                    } else {
+                        ++seen[t];
+                    }
+                }
+            }
+            for (int t = 0; t < cap_tiles; ++t) {
+                const bool in = t >= t0 && t < t1;
+                if (seen[t] != (in ? 1 : 0)) ok = false;
+                if (rg == 0) mult[t] += seen[t];
+            }
+        }
+    }
+    // the splits together cover the range once
+    for (int t = 0; t < cap_tiles; ++t)
+        if (mult[t] != ((t >= kt_lo && t < kt_hi) ? 1 : 0)) ok = false;
+    *min_tile = lo;
+    *max_tile = hi;
+    *partition_ok = ok ? 1 : 0;
     return DR_OK;
 }
 

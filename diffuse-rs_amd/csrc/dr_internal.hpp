@@ -206,6 +206,64 @@ struct QmmArgs {
     const float* residual;   // [n][rows] or nullptr (may alias out)
 };
 
+// The 32-key tiles [kt_lo, kt_hi) that a block of queries at positions
+// qmin..qmax can see through a sliding window (|qpos - kpos| < window,
+// attention.rs:43-47) among nk keys at positions 0..nk-1.
+__host__ __device__ inline void band_tile_range(int nk, int window, int qmin, int qmax, int& kt_lo,
+                                                int& kt_hi) {
+    long lo = (long)qmin - window + 1, hi = (long)qmax + window;
+    if (lo < 0) lo = 0;
+    if (hi > nk) hi = nk;
+    if (hi <= lo) {
+        kt_lo = kt_hi = 0;
+    } else {
+        kt_lo = (int)(lo / 32);
+        kt_hi = (int)((hi + 31) / 32);
+    }
+}
+
+// Key tiles [t0, t1) of split `split` of n_split over a workgroup's key tile
+// range [kt_lo, kt_hi): ceil-sized consecutive pieces, the last ones possibly
+// empty.
+__host__ __device__ inline void split_tile_range(int kt_lo, int kt_hi, int n_split, int split, int& t0,
+                                                 int& t1) {
+    t0 = kt_lo;
+    t1 = kt_hi;
+    if (n_split > 1) {
+        const int ntiles = kt_hi - kt_lo;
+        const int per = (ntiles + n_split - 1) / n_split;
+        const int a = split * per, b = (split + 1) * per;
+        t0 = kt_lo + (a < ntiles ? a : ntiles);
+        t1 = kt_lo + (b < ntiles ? b : ntiles);
+    }
+}
+
+// The key tiles one wave of attn_ring_kernel requests.  Wave w of a workgroup
+// whose key range is tiles [t0, t0 + nt) owns tiles t0 + w, t0 + w + rw, ...
+// (kw of them) and walks them from its krot-th on, krot = row group mod kw,
+// so the row groups of one kv head first request different tiles.  A wave
+// with no tile still issues one K and one V^T DMA (the compiler's vmcnt
+// accounting assumes them); that DMA reads tile min(t0 + w, cap_tiles - 1),
+// which lies inside the cache plane: the tile base is the DMA's scalar
+// offset, which the buffer range check does not cover.  Kernel and host
+// (dr_debug_ring_tiles) both use this.
+struct RingWaveTiles {
+    int t0, wave, rw, kw, krot, idle_tile;
+    __host__ __device__ RingWaveTiles(int t0_, int nt, int wave_, int rw_, int rg, int cap_tiles)
+        : t0(t0_), wave(wave_), rw(rw_) {
+        kw = wave < nt ? (nt - wave + rw - 1) / rw : 0;
+        krot = kw > 1 ? rg % kw : 0;
+        idle_tile = t0 + wave < cap_tiles - 1 ? t0 + wave : cap_tiles - 1;
+    }
+    // the k-th tile this wave multiplies, k < kw
+    __host__ __device__ int at(int k) const {
+        const int kk = k + krot;
+        return t0 + wave + rw * (kk >= kw ? kk - kw : kk);
+    }
+    // the tile of the wave's first K and V^T DMA
+    __host__ __device__ int first_dma() const { return kw > 0 ? at(0) : idle_tile; }
+};
+
 // Masking mode of an attention launch.
 enum MaskMode : int {
     MASK_NONE = 0,  // every key visible (only the key tail is masked)

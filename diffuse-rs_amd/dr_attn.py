@@ -162,6 +162,9 @@ _SIGS = {
     "dr_attention_cached_noalloc": (_I, [_VP, _SZ, ctypes.POINTER(CBatchItem), _SZ, _SZ, OptUsize, OptUsize, _F,
                                          _VP, _F]),
     "dr_attention_step": (_I, [_VP, _SZ, ctypes.POINTER(CStepItem), _SZ, _SZ, OptUsize, OptUsize, _F, _VP, _F, _VP, _F]),
+    "dr_debug_alloc_count": (ctypes.c_long, []),
+    "dr_debug_ring_tiles": (_I, [_SZ, _SZ, _SZ, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong, _SZ,
+                                 ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
 }
 
 
@@ -591,3 +594,19 @@ def quantize_q8k(ctx: Context, act, n: int, cols: int, out) -> None:
     """quantize_rows_q8_k (kernels.rs:79-122) into n * cols/256 BlockQ8K
     (292 bytes each) at device pointer / tensor out."""
     _check(ctx.lib.dr_quantize_q8k(ctx.h, _ptr(act), n, cols, _ptr(out)))
+
+
+def alloc_count() -> int:
+    """Device and pinned host allocations the library has made in this
+    process (dr_debug_alloc_count)."""
+    return int(load().dr_debug_alloc_count())
+
+
+def ring_tiles(head_dim: int, nk: int, cap: int, window: Optional[int], qmin: int, qmax: int,
+               n_split: int) -> tuple:
+    """(min tile, max tile, partition ok) over every DMA the stream kernel's
+    waves issue for one workgroup (dr_debug_ring_tiles); host-only."""
+    lo, hi, ok = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(load().dr_debug_ring_tiles(head_dim, nk, cap, -1 if window is None else window, qmin, qmax,
+                                      n_split, ctypes.byref(lo), ctypes.byref(hi), ctypes.byref(ok)))
+    return lo.value, hi.value, bool(ok.value)

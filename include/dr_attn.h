@@ -245,13 +245,15 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
 
 /*
  * dr_attention_cached without allocating: the same arguments, checks,
- * kernels and results, but the key-split partials (the only device memory
- * the call uses beyond its inputs and outputs) go to a fixed 64 MiB device
- * array that the library holds on every GPU it runs on until the process
- * ends, instead of the context's growing workspace.  No hipMalloc, hipFree
+ * kernels and results, but the device memory the call uses beyond its
+ * inputs and outputs (the key-split partials, and on a DR_PRECISION_HILO
+ * layer whose Q epilogue runs as a pass of its own, the Q copy it writes)
+ * goes to a fixed 64 MiB device array that the library holds on every GPU it
+ * runs on until the process ends, instead of the context's growing
+ * workspaces.  No hipMalloc, hipFree
  * or allocating library routine runs in the call, so it can be made under
  * hipGraph capture, in serving loops and in harnesses that forbid
- * allocation.  A plan whose splits need more than 64 MiB (far beyond the
+ * allocation.  A plan that needs more than 64 MiB (far beyond the
  * configurations here: DiffusionGemma's 512-wide global layer needs 34 MB)
  * returns DR_ERR_INVALID.  Nothing in the array needs to start at zero.
  * Every call on a GPU shares that GPU's array, so calls that overlap on one
@@ -438,6 +440,22 @@ int dr_ctx_set_split_merge(dr_ctx* ctx, int in_kernel);
  * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
  * to the automatic one. */
 int dr_ctx_set_tuning(dr_ctx* ctx, int row_blocks, int key_groups, int n_split);
+
+/* ---- diagnostics (no counterpart in the reference; for tests) */
+/* Device and pinned host allocations the library has made in this process
+ * (every hipMalloc / hipHostMalloc it calls).  Host-only, never fails. */
+long dr_debug_alloc_count(void);
+/* The key tiles the STREAMS kernel's waves request for one workgroup of a
+ * head_dim 128 / 256 problem: nk keys in a cache of cap positions (a
+ * multiple of 64), queries at positions qmin..qmax under a sliding window
+ * (window < 0: none), n_split key splits, every row group.  Computed on the
+ * host by the same code the kernel runs.  min_tile / max_tile: the extremes
+ * of every tile index any wave issues a DMA for (including a wave without
+ * tiles); partition_ok: 1 if each split's waves multiply each tile of its
+ * range exactly once and the splits cover the workgroup's range once. */
+int dr_debug_ring_tiles(size_t head_dim, size_t nk, size_t cap, long long window, long long qmin,
+                        long long qmax, size_t n_split, int* min_tile, int* max_tile,
+                        int* partition_ok);
 
 #ifdef __cplusplus
 }

@@ -119,3 +119,43 @@ def test_split_active_matches_oracle_random(lib):
         assert got == want
         assert np.array_equal(last_a, last_b)
         prev_a, prev_b = seq.copy(), seq.copy()
+
+
+def test_ring_kernel_dma_stays_inside_the_cache_plane(lib):
+    """Every tile the stream kernel's waves request (a wave without tiles too)
+    lies inside the kv head's cache plane, and each split's waves multiply
+    each tile of its range exactly once.  The tile base is the DMA's scalar
+    offset, which the buffer range check does not cover, so a tile past the
+    plane would read the next allocation.  Host evaluation of the kernel's
+    own tile-assignment code (dr_debug_ring_tiles)."""
+    rng = np.random.default_rng(7)
+    cases = [(128, 32, 64, None, 0, 0, 1), (256, 1, 64, None, 0, 0, 1), (128, 768, 768, None, 0, 0, 1),
+             (256, 4352, 4352, 1024, 4096, 4351, 2), (128, 100, 4096, 16, 40, 60, 3)]
+    for _ in range(400):
+        hd = int(rng.choice([128, 256]))
+        n_total = int(rng.integers(1, 5000))
+        nk = int(rng.integers(1, n_total + 1))
+        cap = (n_total + 63) // 64 * 64
+        window = None if rng.random() < 0.4 else int(rng.integers(1, 2048))
+        qmin = int(rng.integers(0, nk))
+        qmax = int(rng.integers(qmin, min(nk, qmin + 300)))
+        cases.append((hd, nk, cap, window, qmin, qmax, int(rng.integers(1, 5))))
+    for hd, nk, cap, window, qmin, qmax, n_split in cases:
+        lo, hi, ok = dr.ring_tiles(hd, nk, cap, window, qmin, qmax, n_split)
+        assert ok, (hd, nk, cap, window, qmin, qmax, n_split)
+        assert 0 <= lo <= hi < cap // 32, (hd, nk, cap, window, qmin, qmax, n_split, lo, hi)
+    # one 32-key tile: seven of eight waves own none; their DMA is clamped to
+    # the plane's last tile (unclamped it would be tile 7 of a 2-tile plane)
+    assert dr.ring_tiles(128, 32, 64, None, 0, 0, 1) == (0, 1, True)
+    with pytest.raises(dr.DrError):
+        dr.ring_tiles(64, 32, 64, None, 0, 0, 1)  # no stream kernel at hd 64
+
+
+def test_alloc_counter_counts_no_device_calls(lib):
+    """The allocation counter is host-side state: readable without a GPU and
+    unchanged by calls that fail before allocating."""
+    before = dr.alloc_count()
+    assert before >= 0
+    rc, _ = _call(dr.AttnShape(2, 3, 2, 2, 8), out_len=5)
+    assert rc == dr.DR_ERR_INVALID
+    assert dr.alloc_count() == before

@@ -111,3 +111,70 @@ def test_noalloc_rejects_workspace_beyond_scratch(dev):
         dev.ctx.set_split(0)
     assert ei.value.status == dr.DR_ERR_INVALID
     say(f"rejected: {ei.value.message}")
+
+
+def test_noalloc_first_call_allocates_nothing(dev):
+    """On a fresh context, dr_attention_cached_noalloc as the first call that
+    needs a split workspace makes no allocation (the library's counter of its
+    hipMalloc / hipHostMalloc calls stands still over two calls, the second
+    smaller), while dr_attention_cached on the same problem then does (the
+    counter sees allocations), with bit-identical results."""
+    h, hd, n_p, n_c1, n_c2 = 8, 128, 1400, 200, 70
+    rng = np.random.default_rng(11)
+    n_t = n_p + n_c1
+    ctx = dr.Context(0)
+    ctx.set_stream(dev.stream.cuda_stream)
+    ctx.set_split(3)
+    cache = dr.StepCache(ctx, n_t, [h], [hd])
+    K = rng.standard_normal((n_t, h * hd), dtype=np.float32)
+    V = rng.standard_normal((n_t, h * hd), dtype=np.float32)
+    cache.store(0, dr.Pass(ctx, range(n_t)), dev.put(K), dev.put(V))
+    calls = []
+    for n_c in (n_c1, n_c2):
+        calls.append((dr.Pass(ctx, range(n_t - n_c, n_t)), dev.put(rng.standard_normal((n_c, h * hd),
+                                                                                        dtype=np.float32)),
+                      dev.empty(n_c * h * hd), dev.empty(n_c * h * hd)))
+    dev.get(calls[-1][3])
+    before = dr.alloc_count()
+    for pc, Q, out, _ in calls:
+        cache.attention(0, [(Q, out, pc)], h, scale=1 / math.sqrt(hd), noalloc=True)
+        assert ctx.last_launch()["n_split"] == 3
+    dev.get(calls[-1][2])
+    assert dr.alloc_count() == before, "dr_attention_cached_noalloc allocated"
+    for pc, Q, _, out in calls:
+        cache.attention(0, [(Q, out, pc)], h, scale=1 / math.sqrt(hd))
+    dev.get(calls[-1][3])
+    assert dr.alloc_count() > before, "dr_attention_cached grows the context's split workspace"
+    for _, _, a, b in calls:
+        ga, gb = dev.get(a), dev.get(b)
+        assert not np.any(np.isnan(ga))
+        assert np.array_equal(ga, gb)
+    ctx.close()
+
+
+def test_noalloc_hilo_layer_with_q_norm_below_the_tile(dev):
+    """A hi/lo layer with a QK-norm at a head dim below its tile (96) runs the
+    Q epilogue into a Q workspace first; the allocation-free entry point puts
+    that workspace in the fixed scratch too: same bits as
+    dr_attention_cached, no allocation."""
+    h, hkv, hd, n_t, n_c = 4, 2, 96, 320, 64
+    rng = np.random.default_rng(12)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.set_precision(0, dr.PRECISION_HILO)
+    K = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    V = rng.standard_normal((n_t, hkv * hd), dtype=np.float32)
+    cache.store(0, dr.Pass(dev.ctx, range(n_t)), dev.put(K), dev.put(V))
+    pc = dr.Pass(dev.ctx, range(n_t - n_c, n_t))
+    Q = dev.put(rng.standard_normal((n_c, h * hd), dtype=np.float32))
+    w = dev.put(rng.uniform(0.5, 1.5, hd).astype(np.float32))
+    outs = [dev.empty(n_c * h * hd) for _ in range(2)]
+    dev.get(outs[1])
+    before = dr.alloc_count()
+    cache.attention(0, [(Q, outs[0], pc)], h, scale=1.0, q_norm_w=w, noalloc=True)
+    assert dev.ctx.last_launch()["kernel"] == dr.KERNEL_HILO
+    dev.get(outs[0])
+    assert dr.alloc_count() == before
+    cache.attention(0, [(Q, outs[1], pc)], h, scale=1.0, q_norm_w=w)
+    a, b = dev.get(outs[0]), dev.get(outs[1])
+    assert not np.any(np.isnan(a))
+    assert np.array_equal(a, b)
