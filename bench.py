@@ -486,11 +486,11 @@ def main() -> int:
         cache.store(layer, p_prompt, dKp, dVp)
     scale = cfg.attn_scale
 
+    # one denoise step of one layer: dr_attention_step, the store of the 256
+    # canvas K/V rows and the attention of attention_block (forward.rs:312-343)
     def step(i: int) -> None:
         Kc, Vc, Q = dsets[i % n_sets]
-        layer = i % N_LAYERS
-        cache.store(layer, p_canvas, Kc, Vc)
-        cache.attention(layer, [(Q, out, p_canvas)], h, scale=scale)
+        cache.step(i % N_LAYERS, [(Q, out, p_canvas, Kc, Vc)], h, scale=scale)
 
     with torch.cuda.stream(stream):
         step(0)
@@ -552,8 +552,36 @@ def main() -> int:
                   "kernel": b_launch.get("kernel"),
                   "timing": "as the roofline's launch timing, Q rows bf16 (values of the f32 sets "
                             "rounded to bf16), out f32"}
-        del qb
-        log(f"attention call, bf16 Q: {bf16_q}")
+        # ... and with bf16 output rows as well (dr_ctx_set_o_dtype): Q and O
+        # 2 bytes per element, the boundary at which the HBM ceiling of C2
+        # rises from 48.8 % to 61 % of the MFMA peak
+        with torch.cuda.stream(stream):
+            out_b = torch.empty(n_c * h * hd, dtype=torch.bfloat16, device=dev)
+        ctx.set_q_dtype(dr.DTYPE_BF16)
+        ctx.set_o_dtype(dr.DTYPE_BF16)
+        try:
+            o_mean_ms, _ = attention_only_ms(
+                torch, stream,
+                lambda i: cache.attention(i % N_LAYERS, [(qb[i % n_sets], out_b, p_canvas)], h, scale=scale),
+                N_LAYERS, reps)
+            o_warm_ms, _ = attention_only_ms(
+                torch, stream, lambda i: cache.attention(0, [(qb[i], out_b, p_canvas)], h, scale=scale),
+                n_sets, reps)
+            o_launch = ctx.last_launch()
+        finally:
+            ctx.set_q_dtype(dr.DTYPE_F32)
+            ctx.set_o_dtype(dr.DTYPE_F32)
+        bf16_q["bf16_q_and_out"] = {
+            "launch_us_mean": round(o_mean_ms * 1e3, 3),
+            "tflops": round(flops / (o_mean_ms / 1e3) / 1e12, 2),
+            "pct_of_peak": round(100 * flops / (o_mean_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 3),
+            "launch_us_one_layer_warm": round(o_warm_ms * 1e3, 3),
+            "tflops_one_layer_warm": round(flops / (o_warm_ms / 1e3) / 1e12, 2),
+            "kernel": o_launch.get("kernel"),
+            "algorithmic_bytes_per_launch": 2 * n_c * h * hd * 2 + 2 * n_t * kvs * 2,
+            "timing": "as above, Q and output rows bf16 (dr_ctx_set_o_dtype)"}
+        del qb, out_b
+        log(f"attention call, bf16 Q (and bf16 Q + out): {bf16_q}")
 
     # ---- timed region: K whole steps, every one a graph replay (a graph of
     # 32 steps, one per layer, and a graph of the remainder)
@@ -625,8 +653,7 @@ def main() -> int:
         def h2d_step(i: int) -> None:
             for d, hsrc in zip(dst, pins[i % 2]):
                 d.copy_(hsrc, non_blocking=True)
-            cache.store(i % N_LAYERS, p_canvas, dst[0], dst[1])
-            cache.attention(i % N_LAYERS, [(dst[2], out, p_canvas)], h, scale=scale)
+            cache.step(i % N_LAYERS, [(dst[2], out, p_canvas, dst[0], dst[1])], h, scale=scale)
 
         with torch.cuda.stream(stream):
             for i in range(3):
@@ -731,8 +758,8 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "C2: LLaDA-8B denoise step, 32/32 heads, hd 128, 512 cached + "
-                               "256 canvas, batch 1 (store canvas K/V + attention; step i on "
-                               "layer i mod 32 of a 32-layer cache)",
+                               "256 canvas, batch 1 (dr_attention_step: store canvas K/V + "
+                               "attention; step i on layer i mod 32 of a 32-layer cache)",
                    "global_batch": 1, "seq_len": n_t, "parallelism": "none (1 GPU)",
                    "timing": mode, "accumulate": "fp32", "q_out_dtype": "f32",
                    "kv_cache_dtype": "bf16", "layers": N_LAYERS},

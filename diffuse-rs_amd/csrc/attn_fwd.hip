@@ -1338,10 +1338,14 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     }
     int hg, qi;
     row_split(r, S.nq, __builtin_amdgcn_rcpf((float)S.nq), a.group, hg, qi);
-    float* orow = S.out + (size_t)qi * a.o_rstride + (size_t)(g * a.group + hg) * a.hd;
+    const size_t o0 = (size_t)qi * a.o_rstride + (size_t)(g * a.group + hg) * a.hd;
+    float* orow = S.out + o0;
     const f32x4 val = acc[0] * __builtin_amdgcn_rcpf(Ls);
     const int c0 = ch * 4;
-    if (a.hd == HD) {
+    if (a.o_bf16) {  // (the per-wave-stream kernel's launches only: hd == HD)
+        const bf16x4 y = {(__bf16)val[0], (__bf16)val[1], (__bf16)val[2], (__bf16)val[3]};
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<uint16_t*>(S.out) + o0 + c0) = y;
+    } else if (a.hd == HD) {
         *reinterpret_cast<f32x4*>(orow + c0) = val;
     } else {
 #pragma unroll

@@ -635,10 +635,21 @@ void attn_ring_kernel(const AttnArgs a) {
     auto store_rows = [&](const f32x4 (&val)[CPT], float l) __attribute__((always_inline)) {
         int ohg, oqi;
         split_row(row, ohg, oqi);
-        float* orow = S.out + (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
+        const size_t o0 = (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
         const float il = __builtin_amdgcn_rcpf(l);
+        if (a.o_bf16) {  // rounded to nearest even, 8-byte pieces
+            uint16_t* orow = reinterpret_cast<uint16_t*>(S.out) + o0;
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), val[k] * il);
+            for (int k = 0; k < CPT; ++k) {
+                const f32x4 v = val[k] * il;
+                const bf16x4 y = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+                gstore(orow + 4 * (ch + TPR * k), y);
+            }
+        } else {
+            float* orow = S.out + o0;
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), val[k] * il);
+        }
     };
     if (a.n_split == 1) {
         if (row_ok) store_rows(acc, L);

@@ -130,6 +130,7 @@ struct dr_ctx {
     int force_rows = 0;  // query rows per compute wave (0: automatic)
     int force_kernel = 0;  // dr::KernelKind (0: automatic)
     int q_bf16 = 0;        // the cached entry points' Q rows are bf16
+    int o_bf16 = 0;        // the cached entry points write bf16 output rows
     int merge_in_kernel = 1;  // key splits of the per-wave-stream kernel merge in-kernel
     dr::LaunchPlan last{};
     bool has_last = false;
@@ -379,6 +380,14 @@ int dr_ctx_set_q_dtype(dr_ctx* ctx, int dtype) {
     if (dtype != DR_DTYPE_F32 && dtype != DR_DTYPE_BF16)
         return fail(DR_ERR_INVALID, "dtype %d not DR_DTYPE_F32 or DR_DTYPE_BF16", dtype);
     ctx->q_bf16 = dtype == DR_DTYPE_BF16 ? 1 : 0;
+    return DR_OK;
+}
+
+int dr_ctx_set_o_dtype(dr_ctx* ctx, int dtype) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_o_dtype: ctx is NULL");
+    if (dtype != DR_DTYPE_F32 && dtype != DR_DTYPE_BF16)
+        return fail(DR_ERR_INVALID, "dtype %d not DR_DTYPE_F32 or DR_DTYPE_BF16", dtype);
+    ctx->o_bf16 = dtype == DR_DTYPE_BF16 ? 1 : 0;
     return DR_OK;
 }
 
@@ -1043,9 +1052,10 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
     // a layer that keeps K's lo half gets f32-accurate scores, unless another
     // kernel family is forced (then the lo half is not read)
     const bool hilo_asked = ctx->force_kernel == dr::KERNEL_AUTO || ctx->force_kernel == dr::KERNEL_HILO;
-    if (a.slot[0].klo && hilo_asked && !a.q_bf16) return plan_hilo(ctx, a, hd, max_nq, max_nk, mask);
-    // bf16 Q rows: only the per-wave-stream kernel reads them
-    const int kernel = a.q_bf16 ? dr::KERNEL_STREAMS
+    const bool bf16_rows = a.q_bf16 || a.o_bf16;
+    if (a.slot[0].klo && hilo_asked && !bf16_rows) return plan_hilo(ctx, a, hd, max_nq, max_nk, mask);
+    // bf16 Q or output rows: only the per-wave-stream kernel reads / writes them
+    const int kernel = bf16_rows ? dr::KERNEL_STREAMS
                                 : (ctx->force_kernel == dr::KERNEL_HILO ? dr::KERNEL_AUTO : ctx->force_kernel);
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
                               mask == dr::MASK_POS ? a.window : -1, a.rope ? a.rot : 0, ctx->n_cu,
@@ -1105,11 +1115,11 @@ static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, float* base) {
 // plan that needs more than it holds is an error).
 // bf16 Q rows are read by the per-wave-stream kernel only.
 static int check_q_dtype(const dr::AttnArgs& a, const dr::LaunchPlan& p, const char* who) {
-    if (!a.q_bf16 || p.kernel == dr::KERNEL_STREAMS) return DR_OK;
+    if ((!a.q_bf16 && !a.o_bf16) || p.kernel == dr::KERNEL_STREAMS) return DR_OK;
     return fail(DR_ERR_UNSUPPORTED,
-                "%s: bf16 Q rows (dr_ctx_set_q_dtype) are read by the per-wave-stream kernel only: head dim "
-                "128 or 256, no per-key masks, a Q epilogue of at most bias, QK-norm and full-rotary RoPE, "
-                "no forced tile shape and no hi/lo layer",
+                "%s: bf16 Q / output rows (dr_ctx_set_q_dtype, dr_ctx_set_o_dtype) are read and written by the "
+                "per-wave-stream kernel only: head dim 128 or 256, no per-key masks, a Q epilogue of at most "
+                "bias, QK-norm and full-rotary RoPE, no forced tile shape and no hi/lo layer",
                 who);
 }
 
@@ -1203,12 +1213,13 @@ static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* 
     a.qn_w = q_norm_w;
     a.qn_eps = q_norm_eps;
     a.q_bf16 = ctx->q_bf16;
+    a.o_bf16 = ctx->o_bf16;
     max_nq = 0;
     const int tile = cache->hd_tile[layer];
-    if (a.q_bf16 && ((hd != 128 && hd != 256) || cache->klo[layer * cache->n_batch]))
+    if ((a.q_bf16 || a.o_bf16) && ((hd != 128 && hd != 256) || cache->klo[layer * cache->n_batch]))
         return fail(DR_ERR_UNSUPPORTED,
-                    "%s: bf16 Q rows (dr_ctx_set_q_dtype) need head dim 128 or 256 and a bf16 layer (head "
-                    "dim %zu%s)",
+                    "%s: bf16 Q / output rows (dr_ctx_set_q_dtype, dr_ctx_set_o_dtype) need head dim 128 or "
+                    "256 and a bf16 layer (head dim %zu%s)",
                     who, hd, cache->klo[layer * cache->n_batch] ? ", hi/lo layer" : "");
     for (size_t b = 0; b < n_items; ++b) {
         const dr_batch_item& it = items[b];

@@ -25,7 +25,7 @@ constexpr int VT_KEYS = 32;
 // and sequence id kseq[j] (nullptr: 0).
 struct AttnSlot {
     const void* q;        // [nq][q_rstride] f32 (bf16 with AttnArgs::q_bf16), head h at h*hd
-    float* out;           // [nq][o_rstride] f32
+    float* out;           // [nq][o_rstride] f32 (bf16 with AttnArgs::o_bf16)
     const int* qpos;      // [nq] sequence positions of the queries (device)
     const int* qseq;      // [nq] or nullptr
     const int* qprefix;   // [nq] per-row causal prefix or nullptr
@@ -71,6 +71,7 @@ struct AttnArgs {
     // counter; no split_merge_kernel follows.  The per-wave-stream kernel only.
     int* ticket;
     int q_bf16;                    // Q rows are bf16 (the per-wave-stream kernel reads them)
+    int o_bf16;                    // output rows are bf16 (the per-wave-stream kernel writes them)
     // the Q/K/V epilogue's Q part (forward.rs:291-310): bias before the
     // QK-norm, RoPE after it, at the query rows' positions (qpos)
     const float* qb;               // [n_head*hd] or nullptr

@@ -128,6 +128,7 @@ _SIGS = {
     "dr_ctx_set_wave_rows": (_I, [_VP, _I]),
     "dr_ctx_set_kernel": (_I, [_VP, _I]),
     "dr_ctx_set_q_dtype": (_I, [_VP, _I]),
+    "dr_ctx_set_o_dtype": (_I, [_VP, _I]),
     "dr_ctx_set_split_merge": (_I, [_VP, _I]),
     "dr_rope_create": (_I, [_VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float, _VP,
                             ctypes.POINTER(ctypes.c_void_p)]),
@@ -340,6 +341,11 @@ class Context:
         """DTYPE_F32 or DTYPE_BF16: the element type of the Q rows of later
         cached attention calls (dr_ctx_set_q_dtype)."""
         _check(self.lib.dr_ctx_set_q_dtype(self.h, dtype))
+
+    def set_o_dtype(self, dtype: int) -> None:
+        """DTYPE_F32 or DTYPE_BF16: the element type of the output rows of
+        later cached attention calls (dr_ctx_set_o_dtype)."""
+        _check(self.lib.dr_ctx_set_o_dtype(self.h, dtype))
 
     def set_split_merge(self, in_kernel: bool) -> None:
         """Key splits of the STREAMS kernel merge in-kernel (True, the

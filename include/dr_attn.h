@@ -426,6 +426,15 @@ int dr_ctx_set_kernel(dr_ctx* ctx, int kernel);
 #define DR_DTYPE_F32 0
 #define DR_DTYPE_BF16 1
 int dr_ctx_set_q_dtype(dr_ctx* ctx, int dtype);
+/* The element type of the output rows that later dr_attention_cached /
+ * _cached_noalloc / _step / _step_epi calls on ctx write (no counterpart in
+ * the reference, whose attention() writes f32; for callers whose Wo
+ * projection reads bf16).  DR_DTYPE_F32 (the default): out points at float
+ * rows.  DR_DTYPE_BF16: out points at bf16 rows of the same shape (uint16
+ * bit patterns), each the f32 result rounded to nearest even; written by the
+ * per-wave-stream kernel, with the same restrictions and errors as
+ * dr_ctx_set_q_dtype's bf16 rows. */
+int dr_ctx_set_o_dtype(dr_ctx* ctx, int dtype);
 /* How key splits of the STREAMS kernel are merged on later calls on ctx (a
  * tuning knob with no counterpart in the reference, for measurement and
  * tests).  1 (the default): in-kernel; the last split of each 32-row block

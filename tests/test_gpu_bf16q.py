@@ -149,3 +149,68 @@ def test_bf16_q_refused_where_the_stream_kernel_cannot_run(dev):
     with pytest.raises(dr.DrError) as ei:
         dev.ctx.set_q_dtype(7)
     assert ei.value.status == dr.DR_ERR_INVALID
+
+
+@pytest.mark.parametrize("cid,n_split,in_kernel", [("C2", 0, True), ("C4", 0, True), ("C5S", 0, True),
+                                                   ("C2", 3, True), ("C2", 2, False)])
+def test_bf16_out_is_the_f32_output_rounded(dev, cid, n_split, in_kernel):
+    """bf16 output rows (dr_ctx_set_o_dtype): each element is the f32 path's
+    output rounded to nearest even, bit for bit, unsplit, with key splits
+    merged in-kernel and by split_merge_kernel; and within the bar of the
+    oracle."""
+    t = dev.t
+    cfg = CONFIGS[cid]
+    rng = np.random.default_rng(config_seed(list(CONFIGS).index(cid), 5))
+    h, hkv, hd, n_t, n_c = cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.n_total, cfg.n_canvas
+    kvs = hkv * hd
+    K = rng.standard_normal((n_t, kvs), dtype=np.float32)
+    V = rng.standard_normal((n_t, kvs), dtype=np.float32)
+    Q = rng.standard_normal((n_c, h * hd), dtype=np.float32)
+    qn = kn = None
+    if cfg.qk_norm:
+        qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+    cache.store(0, dr.Pass(dev.ctx, range(n_t)), dev.put(K), dev.put(V),
+                dev.put(kn) if kn is not None else None, 1e-6)
+    pc = dr.Pass(dev.ctx, range(cfg.n_prompt, n_t))
+    qd = dev.put(Q)
+    qnd = dev.put(qn) if qn is not None else None
+    dev.ctx.set_split(n_split)
+    dev.ctx.set_split_merge(in_kernel)
+    try:
+        out_f = dev.empty(n_c * h * hd)
+        cache.attention(0, [(qd, out_f, pc)], h, sliding_window=cfg.window, scale=cfg.attn_scale,
+                        q_norm_w=qnd, q_norm_eps=1e-6)
+        with t.cuda.stream(dev.stream):
+            out_b = t.full((n_c * h * hd,), float("nan"), dtype=t.bfloat16, device="cuda")
+        dev.ctx.set_o_dtype(dr.DTYPE_BF16)
+        try:
+            cache.attention(0, [(qd, out_b, pc)], h, sliding_window=cfg.window, scale=cfg.attn_scale,
+                            q_norm_w=qnd, q_norm_eps=1e-6)
+            launch = dev.ctx.last_launch()
+        finally:
+            dev.ctx.set_o_dtype(dr.DTYPE_F32)
+    finally:
+        dev.ctx.set_split(0)
+        dev.ctx.set_split_merge(True)
+    say(f"{cid} bf16 out (split {n_split}, in-kernel {in_kernel}): launch {launch}")
+    assert launch["kernel"] == dr.KERNEL_STREAMS
+    if n_split:
+        assert launch["n_split"] == n_split and launch["split_merge"] == (2 if in_kernel else 1)
+    got_f = dev.get(out_f)
+    with t.cuda.stream(dev.stream):
+        want_bits = out_f.to(t.bfloat16).view(t.int16)
+        got_bits = out_b.view(t.int16)
+    assert np.array_equal(dev.get(got_bits), dev.get(want_bits)), cid
+    q_o, k_o = Q.reshape(-1).copy(), K.reshape(-1).copy()
+    if qn is not None:
+        orc.norm_heads(q_o, qn, 1e-6)
+        orc.norm_heads(k_o, kn, 1e-6)
+    s = Shape(n_c, n_t, h, hkv, hd, sliding_window=cfg.window, scale=cfg.attn_scale)
+    want = oracle_run(s, RowsSpec(list(range(cfg.n_prompt, n_t))), RowsSpec(list(range(n_t))), q_o, k_o,
+                      V.reshape(-1).copy())
+    with t.cuda.stream(dev.stream):
+        got_b32 = out_b.float()
+    check(dev.get(got_b32), want, f"{cid} bf16 out vs oracle")
+    assert not np.any(np.isnan(got_f))
