@@ -190,9 +190,16 @@ def hilo_timing(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
 
             def call(i):
                 cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=1.0, q_norm_w=qn)
-            ms, _ = attention_only_ms(torch, stream, call, 4, reps)
+            # (a bf16 layer refuses scale 1.0 unless a kernel family is
+            # forced: the one the planner picks for its shape)
+            if prec is None:
+                ctx.set_kernel(dr.KERNEL_STREAMS if cfg.window else dr.KERNEL_STAGED)
+            try:
+                ms, _ = attention_only_ms(torch, stream, call, 4, reps)
+                entry[f"{label}_kernel"] = ctx.last_launch()["kernel"]
+            finally:
+                ctx.set_kernel(dr.KERNEL_AUTO)
             entry[f"{label}_us_per_call"] = round(ms * 1e3, 3)
-            entry[f"{label}_kernel"] = ctx.last_launch()["kernel"]
             stream.synchronize()
             del cache
         entry["hilo_over_bf16"] = round(entry["hilo_us_per_call"] / entry["bf16_us_per_call"], 3)

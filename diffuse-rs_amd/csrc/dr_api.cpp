@@ -71,6 +71,9 @@ constexpr size_t MAX_POS = (size_t)1 << 30;
 // Row blocks (batch x kv head x 32-row group) whose key splits one call can
 // merge in-kernel: the size of each context's ticket buffer.
 constexpr size_t TICKETS = (size_t)1 << 16;
+// Largest |scale| * sqrt(head_dim) a bf16 layer accepts unless a kernel
+// family is forced (1 at the reference's usual 1/sqrt(head_dim)).
+constexpr double MAX_BF16_SCALE = 2.0;
 
 struct DevBuf {
     void* p = nullptr;
@@ -511,6 +514,29 @@ int dr_cache_create(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n
         }
     }
     *out = c;
+    return DR_OK;
+}
+
+int dr_cache_create_layers(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n_head_kv,
+                           const size_t* head_dim, const int* precision, size_t n_batch,
+                           dr_step_cache** out) {
+    if (precision)
+        for (size_t l = 0; l < n_layer; ++l)
+            if (precision[l] != DR_PRECISION_BF16 && precision[l] != DR_PRECISION_HILO)
+                return fail(DR_ERR_INVALID, "layer %zu: precision %d not DR_PRECISION_BF16 or _HILO", l,
+                            precision[l]);
+    DR_CHECK(dr_cache_create(ctx, n_total, n_layer, n_head_kv, head_dim, n_batch, out));
+    if (precision)
+        for (size_t l = 0; l < n_layer; ++l) {
+            if (precision[l] == DR_PRECISION_BF16) continue;
+            const int rc = dr_cache_set_precision(*out, l, precision[l]);
+            if (rc != DR_OK) {
+                const std::string msg = g_err;
+                dr_cache_destroy(*out);
+                *out = nullptr;
+                return fail(rc, "%s", msg.c_str());
+            }
+        }
     return DR_OK;
 }
 
@@ -1216,6 +1242,19 @@ static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* 
     a.o_bf16 = ctx->o_bf16;
     max_nq = 0;
     const int tile = cache->hd_tile[layer];
+    // bf16 scores hold the 1e-2 bar up to about twice the usual
+    // 1/sqrt(head_dim) scale; Gemma's kq_scale 1.0 (forward.rs:338-341) is
+    // 11-23 times it and moves outputs by ~0.24 on a bf16 layer.  Such a call
+    // needs a DR_PRECISION_HILO layer, unless the caller forced a kernel
+    // family and so asked for bf16 scores.
+    const bool hilo_layer = cache->klo[layer * cache->n_batch] != nullptr;
+    if (!hilo_layer && ctx->force_kernel == dr::KERNEL_AUTO &&
+        std::fabs(scale) * std::sqrt((double)hd) > MAX_BF16_SCALE)
+        return fail(DR_ERR_UNSUPPORTED,
+                    "%s: scale %g is %.1f times 1/sqrt(head_dim %zu), more than bf16 scores hold to the 1e-2 bar; "
+                    "keep layer %zu at DR_PRECISION_HILO (dr_cache_create_layers, dr_cache_set_precision), or force "
+                    "a kernel family (dr_ctx_set_kernel) to accept bf16 scores",
+                    who, scale, std::fabs(scale) * std::sqrt((double)hd), hd, layer);
     if ((a.q_bf16 || a.o_bf16) && ((hd != 128 && hd != 256) || cache->klo[layer * cache->n_batch]))
         return fail(DR_ERR_UNSUPPORTED,
                     "%s: bf16 Q / output rows (dr_ctx_set_q_dtype, dr_ctx_set_o_dtype) need head dim 128 or "

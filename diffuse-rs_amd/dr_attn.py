@@ -148,6 +148,7 @@ _SIGS = {
     "dr_quantize_q8k": (_I, [_VP, _VP, _SZ, _SZ, _VP]),
     "dr_pass_destroy": (None, [_VP]),
     "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
+    "dr_cache_create_layers": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _VP, _SZ, ctypes.POINTER(_VP)]),
     "dr_cache_destroy": (None, [_VP]),
     "dr_cache_set_precision": (_I, [_VP, _SZ, _I]),
     "dr_cache_store": (_I, [_VP, _SZ, _SZ, _VP, _VP, _VP, _VP, _F]),
@@ -457,14 +458,22 @@ class StepCache:
     """dr_step_cache: per-layer bf16 K/V for every position, in HBM."""
 
     def __init__(self, ctx: Context, n_total: int, n_head_kv: Sequence[int],
-                 head_dim: Sequence[int], n_batch: int = 1):
+                 head_dim: Sequence[int], n_batch: int = 1, precision: Optional[Sequence[int]] = None):
+        """precision: per-layer PRECISION_BF16 / PRECISION_HILO
+        (dr_cache_create_layers); None: every layer bf16 (dr_cache_create)."""
         self.ctx = ctx
         hkv, hkv_p, n_layer = _usize_array(n_head_kv)
         hd, hd_p, n2 = _usize_array(head_dim)
         assert n2 == n_layer
         h = ctypes.c_void_p()
-        _check(ctx.lib.dr_cache_create(ctx.h, n_total, n_layer, hkv_p, hd_p, n_batch,
-                                       ctypes.byref(h)))
+        if precision is None:
+            _check(ctx.lib.dr_cache_create(ctx.h, n_total, n_layer, hkv_p, hd_p, n_batch,
+                                           ctypes.byref(h)))
+        else:
+            prec = np.ascontiguousarray(precision, dtype=np.int32)
+            assert prec.size == n_layer
+            _check(ctx.lib.dr_cache_create_layers(ctx.h, n_total, n_layer, hkv_p, hd_p, prec.ctypes.data,
+                                                  n_batch, ctypes.byref(h)))
         self.h = h
         self.n_total = n_total
         self.n_batch = n_batch

@@ -170,6 +170,19 @@ void dr_cache_destroy(dr_step_cache* cache);
 #define DR_PRECISION_BF16 0
 #define DR_PRECISION_HILO 1
 int dr_cache_set_precision(dr_step_cache* cache, size_t layer, int precision);
+/* dr_cache_create with each layer's score precision given up front
+ * (precision: n_layer entries, DR_PRECISION_BF16 or DR_PRECISION_HILO; NULL =
+ * all bf16), so a binding sets it from the layer's attention scale when it
+ * builds the cache: DiffusionGemma, whose layers all use kq_scale 1.0
+ * (forward.rs:338-341), takes DR_PRECISION_HILO for every layer.  A cached
+ * attention call (dr_attention_cached, _noalloc, _step, _step_epi) on a
+ * DR_PRECISION_BF16 layer with |scale| * sqrt(head_dim) > 2 fails with
+ * DR_ERR_UNSUPPORTED, since bf16 scores miss the 1e-2 bar there (outputs move
+ * by ~0.24 at Gemma's 1.0), unless a kernel family was forced with
+ * dr_ctx_set_kernel (then the caller accepts bf16 scores). */
+int dr_cache_create_layers(dr_ctx* ctx, size_t n_total, size_t n_layer, const size_t* n_head_kv,
+                           const size_t* head_dim, const int* precision, size_t n_batch,
+                           dr_step_cache** out);
 
 /* StepCache::store (cache.rs:62-71) for the pass's active positions: row r of
  * k/v ([n_active][n_head_kv][head_dim] f32, device) goes to position

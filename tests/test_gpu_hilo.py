@@ -88,14 +88,53 @@ def test_gemma_scale_one_hilo_meets_tolerance(dev, name):
 
 @pytest.mark.parametrize("name", list(GEMMA))
 def test_gemma_scale_one_bf16_misses_tolerance(dev, name):
-    """The bf16 path on the same inputs: reported, and far outside the bar
+    """The bf16 path on the same inputs is refused (DR_ERR_UNSUPPORTED) unless
+    a kernel family is forced; forced, it runs and lands far outside the bar
     (which is why hi/lo layers exist)."""
     h, hkv, hd, n_p, n_c, window = GEMMA[name]
-    got, wants, info, _ = _problem(dev, h, hkv, hd, n_p, n_c, window, 1.0, None, sum(map(ord, name)))
+    with pytest.raises(dr.DrError) as ei:
+        _problem(dev, h, hkv, hd, n_p, n_c, window, 1.0, None, sum(map(ord, name)))
+    assert ei.value.status == dr.DR_ERR_UNSUPPORTED and "DR_PRECISION_HILO" in ei.value.message
+    # (the family the planner picks for a bf16 layer of this shape)
+    dev.ctx.set_kernel(dr.KERNEL_STREAMS if window else dr.KERNEL_STAGED)
+    try:
+        got, wants, info, _ = _problem(dev, h, hkv, hd, n_p, n_c, window, 1.0, None, sum(map(ord, name)))
+    finally:
+        dev.ctx.set_kernel(dr.KERNEL_AUTO)
     assert info["kernel"] != dr.KERNEL_HILO
     mx, mean = err_stats(got[0], wants[0])
-    say(f"  {name} bf16 at scale 1.0: max-abs {mx:.3e} mean-abs {mean:.3e}")
+    say(f"  {name} bf16 at scale 1.0 (forced): max-abs {mx:.3e} mean-abs {mean:.3e}")
     assert np.isfinite(mx) and mx > TOL_MAX
+
+
+def test_layer_precision_at_create_and_scale_guard(dev):
+    """dr_cache_create_layers sets each layer's precision up front (Gemma:
+    hi/lo everywhere); a bf16 layer takes scales up to twice 1/sqrt(head_dim)
+    and refuses more; a hi/lo layer takes any scale."""
+    h, hkv, hd, n_t, n_c = 8, 4, 128, 256, 64
+    rng = np.random.default_rng(61)
+    cache = dr.StepCache(dev.ctx, n_t, [hkv] * 3, [hd] * 3,
+                         precision=[dr.PRECISION_BF16, dr.PRECISION_HILO, dr.PRECISION_BF16])
+    K = dev.put(rng.standard_normal((n_t, hkv * hd), dtype=np.float32))
+    V = dev.put(rng.standard_normal((n_t, hkv * hd), dtype=np.float32))
+    p_all, p_c = dr.Pass(dev.ctx, range(n_t)), dr.Pass(dev.ctx, range(n_t - n_c, n_t))
+    for layer in range(3):
+        cache.store(layer, p_all, K, V)
+    q = dev.put(rng.standard_normal((n_c, h * hd), dtype=np.float32))
+    out = dev.empty(n_c * h * hd)
+    base = 1 / math.sqrt(hd)
+    cache.attention(0, [(q, out, p_c)], h, scale=1.9 * base)
+    assert dev.ctx.last_launch()["kernel"] != dr.KERNEL_HILO
+    for layer in (0, 2):
+        with pytest.raises(dr.DrError) as ei:
+            cache.attention(layer, [(q, out, p_c)], h, scale=2.1 * base)
+        assert ei.value.status == dr.DR_ERR_UNSUPPORTED
+    cache.attention(1, [(q, out, p_c)], h, scale=1.0)
+    assert dev.ctx.last_launch()["kernel"] == dr.KERNEL_HILO
+    assert not np.any(np.isnan(dev.get(out)))
+    with pytest.raises(dr.DrError) as ei:
+        dr.StepCache(dev.ctx, n_t, [hkv], [hd], precision=[7])
+    assert ei.value.status == dr.DR_ERR_INVALID
 
 
 # (h, hkv, hd, n_prompt, n_canvas, window, prefix, batch, n_split, qk_norm)
