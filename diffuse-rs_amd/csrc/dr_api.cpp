@@ -897,23 +897,46 @@ int dr_cache_split_active_dev(dr_step_cache* cache, size_t batch, const int32_t*
     return DR_OK;
 }
 
-int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
-               size_t n, float* out, const float* residual) {
-    if (!ctx) return fail(DR_ERR_INVALID, "dr_qmatmul: ctx is NULL");
-    if (wtype != DR_WTYPE_Q4K && wtype != DR_WTYPE_Q6K)
-        return fail(DR_ERR_UNSUPPORTED, "dr_qmatmul: weight type %d not built (Q4_K = 12, Q6_K = 14)", wtype);
-    if (cols == 0 || cols % 256 != 0)
-        return fail(DR_ERR_INVALID, "dr_qmatmul: cols %zu is not a positive multiple of 256", cols);
+// GGML block geometry of the weight types dr_qmatmul runs: values and bytes
+// per block (0: not built).
+static void wtype_block(int wtype, size_t& qk, size_t& bytes) {
+    qk = bytes = 0;
+    switch (wtype) {
+        case DR_WTYPE_Q4K: qk = 256, bytes = 144; break;
+        case DR_WTYPE_Q6K: qk = 256, bytes = 210; break;
+        case DR_WTYPE_Q4_0: qk = 32, bytes = 18; break;
+        case DR_WTYPE_Q5_0: qk = 32, bytes = 22; break;
+        case DR_WTYPE_Q8_0: qk = 32, bytes = 34; break;
+        default: break;
+    }
+}
+
+static int qmatmul_impl(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
+                        size_t n, float* out, const float* residual, const float* norm_w, float eps,
+                        const char* who) {
+    if (!ctx) return fail(DR_ERR_INVALID, "%s: ctx is NULL", who);
+    size_t qk, bb;
+    wtype_block(wtype, qk, bb);
+    if (!qk)
+        return fail(DR_ERR_UNSUPPORTED, "%s: weight type %d not built (Q4_0 = 2, Q5_0 = 6, Q8_0 = 8, Q4_K = 12, "
+                    "Q6_K = 14)", who, wtype);
+    if (cols == 0 || cols % qk != 0)
+        return fail(DR_ERR_INVALID, "%s: cols %zu is not a positive multiple of %zu", who, cols, qk);
     if (n == 0 || rows == 0) return DR_OK;
-    if (!w || !act || !out) return fail(DR_ERR_INVALID, "dr_qmatmul: NULL w / act / out");
+    if (!w || !act || !out) return fail(DR_ERR_INVALID, "%s: NULL w / act / out", who);
     if (wtype == DR_WTYPE_Q4K && ((uintptr_t)w & 15))
-        return fail(DR_ERR_INVALID, "dr_qmatmul: Q4_K blocks must start 16-byte aligned (16-byte loads)");
-    const size_t nb = cols / 256;
+        return fail(DR_ERR_INVALID, "%s: Q4_K blocks must start 16-byte aligned (16-byte loads)", who);
+    if (((uintptr_t)w & 1) || ((uintptr_t)act & 15))
+        return fail(DR_ERR_INVALID, "%s: weight blocks must start 2-byte aligned and act 16-byte aligned", who);
+    const size_t nb = cols / qk;
     if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX / 2 || n > (size_t)INT32_MAX / 2 ||
-        (size_t)dr::qmm_rows_padded((int)n) * nb > (size_t)INT32_MAX)
-        return fail(DR_ERR_INVALID, "dr_qmatmul: %zu x %zu x %zu too large", n, rows, cols);
+        (size_t)dr::qmm_rows_padded((int)n) * nb * (qk == 32 ? 64 : 1) > (size_t)INT32_MAX)
+        return fail(DR_ERR_INVALID, "%s: %zu x %zu x %zu too large", who, n, rows, cols);
     DR_CHECK(use_device(ctx));
-    DR_CHECK(grow(ctx->q8k, dr::qmm_workspace_bytes((int)n, (int)cols), ctx->retired));
+    const size_t ws = qk == 32 ? dr::qmm0_workspace_bytes((int)n, (int)cols) : dr::qmm_workspace_bytes((int)n, (int)cols);
+    // (with a post-norm, the rows before the norm follow, 256-byte aligned)
+    const size_t tmp_off = round_up(ws, 256), tmp_bytes = norm_w ? n * rows * sizeof(float) : 0;
+    DR_CHECK(grow(ctx->q8k, tmp_off + tmp_bytes, ctx->retired));
     dr::QmmArgs a{};
     a.wtype = wtype;
     a.w = w;
@@ -925,9 +948,23 @@ int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, 
     a.ws = ctx->q8k.p;
     a.out = out;
     a.residual = residual;
+    a.norm_w = norm_w;
+    a.norm_eps = eps;
+    a.norm_tmp = norm_w ? reinterpret_cast<float*>(static_cast<char*>(ctx->q8k.p) + tmp_off) : nullptr;
     hipError_t e = dr::launch_qmatmul(a, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "qmatmul launch");
     return DR_OK;
+}
+
+int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
+               size_t n, float* out, const float* residual) {
+    return qmatmul_impl(ctx, wtype, w, rows, cols, act, n, out, residual, nullptr, 0.0f, "dr_qmatmul");
+}
+
+int dr_qmatmul_post_norm(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
+                         size_t n, float* out, const float* residual, const float* norm_w, float eps) {
+    if (!norm_w) return fail(DR_ERR_INVALID, "dr_qmatmul_post_norm: norm_w is NULL");
+    return qmatmul_impl(ctx, wtype, w, rows, cols, act, n, out, residual, norm_w, eps, "dr_qmatmul_post_norm");
 }
 
 int dr_qmatmul_expert(dr_ctx* ctx, int wtype, const void* w, size_t n_expert, size_t expert, size_t rows,
@@ -936,16 +973,33 @@ int dr_qmatmul_expert(dr_ctx* ctx, int wtype, const void* w, size_t n_expert, si
     if (expert >= n_expert)
         return fail(DR_ERR_INVALID, "dr_qmatmul_expert: expert index %zu out of range (%zu experts)", expert,
                     n_expert);
-    if (wtype != DR_WTYPE_Q4K && wtype != DR_WTYPE_Q6K)
-        return fail(DR_ERR_UNSUPPORTED, "dr_qmatmul_expert: weight type %d not built (Q4_K = 12, Q6_K = 14)",
-                    wtype);
-    if (cols == 0 || cols % 256 != 0)
-        return fail(DR_ERR_INVALID, "dr_qmatmul_expert: cols %zu is not a positive multiple of 256", cols);
+    size_t qk, bb;
+    wtype_block(wtype, qk, bb);
+    if (!qk)
+        return fail(DR_ERR_UNSUPPORTED, "dr_qmatmul_expert: weight type %d not built (Q4_0 = 2, Q5_0 = 6, "
+                    "Q8_0 = 8, Q4_K = 12, Q6_K = 14)", wtype);
+    if (cols == 0 || cols % qk != 0)
+        return fail(DR_ERR_INVALID, "dr_qmatmul_expert: cols %zu is not a positive multiple of %zu", cols, qk);
     if (!w) return fail(DR_ERR_INVALID, "dr_qmatmul_expert: w is NULL");
-    const size_t bb = wtype == DR_WTYPE_Q4K ? 144 : 210;
-    const size_t expert_bytes = rows * (cols / 256) * bb;
-    return dr_qmatmul(ctx, wtype, static_cast<const uint8_t*>(w) + expert * expert_bytes, rows, cols, act, n, out,
-                      residual);
+    const size_t expert_bytes = rows * (cols / qk) * bb;
+    return qmatmul_impl(ctx, wtype, static_cast<const uint8_t*>(w) + expert * expert_bytes, rows, cols, act, n, out,
+                        residual, nullptr, 0.0f, "dr_qmatmul_expert");
+}
+
+int dr_quantize_q8_0(dr_ctx* ctx, const float* act, size_t n, size_t cols, void* out) {
+    if (!ctx) return fail(DR_ERR_INVALID, "dr_quantize_q8_0: ctx is NULL");
+    if (cols == 0 || cols % 32 != 0)
+        return fail(DR_ERR_INVALID, "dr_quantize_q8_0: cols %zu is not a positive multiple of 32", cols);
+    if (n == 0) return DR_OK;
+    if (!act || !out) return fail(DR_ERR_INVALID, "dr_quantize_q8_0: NULL act / out");
+    if (((uintptr_t)out & 1) || ((uintptr_t)act & 15))
+        return fail(DR_ERR_INVALID, "dr_quantize_q8_0: out must be 2-byte and act 16-byte aligned");
+    if (cols > (size_t)INT32_MAX || (n + 31) / 32 * (cols / 32) > (size_t)INT32_MAX / 4)
+        return fail(DR_ERR_INVALID, "dr_quantize_q8_0: %zu x %zu too large", n, cols);
+    DR_CHECK(use_device(ctx));
+    hipError_t e = dr::launch_quantize_q80(act, (int)n, (int)cols, out, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize_q8_0 launch");
+    return DR_OK;
 }
 
 int dr_quantize_q8k(dr_ctx* ctx, const float* act, size_t n, size_t cols, void* out) {

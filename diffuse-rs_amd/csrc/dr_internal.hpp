@@ -193,10 +193,26 @@ struct QmmLayout {
     __host__ __device__ size_t tb(int t32, int b) const { return (size_t)t32 * nb + b; }
 };
 
+// dr_qmatmul's workspace for the legacy 32-value block types (Q4_0, Q5_0,
+// Q8_0 weights): the Q8_0 activations in the order the int8 MFMA reads them.
+//   qs  int8 [n_pad/32][nb][64 lanes][16]  lane (c, g): values 16 g .. + 15
+//       of block b of row c of the 32-row tile
+//   xd  f32  [n_pad/32][nb][32]  the f16 d of each row's block, as f32
+struct Q0Layout {
+    int8_t* qs;
+    float* xd;
+    int nb;
+    __host__ __device__ Q0Layout(void* ws, int n_pad, int cols) {
+        nb = cols / 32;
+        qs = static_cast<int8_t*>(ws);
+        xd = reinterpret_cast<float*>(qs + (size_t)n_pad * cols);
+    }
+};
+
 // native_matmul (src/model/matmul.rs:120-148) + residual_add (ops.rs:365-370):
 // out[t * rows + r] = vec_dot(w row r, q8k(act row t)) (+ residual).
 struct QmmArgs {
-    int wtype;               // 12 = Q4_K, 14 = Q6_K
+    int wtype;               // 12 = Q4_K, 14 = Q6_K; 2 = Q4_0, 6 = Q5_0, 8 = Q8_0 (Q8_0 activations)
     const void* w;           // rows * cols/256 blocks
     int rows, cols;          // cols a multiple of 256
     const float* act;        // [n][cols]
@@ -205,6 +221,11 @@ struct QmmArgs {
     void* ws;                // workspace of qmm_workspace_bytes(n, cols) bytes (QmmLayout)
     float* out;              // [n][rows]
     const float* residual;   // [n][rows] or nullptr (may alias out)
+    // Gemma's post-attention RMSNorm of each output row before the residual
+    // add (forward.rs:346-350): gain [rows] or nullptr
+    const float* norm_w;
+    float norm_eps;
+    float* norm_tmp;         // with norm_w: [n][rows] f32 for the rows before the norm
 };
 
 // The 32-key tiles [kt_lo, kt_hi) that a block of queries at positions
@@ -344,7 +365,10 @@ hipError_t launch_gather(int hd_tile, const GatherArgs& a, hipStream_t st);
 hipError_t launch_epilogue(const EpiArgs& a, hipStream_t st);
 hipError_t launch_split_active(const SplitArgs& a, hipStream_t st);
 size_t qmm_workspace_bytes(int n, int cols);
+size_t qmm0_workspace_bytes(int n, int cols);  // the legacy block types
 hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st);
+// quantize_row_q8_0 into the reference's BlockQ8_0 layout (34 bytes each)
+hipError_t launch_quantize_q80(const float* act, int n, int cols, void* out, hipStream_t st);
 // quantize_rows_q8_k into the reference's BlockQ8K layout
 hipError_t launch_quantize_q8k(const float* act, int n, int cols, Q8KBlock* out, hipStream_t st);
 

@@ -496,6 +496,221 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The legacy 32-value block types: Q4_0, Q5_0 and Q8_0 weights over Q8_0
+// activations (MatWeight::Q40 and ExpertMat::{Q40, Q50, Q80},
+// src/model/matmul.rs:103-106, 192-194; ActScratch::q80, :73-82).  A block
+// dot is d_w * d_a * sumi with sumi = sum_j w_j a_j over 32 int8 values, so
+// one v_mfma_i32_32x32x32_i8 per block gives the exact sumi of a 32 x 32
+// (activation row x weight row) tile, and a K = 2 f32 MFMA the d_w d_a of
+// every slot (each one f32 product); the combine is sum = fma(sumi, d, sum)
+// in block order.  Every integer is exact, so each output is within
+// (nb + 12) * 2^-24 * sum_i |w_i a_i| of the exact dot, as the reference's
+// own f32 accumulation is (nb = cols / 32).
+
+// quantize_row_q8_0 (candle-core 0.8.4 BlockQ8_0::from_float, ggml's
+// reference): per 32 values of a row, amax = max |x| (a NaN never wins), d =
+// amax / 127, id = d != 0 ? 1 / d : 0 (IEEE divisions, as the reference's),
+// q = round(x * id) half away from zero, saturated to int8; the block's scale
+// is f16(d), round to nearest even.  One wave per (32-row tile, block): lane
+// (c, g) holds values 16 g .. 16 g + 15 of row c.  REF = false writes the
+// operand order of the workspace (Q0Layout), REF = true the reference's
+// BlockQ8_0 (34 bytes: f16 d, int8 qs[32]).  Rows n .. n_pad - 1 are zeros.
+template <bool REF>
+__global__ __launch_bounds__(256) void q80_quantize_kernel(const float* __restrict__ x, int cols, int nb, int n,
+                                                           int n_pad, void* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);  // (tile, block)
+    if (item >= (n_pad / 32) * nb) return;  // (no barrier below: a whole wave leaves)
+    const int t32 = item / nb, b = item - t32 * nb;
+    const int c = lane & 31, g = lane >> 5;
+    const int t = t32 * 32 + c;
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < n) v[k] = gld<f32x4>(x + (size_t)t * cols + (size_t)b * 32 + 16 * g + 4 * k);
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) am = fmaxf(am, fabsf(v[k][e]));
+    am = fmaxf(am, __shfl_xor(am, 32));
+    float d, id;
+    {
+#pragma clang fp contract(off)
+        d = am / 127.0f;
+        id = d != 0.0f ? 1.0f / d : 0.0f;
+    }
+    uint32_t pk[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float q;
+            {
+#pragma clang fp contract(off)
+                q = roundf(v[k][e] * id);
+            }
+            q = q != q ? 0.0f : fminf(fmaxf(q, -128.0f), 127.0f);
+            w |= ((uint32_t)(int)q & 0xFFu) << (8 * e);
+        }
+        pk[k] = w;
+    }
+    const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16)d);
+    if constexpr (REF) {
+        if (t >= n) return;
+        uint8_t* blk = static_cast<uint8_t*>(out) + ((size_t)t * nb + b) * 34;
+        if (g == 0) *reinterpret_cast<uint16_t*>(blk) = dh;
+        uint16_t* q16 = reinterpret_cast<uint16_t*>(blk + 2 + 16 * g);  // (2-byte aligned)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            q16[2 * k] = (uint16_t)(pk[k] & 0xFFFFu);
+            q16[2 * k + 1] = (uint16_t)(pk[k] >> 16);
+        }
+    } else {
+        const Q0Layout L(out, n_pad, cols);
+        const size_t tb = (size_t)t32 * nb + b;
+        *reinterpret_cast<u32x4*>(L.qs + (tb * 64 + lane) * 16) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        if (g == 0) L.xd[tb * 32 + c] = (float)__builtin_bit_cast(_Float16, dh);
+    }
+}
+
+// A signed int8 in each byte of x (each in [0, 255 - off]) minus off, without
+// carries between bytes: (x + 128 - off) stays in 0..255, then flip bit 7.
+__device__ __forceinline__ uint32_t bytes_minus(uint32_t x, uint32_t off4) {
+    return ((x | 0x80808080u) - off4) ^ 0x80808080u;
+}
+// bits 0..3 of b to bit 4 of bytes 0..3
+__device__ __forceinline__ uint32_t bits_to_byte_bit4(uint32_t b) { return ((b * 0x00204081u) & 0x01010101u) << 4; }
+
+// The weight operand of one legacy block for lane (c, g): values 16 g ..
+// 16 g + 15 of the block of weight row c as int8, and the block's f16 d.
+template <int WT>
+__device__ __forceinline__ i32x4 legacy_operand(const uint8_t* blk, int g, uint32_t& dh) {
+    if constexpr (WT == 8) {  // Q8_0: d, int8 qs[32]
+        dh = gld<uint16_t>(blk);
+        return __builtin_bit_cast(i32x4, gld16_a2(blk + 2 + 16 * g));
+    } else if constexpr (WT == 2) {  // Q4_0: d, qs[16]; value j: nibble of byte j % 16 (high for j >= 16) - 8
+        dh = gld<uint16_t>(blk);
+        const u32x4 q = gld16_a2(blk + 2);
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = bytes_minus((g ? q[k] >> 4 : q[k]) & 0x0F0F0F0Fu, 0x08080808u);
+        return __builtin_bit_cast(i32x4, o);
+    } else {  // Q5_0: d, qh (32 bits), qs[16]; value j: nibble | bit j of qh << 4, - 16
+        static_assert(WT == 6, "legacy weight type");
+        dh = gld<uint16_t>(blk);
+        const uint32_t qh = (uint32_t)gld<uint16_t>(blk + 2) | ((uint32_t)gld<uint16_t>(blk + 4) << 16);
+        const u32x4 q = gld16_a2(blk + 6);
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t nib = (g ? q[k] >> 4 : q[k]) & 0x0F0F0F0Fu;
+            const uint32_t hi = bits_to_byte_bit4((qh >> (16 * g + 4 * k)) & 0xFu);
+            o[k] = bytes_minus(nib | hi, 0x10101010u);
+        }
+        return __builtin_bit_cast(i32x4, o);
+    }
+}
+
+// A workgroup (4 waves) owns 32 weight rows x 128 activation rows; wave w the
+// 32 x 32 tile of activation rows 32 w .. 32 w + 31.  Lane (c, g): weight row
+// c of the tile (B operand) and activation row c (A operand), values 16 g ..
+// 16 g + 15 of each block; accumulator slot i is output (activation row
+// 8 (i / 4) + 4 g + i % 4, weight row c).  The next block's operands are
+// loaded before this block's MFMAs.
+template <int WT>
+__global__ __launch_bounds__(256) void qmm0_kernel(const QmmArgs a) {
+    constexpr int BB = WT == 2 ? 18 : (WT == 6 ? 22 : 34);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 31, g = lane >> 5;
+    const int nb = a.cols / 32;
+    const int n_rt = (a.rows + 31) / 32, n_tt = a.n_pad / 128;
+    const int nwg = n_rt * n_tt, hw = blockIdx.x;
+    const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
+    const int rt = lid / n_tt, tt = lid - rt * n_tt;
+    const int r = min(rt * 32 + c, a.rows - 1);
+    const int t32 = tt * 4 + wave;  // this wave's 32-row activation tile
+    const Q0Layout L(a.ws, a.n_pad, a.cols);
+    const uint8_t* wrow = static_cast<const uint8_t*>(a.w) + (size_t)r * nb * BB;
+    const int8_t* abase = L.qs + ((size_t)t32 * nb * 64 + lane) * 16;
+    const float* xbase = L.xd + (size_t)t32 * nb * 32 + c;
+
+    f32x16 sum;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum[i] = 0.0f;
+    const f32x16 z = {};
+    // operands of block b: A (activations), the rows' d (lane (c, 0)), B
+    // (weights) and the weight row's f16 d
+    i32x4 av = gld<i32x4>(abase);
+    float xd = gld<float>(xbase);
+    uint32_t dh;
+    i32x4 bv = legacy_operand<WT>(wrow, g, dh);
+    for (int b = 0; b < nb; ++b) {
+        const int bn = min(b + 1, nb - 1);  // (past the last block: a reload nobody uses)
+        const i32x4 av_n = gld<i32x4>(abase + (size_t)bn * 1024);
+        const float xd_n = gld<float>(xbase + (size_t)bn * 32);
+        uint32_t dh_n;
+        const i32x4 bv_n = legacy_operand<WT>(wrow + (size_t)bn * BB, g, dh_n);
+        const i32x16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, i32x16{}, 0, 0, 0);
+        const float wd = f16_to_f32(dh);
+        const f32x16 dd = __builtin_amdgcn_mfma_f32_32x32x2f32(g == 0 ? xd : 0.0f, g == 0 ? wd : 0.0f, z, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum[i] = __builtin_fmaf((float)acc[i], dd[i], sum[i]);
+        av = av_n;
+        xd = xd_n;
+        bv = bv_n;
+        dh = dh_n;
+    }
+    const int rr = rt * 32 + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = t32 * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+        if (t < a.n && rr < a.rows) {
+            const size_t idx = (size_t)t * a.rows + rr;
+            float v = sum[i];
+            if (a.residual) v += a.residual[idx];
+            a.out[idx] = v;
+        }
+    }
+}
+
+// Gemma's post-attention RMSNorm before the residual add (forward.rs:346-350):
+// row t of x ([n][e], the matmul's output) becomes out = x * scale * w +
+// residual, scale = 1 / (float)sqrt(ss / e + eps) with ss the f64 sum of the
+// row's f32 squares (norm_rows_inplace -> rms_norm_inplace, ops.rs:106-114,
+// 141-145; the sum in another order than the reference's left fold, which
+// may move scale by an ulp).  residual may alias out (not x).  One workgroup
+// per row.
+__global__ __launch_bounds__(256) void post_norm_kernel(const float* __restrict__ x, float* out,
+                                                        const float* __restrict__ w, const float* residual, int e,
+                                                        float eps) {
+    __shared__ double s_part[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float* row = x + (size_t)t * e;
+    double ss = 0.0;
+    for (int i = tid; i < e; i += 256) {
+        const float x = row[i];
+        const float sq = x * x;
+        ss += (double)sq;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+    __syncthreads();
+    const double tot = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
+    const float scale = 1.0f / (float)sqrt(tot / (double)e + (double)eps);
+    for (int i = tid; i < e; i += 256) {
+#pragma clang fp contract(off)
+        float v = row[i] * scale * w[i];
+        if (residual) v = v + residual[(size_t)t * e + i];
+        out[(size_t)t * e + i] = v;
+    }
+}
+
 }  // namespace
 
 size_t qmm_workspace_bytes(int n, int cols) {
@@ -503,8 +718,40 @@ size_t qmm_workspace_bytes(int n, int cols) {
     return n_pad * nb * (QK + 16 * sizeof(uint16_t) + sizeof(float));
 }
 
+size_t qmm0_workspace_bytes(int n, int cols) {
+    const size_t n_pad = (size_t)qmm_rows_padded(n), nb = (size_t)cols / 32;
+    return n_pad * cols + n_pad * nb * sizeof(float);
+}
+
+static bool legacy_wtype(int wt) { return wt == 2 || wt == 6 || wt == 8; }
+
 hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st) {
     if (a.n <= 0 || a.rows <= 0) return hipSuccess;
+    if (legacy_wtype(a.wtype)) {
+        if (a.n_pad != qmm_rows_padded(a.n) || a.cols % 32 != 0) return hipErrorInvalidValue;
+        const int nb = a.cols / 32;
+        const unsigned items = (unsigned)(a.n_pad / 32 * nb);
+        hipLaunchKernelGGL(q80_quantize_kernel<false>, dim3((items + 3) / 4), dim3(256), 0, st, a.act, a.cols, nb,
+                           a.n, a.n_pad, a.ws);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const unsigned nwg = (unsigned)(((a.rows + 31) / 32) * (a.n_pad / 128));
+        QmmArgs b = a;
+        if (a.norm_w) {  // the raw rows to norm_tmp; the residual comes after the norm
+            b.residual = nullptr;
+            b.out = a.norm_tmp;
+        }
+        switch (a.wtype) {
+            case 2: hipLaunchKernelGGL(qmm0_kernel<2>, dim3(nwg), dim3(256), 0, st, b); break;
+            case 6: hipLaunchKernelGGL(qmm0_kernel<6>, dim3(nwg), dim3(256), 0, st, b); break;
+            default: hipLaunchKernelGGL(qmm0_kernel<8>, dim3(nwg), dim3(256), 0, st, b); break;
+        }
+        e = hipGetLastError();
+        if (e != hipSuccess || !a.norm_w) return e;
+        hipLaunchKernelGGL(post_norm_kernel, dim3((unsigned)a.n), dim3(256), 0, st, a.norm_tmp, a.out, a.norm_w,
+                           a.residual, a.rows, a.norm_eps);
+        return hipGetLastError();
+    }
     if (a.n_pad != qmm_rows_padded(a.n) || a.cols % QK != 0) return hipErrorInvalidValue;
     const int nb = a.cols / QK;
     hipLaunchKernelGGL(q8k_quantize_tiles_kernel, dim3((unsigned)(a.n_pad / 32 * nb)), dim3(512), 0, st, a.act,
@@ -512,12 +759,30 @@ hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const unsigned nwg = (unsigned)(((a.rows + 31) / 32) * (a.n_pad / 128));
+    QmmArgs b = a;
+    if (a.norm_w) {  // the raw rows to norm_tmp; the residual comes after the norm
+        b.residual = nullptr;
+        b.out = a.norm_tmp;
+    }
     if (a.wtype == 12)
-        hipLaunchKernelGGL(qmm_kernel<12>, dim3(nwg), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(qmm_kernel<12>, dim3(nwg), dim3(512), 0, st, b);
     else if (a.wtype == 14)
-        hipLaunchKernelGGL(qmm_kernel<14>, dim3(nwg), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(qmm_kernel<14>, dim3(nwg), dim3(512), 0, st, b);
     else
         return hipErrorInvalidValue;
+    e = hipGetLastError();
+    if (e != hipSuccess || !a.norm_w) return e;
+    hipLaunchKernelGGL(post_norm_kernel, dim3((unsigned)a.n), dim3(256), 0, st, a.norm_tmp, a.out, a.norm_w,
+                       a.residual, a.rows, a.norm_eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q80(const float* act, int n, int cols, void* out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int nb = cols / 32, n_pad = (n + 31) / 32 * 32;
+    const unsigned items = (unsigned)(n_pad / 32 * nb);
+    hipLaunchKernelGGL(q80_quantize_kernel<true>, dim3((items + 3) / 4), dim3(256), 0, st, act, cols, nb, n, n_pad,
+                       out);
     return hipGetLastError();
 }
 

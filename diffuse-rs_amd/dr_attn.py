@@ -146,6 +146,8 @@ _SIGS = {
     "dr_qmatmul": (_I, [_VP, _I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP]),
     "dr_qmatmul_expert": (_I, [_VP, _I, _VP, _SZ, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP]),
     "dr_quantize_q8k": (_I, [_VP, _VP, _SZ, _SZ, _VP]),
+    "dr_quantize_q8_0": (_I, [_VP, _VP, _SZ, _SZ, _VP]),
+    "dr_qmatmul_post_norm": (_I, [_VP, _I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP, _VP, _F]),
     "dr_pass_destroy": (None, [_VP]),
     "dr_cache_create": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _SZ, ctypes.POINTER(_VP)]),
     "dr_cache_create_layers": (_I, [_VP, _SZ, _SZ, c_size_p, c_size_p, _VP, _SZ, ctypes.POINTER(_VP)]),
@@ -587,6 +589,7 @@ class StepCache:
 
 
 WTYPE_Q4K, WTYPE_Q6K = 12, 14
+WTYPE_Q4_0, WTYPE_Q5_0, WTYPE_Q8_0 = 2, 6, 8
 
 
 def qmatmul(ctx: Context, wtype: int, w, rows: int, cols: int, act, n: int, out,
@@ -625,3 +628,17 @@ def ring_tiles(head_dim: int, nk: int, cap: int, window: Optional[int], qmin: in
     _check(load().dr_debug_ring_tiles(head_dim, nk, cap, -1 if window is None else window, qmin, qmax,
                                       n_split, ctypes.byref(lo), ctypes.byref(hi), ctypes.byref(ok)))
     return lo.value, hi.value, bool(ok.value)
+
+
+def qmatmul_post_norm(ctx: Context, wtype: int, w, rows: int, cols: int, act, n: int, out, norm_w,
+                      eps: float, residual=None) -> None:
+    """Wo, Gemma's post-attention RMSNorm of each output row, then the
+    residual (forward.rs:346-350; dr_qmatmul_post_norm)."""
+    _check(ctx.lib.dr_qmatmul_post_norm(ctx.h, wtype, _ptr(w), rows, cols, _ptr(act), n, _ptr(out),
+                                        _ptr(residual) or None, _ptr(norm_w), eps))
+
+
+def quantize_q8_0(ctx: Context, act, n: int, cols: int, out) -> None:
+    """quantize_row_q8_0 (matmul.rs:73-82) into n * cols/32 BlockQ8_0
+    (34 bytes each) at device pointer / tensor out."""
+    _check(ctx.lib.dr_quantize_q8_0(ctx.h, _ptr(act), n, cols, _ptr(out)))

@@ -351,9 +351,12 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
                           size_t n_items, size_t n_head, dr_opt_usize sliding_window,
                           dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi);
 
-/* ---- the projection after the attention: Wo on GGUF k-quant weights */
+/* ---- the projection after the attention: Wo on GGUF quantized weights */
 #define DR_WTYPE_Q4K 12 /* GGML type ids */
 #define DR_WTYPE_Q6K 14
+#define DR_WTYPE_Q4_0 2 /* the legacy 32-value block types, over Q8_0 activations */
+#define DR_WTYPE_Q5_0 6
+#define DR_WTYPE_Q8_0 8
 /* MatWeight::forward for Q4_K / Q6_K weights (src/model/matmul.rs:94-106):
  * the activations are quantized to Q8_K (ActScratch::q8k, matmul.rs:64-71,
  * quantize_rows_q8_k of src/kernels.rs:79-122) and native_matmul
@@ -371,6 +374,24 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
  * mins dot|), as the reference's scalar dot is. */
 int dr_qmatmul(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
                size_t n, float* out, const float* residual);
+/* The same for MatWeight::Q40 (matmul.rs:103-106, Q4_0 weights) and the
+ * expert types of ExpertMat (matmul.rs:156-158, 192-194: Q4_0, Q5_0, Q8_0):
+ * wtype DR_WTYPE_Q4_0 / _Q5_0 / _Q8_0, weights rows x cols/32 GGUF blocks of
+ * 18 / 22 / 34 bytes (2-byte aligned), cols a multiple of 32; the
+ * activations are quantized to Q8_0 (ActScratch::q80, matmul.rs:73-82:
+ * candle-core 0.8.4's BlockQ8_0::from_float, see dr_quantize_q8_0) and each
+ * output is vec_dot(weight row r, activation row t): per block d_w * d_a times
+ * the exact integer dot, summed over blocks in f32; within (cols / 32 + 12) *
+ * 2^-24 * sum_i |w_i a_i| of the exact value, as the reference's own f32
+ * sum is.  act must be 16-byte aligned. */
+
+/* Wo with Gemma's post-attention RMSNorm (src/model/forward.rs:346-350): out =
+ * rms_norm_inplace(act . W^T, norm_w, eps) (ops.rs:106-114, each of the n
+ * output rows of `rows` values, f64 sum of f32 squares) + residual (NULL:
+ * none).  Any weight type of dr_qmatmul; norm_w: [rows] device floats.  One
+ * more launch after the matmul (a row's norm needs the whole row). */
+int dr_qmatmul_post_norm(dr_ctx* ctx, int wtype, const void* w, size_t rows, size_t cols, const float* act,
+                         size_t n, float* out, const float* residual, const float* norm_w, float eps);
 
 /* ExpertMat::forward_expert (src/model/matmul.rs:176-213): dr_qmatmul on
  * expert `expert`'s slice of a [n_expert][rows][cols] stack of Q4_K / Q6_K
@@ -384,6 +405,14 @@ int dr_qmatmul_expert(dr_ctx* ctx, int wtype, const void* w, size_t n_expert, si
  * out, n * cols / 256 blocks of the reference's BlockQ8K (292 bytes: f32 d,
  * int8 qs[256], int16 bsums[16]; kernels.rs:37-41), 4-byte aligned. */
 int dr_quantize_q8k(dr_ctx* ctx, const float* act, size_t n, size_t cols, void* out);
+
+/* quantize_row_q8_0 (candle-core 0.8.4 BlockQ8_0::from_float, which
+ * ActScratch::q80 calls, src/model/matmul.rs:73-82), the quantization
+ * dr_qmatmul applies to its activations for the legacy weight types: act
+ * [n][cols] f32 (cols a multiple of 32, 16-byte aligned) -> out, n * cols /
+ * 32 blocks of 34 bytes (f16 d = amax / 127 rounded to nearest even, int8
+ * qs[32] = round(x / d) half away from zero), 2-byte aligned. */
+int dr_quantize_q8_0(dr_ctx* ctx, const float* act, size_t n, size_t cols, void* out);
 
 /* Launch configuration of the last attention kernel this context enqueued
  * (for measurement): key splits across workgroups, workgroups, waves per

@@ -34,7 +34,22 @@
  *   or_vec_dot_q6k_q8k      src/kernels.rs:313-347         (ggml's generic Q6_K dot)
  *   or_qmatmul              src/model/matmul.rs:120-148    (native_matmul:
  *                           out[t*rows + r] = vec_dot(weight row r, act row t)),
- *                           plus residual_add, src/model/ops.rs:365-370
+ *                           plus residual_add, src/model/ops.rs:365-370; the
+ *                           legacy types' dispatch of matmul.rs:103-106,192-194
+ *   or_dequant_q4_0         src/kernels.rs:165-173         (dequantize_q4_0_row)
+ *   or_dequant_q8_0         src/kernels.rs:176-183         (dequantize_q8_0_row)
+ *   or_dequant_q5_0         ggml's Q5_0 layout (d, qh[4], qs[16]), which
+ *                           candle-core 0.8.4's BlockQ5_0 holds
+ *   or_quantize_q8_0        ActScratch::q80 (matmul.rs:73-82) ->
+ *                           candle-core 0.8.4 BlockQ8_0::from_float, ggml's
+ *                           quantize_row_q8_0 (candle is not vendored: the
+ *                           published algorithm, restated)
+ *   or_vec_dot_q4_0_q8_0,   the generic block dots of ggml / candle-core
+ *   or_vec_dot_q5_0_q8_0,   0.8.4 (vec_dot_unopt): per block sumi of the
+ *   or_vec_dot_q8_0_q8_0    integer products, sumf += sumi * d_w * d_a
+ *   or_post_norm_residual   forward.rs:346-350: norm_rows_inplace
+ *                           (ops.rs:141-145 -> rms_norm_inplace :106-114) of
+ *                           Wo's output, then residual_add (ops.rs:365-370)
  *
  * Numerics follow Rust semantics: no FMA contraction outside the explicit
  * _mm256_fmadd_ps calls (build with -ffp-contract=off), f32::exp = libm expf,
@@ -543,12 +558,156 @@ float or_vec_dot_q6k_q8k(const uint8_t* x, const or_q8k_t* y, size_t nb) {
     return sumf;
 }
 
+/* ---- the legacy 32-value block types: Q4_0 (18 bytes: f16 d, 16 bytes of
+ * nibbles), Q5_0 (22 bytes: f16 d, 32 high bits, 16 bytes of nibbles), Q8_0
+ * (34 bytes: f16 d, 32 int8), and Q8_0 activations. */
+#define OR_Q0 32
+
+typedef struct {
+    uint16_t d;
+    int8_t qs[OR_Q0];
+} or_q80_t; /* packed: 34 bytes */
+
+/* Value j (0..31) of a legacy block, before the scale: Q4_0 nibble j of
+ * byte j % 16 (low nibble for j < 16, high for j >= 16) - 8
+ * (kernels.rs:168-170); Q5_0 the same nibble with bit j of qh as bit 4,
+ * - 16; Q8_0 the int8 itself (kernels.rs:179-180). */
+static int legacy_value(int wtype, const uint8_t* blk, int j) {
+    if (wtype == 2) {
+        const uint8_t q = blk[2 + (j & 15)];
+        return (int)(j < 16 ? (q & 0x0F) : (q >> 4)) - 8;
+    }
+    if (wtype == 6) {
+        uint32_t qh;
+        memcpy(&qh, blk + 2, 4);
+        const uint8_t q = blk[6 + (j & 15)];
+        const int nib = j < 16 ? (q & 0x0F) : (q >> 4);
+        return (nib | (int)(((qh >> j) & 1u) << 4)) - 16;
+    }
+    return (int)(int8_t)blk[2 + j];
+}
+
+static size_t legacy_bytes(int wtype) { return wtype == 2 ? 18 : (wtype == 6 ? 22 : 34); }
+
+static void dequant_legacy(int wtype, const uint8_t* blocks, size_t nb, float* out) {
+    const size_t bb = legacy_bytes(wtype);
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* x = blocks + b * bb;
+        uint16_t hd;
+        memcpy(&hd, x, 2);
+        const float d = or_f16_to_f32(hd);
+        for (int j = 0; j < OR_Q0; j++) out[b * OR_Q0 + j] = d * (float)legacy_value(wtype, x, j);
+    }
+}
+void or_dequant_q4_0(const uint8_t* blocks, size_t nb, float* out) { dequant_legacy(2, blocks, nb, out); }
+void or_dequant_q5_0(const uint8_t* blocks, size_t nb, float* out) { dequant_legacy(6, blocks, nb, out); }
+void or_dequant_q8_0(const uint8_t* blocks, size_t nb, float* out) { dequant_legacy(8, blocks, nb, out); }
+
+/* f32 -> f16, round to nearest even (the half crate's f16::from_f32);
+ * finite inputs below 65520 in magnitude, as a block scale amax / 127 is. */
+static uint16_t f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to inf */
+    if (ax < 0x38800000u) {                                     /* f16 subnormal or zero */
+        if (ax < 0x33000000u) return (uint16_t)sign;            /* below half the smallest subnormal */
+        /* |f| = m * 2^(e - 150); in units of the smallest subnormal 2^-24
+         * that is m >> (126 - e), rounded to nearest even (a round-up to
+         * 1024 is the smallest normal's encoding) */
+        const uint32_t e = ax >> 23, m = (ax & 0x7FFFFFu) | 0x800000u;
+        const uint32_t sh = 126u - e; /* 14 .. 24 */
+        const uint32_t q = m >> sh, rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        const uint32_t r = q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+        return (uint16_t)(sign | r);
+    }
+    const uint32_t e = (ax >> 23) - 112, m = ax & 0x7FFFFFu;
+    uint32_t h = (e << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++; /* (a carry into the exponent is right) */
+    return (uint16_t)(sign | h);
+}
+uint16_t or_f32_to_f16(float f) { return f32_to_f16(f); }
+
+/* quantize_row_q8_0 (candle-core 0.8.4 BlockQ8_0::from_float, as ggml):
+ * per 32 values amax = max |x| (f32::max, which ignores a NaN), d = amax /
+ * 127, id = d != 0 ? 1 / d : 0, q = round(x * id) (half away from zero,
+ * saturating to int8 as Rust's `as i8`), stored d = f16(d). */
+void or_quantize_q8_0(const float* src, size_t n, size_t cols, or_q80_t* dst) {
+    const size_t nb = cols / OR_Q0;
+    for (size_t t = 0; t < n; t++)
+        for (size_t b = 0; b < nb; b++) {
+            const float* xs = src + t * cols + b * OR_Q0;
+            or_q80_t* y = dst + t * nb + b;
+            float amax = 0.0f;
+            for (int j = 0; j < OR_Q0; j++) amax = fmaxf(amax, fabsf(xs[j]));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            y->d = f32_to_f16(d);
+            for (int j = 0; j < OR_Q0; j++) {
+                float v = roundf(xs[j] * id);
+                if (v != v) v = 0.0f;
+                v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
+                y->qs[j] = (int8_t)v;
+            }
+        }
+}
+
+/* The generic legacy block dots (ggml / candle-core 0.8.4 vec_dot_unopt):
+ * sumf += (float)sumi * d_w * d_a per block, in block order. */
+static float vec_dot_legacy_q8_0(int wtype, const uint8_t* x, const or_q80_t* y, size_t nb) {
+    const size_t bb = legacy_bytes(wtype);
+    float sumf = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* xb = x + b * bb;
+        int32_t sumi = 0;
+        for (int j = 0; j < OR_Q0; j++) sumi += legacy_value(wtype, xb, j) * (int32_t)y[b].qs[j];
+        uint16_t hd;
+        memcpy(&hd, xb, 2);
+        sumf += (float)sumi * or_f16_to_f32(hd) * or_f16_to_f32(y[b].d);
+    }
+    return sumf;
+}
+float or_vec_dot_q4_0_q8_0(const uint8_t* x, const or_q80_t* y, size_t nb) { return vec_dot_legacy_q8_0(2, x, y, nb); }
+float or_vec_dot_q5_0_q8_0(const uint8_t* x, const or_q80_t* y, size_t nb) { return vec_dot_legacy_q8_0(6, x, y, nb); }
+float or_vec_dot_q8_0_q8_0(const uint8_t* x, const or_q80_t* y, size_t nb) { return vec_dot_legacy_q8_0(8, x, y, nb); }
+
+/* Gemma's step after Wo (forward.rs:346-350): each of the n rows of cur
+ * ([n][e]) RMS-normalised in place with gain w and eps (norm_rows_inplace,
+ * ops.rs:141-145 -> rms_norm_inplace :106-114), then residual_add
+ * (ops.rs:365-370): cur += residual. */
+void or_post_norm_residual(float* cur, const float* w, const float* residual, size_t n, size_t e, float eps) {
+    for (size_t t = 0; t < n; t++) {
+        or_rms_norm_inplace(cur + t * e, w, e, eps);
+        if (residual)
+            for (size_t i = 0; i < e; i++) cur[t * e + i] = cur[t * e + i] + residual[t * e + i];
+    }
+}
+
 /* native_matmul (src/model/matmul.rs:120-148) over f32 activations quantized
  * to Q8_K (ActScratch::q8k, matmul.rs:64-71): out[t*rows + r] = vec_dot(weight
  * row r, activation row t); with residual (non-NULL), then residual_add
  * (ops.rs:365-370): out += residual.  wtype 12 = Q4_K, 14 = Q6_K (GGML ids). */
 void or_qmatmul(int wtype, const uint8_t* w, size_t rows, size_t cols, const float* act, size_t n,
                 float* out, const float* residual) {
+    if (wtype == 2 || wtype == 6 || wtype == 8) {
+        /* Q4_0 / Q5_0 / Q8_0 weights over Q8_0 activations (matmul.rs:103-106,
+         * 192-194: ActScratch::q80) */
+        const size_t nb0 = cols / OR_Q0, bb0 = legacy_bytes(wtype);
+        or_q80_t* q0 = (or_q80_t*)malloc((n * nb0 > 0 ? n * nb0 : 1) * sizeof(or_q80_t));
+        or_quantize_q8_0(act, n, cols, q0);
+#pragma omp parallel for schedule(static)
+        for (long long r = 0; r < (long long)rows; r++)
+            for (size_t t = 0; t < n; t++) {
+                float v = vec_dot_legacy_q8_0(wtype, w + (size_t)r * nb0 * bb0, q0 + t * nb0, nb0);
+                if (residual) v += residual[t * rows + (size_t)r];
+                out[t * rows + (size_t)r] = v;
+            }
+        free(q0);
+        return;
+    }
     const size_t nb = cols / OR_QK, bb = wtype == 12 ? 144 : 210;
     or_q8k_t* q = (or_q8k_t*)malloc((n * nb > 0 ? n * nb : 1) * sizeof(or_q8k_t));
     or_quantize_q8k(act, n, cols, q);

@@ -87,6 +87,15 @@ def load() -> ctypes.CDLL:
     lib.or_vec_dot_q6k_q8k.restype = ctypes.c_float
     lib.or_qmatmul.argtypes = [ctypes.c_int, P, ctypes.c_size_t, ctypes.c_size_t, P, ctypes.c_size_t,
                                P, P]
+    for nm in ("or_dequant_q4_0", "or_dequant_q5_0", "or_dequant_q8_0"):
+        getattr(lib, nm).argtypes = [P, ctypes.c_size_t, P]
+    lib.or_f32_to_f16.argtypes = [ctypes.c_float]
+    lib.or_f32_to_f16.restype = ctypes.c_uint16
+    lib.or_quantize_q8_0.argtypes = [P, ctypes.c_size_t, ctypes.c_size_t, P]
+    for nm in ("or_vec_dot_q4_0_q8_0", "or_vec_dot_q5_0_q8_0", "or_vec_dot_q8_0_q8_0"):
+        getattr(lib, nm).argtypes = [P, P, ctypes.c_size_t]
+        getattr(lib, nm).restype = ctypes.c_float
+    lib.or_post_norm_residual.argtypes = [P, P, P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_float]
     lib.or_cache_gather.argtypes = [P, P, ctypes.c_size_t, c_size_p, ctypes.c_size_t, P, P]
     lib.or_split_active.argtypes = [P, P, P, P, ctypes.c_size_t, ctypes.c_size_t,
                                     ctypes.c_size_t, c_size_p, c_size_p, c_size_p, c_size_p]
@@ -225,6 +234,13 @@ def split_active(prev_seq, last_changed: np.ndarray, seq, is_masked, step: int,
 QK_K = 256
 Q4K_BYTES, Q6K_BYTES = 144, 210
 WTYPE_Q4K, WTYPE_Q6K = 12, 14  # GGML type ids
+# the legacy 32-value block types (GGML ids) and their block bytes
+QK0 = 32
+WTYPE_Q4_0, WTYPE_Q5_0, WTYPE_Q8_0 = 2, 6, 8
+LEGACY_BYTES = {WTYPE_Q4_0: 18, WTYPE_Q5_0: 22, WTYPE_Q8_0: 34}
+# Q8_0 block, 34 bytes (f16 d, int8 qs[32])
+Q80_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", (QK0,))])
+assert Q80_DTYPE.itemsize == 34
 # Q8_K block, 292 bytes (src/kernels.rs:37-41)
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (QK_K,)), ("bsums", "<i2", (QK_K // 16,))])
 assert Q8K_DTYPE.itemsize == 292
@@ -243,11 +259,46 @@ def quantize_q8k(x: np.ndarray, n: int, cols: int) -> np.ndarray:
 
 
 def dequant(wtype: int, blocks: np.ndarray, nb: int) -> np.ndarray:
+    """nb blocks of wtype to f32 (QK_K values per k-quant block, QK0 per
+    legacy block)."""
     b = np.ascontiguousarray(blocks, np.uint8)
-    out = np.zeros(nb * QK_K, np.float32)
-    fn = load().or_dequant_q4k if wtype == WTYPE_Q4K else load().or_dequant_q6k
+    lib = load()
+    fn = {WTYPE_Q4K: lib.or_dequant_q4k, WTYPE_Q6K: lib.or_dequant_q6k, WTYPE_Q4_0: lib.or_dequant_q4_0,
+          WTYPE_Q5_0: lib.or_dequant_q5_0, WTYPE_Q8_0: lib.or_dequant_q8_0}[wtype]
+    out = np.zeros(nb * (QK0 if wtype in LEGACY_BYTES else QK_K), np.float32)
     fn(b.ctypes.data, nb, out.ctypes.data)
     return out
+
+
+def f32_to_f16(x: float) -> int:
+    return int(load().or_f32_to_f16(x))
+
+
+def quantize_q8_0(x: np.ndarray, n: int, cols: int) -> np.ndarray:
+    """quantize_row_q8_0: n rows of cols f32 -> n * cols / 32 Q8_0 blocks."""
+    src = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(n * cols // QK0, Q80_DTYPE)
+    load().or_quantize_q8_0(src.ctypes.data, n, cols, out.ctypes.data)
+    return out
+
+
+def vec_dot_legacy(wtype: int, x_blocks: np.ndarray, y_blocks: np.ndarray, nb: int) -> float:
+    """Q4_0 / Q5_0 / Q8_0 weight blocks . Q8_0 activation blocks."""
+    xb = np.ascontiguousarray(x_blocks, np.uint8)
+    yb = np.ascontiguousarray(y_blocks, Q80_DTYPE)
+    lib = load()
+    fn = {WTYPE_Q4_0: lib.or_vec_dot_q4_0_q8_0, WTYPE_Q5_0: lib.or_vec_dot_q5_0_q8_0,
+          WTYPE_Q8_0: lib.or_vec_dot_q8_0_q8_0}[wtype]
+    return float(fn(xb.ctypes.data, yb.ctypes.data, nb))
+
+
+def post_norm_residual(cur: np.ndarray, w: np.ndarray, residual, n: int, e: int, eps: float) -> None:
+    """Gemma's post-attention norm then residual add (forward.rs:346-350), in place."""
+    assert cur.dtype == np.float32 and cur.flags.c_contiguous
+    res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    ww = np.ascontiguousarray(w, np.float32)
+    load().or_post_norm_residual(cur.ctypes.data, ww.ctypes.data, None if res is None else res.ctypes.data, n, e,
+                                 eps)
 
 
 def vec_dot(wtype: int, x_blocks: np.ndarray, y_blocks: np.ndarray, nb: int) -> float:

@@ -299,3 +299,40 @@ def kquant_bound(orc, wtype: int, w, rows: int, cols: int, x: np.ndarray, n: int
     T = np.abs(kquant_acts_f64(orc, x, n, cols)) @ kquant_dequant_f64(orc, wtype, w, rows, cols, True).T
     r = 0.0 if res is None else np.abs(np.asarray(res, np.float64).reshape(n, rows))
     return 2.0 * (nb + 12) * 2.0 ** -24 * (T + r)
+
+
+def legacy_weights(rng: np.random.Generator, wtype: int, rows: int, cols: int) -> np.ndarray:
+    """rows * cols/32 random legacy blocks (Q4_0 = 2: 18 bytes, Q5_0 = 6: 22,
+    Q8_0 = 8: 34) with a sane positive f16 d at bytes 0..1; the quant bytes
+    are arbitrary."""
+    bb = {2: 18, 6: 22, 8: 34}[wtype]
+    nb = cols // 32
+    w = rng.integers(0, 256, (rows * nb, bb), dtype=np.uint8)
+    w[:, 0:2] = np.float16(rng.uniform(1e-3, 0.05, rows * nb)).view(np.uint8).reshape(-1, 2)
+    return w.reshape(-1)
+
+
+def legacy_dequant_f64(orc, wtype: int, w: np.ndarray, rows: int, cols: int, magnitude: bool = False):
+    """[rows][cols] float64 of the dequantized legacy blocks (|.| with magnitude)."""
+    nb = cols // 32
+    deq = orc.dequant(wtype, np.asarray(w, np.uint8), rows * nb).astype(np.float64).reshape(rows, cols)
+    return np.abs(deq) if magnitude else deq
+
+
+def legacy_acts_f64(orc, x: np.ndarray, n: int, cols: int) -> np.ndarray:
+    """[n][cols] float64 of the Q8_0 activations f16(d) * qs (quantize_row_q8_0)."""
+    q = orc.quantize_q8_0(x, n, cols)
+    d = q["d"].view(np.float16).astype(np.float64)
+    return (q["qs"].astype(np.float64) * d[:, None]).reshape(n, cols)
+
+
+def legacy_bound(orc, wtype: int, w, rows: int, cols: int, x: np.ndarray, n: int, res=None) -> np.ndarray:
+    """[n][rows] bound on |a legacy-type Wo output - another one|: every block's
+    integer dot is exact; its f32 combine with d_w and d_a, however ordered,
+    is within (nb + 12) * 2^-24 * T of the exact value, T = sum_i |w_i| |x_i|
+    (dequantized values); twice that between two computations, plus the
+    residual add's rounding on each side."""
+    nb = cols // 32
+    T = np.abs(legacy_acts_f64(orc, x, n, cols)) @ legacy_dequant_f64(orc, wtype, w, rows, cols, True).T
+    r = 0.0 if res is None else np.abs(np.asarray(res, np.float64).reshape(n, rows))
+    return 2.0 * (nb + 12) * 2.0 ** -24 * (T + r)

@@ -617,3 +617,172 @@ def test_q6k_values_bijective_and_scale_per_16():
             (idx,) = np.nonzero(d)
             assert len(idx) == 1 and d[idx[0]] == 16 * int(sc[idx[0] // 16]), (byte, pair)
     assert np.all(hit == 1)
+
+
+# ---- the legacy 32-value block types and Q8_0 activations
+
+def test_dequantize_q8_0_reference_vector():
+    """kernels.rs:382-395 (test_dequantize_q8_0_row): two blocks, d = 0.5
+    (0x3800), quants blk * 32 + i - 40: value i is 0.5 * (i - 40)."""
+    b = bytearray()
+    for blk in range(2):
+        b += (0x3800).to_bytes(2, "little")
+        b += bytes(((blk * 32 + i - 40) & 0xFF) for i in range(32))
+    out = orc.dequant(orc.WTYPE_Q8_0, np.frombuffer(bytes(b), np.uint8), 2)
+    assert np.array_equal(out, (0.5 * (np.arange(64) - 40)).astype(np.float32))
+
+
+def test_q4_0_nibble_order_closed_form():
+    """dequantize_q4_0_row (kernels.rs:165-173): byte i's low nibble is value
+    i, its high nibble value i + 16, each minus 8, times d (a swapped nibble
+    order or a missing -8 fails)."""
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    lo, hi = np.arange(16) % 16, (np.arange(16) * 7 + 3) % 16
+    b[2:] = (hi << 4) | lo
+    out = orc.dequant(orc.WTYPE_Q4_0, b, 1)
+    want = np.concatenate([lo - 8, hi - 8]).astype(np.float32) * np.float32(0.25)
+    assert np.array_equal(out, want)
+
+
+def test_q5_0_fields_bijective():
+    """Q5_0 (ggml's layout: f16 d, 32 high bits, 16 nibble bytes): with every
+    field zero each value is -16 d; raising a nibble's low bit moves exactly
+    one value by d, raising one of the 32 high bits exactly one value by 16 d,
+    and value j takes high bit j (nibbles as Q4_0's)."""
+    b = np.zeros(22, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    base = orc.dequant(orc.WTYPE_Q5_0, b, 1)
+    assert np.array_equal(base, np.full(32, -16.0, np.float32))
+    hit = np.zeros(32, int)
+    for byte in range(16):
+        for shift in (0, 4):
+            bb = b.copy()
+            bb[6 + byte] = 1 << shift
+            (idx,) = np.nonzero(orc.dequant(orc.WTYPE_Q5_0, bb, 1) - base)
+            assert list(idx) == [byte + (16 if shift else 0)]
+            hit[idx[0]] += 1
+    for bit in range(32):
+        bb = b.copy()
+        bb[2 + bit // 8] = 1 << (bit % 8)
+        d = orc.dequant(orc.WTYPE_Q5_0, bb, 1) - base
+        (idx,) = np.nonzero(d)
+        assert list(idx) == [bit] and d[bit] == 16.0
+    assert np.all(hit == 1)
+
+
+def test_f32_to_f16_is_round_to_nearest_even():
+    """The oracle's f16 rounding of the Q8_0 scale against numpy's (IEEE round
+    to nearest even), over normals, subnormals, exact ties and overflow."""
+    rng = np.random.default_rng(90)
+    xs = np.concatenate([rng.uniform(-1, 1, 2000) * 10.0 ** rng.integers(-9, 5, 2000),
+                         np.array([0.0, -0.0, 6.1e-5, 5.96e-8, 2.98e-8, 65504.0, 65519.0, 65520.0, 1e-30])])
+    # exact ties of f16 (a value halfway between two neighbours)
+    f = np.float16(rng.uniform(0.001, 1000, 200))
+    nxt = np.nextafter(f, np.float16(np.inf))
+    xs = np.concatenate([xs, ((f.astype(np.float64) + nxt.astype(np.float64)) / 2)])
+    xs = xs.astype(np.float32)
+    got = np.array([orc.f32_to_f16(float(x)) for x in xs], np.uint16)
+    want = xs.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want), xs[got != want][:5]
+
+
+def test_q8_0_quantize_invariants():
+    """quantize_row_q8_0: d = f16(amax / 127), the largest magnitude maps to
+    +-127, every q is round(x / d32) (half away from zero, d32 = amax / 127 in
+    f32), an all-zero block has d = 0 and zero quants."""
+    rng = np.random.default_rng(91)
+    x = (rng.standard_normal(6 * 64) * rng.uniform(0.01, 30, 6 * 64)).astype(np.float32)
+    x[32:64] = 0.0
+    x[70] = -5.0 * np.abs(x[64:96]).max()
+    q = orc.quantize_q8_0(x, 6, 64)
+    xb = x.reshape(-1, 32)
+    for b in range(q.size):
+        amax = np.float32(np.abs(xb[b]).max())
+        d32 = np.float32(amax / np.float32(127.0))
+        assert q["d"][b] == np.float32(d32).astype(np.float16).view(np.uint16)
+        if amax == 0:
+            assert not np.any(q["qs"][b])
+            continue
+        inv = np.float32(np.float32(1.0) / d32)
+        prod = (xb[b] * inv).astype(np.float32)
+        want = np.sign(prod) * np.floor(np.abs(prod) + 0.5)  # round half away from zero
+        assert np.array_equal(q["qs"][b].astype(np.float32), want)
+        assert abs(int(q["qs"][b][int(np.argmax(np.abs(xb[b])))])) == 127
+    assert q["qs"][2][70 - 64] == -127
+
+
+@pytest.mark.parametrize("wtype", [orc.WTYPE_Q4_0, orc.WTYPE_Q5_0, orc.WTYPE_Q8_0])
+def test_legacy_dot_equals_dequantized_dot(wtype):
+    """Each legacy block dot equals the float64 dot of the dequantized blocks
+    with the Q8_0 activations, within the f32 bound, on random blocks."""
+    from helpers import legacy_weights
+    rng = np.random.default_rng(92 + wtype)
+    nb = 6
+    w = legacy_weights(rng, wtype, 1, 32 * nb)
+    x = rng.standard_normal(32 * nb).astype(np.float32)
+    y = orc.quantize_q8_0(x, 1, 32 * nb)
+    got = orc.vec_dot_legacy(wtype, w, y, nb)
+    wv = orc.dequant(wtype, w, nb).astype(np.float64)
+    yv = y["qs"].astype(np.float64) * y["d"].view(np.float16).astype(np.float64)[:, None]
+    want = float(np.dot(wv, yv.reshape(-1)))
+    T = float(np.dot(np.abs(wv), np.abs(yv.reshape(-1))))
+    assert abs(got - want) <= (nb + 12) * 2.0 ** -24 * T, (got, want)
+    assert abs(want) > 1e-3
+
+
+@pytest.mark.parametrize("wtype", [orc.WTYPE_Q4_0, orc.WTYPE_Q5_0, orc.WTYPE_Q8_0])
+def test_qmatmul_legacy_composition_vs_f64_dequant(wtype):
+    """or_qmatmul on Q4_0 / Q5_0 / Q8_0 weights (matmul.rs:103-106, 192-194,
+    over Q8_0 activations) against a float64 composition X @ W^T + residual,
+    within the bound; the transposed output, swapped weight rows, swapped
+    activation rows and a dropped last block each break it."""
+    from helpers import legacy_acts_f64, legacy_bound, legacy_dequant_f64, legacy_weights
+    rng = np.random.default_rng(17 + wtype)
+    rows, cols, n = 9, 160, 5
+    w = legacy_weights(rng, wtype, rows, cols)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    x[1, :32] = 0.0
+    res = rng.standard_normal((n, rows)).astype(np.float32)
+    got = orc.qmatmul(wtype, w, rows, cols, x, n, res).reshape(n, rows).astype(np.float64)
+    W = legacy_dequant_f64(orc, wtype, w, rows, cols)
+    X = legacy_acts_f64(orc, x, n, cols)
+    want = X @ W.T + res
+    tol = legacy_bound(orc, wtype, w, rows, cols, x, n, res) + \
+        2.0 ** -24 * (np.abs(X) @ legacy_dequant_f64(orc, wtype, w, rows, cols, True).T)
+    err = np.abs(got - want)
+    assert np.all(err <= tol), float(np.max(err / tol))
+    assert np.max(np.abs(want)) > 0.1
+    bad_t = want.reshape(-1)[np.arange(n * rows).reshape(rows, n).T.reshape(-1)].reshape(n, rows)
+    X_drop = X.copy()
+    X_drop[:, -32:] = 0.0
+    for name, wrong in (("transposed", bad_t), ("weight rows swapped", X @ W[[1, 0] + list(range(2, rows))].T + res),
+                        ("activation rows swapped", X[[1, 0] + list(range(2, n))] @ W.T + res),
+                        ("last block dropped", X_drop @ W.T + res)):
+        assert np.any(np.abs(got - wrong) > tol), name
+
+
+def test_post_norm_residual_closed_form_and_f64():
+    """forward.rs:346-350: a row of equal values c normalises to
+    sign(c) / sqrt(1 + eps / c^2) * w, then the residual is added; random rows
+    match a float64 RMSNorm within a few ulp; without the residual the rows are
+    only normalised; a forgotten gain or residual is caught."""
+    e, eps = 96, 1e-6
+    w = np.linspace(0.5, 1.5, e).astype(np.float32)
+    cur = np.full((1, e), 3.0, np.float32)
+    res = np.arange(e, dtype=np.float32).reshape(1, e)
+    orc.post_norm_residual(cur, w, res, 1, e, eps)
+    want = (1.0 / np.sqrt(1.0 + eps / 9.0)) * w.astype(np.float64) + res.astype(np.float64)
+    assert np.allclose(cur, want, rtol=3e-7, atol=1e-6)
+    rng = np.random.default_rng(93)
+    x = (rng.standard_normal((4, e)) * 7).astype(np.float32)
+    r = rng.standard_normal((4, e)).astype(np.float32)
+    got = x.copy()
+    orc.post_norm_residual(got, w, r, 4, e, eps)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + eps) * w + r
+    assert np.max(np.abs(got - ref)) <= 1e-5
+    assert np.max(np.abs(got - (ref - r))) > 0.1 and np.max(np.abs(got - (ref - r) / w - r)) > 0.1
+    only = x.copy()
+    orc.post_norm_residual(only, w, None, 4, e, eps)
+    assert np.max(np.abs(only - (ref - r))) <= 1e-5
