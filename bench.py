@@ -382,6 +382,32 @@ def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
              "us_per_call": round(ms * 1e3, 3), "int_tops": round(ops / (ms / 1e3) / 1e12, 2),
              "frac_of_int8_mfma_peak": round(ops / (ms / 1e3) / 1e12 / PEAK_INT8_TOPS, 4),
              "bytes": nbytes, "gbs": round(nbytes / (ms / 1e3) / 1e9, 1)}
+    # the same Wo on Q4_0 weights (MatWeight::Q40, Q8_0 activations), and the
+    # Q4_K Wo with Gemma's post-attention RMSNorm before the residual add
+    import numpy as np
+    rng = np.random.default_rng(8)
+    w0 = rng.integers(0, 256, (rows * (cols // 32), 18), dtype=np.uint8)
+    w0[:, 0:2] = np.float16(rng.uniform(1e-3, 0.05, rows * (cols // 32))).view(np.uint8).reshape(-1, 2)
+    g = rng.uniform(0.5, 1.5, rows).astype(np.float32)
+    with torch.cuda.stream(stream):
+        dw0 = torch.from_numpy(w0.reshape(-1)).cuda()
+        dg = torch.from_numpy(g).cuda()
+    stream.synchronize()
+
+    def call0(i):
+        dr.qmatmul(ctx, dr.WTYPE_Q4_0, dw0, rows, cols, dx, n, out, dres)
+    ms0, _ = attention_only_ms(torch, stream, call0, 4, reps)
+    nbytes0 = rows * (cols // 32) * 18 + 4 * n * cols + 8 * n * rows
+    res_d["q4_0"] = {"us_per_call": round(ms0 * 1e3, 3), "int_tops": round(ops / (ms0 / 1e3) / 1e12, 2),
+                     "frac_of_int8_mfma_peak": round(ops / (ms0 / 1e3) / 1e12 / PEAK_INT8_TOPS, 4),
+                     "bytes": nbytes0, "gbs": round(nbytes0 / (ms0 / 1e3) / 1e9, 1)}
+
+    def call_pn(i):
+        dr.qmatmul_post_norm(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dg, 1e-6, dres)
+    ms_pn, _ = attention_only_ms(torch, stream, call_pn, 4, reps)
+    res_d["q4k_post_norm"] = {"us_per_call": round(ms_pn * 1e3, 3),
+                              "timing": "Wo, then the row RMSNorm and residual add (forward.rs:346-350)"}
+    del dw0, dg
     log(f"qmatmul: {res_d}")
     return res_d, (w.reshape(-1), rows, cols, x, n, res)
 

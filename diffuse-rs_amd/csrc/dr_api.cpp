@@ -705,7 +705,8 @@ static int check_slot(const dr_step_cache* c, size_t layer, size_t batch, const 
 // the Q/K/V epilogue (forward.rs:291-310) applied on the way when asked.
 static int store_rows(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
                       const float* k, const float* v, const float* k_norm_w, float eps,
-                      const float* kb, const float* vb, int v_norm, const dr_rope* rope);
+                      const float* kb, const float* vb, int v_norm, const dr_rope* rope,
+                      size_t kv_stride = 0);
 
 int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
                    const float* k, const float* v, const float* k_norm_w, float eps) {
@@ -714,7 +715,8 @@ int dr_cache_store(dr_step_cache* cache, size_t layer, size_t batch, const dr_pa
 
 static int store_rows(dr_step_cache* cache, size_t layer, size_t batch, const dr_pass* pass,
                       const float* k, const float* v, const float* k_norm_w, float eps,
-                      const float* kb, const float* vb, int v_norm, const dr_rope* rope) {
+                      const float* kb, const float* vb, int v_norm, const dr_rope* rope,
+                      size_t kv_stride) {
     DR_CHECK(check_slot(cache, layer, batch, "dr_cache_store"));
     if (!pass) return fail(DR_ERR_INVALID, "dr_cache_store: pass is NULL");
     if (pass->ctx != cache->ctx) return fail(DR_ERR_INVALID, "dr_cache_store: pass and cache use different contexts");
@@ -739,7 +741,8 @@ static int store_rows(dr_step_cache* cache, size_t layer, size_t batch, const dr
     a.vlo = cache->vlo[layer * cache->n_batch + batch];
     a.kn_w = k_norm_w;
     a.kn_eps = eps;
-    a.vec = a.hd == cache->hd_tile[layer] && (((uintptr_t)k | (uintptr_t)v) & 15) == 0;
+    a.rstride = kv_stride ? (int)kv_stride : a.n_head_kv * a.hd;
+    a.vec = a.hd == cache->hd_tile[layer] && (((uintptr_t)k | (uintptr_t)v) & 15) == 0 && a.rstride % 4 == 0;
     a.batch = (int)batch;
     a.n_batch = (int)cache->n_batch;
     a.kb = kb;
@@ -1154,16 +1157,19 @@ static size_t hilo_q_bytes(const dr::AttnArgs& a, const dr::LaunchPlan& p) {
     if (p.kernel != dr::KERNEL_HILO || (!a.qn_w && !a.qb && !a.rope)) return 0;
     if (!a.qb && !a.rope && a.hd == p.hd_tile) return 0;
     size_t total = 0;
-    for (int b = 0; b < a.n_batch; ++b) total += (size_t)a.slot[b].nq * a.q_rstride;
+    for (int b = 0; b < a.n_batch; ++b) total += (size_t)a.slot[b].nq * a.n_head * a.hd;
     return total * sizeof(float);
 }
 
+// (the copy packs the rows: the epilogue pass reads [nq][n_head * hd])
 static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, float* base) {
+    const size_t row = (size_t)a.n_head * a.hd;
     for (int b = 0; b < a.n_batch; ++b) {
         dr::AttnSlot& s = a.slot[b];
-        const size_t n = (size_t)s.nq * a.q_rstride;
+        const size_t n = (size_t)s.nq * row;
         if (n == 0) continue;
-        DR_HIP(hipMemcpyAsync(base, s.q, n * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+        DR_HIP(hipMemcpy2DAsync(base, row * sizeof(float), s.q, (size_t)a.q_rstride * sizeof(float),
+                                row * sizeof(float), (size_t)s.nq, hipMemcpyDeviceToDevice, ctx->stream));
         dr::EpiArgs e{};
         e.q = base;
         e.pos = s.qpos;
@@ -1187,6 +1193,7 @@ static int hilo_prepare_q(dr_ctx* ctx, dr::AttnArgs& a, float* base) {
     a.qb = nullptr;
     a.rope = nullptr;
     a.rot = 0;
+    a.q_rstride = (int)row;
     return DR_OK;
 }
 
@@ -1408,17 +1415,21 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
     return launch_plan(cache->ctx, a, p);
 }
 
-int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item* items,
-                          size_t n_items, size_t n_head, dr_opt_usize sliding_window,
-                          dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi) {
-    if (!epi) return fail(DR_ERR_INVALID, "dr_attention_step_epi: epi is NULL");
-    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "dr_attention_step_epi: no items");
+// dr_attention_step_epi and dr_attention_step_rows: the store of each item's
+// rows (with the K / V part of the epilogue) and the attention (with its Q
+// part); Q rows q_stride and K / V rows kv_stride elements apart (0: packed).
+static int step_impl(dr_step_cache* cache, size_t layer, const dr_step_item* items, size_t n_items,
+                     size_t n_head, dr_opt_usize sliding_window, dr_opt_usize causal_prefix, float scale,
+                     const dr_epilogue* epi, size_t q_stride, size_t kv_stride, const char* who) {
+    static const dr_epilogue none{};
+    if (!epi) epi = &none;
+    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "%s: no items", who);
     if (n_items > (size_t)dr::MAX_BATCH)
-        return fail(DR_ERR_INVALID, "dr_attention_step_epi: %zu items > %d", n_items, dr::MAX_BATCH);
+        return fail(DR_ERR_INVALID, "%s: %zu items > %d", who, n_items, dr::MAX_BATCH);
     const dr_rope* rope = epi->rope;
     if (rope) {
         if (!cache || rope->ctx != cache->ctx)
-            return fail(DR_ERR_INVALID, "dr_attention_step_epi: rope uses another context");
+            return fail(DR_ERR_INVALID, "%s: rope uses another context", who);
         if (rope->rope_dim % 8 != 0)
             return fail(DR_ERR_UNSUPPORTED, "rope_dim %zu is not a multiple of 8 (use dr_qkv_epilogue)",
                         rope->rope_dim);
@@ -1434,7 +1445,14 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
     dr::AttnArgs a;
     int max_nq = 0;
     DR_CHECK(cached_args(cache, layer, bi, n_items, n_head, sliding_window, causal_prefix, scale,
-                         epi->q_norm_w, epi->eps, "dr_attention_step_epi", a, max_nq));
+                         epi->q_norm_w, epi->eps, who, a, max_nq));
+    const size_t q_row = n_head * (size_t)a.hd, kv_row = (size_t)a.n_head_kv * a.hd;
+    if (q_stride && (q_stride < q_row || q_stride > (size_t)INT32_MAX || q_stride % 4 != 0))
+        return fail(DR_ERR_INVALID, "%s: q_stride %zu is not a multiple of 4 of at least n_head * head_dim %zu", who,
+                    q_stride, q_row);
+    if (kv_stride && (kv_stride < kv_row || kv_stride > (size_t)INT32_MAX))
+        return fail(DR_ERR_INVALID, "%s: kv_stride %zu < n_head_kv * head_dim %zu", who, kv_stride, kv_row);
+    if (q_stride) a.q_rstride = (int)q_stride;
     for (size_t b = 0; b < n_items; ++b)
         if (items[b].pass->n > 0 && (!items[b].k || !items[b].v))
             return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
@@ -1444,12 +1462,36 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
     const int mask = mask_of(sliding_window, causal_prefix);
     const int qepi = (epi->bq || rope) ? dr::QEPI_FULL : (epi->q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
     const dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total, mask, qepi);
-    if (max_nq > 0) DR_CHECK(check_q_dtype(a, p, "dr_attention_step_epi"));  // (before any store)
+    if (max_nq > 0) DR_CHECK(check_q_dtype(a, p, who));  // (before any store)
     for (size_t b = 0; b < n_items; ++b)
         DR_CHECK(store_rows(cache, layer, b, items[b].pass, items[b].k, items[b].v, epi->k_norm_w,
-                            epi->eps, epi->bk, epi->bv, epi->v_norm, rope));
+                            epi->eps, epi->bk, epi->bv, epi->v_norm, rope, kv_stride));
     if (max_nq == 0) return DR_OK;
     return launch_plan(cache->ctx, a, p);
+}
+
+int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item* items,
+                          size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                          dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi) {
+    if (!epi) return fail(DR_ERR_INVALID, "dr_attention_step_epi: epi is NULL");
+    return step_impl(cache, layer, items, n_items, n_head, sliding_window, causal_prefix, scale, epi, 0, 0,
+                     "dr_attention_step_epi");
+}
+
+int dr_attention_step_rows(dr_step_cache* cache, size_t layer, const dr_step_item_rows* items,
+                           size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                           dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi) {
+    if (!items || n_items < 1) return fail(DR_ERR_INVALID, "dr_attention_step_rows: no items");
+    if (n_items > (size_t)dr::MAX_BATCH)
+        return fail(DR_ERR_INVALID, "dr_attention_step_rows: %zu items > %d", n_items, dr::MAX_BATCH);
+    dr_step_item it[dr::MAX_BATCH];
+    for (size_t b = 0; b < n_items; ++b) {
+        if (items[b].q_stride != items[0].q_stride || items[b].kv_stride != items[0].kv_stride)
+            return fail(DR_ERR_INVALID, "dr_attention_step_rows: item %zu has other strides than item 0", b);
+        it[b] = dr_step_item{items[b].q, items[b].out, items[b].pass, items[b].k, items[b].v};
+    }
+    return step_impl(cache, layer, it, n_items, n_head, sliding_window, causal_prefix, scale, epi,
+                     items[0].q_stride, items[0].kv_stride, "dr_attention_step_rows");
 }
 
 int dr_attention(float* out, size_t out_len, const float* q, size_t q_len, const float* k,

@@ -81,8 +81,9 @@ struct AttnArgs {
 static_assert(offsetof(AttnArgs, slot) == 64, "scalar block of AttnArgs is one 64-byte line");
 
 struct StoreArgs {
-    const float* k;      // [n][n_head_kv][hd] f32 rows
+    const float* k;      // [n][rstride] f32 rows, kv head g at g * hd
     const float* v;
+    int rstride;         // elements between rows (0: n_head_kv * hd)
     const int* pos;      // [n] strictly ascending destination positions (device);
                          // nullptr: row r -> r
     int n;

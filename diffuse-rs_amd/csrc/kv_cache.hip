@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const StoreArgs a) {
     const int r = r0 + rl;
     const bool ok = r < a.n;
     const int d0 = dc * SD + part * SPT;  // first head-dim entry of this thread
-    const size_t row = ((size_t)(ok ? r : 0) * a.n_head_kv + g) * a.hd;
+    const size_t row = (size_t)(ok ? r : 0) * a.rstride + (size_t)g * a.hd;
     f32x4 xk[V4], xv[V4];
     if (ok && a.vec) {
 #pragma unroll
@@ -416,8 +416,8 @@ __global__ __launch_bounds__(256) void kv_store_tiles_kernel(const StoreArgs a) 
     const int tid = threadIdx.x;
     const int rg = tid % NRG, dc = tid / NRG;
     const int r0 = tb * VT_KEYS + rg * RPG;  // first row of this thread
-    const size_t rstride = (size_t)a.n_head_kv * HD;
-    const size_t src = ((size_t)r0 * a.n_head_kv + g) * HD + 4 * dc;
+    const size_t rstride = (size_t)a.rstride;
+    const size_t src = (size_t)r0 * rstride + (size_t)g * HD + 4 * dc;
     f32x4 xk[RPG], xv[RPG];
 #pragma unroll
     for (int j = 0; j < RPG; ++j) {
@@ -574,6 +574,8 @@ hipError_t launch_store(int hd_tile, const StoreArgs& args, hipStream_t st) {
     if (args.n <= 0) return hipSuccess;
     if (hd_tile != 64 && hd_tile != 128 && hd_tile != 256 && hd_tile != 512) return hipErrorInvalidValue;
     StoreArgs a = args;
+    if (a.rstride == 0) a.rstride = a.n_head_kv * a.hd;  // (packed rows)
+    if (a.rstride < a.n_head_kv * a.hd) return hipErrorInvalidValue;
     // Batch slot b of nb: the attention launch puts the slot's kv heads on
     // XCDs [8b/nb, 8(b+1)/nb).
     const int nb = a.n_batch > 0 ? a.n_batch : 1;

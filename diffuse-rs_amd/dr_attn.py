@@ -79,6 +79,12 @@ class CStepItem(ctypes.Structure):
                 ("k", ctypes.c_void_p), ("v", ctypes.c_void_p)]
 
 
+class CStepItemRows(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("out", ctypes.c_void_p), ("pass_", ctypes.c_void_p),
+                ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("q_stride", ctypes.c_size_t),
+                ("kv_stride", ctypes.c_size_t)]
+
+
 class CEpilogue(ctypes.Structure):
     _fields_ = [("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
                 ("q_norm_w", ctypes.c_void_p), ("k_norm_w", ctypes.c_void_p),
@@ -136,6 +142,8 @@ _SIGS = {
     "dr_attention_step_epi": (_I, [_VP, ctypes.c_size_t, ctypes.POINTER(CStepItem), ctypes.c_size_t,
                                    ctypes.c_size_t, OptUsize, OptUsize, ctypes.c_float,
                                    ctypes.POINTER(CEpilogue)]),
+    "dr_attention_step_rows": (_I, [_VP, ctypes.c_size_t, ctypes.POINTER(CStepItemRows), ctypes.c_size_t,
+                                    ctypes.c_size_t, OptUsize, OptUsize, ctypes.c_float, ctypes.POINTER(CEpilogue)]),
     "dr_qkv_epilogue": (_I, [_VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, ctypes.c_size_t,
                              ctypes.c_size_t, _VP, _VP, _VP, _VP, _VP, _I, ctypes.c_float, _VP]),
     "dr_ctx_set_tuning": (_I, [_VP, _I, _I, _I]),
@@ -573,6 +581,24 @@ class StepCache:
                         _ptr(q_norm_w) or None, _ptr(k_norm_w) or None, 1 if v_norm else 0, eps,
                         rope.h.value if rope is not None else None)
         _check(self.ctx.lib.dr_attention_step_epi(
+            self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
+            scale, ctypes.byref(epi)))
+
+    def step_rows(self, layer: int, items: Sequence[tuple], n_head: int, q_stride: int, kv_stride: int,
+                  sliding_window: Optional[int] = None, causal_prefix: Optional[int] = None,
+                  scale: float = 1.0, bq=None, bk=None, bv=None, q_norm_w=None, k_norm_w=None,
+                  v_norm: bool = False, eps: float = 1e-6, rope: "Rope | None" = None) -> None:
+        """step_epi() on strided rows (dr_attention_step_rows): items = (q, out,
+        Pass, k, v) with q / k / v device addresses (ints or tensors) whose rows
+        are q_stride / kv_stride floats apart, e.g. the Q, K and V parts of
+        fused QKV rows."""
+        arr = (CStepItemRows * len(items))()
+        for i, (q, out, p, k, v) in enumerate(items):
+            arr[i] = CStepItemRows(_ptr(q), _ptr(out), p.h, _ptr(k), _ptr(v), q_stride, kv_stride)
+        epi = CEpilogue(_ptr(bq) or None, _ptr(bk) or None, _ptr(bv) or None,
+                        _ptr(q_norm_w) or None, _ptr(k_norm_w) or None, 1 if v_norm else 0, eps,
+                        rope.h.value if rope is not None else None)
+        _check(self.ctx.lib.dr_attention_step_rows(
             self.h, layer, arr, len(items), n_head, _opt(sliding_window), _opt(causal_prefix),
             scale, ctypes.byref(epi)))
 

@@ -351,6 +351,27 @@ int dr_attention_step_epi(dr_step_cache* cache, size_t layer, const dr_step_item
                           size_t n_items, size_t n_head, dr_opt_usize sliding_window,
                           dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi);
 
+/* One batch slot of a denoise-step layer whose Q, K and V rows lie at row
+ * strides: the rows of a fused QKV projection (Qkv::Fused,
+ * src/model/forward.rs:281-289), [n][n_head*hd + 2*n_head_kv*hd], are read
+ * in place with q = row, k = row + n_head*hd, v = k + n_head_kv*hd and both
+ * strides the fused row length -- no copy into separate Q / K / V buffers. */
+typedef struct {
+    const float* q;   /* device, row t at q + t * q_stride: [n_head][head_dim] f32 */
+    float* out;       /* device, [n_active][n_head * head_dim] f32, overwritten */
+    const dr_pass* pass;
+    const float* k;   /* device, row t at k + t * kv_stride: [n_head_kv][head_dim] f32 */
+    const float* v;   /* device, row t at v + t * kv_stride */
+    size_t q_stride;  /* elements between Q rows, a multiple of 4 (0: n_head * head_dim) */
+    size_t kv_stride; /* elements between K rows and between V rows (0: n_head_kv * head_dim) */
+} dr_step_item_rows;
+/* dr_attention_step_epi on strided rows (every item with the same strides);
+ * epi may be NULL (no epilogue: dr_attention_step without norms).  Same
+ * results as copying the rows apart and calling dr_attention_step_epi. */
+int dr_attention_step_rows(dr_step_cache* cache, size_t layer, const dr_step_item_rows* items,
+                           size_t n_items, size_t n_head, dr_opt_usize sliding_window,
+                           dr_opt_usize causal_prefix, float scale, const dr_epilogue* epi);
+
 /* ---- the projection after the attention: Wo on GGUF quantized weights */
 #define DR_WTYPE_Q4K 12 /* GGML type ids */
 #define DR_WTYPE_Q6K 14
