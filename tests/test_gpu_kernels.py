@@ -16,7 +16,7 @@ import pytest
 
 import dr_attn as dr
 import oracle as orc
-from helpers import TOL_MAX, TOL_MEAN, RowsSpec, Shape, as_kernel_sees, err_stats
+from helpers import check_raw, TOL_MAX, TOL_MEAN, RowsSpec, Shape, as_kernel_sees, err_stats
 
 pytestmark = pytest.mark.gpu
 
@@ -116,18 +116,21 @@ def _run(dev, name, kernel, hd=128):
     got = [dev.get(o) for o in outs]
     s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, causal_prefix=prefix, scale=1 / math.sqrt(hd))
     qr, kr = RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t)))
-    wants = []
+    wants, raws = [], []
     for Q, K, V in ins:
         q, k = Q.reshape(-1).copy(), K.reshape(-1).copy()
         if qk_norm:
             orc.norm_heads(q, qn, 1e-6)
             orc.norm_heads(k, kn, 1e-6)
         want = np.zeros(n_c * h * hd, np.float32)
-        # the oracle on the operands as the kernel rounds them: the bar of the
-        # masked cases, where few keys are visible per row
+        # the oracle on the operands as the kernel rounds them: the kernel's
+        # own arithmetic at the standard bar on every row
         orc.attention(want, *as_kernel_sees(q, k, V.reshape(-1).copy(), 1 / math.sqrt(hd)), s, qr, kr,
                       threads=0)
         wants.append(want)
+        raws.append((q, k, V.reshape(-1).copy()))
+    for b, (g, (q, k, v)) in enumerate(zip(got, raws)):  # and the raw f32 inputs
+        check_raw(orc, g, q, k, v, s, qr, kr, f"{name} batch {b}", say)
     return got, wants, info
 
 

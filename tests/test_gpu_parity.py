@@ -17,8 +17,8 @@ import pytest
 
 import dr_attn as dr
 import oracle as orc
-from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, Config, RowsSpec, Shape, as_kernel_sees, closed_form,
-                     config_seed, err_stats, golden_cases, materialise)
+from helpers import (CONFIGS, TOL_MAX, TOL_MEAN, Config, RowsSpec, Shape, as_kernel_sees, check_raw,
+                     closed_form, config_seed, err_stats, golden_cases, materialise)
 
 pytestmark = pytest.mark.gpu
 
@@ -334,6 +334,8 @@ def test_wave_rows_16_and_32_vs_oracle(dev, hd, window, prefix):
             assert dev.ctx.last_launch()["rows_per_wave"] == rows
             got[rows] = dev.get(out)
             check(got[rows], want, f"rows {rows} window {window} prefix {prefix}")
+            check_raw(orc, got[rows], Q.reshape(-1), K.reshape(-1), V.reshape(-1), s, qr, kr,
+                      f"rows {rows} window {window} prefix {prefix}", say)
     finally:
         dev.ctx.set_wave_rows(0)
     assert np.max(np.abs(got[16] - got[32])) < 1e-5
@@ -964,4 +966,6 @@ def test_batched_plans_vs_oracle(dev, h, hkv, hd, batch, window, prefix):
         Q, K, V = ins[b]
         want = oracle_run(s, qr, kr, *as_kernel_sees(Q.reshape(-1).copy(), K.reshape(-1).copy(),
                                                      V.reshape(-1).copy(), scale))
-        check(dev.get(outs[b]), want, f"batch {b}")
+        got = dev.get(outs[b])
+        check(got, want, f"batch {b}")
+        check_raw(orc, got, Q.reshape(-1), K.reshape(-1), V.reshape(-1), s, qr, kr, f"batch {b}", say)

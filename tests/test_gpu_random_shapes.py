@@ -20,7 +20,7 @@ import pytest
 
 import dr_attn as dr
 import oracle as orc
-from helpers import TOL_MAX, TOL_MEAN, RowsSpec, Shape, as_kernel_sees, err_stats
+from helpers import check_raw, TOL_MAX, TOL_MEAN, RowsSpec, Shape, as_kernel_sees, err_stats
 
 from test_gpu_kernels import dev, say  # noqa: F401
 
@@ -136,6 +136,7 @@ def test_random_shape_vs_oracle(dev, seed):
             orc.attention(want, q, k, V.reshape(-1).copy(), s, qr, kr, threads=0)
         else:
             orc.attention(want, *as_kernel_sees(q, k, V.reshape(-1).copy(), scale), s, qr, kr, threads=0)
+            check_raw(orc, got, q, k, V.reshape(-1).copy(), s, qr, kr, f"seed {seed} batch {b}", say)
         # rows with no visible key are NaN in both
         assert np.array_equal(np.isnan(got), np.isnan(want)), (seed, b)
         mx, mean = err_stats(got, want)
