@@ -1449,7 +1449,8 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
-                          int force_split, int force_rows, int force_kernel, bool merge_in_kernel) {
+                          int force_split, int force_rows, int force_kernel, bool merge_in_kernel,
+                          int key_band) {
     LaunchPlan p{};
     p.hd_tile = hd <= 64 ? 64 : (hd <= 128 ? 128 : (hd <= 256 ? 256 : 512));
     p.block_n = BN;
@@ -1466,18 +1467,31 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     // every K/V byte of its key range through its CU, so the call is bound by
     // that stream; independent per-wave DMA keeps it nearer the CU's rate
     // than the staged kernel's shared super-tiles.  Picked when the one-block
-    // workgroups fit one round of the CUs, and at head dim 256 only for a
-    // sliding window of at most 1024 (each workgroup's band is then at most
-    // ~2k keys, and the staged kernel's 64-row blocks would need a key split:
-    // DiffusionGemma's sliding layers take 21.6 against 28.7 us; on its
-    // global layers the 64-row split blocks win, 34.3 against 37.4).  When
-    // one-block workgroups would take more than one round of the CUs (C3's
-    // GQA rows: 448 blocks on 256 CUs), the staged kernel's 64-row workgroups
-    // read each K/V tile once for twice the rows and keep them.
+    // workgroups fit one round of the CUs, and at head dim 256 when each
+    // workgroup's key band is short: a sliding window of at most 1024 (a band
+    // of at most ~2k keys, where the staged kernel's 64-row blocks would need
+    // a key split: DiffusionGemma's sliding layers take 21.6 against
+    // 28.7 us), or a band of at most 4608 keys that two in-kernel-merged
+    // splits fill the chip with (16/8 heads, 256 queries, no window: 18.3
+    // against 28.9 us at 1280 keys, 23.2 against 30.1 at 2304, a tie at
+    // 4352; at 8448 and 16640 keys the staged kernel's 64-row split blocks
+    // win, 57.0 against 62.2 and 94.4 against 109.4; window 2500 over 6256
+    // keys, canvas rows at the end, a 2755-key band: 27.4 against 34.3).  When one-block
+    // workgroups would take more than one round of the CUs (C3's GQA rows:
+    // 448 blocks on 256 CUs), the staged kernel's 64-row workgroups read each
+    // K/V tile once for twice the rows and keep them.
     const int ring_blocks = n_batch * n_head_kv * row_blocks;
     const int rw = ring_waves(hd);
     const bool ring_ok = rw > 0 && mask != MASK_KEYS && (qepi != QEPI_FULL || rot == 0 || rot == hd);
-    const bool ring_auto = ring_blocks <= cus && (hd == 128 || (window >= 0 && window <= 1024));
+    // keys of the widest band a workgroup reads: from the query rows'
+    // positions when the caller knows them, else the window's worst case
+    // (plus a tile for the band's alignment)
+    int band = window >= 0 && 2 * window + BN < max_nk ? 2 * window + BN : max_nk;
+    if (key_band > 0 && key_band + BN < band) band = key_band + BN;
+    const bool ring_short_band = hd == 256 && merge_in_kernel && 2 * ring_blocks <= cus && band <= 4608 &&
+                                 ntiles >= 2 * rw;
+    const bool ring_auto =
+        ring_blocks <= cus && (hd == 128 || (window >= 0 && window <= 1024) || ring_short_band);
     if (ring_ok && (force_kernel == KERNEL_STREAMS || (force_kernel == KERNEL_AUTO && ring_auto)) &&
         force_rb <= 0 && force_kq <= 0 && force_rows <= 0) {
         p.kernel = KERNEL_STREAMS;

@@ -1143,7 +1143,7 @@ static dr::LaunchPlan plan_for(dr_ctx* ctx, const dr::AttnArgs& a, int hd, int m
     return dr::plan_attention(hd, a.n_batch, a.n_head_kv, a.group, max_nq, max_nk, mask, qepi,
                               mask == dr::MASK_POS ? a.window : -1, a.rope ? a.rot : 0, ctx->n_cu,
                               ctx->force_rb, ctx->force_kq, ctx->force_split, ctx->force_rows, kernel,
-                              ctx->merge_in_kernel != 0);
+                              ctx->merge_in_kernel != 0, a.key_band);
 }
 
 // The hi/lo kernel reads plain Q: with a Q epilogue (bias, QK-norm, RoPE),
@@ -1347,6 +1347,19 @@ static int cached_args(dr_step_cache* cache, size_t layer, const dr_batch_item* 
         const dr_pass* ps = it.pass;
         s.qpos0 = ps->n > 0 && ps->max_pos - ps->min_pos + 1 == ps->n ? (int)ps->min_pos : -1;
         max_nq = std::max(max_nq, s.nq);
+    }
+    // the keys any row block can see, for the planner: the union of the
+    // items' sliding-window bands [min_pos - w + 1, max_pos + w) in the cache
+    a.key_band = (int)cache->n_total;
+    if (a.window >= 0) {
+        long long lo = (long long)cache->n_total, hi = 0;
+        for (size_t b = 0; b < n_items; ++b) {
+            const dr_pass* ps = items[b].pass;
+            if (ps->n == 0) continue;
+            lo = std::min(lo, std::max(0LL, (long long)ps->min_pos - a.window + 1));
+            hi = std::max(hi, std::min((long long)cache->n_total, (long long)ps->max_pos + a.window));
+        }
+        a.key_band = (int)std::max(0LL, hi - lo);
     }
     return DR_OK;
 }

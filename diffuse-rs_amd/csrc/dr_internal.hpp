@@ -77,6 +77,9 @@ struct AttnArgs {
     const float* qb;               // [n_head*hd] or nullptr
     const float* rope;             // [max_len][rot/2][2] (sin, cos) table or nullptr
     int rot;                       // rotated dims (a multiple of 8)
+    // (host planning only) an upper bound on the keys any row block can see
+    // (the union of the query rows' sliding-window bands), 0: not known
+    int key_band;
 };
 static_assert(offsetof(AttnArgs, slot) == 64, "scalar block of AttnArgs is one 64-byte line");
 
@@ -342,7 +345,8 @@ enum QEpilogue : int {
 // to ring_merge_splits) will be merged in-kernel, which makes them cheaper.
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
-                          int force_split, int force_rows, int force_kernel, bool merge_in_kernel);
+                          int force_split, int force_rows, int force_kernel, bool merge_in_kernel,
+                          int key_band = 0);
 
 // Bytes of split workspace a plan needs (part_o + part_ml).
 size_t split_workspace_bytes(const LaunchPlan& p, int n_batch, int n_head_kv);

@@ -78,6 +78,9 @@ CASES_256 = {
     "qk_norm": (4, 4, 400, 96, 1, None, None, True, 0),
     "split2": (4, 4, 900, 64, 1, None, None, False, 2),
     "split3_window": (4, 2, 1500, 64, 1, 400, None, False, 3),
+    # no window, 1256 keys, 64 one-block workgroups: the planner's choice
+    # (run under DR_KERNEL_AUTO by test_planner_hd256_key_band)
+    "global_auto": (8, 4, 1000, 256, 1, None, None, False, 0),
 }
 
 
@@ -149,7 +152,7 @@ def test_kernel_family_vs_oracle(dev, name, kernel):
 
 
 @pytest.mark.parametrize("kernel", [dr.KERNEL_STAGED, dr.KERNEL_STREAMS], ids=["staged", "streams"])
-@pytest.mark.parametrize("name", list(CASES_256))
+@pytest.mark.parametrize("name", [n for n in CASES_256 if n != "global_auto"])
 def test_kernel_family_hd256_vs_oracle(dev, name, kernel):
     got, wants, info = _run(dev, name, kernel, hd=256)
     say(f"hd 256 {name} kernel {kernel}: launch {info}")
@@ -201,3 +204,42 @@ def test_planner_picks_streams_for_one_round(dev):
         items = [(q, dev.empty(n_c * h * hd), pc) for _ in range(2 if hkv == 4 else 1)]
         cache.attention(0, items, h, scale=0.1)
         assert dev.ctx.last_launch()["kernel"] == want, (h, hkv)
+
+
+def test_planner_hd256_key_band(dev):
+    """Head dim 256: the per-wave-stream kernel with two in-kernel-merged key
+    splits where those splits fill the chip in one round and every row
+    block's key band (the union of the rows' windows, from the passes'
+    positions) holds at most 4608 keys; the staged kernel's 64-row split
+    blocks otherwise.  Then the planner's choice on one such shape against
+    the oracle."""
+    hd = 256
+    # (h, hkv, n_prompt, n_canvas, window, kernel, n_split or 0 for any)
+    cases = (
+        (16, 8, 4096, 256, None, dr.KERNEL_STREAMS, 2),   # C5 global: 4352 keys
+        (16, 8, 8192, 256, None, dr.KERNEL_STAGED, 0),    # 8448 keys
+        (16, 8, 6000, 256, 2500, dr.KERNEL_STREAMS, 2),   # band [3501, 6256): 2755 keys
+        (16, 8, 6000, 256, 5000, dr.KERNEL_STAGED, 0),    # band [1001, 6256): 5255 keys
+        (32, 16, 4096, 256, None, dr.KERNEL_STAGED, 0),   # 256 one-block workgroups: no room to split
+    )
+    for h, hkv, n_p, n_c, window, want, n_split in cases:
+        n_t = n_p + n_c
+        cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+        z = dev.put(np.zeros((n_t, hkv * hd), np.float32))
+        cache.store(0, dr.Pass(dev.ctx, range(n_t)), z, z)
+        q = dev.put(np.zeros((n_c, h * hd), np.float32))
+        cache.attention(0, [(q, dev.empty(n_c * h * hd), dr.Pass(dev.ctx, range(n_p, n_t)))], h,
+                        sliding_window=window, scale=1 / math.sqrt(hd))
+        info = dev.ctx.last_launch()
+        say(f"h {h}/{hkv} keys {n_t} window {window}: launch {info}")
+        assert info["kernel"] == want, (h, hkv, n_t, window)
+        if n_split:
+            assert info["n_split"] == n_split and info["split_merge"] == 2
+        del cache
+    got, wants, info = _run(dev, "global_auto", dr.KERNEL_AUTO, hd=256)
+    say(f"global_auto: launch {info}")
+    assert info["kernel"] == dr.KERNEL_STREAMS and info["n_split"] == 2 and info["split_merge"] == 2
+    for g, w in zip(got, wants):
+        mx, mean = err_stats(g, w)
+        say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
+        assert mx <= TOL_MAX and mean <= TOL_MEAN, (mx, mean)

@@ -54,8 +54,10 @@ def dev():
 # (h, hkv, hd, n_prompt, n_canvas first call, n_canvas second call, window, forced splits)
 SHAPES = {
     "hd128_split3": (8, 8, 128, 1400, 200, 70, None, 3),
-    # a window above 1024 keeps hd 256 on the staged kernel, which splits the keys by itself
-    "hd256_window_auto_split": (16, 8, 256, 2048, 256, 100, 1500, 0),
+    # a key band above 4608 (window 5000 from the last 256 or 100 of 6256
+    # positions: 5255 or 5099 keys) keeps hd 256 on the staged kernel, which
+    # splits the keys by itself
+    "hd256_window_auto_split": (16, 8, 256, 6000, 256, 100, 5000, 0),
     # the per-wave-stream kernel (hd 256, window <= 1024) with forced splits
     "hd256_streams_split2": (16, 8, 256, 2048, 256, 100, 700, 2),
 }
