@@ -148,6 +148,11 @@ struct dr_ctx {
     // on the context: it is freed when the last of them is destroyed, so the
     // objects that use it may be destroyed before or after it
     std::atomic<int> refs{1};
+    // set while a host thread is inside an entry point that uses the
+    // context's workspaces, tickets or launch record (CtxUse)
+    std::atomic<bool> busy{false};
+    // dr_ctx_set_stream: the new stream waits on this, recorded on the old one
+    hipEvent_t switch_ev = nullptr;
 };
 
 struct dr_pass {
@@ -236,6 +241,48 @@ int upload_pass(dr_pass* p, const size_t* active, size_t n) {
 std::mutex g_default_mu;
 dr_ctx* g_default_ctx = nullptr;
 
+// One host thread at a time per context: an entry point that uses the
+// context's workspaces, split tickets or launch record holds this for the
+// call, and a second thread that arrives meanwhile gets DR_ERR_BUSY instead
+// of racing on them.
+class CtxUse {
+  public:
+    explicit CtxUse(dr_ctx* c) : c_(c), ok_(!c->busy.exchange(true, std::memory_order_acquire)) {}
+    ~CtxUse() {
+        if (ok_) c_->busy.store(false, std::memory_order_release);
+    }
+    CtxUse(const CtxUse&) = delete;
+    CtxUse& operator=(const CtxUse&) = delete;
+    bool ok() const { return ok_; }
+
+  private:
+    dr_ctx* c_;
+    bool ok_;
+};
+
+#define DR_CTX_USE(ctx, who)                                                                          \
+    CtxUse ctx_use_(ctx);                                                                             \
+    if (!ctx_use_.ok())                                                                               \
+        return fail(DR_ERR_BUSY, "%s: the context is in use by another thread (one thread at a time)", \
+                    who)
+
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// dr_attention_cached_noalloc's device scratch is one array per GPU, shared
+// by every context: a call on another stream than the previous call on that
+// GPU first waits (on the device) for the previous call's kernels, so two
+// calls never use it at once.  The event is made at dr_ctx_create, so the
+// call itself creates nothing.
+struct ScratchOrder {
+    std::mutex mu;
+    hipEvent_t done = nullptr;   // recorded after each call's launches
+    hipStream_t last = nullptr;  // the stream of the previous call
+};
+ScratchOrder g_scratch_order[64];
+
 }  // namespace
 
 extern "C" {
@@ -276,8 +323,21 @@ int dr_ctx_create(int device, dr_ctx** out) {
         delete c;
         return hip_fail(e, "hipGetSymbolAddress(scratch)");
     }
+    e = hipEventCreateWithFlags(&c->switch_ev, hipEventDisableTiming);
+    if (e == hipSuccess && device < 64) {
+        ScratchOrder& so = g_scratch_order[device];
+        std::lock_guard<std::mutex> lk(so.mu);
+        if (!so.done) e = hipEventCreateWithFlags(&so.done, hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        if (c->switch_ev) (void)hipEventDestroy(c->switch_ev);
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return hip_fail(e, "hipEventCreateWithFlags");
+    }
     e = hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device);
     if (e != hipSuccess) {
+        (void)hipEventDestroy(c->switch_ev);
         (void)hipStreamDestroy(c->own);
         delete c;
         return hip_fail(e, "hipDeviceGetAttribute");
@@ -292,6 +352,7 @@ int dr_ctx_create(int device, dr_ctx** out) {
     }
     if (e != hipSuccess) {
         release(c->tick);
+        (void)hipEventDestroy(c->switch_ev);
         (void)hipStreamDestroy(c->own);
         delete c;
         return hip_fail(e, "ticket buffer");
@@ -302,7 +363,17 @@ int dr_ctx_create(int device, dr_ctx** out) {
 
 int dr_ctx_set_stream(dr_ctx* ctx, void* stream) {
     if (!ctx) return fail(DR_ERR_INVALID, "dr_ctx_set_stream: ctx is NULL");
-    ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own;
+    DR_CTX_USE(ctx, "dr_ctx_set_stream");
+    hipStream_t ns = stream ? static_cast<hipStream_t>(stream) : ctx->own;
+    if (ns != ctx->stream && !capturing(ctx->stream) && !capturing(ns)) {
+        // the new stream starts after the work already queued on the old one,
+        // so the context's workspaces and split tickets are never in use on
+        // both (a stream under graph capture is ordered by its graph instead)
+        DR_CHECK(use_device(ctx));
+        DR_HIP(hipEventRecord(ctx->switch_ev, ctx->stream));
+        DR_HIP(hipStreamWaitEvent(ns, ctx->switch_ev, 0));
+    }
+    ctx->stream = ns;
     return DR_OK;
 }
 
@@ -325,6 +396,7 @@ void ctx_free(dr_ctx* ctx) {
         release(*b);
     for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    if (ctx->switch_ev) (void)hipEventDestroy(ctx->switch_ev);
     delete ctx;
 }
 
@@ -927,6 +999,7 @@ static int qmatmul_impl(dr_ctx* ctx, int wtype, const void* w, size_t rows, size
         return fail(DR_ERR_INVALID, "%s: cols %zu is not a positive multiple of %zu", who, cols, qk);
     if (n == 0 || rows == 0) return DR_OK;
     if (!w || !act || !out) return fail(DR_ERR_INVALID, "%s: NULL w / act / out", who);
+    DR_CTX_USE(ctx, who);
     if (wtype == DR_WTYPE_Q4K && ((uintptr_t)w & 15))
         return fail(DR_ERR_INVALID, "%s: Q4_K blocks must start 16-byte aligned (16-byte loads)", who);
     if (((uintptr_t)w & 1) || ((uintptr_t)act & 15))
@@ -1377,6 +1450,7 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
     DR_CHECK(cached_args(cache, layer, items, n_items, n_head, sliding_window, causal_prefix,
                          scale, q_norm_w, q_norm_eps, "dr_attention_cached", a, max_nq));
     if (max_nq == 0) return DR_OK;
+    DR_CTX_USE(cache->ctx, "dr_attention_cached");
     DR_CHECK(use_device(cache->ctx));
     return launch_planned(cache->ctx, a, a.hd, max_nq, (int)cache->n_total,
                           mask_of(sliding_window, causal_prefix),
@@ -1392,11 +1466,24 @@ int dr_attention_cached_noalloc(dr_step_cache* cache, size_t layer, const dr_bat
     DR_CHECK(cached_args(cache, layer, items, n_items, n_head, sliding_window, causal_prefix,
                          scale, q_norm_w, q_norm_eps, "dr_attention_cached_noalloc", a, max_nq));
     if (max_nq == 0) return DR_OK;
-    DR_CHECK(use_device(cache->ctx));
-    const dr::LaunchPlan p = plan_for(cache->ctx, a, a.hd, max_nq, (int)cache->n_total,
+    dr_ctx* ctx = cache->ctx;
+    DR_CTX_USE(ctx, "dr_attention_cached_noalloc");
+    DR_CHECK(use_device(ctx));
+    const dr::LaunchPlan p = plan_for(ctx, a, a.hd, max_nq, (int)cache->n_total,
                                       mask_of(sliding_window, causal_prefix),
                                       q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE);
-    return launch_plan(cache->ctx, a, p, true);
+    // calls on this GPU from different streams take turns with its scratch
+    // (under graph capture the graph orders them)
+    ScratchOrder& so = g_scratch_order[ctx->device];
+    std::lock_guard<std::mutex> lk(so.mu);
+    const bool cap = capturing(ctx->stream);
+    if (!cap && so.last && so.last != ctx->stream) DR_HIP(hipStreamWaitEvent(ctx->stream, so.done, 0));
+    DR_CHECK(launch_plan(ctx, a, p, true));
+    if (!cap) {
+        DR_HIP(hipEventRecord(so.done, ctx->stream));
+        so.last = ctx->stream;
+    }
+    return DR_OK;
 }
 
 int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* items,
@@ -1416,6 +1503,7 @@ int dr_attention_step(dr_step_cache* cache, size_t layer, const dr_step_item* it
         if (items[b].pass->n > 0 && (!items[b].k || !items[b].v))
             return fail(DR_ERR_INVALID, "item %zu: k/v is NULL", b);
     if (max_nq == 0) return DR_OK;
+    DR_CTX_USE(cache->ctx, "dr_attention_step");
     DR_CHECK(use_device(cache->ctx));
     const int mask = mask_of(sliding_window, causal_prefix);
     const int qepi = q_norm_w ? dr::QEPI_NORM : dr::QEPI_NONE;
@@ -1459,6 +1547,7 @@ static int step_impl(dr_step_cache* cache, size_t layer, const dr_step_item* ite
     int max_nq = 0;
     DR_CHECK(cached_args(cache, layer, bi, n_items, n_head, sliding_window, causal_prefix, scale,
                          epi->q_norm_w, epi->eps, who, a, max_nq));
+    DR_CTX_USE(cache->ctx, who);
     const size_t q_row = n_head * (size_t)a.hd, kv_row = (size_t)a.n_head_kv * a.hd;
     if (q_stride && (q_stride < q_row || q_stride > (size_t)INT32_MAX || q_stride % 4 != 0))
         return fail(DR_ERR_INVALID, "%s: q_stride %zu is not a multiple of 4 of at least n_head * head_dim %zu", who,

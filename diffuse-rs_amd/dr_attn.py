@@ -26,7 +26,7 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "lib" / "libdr_attn.so"
 HEADER_PATH = HERE.parent / "include" / "dr_attn.h"
 
-DR_OK, DR_ERR_INVALID, DR_ERR_NO_DEVICE, DR_ERR_OOM, DR_ERR_HIP, DR_ERR_UNSUPPORTED = range(6)
+DR_OK, DR_ERR_INVALID, DR_ERR_NO_DEVICE, DR_ERR_OOM, DR_ERR_HIP, DR_ERR_UNSUPPORTED, DR_ERR_BUSY = range(7)
 KERNEL_AUTO, KERNEL_STAGED, KERNEL_STREAMS, KERNEL_HILO = range(4)
 DTYPE_F32, DTYPE_BF16 = 0, 1
 PRECISION_BF16, PRECISION_HILO = 0, 1  # dr_cache_set_precision
@@ -37,6 +37,7 @@ STATUS_NAMES = {
     DR_ERR_OOM: "DR_ERR_OOM",
     DR_ERR_HIP: "DR_ERR_HIP",
     DR_ERR_UNSUPPORTED: "DR_ERR_UNSUPPORTED",
+    DR_ERR_BUSY: "DR_ERR_BUSY",
 }
 
 c_size_p = ctypes.POINTER(ctypes.c_size_t)

@@ -12,8 +12,11 @@
  * reference's attention() is infallible and panics on bad input; a Rust shim
  * maps a nonzero status to panic!().
  *
- * Threading: a dr_ctx owns one HIP stream and is not thread-safe (mirrors the
- * reference's single-threaded `&mut Model` discipline, server.rs:350-351).
+ * Threading: a dr_ctx owns one HIP stream and serves one host thread at a
+ * time (mirrors the reference's single-threaded `&mut Model` discipline,
+ * server.rs:350-351): an entry point that uses its workspaces, split tickets
+ * or launch record (attention, step, qmatmul, dr_ctx_set_stream) returns
+ * DR_ERR_BUSY to a second thread that calls while the first is inside.
  * dr_attention() uses one process-wide context, serialised internally.
  */
 #ifndef DR_ATTN_H
@@ -32,7 +35,8 @@ typedef enum {
     DR_ERR_NO_DEVICE = 2,   /* no HIP device visible */
     DR_ERR_OOM = 3,         /* device allocation failed */
     DR_ERR_HIP = 4,         /* a HIP runtime call failed */
-    DR_ERR_UNSUPPORTED = 5  /* valid for the reference, not built here (e.g. head_dim > 512) */
+    DR_ERR_UNSUPPORTED = 5, /* valid for the reference, not built here (e.g. head_dim > 512) */
+    DR_ERR_BUSY = 6         /* the context is in use by another host thread */
 } dr_status;
 
 /* Option<usize>: present == 0 means None. */
@@ -108,7 +112,12 @@ typedef struct dr_ctx dr_ctx;
 
 /* Create a context on `device` with its own (default-priority) stream. */
 int dr_ctx_create(int device, dr_ctx** out);
-/* Use the caller's hipStream_t (cast to void*) instead of the context's own. */
+/* Use the caller's hipStream_t (cast to void*; NULL: the context's own) for
+ * later calls.  The new stream first waits (on the device) for the work
+ * already queued on the old one, so the context's workspaces and split
+ * tickets are never in use on both; the old stream must still exist.  (When
+ * either stream is under graph capture, no wait is inserted: the graph's own
+ * dependencies order the calls.) */
 int dr_ctx_set_stream(dr_ctx* ctx, void* stream);
 /* The hipStream_t the context enqueues on. */
 void* dr_ctx_stream(dr_ctx* ctx);
@@ -269,8 +278,12 @@ int dr_attention_cached(dr_step_cache* cache, size_t layer, const dr_batch_item*
  * allocation.  A plan that needs more than 64 MiB (far beyond the
  * configurations here: DiffusionGemma's 512-wide global layer needs 34 MB)
  * returns DR_ERR_INVALID.  Nothing in the array needs to start at zero.
- * Every call on a GPU shares that GPU's array, so calls that overlap on one
- * GPU (different streams or host threads) race; calls on one stream do not.
+ * Every call on a GPU shares that GPU's array: a call on another stream than
+ * the previous call on that GPU (from any context) first waits, on the
+ * device, for that call's kernels, through an event made at dr_ctx_create,
+ * so no two calls use the array at once.  Calls captured into a hipGraph are
+ * ordered by the graph alone: two captured calls on one GPU must not run
+ * concurrently.
  * This entry point has no counterpart in the reference; it is for callers
  * that cannot allocate.
  */
@@ -505,8 +518,9 @@ int dr_ctx_set_o_dtype(dr_ctx* ctx, int dtype);
  * with agent-scope (L2-coherent) accesses, counted by per-block tickets that
  * dr_ctx_create allocates and zeroes and each merge resets.  0: a second
  * kernel merges them, as for the other kernel families.  Both give the same
- * bits.  Calls on one context that overlap on the device share its tickets
- * and split workspace, and race. */
+ * bits.  A context's calls never overlap on the device (one stream at a
+ * time, ordered across dr_ctx_set_stream), so its tickets and split
+ * workspace are used by one call at a time. */
 int dr_ctx_set_split_merge(dr_ctx* ctx, int in_kernel);
 /* Override the workgroup shape (32-row query blocks x key groups) and the
  * key split for later calls on ctx; 0 = automatic, unbuilt shapes fall back
