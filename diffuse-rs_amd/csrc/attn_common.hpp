@@ -21,9 +21,14 @@ constexpr int BN = 32;                     // keys per tile (one MFMA key block)
 static_assert(BN == VT_KEYS, "a key tile is one V^T tile of the cache");
 constexpr float RESCALE_THRESHOLD = 8.0f;  // log2 units
 
-// 16-byte-chunk swizzle for an LDS row holding CH chunks.  Keeps 8 (32-bank
-// LDS) or 16 (64-bank LDS) consecutive rows read at the same logical chunk on
-// distinct banks.
+// 16-byte-chunk swizzle for an LDS row holding CH chunks, so that the rows
+// that one MFMA operand read takes at the same logical chunk sit on distinct
+// banks.  The 64-byte rows of a V^T tile (CH 4; the read takes row d = 32 db
+// + col, chunks 2 hf + s) use (d >> 2) & 3, which SQ_LDS_BANK_CONFLICT
+// measures conflict-free on MI355X.  ((d >> 1) ^ (d >> 3)) & 3, conflict-free
+// for a 32-bank LDS read 8 lanes at a time, cost 32 conflict cycles per wave
+// and tile there, 17-32 % of the LDS-active cycles at C2, C4 and C5's global
+// layer, and ((d >> 2) ^ (d >> 4)) & 3 as many.)
 template <int CH>
 __device__ __forceinline__ int swz(int row) {
     if constexpr (CH >= 16) {
@@ -32,7 +37,7 @@ __device__ __forceinline__ int swz(int row) {
         return (row & 7) ^ ((row >> 3) & 1);
     } else {
         static_assert(CH == 4, "unsupported row width");
-        return ((row >> 1) ^ (row >> 3)) & 3;
+        return (row >> 2) & 3;
     }
 }
 

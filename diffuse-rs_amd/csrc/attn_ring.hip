@@ -606,9 +606,17 @@ void attn_ring_kernel(const AttnArgs a) {
                     f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
     }
     lds_barrier();
-    // thread tid: row rr = tid / TPR, chunks ch + TPR k, k < CPT
+    // thread tid: row rr = tid / TPR, chunks cidx(k) = ch + TPR k', k < CPT,
+    // where k' = k except at head dim 256: there a wave's 64 lanes are 8 rows
+    // of 8 and every read below would take the same 8-chunk block of 8 rows
+    // (half of a bank sweep, 4 lanes per bank), so odd rows take the blocks in
+    // the other order (k' = k ^ 1).  Every access of the final pass uses the
+    // same mapping.
     constexpr int CPT = HD / 4 / TPR;
     const int rr = tid / TPR, ch = tid % TPR;
+    auto cidx = [&](int k) __attribute__((always_inline)) {
+        return ch + TPR * (HD == 256 ? (k ^ (rr & 1)) : k);
+    };
     const int row = wg_row0 + rr;
     const bool row_ok = row < rows_total;
     f32x4 acc[CPT];
@@ -628,7 +636,7 @@ void attn_ring_kernel(const AttnArgs a) {
             const float* prow = reinterpret_cast<const float*>(smem + w * 2 * RT) + rr * RHD;
 #pragma unroll
             for (int k = 0; k < CPT; ++k)
-                acc[k] += wt * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + TPR * k) ^ rr));
+                acc[k] += wt * *reinterpret_cast<const f32x4*>(prow + 4 * (cidx(k) ^ rr));
             L += wt * sl[w * 32 + rr];
         }
     }
@@ -643,12 +651,12 @@ void attn_ring_kernel(const AttnArgs a) {
             for (int k = 0; k < CPT; ++k) {
                 const f32x4 v = val[k] * il;
                 const bf16x4 y = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
-                gstore(orow + 4 * (ch + TPR * k), y);
+                gstore(orow + 4 * cidx(k), y);
             }
         } else {
             float* orow = S.out + o0;
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), val[k] * il);
+            for (int k = 0; k < CPT; ++k) gstore(orow + 4 * cidx(k), val[k] * il);
         }
     };
     if (a.n_split == 1) {
@@ -663,7 +671,7 @@ void attn_ring_kernel(const AttnArgs a) {
         if (row_ok) {
             const size_t prow = (size_t)split * plane + prow0;
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) gstore(a.part_o + prow * RHD + 4 * (ch + TPR * k), acc[k]);
+            for (int k = 0; k < CPT; ++k) gstore(a.part_o + prow * RHD + 4 * cidx(k), acc[k]);
             if (ch == 0) gstore(a.part_ml + prow * 2, make_float2(M, L));
         }
         return;
@@ -681,7 +689,7 @@ void attn_ring_kernel(const AttnArgs a) {
     if (row_ok) {
         const int po = (int)(((size_t)split * plane + prow0) * RHD * 4);
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) store_sc1(ro, po + 16 * (ch + TPR * k), acc[k]);
+        for (int k = 0; k < CPT; ++k) store_sc1(ro, po + 16 * cidx(k), acc[k]);
         if (ch == 0) store2_sc1(rm, (int)(((size_t)split * plane + prow0) * 8), M, L);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -715,7 +723,7 @@ void attn_ring_kernel(const AttnArgs a) {
             l[j] = ml.y;
             const int po = (int)(((size_t)sp * plane + prow0) * RHD * 4);
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) so[j][k] = load_sc1(ro, po + 16 * (ch + TPR * k));
+            for (int k = 0; k < CPT; ++k) so[j][k] = load_sc1(ro, po + 16 * cidx(k));
         }
         if (j >= a.n_split) m[j] = -INFINITY;
     }
