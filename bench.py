@@ -191,9 +191,11 @@ def hilo_timing(torch, dr, ctx, stream, CONFIGS, reps: int) -> dict:
             def call(i):
                 cache.attention(0, items, cfg.n_head, sliding_window=cfg.window, scale=1.0, q_norm_w=qn)
             # (a bf16 layer refuses scale 1.0 unless a kernel family is
-            # forced: the one the planner picks for its shape)
+            # forced: the one the planner picks for its shape at the usual
+            # scale -- the stream kernel at head dim 256, C5's sliding and
+            # global layers; the staged kernel at 512)
             if prec is None:
-                ctx.set_kernel(dr.KERNEL_STREAMS if cfg.window else dr.KERNEL_STAGED)
+                ctx.set_kernel(dr.KERNEL_STREAMS if cfg.head_dim in (128, 256) else dr.KERNEL_STAGED)
             try:
                 ms, _ = attention_only_ms(torch, stream, call, 4, reps)
                 entry[f"{label}_kernel"] = ctx.last_launch()["kernel"]

@@ -198,6 +198,9 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 // state (Mx, Ls, acc) as softmax states merge: weights exp2(m_j - max), a
 // state with m_j = -inf weighs 0.  Every kernel that merges splits calls this,
 // with the operations spelled out (no contraction), so they agree bit for bit.
+// No branch: when every state so far has m = -inf the running state is (-inf,
+// 0, 0), f and every weight are 0, and it stays so (an early return let the
+// compiler sink the l and o loads behind the m loads' wait).
 template <int SG, int C>
 __device__ __forceinline__ void merge_split_states(float& Mx, float& Ls, f32x4 (&acc)[C],
                                                    const float (&m)[SG], const float (&l)[SG],
@@ -206,7 +209,6 @@ __device__ __forceinline__ void merge_split_states(float& Mx, float& Ls, f32x4 (
     float nm = Mx;
 #pragma unroll
     for (int j = 0; j < SG; ++j) nm = __builtin_fmaxf(nm, m[j]);
-    if (nm == -INFINITY) return;  // no visible key in these splits
     const float f = Mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mx - nm);
 #pragma unroll
     for (int c = 0; c < C; ++c) acc[c] = acc[c] * f;

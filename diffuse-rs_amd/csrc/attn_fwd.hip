@@ -54,6 +54,8 @@
 // into the LDS of the last pipeline stage, before that stage is first used.
 #include "attn_common.hpp"
 
+#include <type_traits>
+
 #include <limits.h>
 #include <math.h>
 
@@ -1310,7 +1312,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
 template <int HD>
 __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     constexpr int CHUNKS = HD / 4;
-    constexpr int SG = 4;  // splits whose loads are issued together
+    constexpr int SG = 8;  // splits whose loads are issued together
     const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
     const size_t item = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (item >= plane * CHUNKS) return;
@@ -1318,24 +1320,50 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     const int ch = (int)(item % CHUNKS);
     const int bg = (int)(prow / a.part_rows), r = (int)(prow % a.part_rows);
     const int b = bg / a.n_head_kv, g = bg % a.n_head_kv;
-    const AttnSlot& S = a.slot[b];
-    if (r >= a.group * S.nq) return;
+    // (a row past the slot's rows is merged from whatever its workspace row
+    // holds and not stored: testing first put a wait for the slot's row
+    // count, a dynamically indexed argument, in front of every partial load)
     float Mx = -INFINITY, Ls = 0.0f;
     f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
-    for (int s0 = 0; s0 < a.n_split; s0 += SG) {
-        float m[SG], l[SG];
-        f32x4 o[SG][1];
+    // Partials within 2^31 bytes (the usual case) are read with buffer loads:
+    // one per-thread offset and the split's plane offset as a scalar, so the
+    // SG loads of a group need no address registers of their own (with 64-bit
+    // addresses the compiler held back loads until earlier ones returned).
+    auto groups = [&](auto buffered) __attribute__((always_inline)) {
+        constexpr bool BUF = decltype(buffered)::value;
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o, 0xffffffffu);
+        const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.part_ml, 0xffffffffu);
+        const int vo = (int)((prow * HD + ch * 4) * 4), vm = (int)(prow * 8);
+        for (int s0 = 0; s0 < a.n_split; s0 += SG) {
+            float m[SG], l[SG];
+            f32x4 o[SG][1];
 #pragma unroll
-        for (int j = 0; j < SG; ++j) {
-            const int sp = min(s0 + j, a.n_split - 1);
-            const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + ((size_t)sp * plane + prow) * 2);
-            o[j][0] = *reinterpret_cast<const f32x4*>(a.part_o + ((size_t)sp * plane + prow) * HD + ch * 4);
-            const bool in = s0 + j < a.n_split;
-            m[j] = in ? ml.x : -INFINITY;
-            l[j] = ml.y;
+            for (int j = 0; j < SG; ++j) {
+                const int sp = min(s0 + j, a.n_split - 1);
+                float2 ml;
+                if constexpr (BUF) {
+                    const auto w = __builtin_amdgcn_raw_buffer_load_b64(rm, vm, (int)((size_t)sp * plane * 8), 0);
+                    ml = make_float2(__uint_as_float(w[0]), __uint_as_float(w[1]));
+                    o[j][0] = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, vo, (int)((size_t)sp * plane * HD * 4), 0));
+                } else {
+                    ml = *reinterpret_cast<const float2*>(a.part_ml + ((size_t)sp * plane + prow) * 2);
+                    o[j][0] = *reinterpret_cast<const f32x4*>(a.part_o + ((size_t)sp * plane + prow) * HD + ch * 4);
+                }
+                const bool in = s0 + j < a.n_split;
+                m[j] = in ? ml.x : -INFINITY;
+                l[j] = ml.y;
+            }
+            __builtin_amdgcn_sched_barrier(0);  // (every load above before any wait)
+            merge_split_states<SG, 1>(Mx, Ls, acc, m, l, o);
         }
-        merge_split_states<SG, 1>(Mx, Ls, acc, m, l, o);
-    }
+    };
+    if ((size_t)a.n_split * plane * HD * 4 <= 0x7fffffffu)  // (uniform)
+        groups(std::integral_constant<bool, true>{});
+    else
+        groups(std::integral_constant<bool, false>{});
+    const AttnSlot& S = a.slot[b];
+    if (r >= a.group * S.nq) return;
     int hg, qi;
     row_split(r, S.nq, __builtin_amdgcn_rcpf((float)S.nq), a.group, hg, qi);
     const size_t o0 = (size_t)qi * a.o_rstride + (size_t)(g * a.group + hg) * a.hd;

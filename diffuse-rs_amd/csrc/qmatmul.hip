@@ -182,13 +182,18 @@ __global__ __launch_bounds__(512) void q8k_quantize_tiles_kernel(const float* __
     __shared__ __attribute__((aligned(16))) float s_xd[32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t32 = blockIdx.x / nb, b = blockIdx.x - t32 * nb;
+    // every load unconditional (rows past n read row n - 1, then count as
+    // zeros): a load behind a branch made the compiler wait for the loads
+    // before it, two round trips instead of one
     f32x4 v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int t = t32 * 32 + 4 * wave + k;
-        v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < n) v[k] = gld<f32x4>(x + (size_t)t * cols + (size_t)b * QK + 4 * lane);
+        v[k] = gld<f32x4>(x + (size_t)min(t, n - 1) * cols + (size_t)b * QK + 4 * lane);
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (t32 * 32 + 4 * wave + k >= n) v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int c = 4 * wave + k;
@@ -525,12 +530,13 @@ __global__ __launch_bounds__(256) void q80_quantize_kernel(const float* __restri
     const int t32 = item / nb, b = item - t32 * nb;
     const int c = lane & 31, g = lane >> 5;
     const int t = t32 * 32 + c;
+    // (unconditional loads, as in q8k_quantize_tiles_kernel)
     f32x4 v[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < n) v[k] = gld<f32x4>(x + (size_t)t * cols + (size_t)b * 32 + 16 * g + 4 * k);
-    }
+    for (int k = 0; k < 4; ++k) v[k] = gld<f32x4>(x + (size_t)min(t, n - 1) * cols + (size_t)b * 32 + 16 * g + 4 * k);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (t >= n) v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float am = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
