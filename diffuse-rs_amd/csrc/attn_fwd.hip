@@ -1549,6 +1549,14 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
         if (split < 1) split = 1;
         p.n_split = split;
         p.n_workgroups = base * split;
+        // rotated tile walks while the K/V that one XCD's workgroups read fits
+        // its L2 (4 MB, part of it left to Q, O and partials): the kv heads an
+        // XCD holds (consecutive workgroups: a head's row groups and splits)
+        // times a head's keys (its band) times 4 * head dim bytes
+        const int per_head = p.rowgroups * split;
+        const int per_xcd = (p.n_workgroups + 7) / 8;
+        const long long heads = per_xcd <= per_head ? 1 : (per_xcd + per_head - 1) / per_head;
+        p.rotate = heads * (long long)(band < max_nk ? band : max_nk) * hd * 4 <= (3LL << 20);
         return p;
     }
     // Head dims up to 128: one row block of four key groups with four DMA
@@ -1640,6 +1648,7 @@ hipError_t launch_attention(const LaunchPlan& p, AttnArgs& a, hipStream_t st) {
     a.mg_rowgroups = div_magic(a.rowgroups, p.n_workgroups);
     a.mg_hkv = div_magic(a.n_head_kv, p.n_workgroups);
     a.part_rows = p.rowgroups * p.rb * 32;
+    a.ring_rot = p.rotate ? 1 : 0;
     if (p.kernel != KERNEL_STREAMS) a.ticket = nullptr;  // (the others always merge in a second kernel)
     hipError_t e = p.kernel == KERNEL_STREAMS ? launch_ring(p, a, st)
                    : p.kernel == KERNEL_HILO  ? launch_hilo(p, a, st)

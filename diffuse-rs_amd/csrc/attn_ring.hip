@@ -286,16 +286,14 @@ void attn_ring_kernel(const AttnArgs a) {
     // Wave w takes tiles t0 + w, t0 + w + RW, ...: a fixed assignment, so
     // every call sums each row's keys in the same order (bit-identical
     // results run to run; claiming tiles dynamically balanced the waves'
-    // finishing times but made the summation order depend on timing).  Each
-    // row group walks its waves' lists from a different point (rotated by
-    // the row group), so the row groups of one kv head, which share an XCD,
-    // first request different tiles: the head's K/V comes from HBM in one
-    // round, and later tiles are L2 hits.
+    // finishing times but made the summation order depend on timing).  Row
+    // group rg starts its walk at a rotated point when the launch asks
+    // (RingWaveTiles).
     // (The first DMA is issued even when the wave has no tile, unconditional
     // for the compiler's wait accounting; its data is never used, and it reads
     // a tile clamped into the cache plane, since the tile base goes in the
     // DMA's scalar offset, which the descriptor's range check excludes.)
-    const RingWaveTiles wt(t0, nt, wave, RW, rg, a.cap / BN);
+    const RingWaveTiles wt(t0, nt, wave, RW, a.ring_rot ? rg : 0, a.cap / BN);
     const int kw = wt.kw;  // this wave's tiles
     auto tile_at = [&](int k) __attribute__((always_inline)) { return wt.at(k); };
     issue_k(wt.first_dma());

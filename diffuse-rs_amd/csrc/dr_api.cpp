@@ -1778,7 +1778,7 @@ int dr_debug_ring_tiles(size_t head_dim, size_t nk, size_t cap, long long window
     for (int split = 0; split < (int)n_split; ++split) {
         int t0, t1;
         dr::split_tile_range(kt_lo, kt_hi, (int)n_split, split, t0, t1);
-        for (int rg = 0; rg < 24; ++rg) {  // (the row group only rotates each wave's order)
+        for (int rg = 0; rg < 24; ++rg) {  // (a rotated walk only reorders each wave's tiles)
             std::vector<int> seen(cap_tiles, 0);
             for (int w = 0; w < rw; ++w) {
                 const dr::RingWaveTiles wt(t0, t1 - t0, w, rw, rg, cap_tiles);

@@ -80,6 +80,7 @@ struct AttnArgs {
     // (host planning only) an upper bound on the keys any row block can see
     // (the union of the query rows' sliding-window bands), 0: not known
     int key_band;
+    int ring_rot;  // the per-wave-stream kernel rotates each row group's tile walk
 };
 static_assert(offsetof(AttnArgs, slot) == 64, "scalar block of AttnArgs is one 64-byte line");
 
@@ -266,19 +267,25 @@ __host__ __device__ inline void split_tile_range(int kt_lo, int kt_hi, int n_spl
 
 // The key tiles one wave of attn_ring_kernel requests.  Wave w of a workgroup
 // whose key range is tiles [t0, t0 + nt) owns tiles t0 + w, t0 + w + rw, ...
-// (kw of them) and walks them from its krot-th on, krot = row group mod kw,
-// so the row groups of one kv head first request different tiles.  A wave
-// with no tile still issues one K and one V^T DMA (the compiler's vmcnt
-// accounting assumes them); that DMA reads tile min(t0 + w, cap_tiles - 1),
-// which lies inside the cache plane: the tile base is the DMA's scalar
-// offset, which the buffer range check does not cover.  Kernel and host
-// (dr_debug_ring_tiles) both use this.
+// (kw of them) and walks them from its krot-th on, krot = rot mod kw with rot
+// the row group when the launch rotates (else 0).  Rotated, the row groups of
+// one kv head, which share an XCD, first request different tiles, so the
+// head's K/V comes from HBM in one round and later tiles hit in L2 -- right
+// while a head's K/V fits that L2 (C2: the 32-layer step 15.34 -> 15.16 us);
+// beyond it the rotated walks keep the whole head in play and the L2
+// thrashes (C5's global layer fetched 128 MB per call rotated, 44 unrotated),
+// so the planner turns it off there (LaunchPlan::rotate).  A wave with no
+// tile still issues one K and one V^T DMA (the compiler's vmcnt accounting
+// assumes them); that DMA reads tile min(t0 + w, cap_tiles - 1), which lies
+// inside the cache plane: the tile base is the DMA's scalar offset, which the
+// buffer range check does not cover.  Kernel and host (dr_debug_ring_tiles)
+// both use this.
 struct RingWaveTiles {
     int t0, wave, rw, kw, krot, idle_tile;
-    __host__ __device__ RingWaveTiles(int t0_, int nt, int wave_, int rw_, int rg, int cap_tiles)
+    __host__ __device__ RingWaveTiles(int t0_, int nt, int wave_, int rw_, int rot, int cap_tiles)
         : t0(t0_), wave(wave_), rw(rw_) {
         kw = wave < nt ? (nt - wave + rw - 1) / rw : 0;
-        krot = kw > 1 ? rg % kw : 0;
+        krot = kw > 1 ? rot % kw : 0;
         idle_tile = t0 + wave < cap_tiles - 1 ? t0 + wave : cap_tiles - 1;
     }
     // the k-th tile this wave multiplies, k < kw
@@ -312,6 +319,7 @@ struct LaunchPlan {
     bool w16;        // two 16-row compute waves per (row block, key group)
     int kernel;      // KernelKind
     int merge;       // set at launch: 0 no split, 1 split_merge_kernel, 2 in-kernel
+    bool rotate;     // KERNEL_STREAMS: rotate the row groups' tile walks (RingWaveTiles)
 };
 
 // Attention kernel families.  STAGED: attn_fwd_kernel, the workgroup's waves
