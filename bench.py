@@ -717,6 +717,42 @@ def main() -> int:
         log(f"step with host upload: {h2d}")
         del pins, dst
 
+    # ---- a C2 step whose active rows are a scattered split_active set
+    # (StepCache::split_active, cache.rs:85-114): mid-denoise, about half of
+    # the canvas still masked at random positions and a seventh of the rest
+    # changed since the previous step.  Those rows are the step's queries and
+    # the rows it stores (at scattered positions: the position-list store
+    # kernel), attending over all 768 keys of the 32-layer cache.
+    scattered = None
+    if not args.no_others:
+        rs = np.random.default_rng(config_seed(1, 99))
+        seq = rs.integers(5, 30000, n_t).astype(np.int32)
+        masked = np.zeros(n_t, np.uint8)
+        masked[n_p:] = rs.random(n_c) < 0.5
+        seq[masked.astype(bool)] = 4
+        prev = seq.copy()
+        changed = (masked == 0) & (np.arange(n_t) >= n_p) & (rs.random(n_t) < 1 / 7)
+        prev[changed] = 9
+        act, _ = dr.split_active(prev, np.zeros(n_t, np.int32), seq, masked, 5)
+        n_a = len(act)
+        runs = 1 + sum(1 for x, y in zip(act, act[1:]) if y != x + 1)
+        p_act = dr.Pass(ctx, act)
+        with torch.cuda.stream(stream):
+            kq, kk, kv = dsets[0][2][:n_a].contiguous(), dsets[0][0][:n_a].contiguous(), dsets[0][1][:n_a].contiguous()
+            oa = torch.empty(n_a * h * hd, dtype=torch.float32, device=dev)
+        stream.synchronize()
+        reps_s = max(2, min(64, args.steps // N_LAYERS))
+        s_ms, _ = attention_only_ms(
+            torch, stream, lambda i: cache.step(i % N_LAYERS, [(kq, oa, p_act, kk, kv)], h, scale=scale),
+            N_LAYERS, reps_s)
+        fl_s = 4.0 * h * hd * n_a * n_t
+        scattered = {"n_active": n_a, "contiguous_runs": runs, "us_per_step": round(s_ms * 1e3, 3),
+                     "tflops": round(fl_s / (s_ms / 1e3) / 1e12, 2),
+                     "timing": "HIP events around graph replays of 32 steps, one per layer: the store of the "
+                               "active rows (position list) and their attention over 768 keys"}
+        log(f"step with scattered active rows: {scattered}")
+        del kq, kk, kv, oa
+
     achieved = flops / (attn_mean_ms / 1e3) / 1e12
     traffic, traffic_src = measured_traffic("C2")
     algo_bytes = (n_c * h * hd * 4) * 2 + 2 * n_t * kvs * 2  # Q f32 + O f32 + K,V bf16
@@ -817,6 +853,7 @@ def main() -> int:
         "dropin_dr_attention": dropin,
         "qkv_epilogue": epi,
         "split_active": split,
+        "scattered_step": scattered,
         "wo_qmatmul": qmm,
         "precision_hilo": hilo,
     }
