@@ -350,6 +350,33 @@ __device__ __forceinline__ void prep(const RawBlock<14>& r, int c, int lane, u32
     }
 }
 
+// The residual of a lane's 16 outputs (activation rows t0 + 8 (i / 4) + 4 g
+// + i % 4, weight row rr), every index clamped in bounds so that all 16
+// loads are in flight together: a load behind a per-lane bounds check would
+// be waited for before the next one issues.
+__device__ __forceinline__ void load_residual(const QmmArgs& a, int t0, int g, int rr, float (&rv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) rv[i] = 0.0f;
+    if (!a.residual) return;
+    const int rc = min(rr, a.rows - 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = min(t0 + 8 * (i >> 2) + 4 * g + (i & 3), a.n - 1);
+        rv[i] = gld<float>(a.residual + (size_t)t * a.rows + rc);
+    }
+}
+// out[t][rr] = sum (+ residual) for the lane's outputs inside the problem.
+__device__ __forceinline__ void store_tile(const QmmArgs& a, int t0, int g, int rr, const f32x16& sum,
+                                           const float (&rv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = t0 + 8 * (i >> 2) + 4 * g + (i & 3);
+        float v = sum[i];
+        if (a.residual) v += rv[i];
+        if (t < a.n && rr < a.rows) a.out[(size_t)t * a.rows + rr] = v;
+    }
+}
+
 template <int WT>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     constexpr bool Q4 = WT == 12;
@@ -477,6 +504,9 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
         body(it + 1, S[1], S[0], R[0], R[1], 1);
     }
     if (it < nh) body(it, S[0], S[1], R[1], R[0], 0);
+    const int rr = rt * 32 + col;
+    float rv[16];
+    if (kh == 0) load_residual(a, tc, g, rr, rv);
     if (pending) combine(P);
 
     // ---- half 1's partial sums to LDS; half 0 adds them (and the residual)
@@ -487,17 +517,9 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     }
     lds_barrier();
     if (kh == 0) {
-        const int rr = rt * 32 + col;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float v = sum[i] + red[(c * 16 + i) * 64 + lane];
-            const int t = tc + 8 * (i >> 2) + 4 * g + (i & 3);
-            if (t < a.n && rr < a.rows) {
-                const size_t idx = (size_t)t * a.rows + rr;
-                if (a.residual) v += a.residual[idx];
-                a.out[idx] = v;
-            }
-        }
+        for (int i = 0; i < 16; ++i) sum[i] = sum[i] + red[(c * 16 + i) * 64 + lane];
+        store_tile(a, tc, g, rr, sum, rv);
     }
 }
 
@@ -592,46 +614,71 @@ __device__ __forceinline__ uint32_t bytes_minus(uint32_t x, uint32_t off4) {
 // bits 0..3 of b to bit 4 of bytes 0..3
 __device__ __forceinline__ uint32_t bits_to_byte_bit4(uint32_t b) { return ((b * 0x00204081u) & 0x01010101u) << 4; }
 
-// The weight operand of one legacy block for lane (c, g): values 16 g ..
-// 16 g + 15 of the block of weight row c as int8, and the block's f16 d.
+// The raw bytes of one legacy block that lane (c, g) needs: the f16 d, the
+// 16 value bytes of its half (Q8_0), or the 16 nibble bytes (Q4_0, Q5_0)
+// and the 32 high bits (Q5_0).
 template <int WT>
-__device__ __forceinline__ i32x4 legacy_operand(const uint8_t* blk, int g, uint32_t& dh) {
-    if constexpr (WT == 8) {  // Q8_0: d, int8 qs[32]
-        dh = gld<uint16_t>(blk);
-        return __builtin_bit_cast(i32x4, gld16_a2(blk + 2 + 16 * g));
-    } else if constexpr (WT == 2) {  // Q4_0: d, qs[16]; value j: nibble of byte j % 16 (high for j >= 16) - 8
-        dh = gld<uint16_t>(blk);
-        const u32x4 q = gld16_a2(blk + 2);
+struct LegacyRaw {
+    u32x4 q;
+    uint32_t dh, qh;
+};
+template <int WT>
+__device__ __forceinline__ void load_legacy(const uint8_t* blk, int g, LegacyRaw<WT>& r) {
+    r.dh = gld<uint16_t>(blk);
+    if constexpr (WT == 8) {
+        r.q = gld16_a2(blk + 2 + 16 * g);
+        r.qh = 0;
+    } else if constexpr (WT == 2) {
+        r.q = gld16_a2(blk + 2);
+        r.qh = 0;
+    } else {
+        r.qh = (uint32_t)gld<uint16_t>(blk + 2) | ((uint32_t)gld<uint16_t>(blk + 4) << 16);
+        r.q = gld16_a2(blk + 6);
+    }
+}
+// The weight operand of lane (c, g): values 16 g .. 16 g + 15 of the block
+// as int8 (Q8_0: the bytes; Q4_0: nibble of byte j % 16 (high for j >= 16)
+// - 8; Q5_0: that nibble | bit j of qh << 4, - 16).
+template <int WT>
+__device__ __forceinline__ i32x4 legacy_operand(const LegacyRaw<WT>& r, int g) {
+    if constexpr (WT == 8) {
+        return __builtin_bit_cast(i32x4, r.q);
+    } else if constexpr (WT == 2) {
         u32x4 o;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = bytes_minus((g ? q[k] >> 4 : q[k]) & 0x0F0F0F0Fu, 0x08080808u);
+        for (int k = 0; k < 4; ++k) o[k] = bytes_minus((g ? r.q[k] >> 4 : r.q[k]) & 0x0F0F0F0Fu, 0x08080808u);
         return __builtin_bit_cast(i32x4, o);
-    } else {  // Q5_0: d, qh (32 bits), qs[16]; value j: nibble | bit j of qh << 4, - 16
+    } else {
         static_assert(WT == 6, "legacy weight type");
-        dh = gld<uint16_t>(blk);
-        const uint32_t qh = (uint32_t)gld<uint16_t>(blk + 2) | ((uint32_t)gld<uint16_t>(blk + 4) << 16);
-        const u32x4 q = gld16_a2(blk + 6);
         u32x4 o;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const uint32_t nib = (g ? q[k] >> 4 : q[k]) & 0x0F0F0F0Fu;
-            const uint32_t hi = bits_to_byte_bit4((qh >> (16 * g + 4 * k)) & 0xFu);
+            const uint32_t nib = (g ? r.q[k] >> 4 : r.q[k]) & 0x0F0F0F0Fu;
+            const uint32_t hi = bits_to_byte_bit4((r.qh >> (16 * g + 4 * k)) & 0xFu);
             o[k] = bytes_minus(nib | hi, 0x10101010u);
         }
         return __builtin_bit_cast(i32x4, o);
     }
 }
 
-// A workgroup (4 waves) owns 32 weight rows x 128 activation rows; wave w the
-// 32 x 32 tile of activation rows 32 w .. 32 w + 31.  Lane (c, g): weight row
-// c of the tile (B operand) and activation row c (A operand), values 16 g ..
-// 16 g + 15 of each block; accumulator slot i is output (activation row
-// 8 (i / 4) + 4 g + i % 4, weight row c).  The next block's operands are
-// loaded before this block's MFMAs.
+// A workgroup (8 waves, two per SIMD) owns 32 weight rows x 128 activation
+// rows: wave w the 32 x 32 tile of activation rows 32 (w % 4) .. + 31 over
+// half w / 4 of the blocks (the halves' partial sums meet in LDS, so every
+// output is summed in one fixed order).  Lane (c, g): weight row c of the
+// tile (B operand) and activation row c (A operand), values 16 g .. 16 g +
+// 15 of each block; accumulator slot i is output (activation row 8 (i / 4) +
+// 4 g + i % 4, weight row c).  Each wave keeps the operands of its next QD
+// blocks in flight (a ring of registers, unrolled so that nothing is copied
+// and every wait counts only the loads it needs), and a block's combine runs
+// after the next block's MFMAs are issued.
+constexpr int QD = 4;
 template <int WT>
-__global__ __launch_bounds__(256) void qmm0_kernel(const QmmArgs a) {
+__global__ __launch_bounds__(512) void qmm0_kernel(const QmmArgs a) {
     constexpr int BB = WT == 2 ? 18 : (WT == 6 ? 22 : 34);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ float s_red[4][16][64];  // half 1's partial sums
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // (uniform: scalar branches)
+    const int w4 = wave & 3, kh = wave >> 2;
     const int c = lane & 31, g = lane >> 5;
     const int nb = a.cols / 32;
     const int n_rt = (a.rows + 31) / 32, n_tt = a.n_pad / 128;
@@ -639,48 +686,74 @@ __global__ __launch_bounds__(256) void qmm0_kernel(const QmmArgs a) {
     const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
     const int rt = lid / n_tt, tt = lid - rt * n_tt;
     const int r = min(rt * 32 + c, a.rows - 1);
-    const int t32 = tt * 4 + wave;  // this wave's 32-row activation tile
+    const int t32 = tt * 4 + w4;  // this wave's 32-row activation tile
     const Q0Layout L(a.ws, a.n_pad, a.cols);
     const uint8_t* wrow = static_cast<const uint8_t*>(a.w) + (size_t)r * nb * BB;
     const int8_t* abase = L.qs + ((size_t)t32 * nb * 64 + lane) * 16;
     const float* xbase = L.xd + (size_t)t32 * nb * 32 + c;
+    const int nh = (nb + 1) / 2;
+    const int kb0 = kh ? nh : 0, kcnt = kh ? nb - nh : nh;
+    const int blast = kb0 + (kcnt > 0 ? kcnt - 1 : 0);
 
+    struct Stage {
+        i32x4 av;
+        float xd;  // lane (c, 0): the Q8_0 d of activation row c
+        LegacyRaw<WT> raw;
+    };
+    // (blocks past the wave's last reload that block: in bounds, unused)
+    auto load = [&](int j, Stage& st) __attribute__((always_inline)) {
+        const int b = min(kb0 + j, blast);
+        st.av = gld<i32x4>(abase + (size_t)b * 1024);
+        st.xd = gld<float>(xbase + (size_t)b * 32);
+        load_legacy<WT>(wrow + (size_t)b * BB, g, st.raw);
+    };
+    struct Products {
+        i32x16 acc;
+        f32x16 dd;
+    };
     f32x16 sum;
 #pragma unroll
     for (int i = 0; i < 16; ++i) sum[i] = 0.0f;
     const f32x16 z = {};
-    // operands of block b: A (activations), the rows' d (lane (c, 0)), B
-    // (weights) and the weight row's f16 d
-    i32x4 av = gld<i32x4>(abase);
-    float xd = gld<float>(xbase);
-    uint32_t dh;
-    i32x4 bv = legacy_operand<WT>(wrow, g, dh);
-    for (int b = 0; b < nb; ++b) {
-        const int bn = min(b + 1, nb - 1);  // (past the last block: a reload nobody uses)
-        const i32x4 av_n = gld<i32x4>(abase + (size_t)bn * 1024);
-        const float xd_n = gld<float>(xbase + (size_t)bn * 32);
-        uint32_t dh_n;
-        const i32x4 bv_n = legacy_operand<WT>(wrow + (size_t)bn * BB, g, dh_n);
-        const i32x16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, i32x16{}, 0, 0, 0);
-        const float wd = f16_to_f32(dh);
-        const f32x16 dd = __builtin_amdgcn_mfma_f32_32x32x2f32(g == 0 ? xd : 0.0f, g == 0 ? wd : 0.0f, z, 0, 0, 0);
+    Products P;
+    bool pending = false;  // (uniform)
+    auto combine = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sum[i] = __builtin_fmaf((float)acc[i], dd[i], sum[i]);
-        av = av_n;
-        xd = xd_n;
-        bv = bv_n;
-        dh = dh_n;
+        for (int i = 0; i < 16; ++i) sum[i] = __builtin_fmaf((float)P.acc[i], P.dd[i], sum[i]);
+    };
+    Stage S[QD];
+#pragma unroll
+    for (int j = 0; j < QD; ++j) load(j, S[j]);
+    for (int it = 0; it < kcnt; it += QD) {
+#pragma unroll
+        for (int j = 0; j < QD; ++j) {
+            if (it + j < kcnt) {
+                const i32x4 bv = legacy_operand<WT>(S[j].raw, g);
+                const float wd = f16_to_f32(S[j].raw.dh);
+                Products np;
+                np.acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(S[j].av, bv, i32x16{}, 0, 0, 0);
+                np.dd = __builtin_amdgcn_mfma_f32_32x32x2f32(g == 0 ? S[j].xd : 0.0f, g == 0 ? wd : 0.0f, z, 0, 0,
+                                                             0);
+                if (pending) combine();
+                P = np;
+                pending = true;
+            }
+            load(it + j + QD, S[j]);
+        }
     }
     const int rr = rt * 32 + c;
+    float rv[16];
+    if (kh == 0) load_residual(a, t32 * 32, g, rr, rv);
+    if (pending) combine();
+    if (kh == 1) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int t = t32 * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-        if (t < a.n && rr < a.rows) {
-            const size_t idx = (size_t)t * a.rows + rr;
-            float v = sum[i];
-            if (a.residual) v += a.residual[idx];
-            a.out[idx] = v;
-        }
+        for (int i = 0; i < 16; ++i) s_red[w4][i][lane] = sum[i];
+    }
+    lds_barrier();
+    if (kh == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum[i] = sum[i] + s_red[w4][i][lane];
+        store_tile(a, t32 * 32, g, rr, sum, rv);
     }
 }
 
@@ -690,18 +763,45 @@ __global__ __launch_bounds__(256) void qmm0_kernel(const QmmArgs a) {
 // row's f32 squares (norm_rows_inplace -> rms_norm_inplace, ops.rs:106-114,
 // 141-145; the sum in another order than the reference's left fold, which
 // may move scale by an ulp).  residual may alias out (not x).  One workgroup
-// per row.
+// per row; rows whose length is a multiple of 4 (with 16-byte aligned
+// buffers) are read as 16-byte pieces,
+// PN_PIECES per thread issued together, so a row costs one round trip per
+// 4 * 256 * PN_PIECES values rather than one per 256.
+constexpr int PN_PIECES = 4;
 __global__ __launch_bounds__(256) void post_norm_kernel(const float* __restrict__ x, float* out,
                                                         const float* __restrict__ w, const float* residual, int e,
                                                         float eps) {
     __shared__ double s_part[4];
     const int t = blockIdx.x, tid = threadIdx.x;
     const float* row = x + (size_t)t * e;
+    const bool vec = (e & 3) == 0 &&
+                     (((uintptr_t)x | (uintptr_t)out | (uintptr_t)w | (uintptr_t)residual) & 15) == 0;
     double ss = 0.0;
-    for (int i = tid; i < e; i += 256) {
-        const float x = row[i];
-        const float sq = x * x;
-        ss += (double)sq;
+    if (vec) {
+        const int e4 = e >> 2;
+        for (int i0 = 0; i0 < e4; i0 += 256 * PN_PIECES) {
+            f32x4 v[PN_PIECES];
+#pragma unroll
+            for (int k = 0; k < PN_PIECES; ++k) {
+                const int i = i0 + tid + 256 * k;
+                v[k] = gld<f32x4>(row + 4 * (size_t)min(i, e4 - 1));
+                if (i >= e4) v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int k = 0; k < PN_PIECES; ++k)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma clang fp contract(off)
+                    const float sq = v[k][j] * v[k][j];
+                    ss += (double)sq;
+                }
+        }
+    } else {
+        for (int i = tid; i < e; i += 256) {
+#pragma clang fp contract(off)
+            const float sq = row[i] * row[i];
+            ss += (double)sq;
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
@@ -709,11 +809,42 @@ __global__ __launch_bounds__(256) void post_norm_kernel(const float* __restrict_
     __syncthreads();
     const double tot = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
     const float scale = 1.0f / (float)sqrt(tot / (double)e + (double)eps);
-    for (int i = tid; i < e; i += 256) {
+    float* orow = out + (size_t)t * e;
+    const float* rrow = residual ? residual + (size_t)t * e : nullptr;
+    if (vec) {
+        const int e4 = e >> 2;
+        for (int i0 = 0; i0 < e4; i0 += 256 * PN_PIECES) {
+            f32x4 v[PN_PIECES], g[PN_PIECES], r[PN_PIECES];
+#pragma unroll
+            for (int k = 0; k < PN_PIECES; ++k) {
+                const size_t i = 4 * (size_t)min(i0 + tid + 256 * k, e4 - 1);
+                v[k] = gld<f32x4>(row + i);
+                g[k] = gld<f32x4>(w + i);
+                r[k] = rrow ? gld<f32x4>(rrow + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int k = 0; k < PN_PIECES; ++k) {
+                const int i = i0 + tid + 256 * k;
+                if (i < e4) {
+                    f32x4 o;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
 #pragma clang fp contract(off)
-        float v = row[i] * scale * w[i];
-        if (residual) v = v + residual[(size_t)t * e + i];
-        out[(size_t)t * e + i] = v;
+                        float y = v[k][j] * scale * g[k][j];
+                        if (rrow) y = y + r[k][j];
+                        o[j] = y;
+                    }
+                    *(__attribute__((address_space(1))) f32x4*)(orow + 4 * (size_t)i) = o;
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < e; i += 256) {
+#pragma clang fp contract(off)
+            float y = row[i] * scale * w[i];
+            if (rrow) y = y + rrow[i];
+            orow[i] = y;
+        }
     }
 }
 
@@ -748,9 +879,9 @@ hipError_t launch_qmatmul(const QmmArgs& a, hipStream_t st) {
             b.out = a.norm_tmp;
         }
         switch (a.wtype) {
-            case 2: hipLaunchKernelGGL(qmm0_kernel<2>, dim3(nwg), dim3(256), 0, st, b); break;
-            case 6: hipLaunchKernelGGL(qmm0_kernel<6>, dim3(nwg), dim3(256), 0, st, b); break;
-            default: hipLaunchKernelGGL(qmm0_kernel<8>, dim3(nwg), dim3(256), 0, st, b); break;
+            case 2: hipLaunchKernelGGL(qmm0_kernel<2>, dim3(nwg), dim3(512), 0, st, b); break;
+            case 6: hipLaunchKernelGGL(qmm0_kernel<6>, dim3(nwg), dim3(512), 0, st, b); break;
+            default: hipLaunchKernelGGL(qmm0_kernel<8>, dim3(nwg), dim3(512), 0, st, b); break;
         }
         e = hipGetLastError();
         if (e != hipSuccess || !a.norm_w) return e;

@@ -120,14 +120,18 @@ def test_qmatmul_legacy_expert_slice(dev, wtype):
 
 
 @pytest.mark.parametrize("wtype", [orc.WTYPE_Q4K, orc.WTYPE_Q4_0])
-def test_qmatmul_post_norm_vs_oracle(dev, wtype):
+@pytest.mark.parametrize("rows,shift", [(768, 0), (4100, 0), (770, 0), (768, 1)])
+def test_qmatmul_post_norm_vs_oracle(dev, wtype, rows, shift):
     """Gemma's step after the attention (forward.rs:345-350): Wo, the
     post-attention RMSNorm of each output row (norm_rows_inplace), then the
     residual; against the oracle's qmatmul followed by its post-norm, with
     and without a residual.  A norm over the wrong axis (per column) or
-    without the gain is caught by the bar."""
-    rng = np.random.default_rng(51 + wtype)
-    rows, cols, n, eps = 768, 512, 40, 1e-6
+    without the gain is caught by the bar.  Rows of 768 and 4100 values take
+    the norm's 16-byte path (4100: a second pass over the row and a partial
+    last piece); 770 values, and an output / residual buffer that starts one
+    float past a 16-byte boundary (shift 1), take its per-value path."""
+    rng = np.random.default_rng(51 + wtype + rows)
+    cols, n, eps = 512, 40, 1e-6
     if wtype == orc.WTYPE_Q4K:
         w = kquant_weights(rng, wtype, rows, cols)
     else:
@@ -141,7 +145,12 @@ def test_qmatmul_post_norm_vs_oracle(dev, wtype):
     for residual in (res, None):
         want = mm.copy()
         orc.post_norm_residual(want, g, residual, n, rows, eps)
-        out = dev.put(residual.reshape(-1)) if residual is not None else dev.empty(n * rows)
+        say(f"post-norm wtype {wtype} rows {rows} shift {shift} residual {residual is not None}")
+        if residual is not None:
+            buf = dev.put(np.concatenate([np.zeros(shift, np.float32), residual.reshape(-1)]))
+        else:
+            buf = dev.empty(n * rows + shift)
+        out = buf[shift:]
         dr.qmatmul_post_norm(dev.ctx, wtype, dev.put(w), rows, cols, dev.put(x), n, out, dev.put(g), eps,
                              out if residual is not None else None)
         got = dev.get(out).reshape(n, rows)
