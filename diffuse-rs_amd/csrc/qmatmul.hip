@@ -667,15 +667,24 @@ __device__ __forceinline__ i32x4 legacy_operand(const LegacyRaw<WT>& r, int g) {
 // output is summed in one fixed order).  Lane (c, g): weight row c of the
 // tile (B operand) and activation row c (A operand), values 16 g .. 16 g +
 // 15 of each block; accumulator slot i is output (activation row 8 (i / 4) +
-// 4 g + i % 4, weight row c).  Each wave keeps the operands of its next QD
-// blocks in flight (a ring of registers, unrolled so that nothing is copied
-// and every wait counts only the loads it needs), and a block's combine runs
-// after the next block's MFMAs are issued.
-constexpr int QD = 4;
+// 4 g + i % 4, weight row c).
+//
+// The four waves of a half need the same weight operands.  Loaded by each
+// wave, 16 bytes per lane from 32 rows a row apart, they kept the texture
+// address unit busy for almost the whole kernel; so the blocks go in groups
+// of QG: wave w % 4 of a half loads block w % 4 of the next group and forms
+// its operand (and d) into LDS, double-buffered, one barrier per group, and
+// every wave reads its operands from there.  Each wave keeps the activation
+// operands of its next QG blocks in flight (a ring of registers, unrolled so
+// that nothing is copied and every wait counts only the loads it needs), and
+// a block's combine runs after the next block's MFMAs are issued.
+constexpr int QG = 4;
 template <int WT>
 __global__ __launch_bounds__(512) void qmm0_kernel(const QmmArgs a) {
     constexpr int BB = WT == 2 ? 18 : (WT == 6 ? 22 : 34);
-    __shared__ float s_red[4][16][64];  // half 1's partial sums
+    __shared__ u32x4 s_w[2][2][QG][64];  // [buffer][half][block of the group][lane]: B operands
+    __shared__ float s_d[2][2][QG][32];  // the weight rows' d
+    __shared__ float s_red[4][16][64];   // half 1's partial sums
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // (uniform: scalar branches)
     const int w4 = wave & 3, kh = wave >> 2;
@@ -694,18 +703,24 @@ __global__ __launch_bounds__(512) void qmm0_kernel(const QmmArgs a) {
     const int nh = (nb + 1) / 2;
     const int kb0 = kh ? nh : 0, kcnt = kh ? nb - nh : nh;
     const int blast = kb0 + (kcnt > 0 ? kcnt - 1 : 0);
+    const int ngroups = (nh + QG - 1) / QG;  // the same for both halves: every wave meets every barrier
 
     struct Stage {
         i32x4 av;
         float xd;  // lane (c, 0): the Q8_0 d of activation row c
-        LegacyRaw<WT> raw;
     };
     // (blocks past the wave's last reload that block: in bounds, unused)
-    auto load = [&](int j, Stage& st) __attribute__((always_inline)) {
+    auto load_a = [&](int j, Stage& st) __attribute__((always_inline)) {
         const int b = min(kb0 + j, blast);
         st.av = gld<i32x4>(abase + (size_t)b * 1024);
         st.xd = gld<float>(xbase + (size_t)b * 32);
-        load_legacy<WT>(wrow + (size_t)b * BB, g, st.raw);
+    };
+    auto load_w = [&](int grp, LegacyRaw<WT>& raw) __attribute__((always_inline)) {
+        load_legacy<WT>(wrow + (size_t)min(kb0 + grp * QG + w4, blast) * BB, g, raw);
+    };
+    auto form = [&](int buf, const LegacyRaw<WT>& raw) __attribute__((always_inline)) {
+        s_w[buf][kh][w4][lane] = __builtin_bit_cast(u32x4, legacy_operand<WT>(raw, g));
+        if (g == 0) s_d[buf][kh][w4][c] = f16_to_f32(raw.dh);
     };
     struct Products {
         i32x16 acc;
@@ -721,15 +736,23 @@ __global__ __launch_bounds__(512) void qmm0_kernel(const QmmArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) sum[i] = __builtin_fmaf((float)P.acc[i], P.dd[i], sum[i]);
     };
-    Stage S[QD];
+
+    LegacyRaw<WT> raw;
+    load_w(0, raw);
+    Stage S[QG];
 #pragma unroll
-    for (int j = 0; j < QD; ++j) load(j, S[j]);
-    for (int it = 0; it < kcnt; it += QD) {
+    for (int j = 0; j < QG; ++j) load_a(j, S[j]);
+    form(0, raw);
+    lds_barrier();
+    for (int grp = 0; grp < ngroups; ++grp) {
+        const int buf = grp & 1;
+        load_w(grp + 1, raw);  // (past the last group: a reload nobody reads)
 #pragma unroll
-        for (int j = 0; j < QD; ++j) {
-            if (it + j < kcnt) {
-                const i32x4 bv = legacy_operand<WT>(S[j].raw, g);
-                const float wd = f16_to_f32(S[j].raw.dh);
+        for (int j = 0; j < QG; ++j) {
+            const int it = grp * QG + j;
+            if (it < kcnt) {
+                const i32x4 bv = __builtin_bit_cast(i32x4, s_w[buf][kh][j][lane]);
+                const float wd = s_d[buf][kh][j][c];
                 Products np;
                 np.acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(S[j].av, bv, i32x16{}, 0, 0, 0);
                 np.dd = __builtin_amdgcn_mfma_f32_32x32x2f32(g == 0 ? S[j].xd : 0.0f, g == 0 ? wd : 0.0f, z, 0, 0,
@@ -738,8 +761,10 @@ __global__ __launch_bounds__(512) void qmm0_kernel(const QmmArgs a) {
                 P = np;
                 pending = true;
             }
-            load(it + j + QD, S[j]);
+            load_a(it + QG, S[j]);
         }
+        form(buf ^ 1, raw);
+        lds_barrier();
     }
     const int rr = rt * 32 + c;
     float rv[16];
