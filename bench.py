@@ -367,6 +367,20 @@ def _wo_inputs(torch, stream):
     return n, rows, cols, nb, w, x, res, dw, dx, dres, out
 
 
+def _wo_extra_inputs(torch, stream, rows, cols):
+    """Q4_0 blocks (sane f16 scales) for the same Wo, and a post-norm gain."""
+    import numpy as np
+    rng = np.random.default_rng(8)
+    w0 = rng.integers(0, 256, (rows * (cols // 32), 18), dtype=np.uint8)
+    w0[:, 0:2] = np.float16(rng.uniform(1e-3, 0.05, rows * (cols // 32))).view(np.uint8).reshape(-1, 2)
+    g = rng.uniform(0.5, 1.5, rows).astype(np.float32)
+    with torch.cuda.stream(stream):
+        dw0 = torch.from_numpy(w0.reshape(-1)).cuda()
+        dg = torch.from_numpy(g).cuda()
+    stream.synchronize()
+    return dw0, dg
+
+
 def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
     """Wo + residual on Q4_K weights (dr_qmatmul) at LLaDA-8B's shape for the
     C2 step: 256 canvas rows x 4096 x 4096, synthetic blocks.  Ops = 2 * n *
@@ -386,15 +400,7 @@ def qmatmul_timing(torch, dr, ctx, stream, reps: int) -> dict:
              "bytes": nbytes, "gbs": round(nbytes / (ms / 1e3) / 1e9, 1)}
     # the same Wo on Q4_0 weights (MatWeight::Q40, Q8_0 activations), and the
     # Q4_K Wo with Gemma's post-attention RMSNorm before the residual add
-    import numpy as np
-    rng = np.random.default_rng(8)
-    w0 = rng.integers(0, 256, (rows * (cols // 32), 18), dtype=np.uint8)
-    w0[:, 0:2] = np.float16(rng.uniform(1e-3, 0.05, rows * (cols // 32))).view(np.uint8).reshape(-1, 2)
-    g = rng.uniform(0.5, 1.5, rows).astype(np.float32)
-    with torch.cuda.stream(stream):
-        dw0 = torch.from_numpy(w0.reshape(-1)).cuda()
-        dg = torch.from_numpy(g).cuda()
-    stream.synchronize()
+    dw0, dg = _wo_extra_inputs(torch, stream, rows, cols)
 
     def call0(i):
         dr.qmatmul(ctx, dr.WTYPE_Q4_0, dw0, rows, cols, dx, n, out, dres)
@@ -420,7 +426,8 @@ N_LAYERS = 32  # LLaDA-8B
 def profile_only(args, torch, dr, CONFIGS) -> int:
     """--only CFG: `calls` eager attention calls of one config (for rocprofv3
     runs: kernel trace and counters of that config's launches).  --only wo:
-    `calls` dr_qmatmul calls at LLaDA-8B's Wo.  --precision hilo: the config
+    `calls` dr_qmatmul calls at LLaDA-8B's Wo (wo_q40: on Q4_0 weights;
+    wo_pn: Q4_K with Gemma's post-attention norm).  --precision hilo: the config
     on a hi/lo-precision layer at scale 1.0 with QK-norm (Gemma's operating
     point)."""
     import dataclasses
@@ -437,13 +444,19 @@ def profile_only(args, torch, dr, CONFIGS) -> int:
                 torch.neg(src, out=dst)
         stream.synchronize()
         del src, dst
-    if args.only == "wo":
+    if args.only in ("wo", "wo_q40", "wo_pn"):
         n, rows, cols, nb, w, x, res, dw, dx, dres, out = _wo_inputs(torch, stream)
+        dw0, dg = _wo_extra_inputs(torch, stream, rows, cols)
         with torch.cuda.stream(stream):
             for _ in range(args.calls):
-                dr.qmatmul(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dres)
+                if args.only == "wo":
+                    dr.qmatmul(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dres)
+                elif args.only == "wo_q40":
+                    dr.qmatmul(ctx, dr.WTYPE_Q4_0, dw0, rows, cols, dx, n, out, dres)
+                else:
+                    dr.qmatmul_post_norm(ctx, dr.WTYPE_Q4K, dw, rows, cols, dx, n, out, dg, 1e-6, dres)
         stream.synchronize()
-        print(json.dumps({"only": "wo", "calls": args.calls}), flush=True)
+        print(json.dumps({"only": args.only, "calls": args.calls}), flush=True)
         return 0
     cfg = CONFIGS[args.only] if args.only in CONFIGS else EXTRA_CONFIGS[args.only]
     prec = None

@@ -1509,13 +1509,16 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
     // 448 blocks on 256 CUs), the staged kernel's 64-row workgroups read each
     // K/V tile once for twice the rows and keep them.
     const int ring_blocks = n_batch * n_head_kv * row_blocks;
-    const int rw = ring_waves(hd);
-    const bool ring_ok = rw > 0 && mask != MASK_KEYS && (qepi != QEPI_FULL || rot == 0 || rot == hd);
     // keys of the widest band a workgroup reads: from the query rows'
     // positions when the caller knows them, else the window's worst case
     // (plus a tile for the band's alignment)
     int band = window >= 0 && 2 * window + BN < max_nk ? 2 * window + BN : max_nk;
     if (key_band > 0 && key_band + BN < band) band = key_band + BN;
+    const int band_tiles = ((band < max_nk ? band : max_nk) + BN - 1) / BN;
+    // waves per workgroup for the unsplit band (the split below is sized with
+    // it; the final count follows from the tiles a split workgroup streams)
+    const int rw = ring_waves(hd, band_tiles);
+    const bool ring_ok = rw > 0 && mask != MASK_KEYS && (qepi != QEPI_FULL || rot == 0 || rot == hd);
     const bool ring_short_band = hd == 256 && merge_in_kernel && 2 * ring_blocks <= cus && band <= 4608 &&
                                  ntiles >= 2 * rw;
     const bool ring_auto =
@@ -1524,9 +1527,7 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
         force_rb <= 0 && force_kq <= 0 && force_rows <= 0) {
         p.kernel = KERNEL_STREAMS;
         p.rb = 1;
-        p.kq = rw;
         p.w16 = false;
-        p.waves = rw;
         p.stages = 1;
         p.qepi = false;  // the Q bias, norm and RoPE are runtime operands of the kernel
         p.rowgroups = row_blocks < 1 ? 1 : row_blocks;
@@ -1549,6 +1550,10 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
         if (split < 1) split = 1;
         p.n_split = split;
         p.n_workgroups = base * split;
+        // (a split only shortens a workgroup's stream: never more waves than rw,
+        // so the split's cap of a tile per wave still holds)
+        p.waves = ring_waves(hd, (band_tiles + split - 1) / split);
+        p.kq = p.waves;
         // rotated tile walks while the K/V that one XCD's workgroups read fits
         // its L2 (4 MB, part of it left to Q, O and partials): the kv heads an
         // XCD holds (consecutive workgroups: a head's row groups and splits)

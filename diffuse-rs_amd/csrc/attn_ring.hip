@@ -11,13 +11,13 @@
 // once, 384 KB per call at LLaDA-8B's 768 keys, so the L2 -> CU stream (64 B
 // per clock per CU on MI355X) bounds the call, not the MFMAs.  The stream
 // reaches that rate only with several waves issuing loads independently.
-// So each of the workgroup's 8 waves is a key group of its own: wave w owns the
-// 32-key tiles w, w + 8, w + 16, ... of the range and runs all 32 query rows
+// So each of the workgroup's 4 waves is a key group of its own: wave w owns the
+// 32-key tiles w, w + 4, w + 8, ... of the range and runs all 32 query rows
 // against them.  It moves each of its tiles into its own slice of LDS with
 // buffer_load ... lds (K tile and V^T tile in separate 8 KB buffers) and
 // waits on its own vmcnt, so no workgroup barrier sits in the key loop.  The
 // next K tile is requested as soon as the QK^T product has read the current
-// one, the next V^T tile as soon as the PV product has.  The 8 partial softmax
+// one, the next V^T tile as soon as the PV product has.  The 4 partial softmax
 // states of each row are merged through LDS at the end, which also stages
 // coalesced full-row output stores.
 //
@@ -38,13 +38,19 @@
 namespace dr {
 namespace {
 
-// Geometry per head dim.  hd 128: 8 waves, two per SIMD.  hd 256: a wave's
-// O^T (128 registers) and Q^T fragments (64) fill most of a SIMD's register
-// file, and its K + V^T tiles take 32 KB of LDS, so the workgroup has 4
-// waves, one per SIMD; each still streams its own tiles.
-template <int HD>
+// Geometry per head dim and wave count W (each wave streams its own tiles).
+// hd 256: 4 waves, one per SIMD (a wave's O^T, 128 registers, and Q^T
+// fragments, 64, fill most of a SIMD's register file; its K + V^T tiles take
+// 32 KB of LDS).  hd 128: 4 or 8 waves, chosen by the planner from the tiles
+// a workgroup streams (ring_waves).  Short streams take 4: at LLaDA-8B's 768
+// keys (24 tiles) 8 waves, two per SIMD, took 11.4 us per call over a 32-layer
+// cache against 10.9 for 4, since their first tiles made a larger start burst
+// through HBM and they leave twice the partial rows to merge.  Long streams
+// take 8, whose loads keep twice the bytes in flight: at 40 - 80 tiles 4 waves
+// were 1 - 6 % slower.
+template <int HD, int W>
 struct Ring {
-    static constexpr int RW = HD == 128 ? 8 : 4;  // waves (key groups) per workgroup
+    static constexpr int RW = W;                  // waves (key groups) per workgroup
     static constexpr int RT = BN * HD;            // bf16 elements per K tile (and per V^T tile)
     static constexpr int KCH = HD / 8;            // 16-byte chunks per K row
     static constexpr int VCH = BN / 8;            // 16-byte chunks per V^T row
@@ -63,10 +69,10 @@ struct Ring {
     static_assert(NDMA < 32, "two tiles of DMA fit the vmcnt counter");
 };
 
-template <int HD, int MODE>
-__global__ __launch_bounds__(Ring<HD>::RW * 64) __attribute__((amdgpu_waves_per_eu(Ring<HD>::RW / 4, Ring<HD>::RW / 4)))
+template <int HD, int MODE, int W>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
 void attn_ring_kernel(const AttnArgs a) {
-    using G = Ring<HD>;
+    using G = Ring<HD, W>;
     constexpr int RW = G::RW, RT = G::RT, R_KCH = G::KCH, R_VCH = G::VCH, NDMA = G::NDMA;
     constexpr int RHD = HD, TPR = G::TPR, QP = G::QP, KS = G::KS, DB = G::DB;
     constexpr int RING_BYTES = G::RING_BYTES, ML_OFF = G::ML_OFF;
@@ -605,15 +611,15 @@ void attn_ring_kernel(const AttnArgs a) {
     }
     lds_barrier();
     // thread tid: row rr = tid / TPR, chunks cidx(k) = ch + TPR k', k < CPT,
-    // where k' = k except at head dim 256: there a wave's 64 lanes are 8 rows
-    // of 8 and every read below would take the same 8-chunk block of 8 rows
-    // (half of a bank sweep, 4 lanes per bank), so odd rows take the blocks in
-    // the other order (k' = k ^ 1).  Every access of the final pass uses the
-    // same mapping.
+    // where k' = k except with 8 threads per row: there a wave's 64 lanes are
+    // 8 rows of 8 and every read below would take the same 8-chunk block of 8
+    // rows (half of a bank sweep, 4 lanes per bank), so odd rows take the
+    // blocks in the other order (k' = k ^ 1).  Every access of the final pass
+    // uses the same mapping.
     constexpr int CPT = HD / 4 / TPR;
     const int rr = tid / TPR, ch = tid % TPR;
     auto cidx = [&](int k) __attribute__((always_inline)) {
-        return ch + TPR * (HD == 256 ? (k ^ (rr & 1)) : k);
+        return ch + TPR * (TPR == 8 ? (k ^ (rr & 1)) : k);
     };
     const int row = wg_row0 + rr;
     const bool row_ok = row < rows_total;
@@ -729,48 +735,55 @@ void attn_ring_kernel(const AttnArgs a) {
     store_rows(macc, Ls);
 }
 
-template <int HD, int MODE>
+template <int HD, int MODE, int W>
 hipError_t launch_ring_mode(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     static bool attr_set = false;
-    auto fn = attn_ring_kernel<HD, MODE>;
+    auto fn = attn_ring_kernel<HD, MODE, W>;
+    constexpr int lds = Ring<HD, W>::LDS;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, Ring<HD>::LDS);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(Ring<HD>::RW * 64), Ring<HD>::LDS, st, a);
+    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(W * 64), lds, st, a);
     return hipGetLastError();
 }
 
-template <int HD>
+template <int HD, int W>
 hipError_t launch_ring_hd(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     switch (p.mask) {
-        case MASK_NONE: return launch_ring_mode<HD, MASK_NONE>(p, a, st);
-        case MASK_POS: return launch_ring_mode<HD, MASK_POS>(p, a, st);
+        case MASK_NONE: return launch_ring_mode<HD, MASK_NONE, W>(p, a, st);
+        case MASK_POS: return launch_ring_mode<HD, MASK_POS, W>(p, a, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-int ring_waves(int hd) {
-    return hd == 128 ? Ring<128>::RW : (hd == 256 ? Ring<256>::RW : 0);
+// The tiles one workgroup streams above which head dim 128 takes 8 waves.
+constexpr int RING8_MIN_TILES = 33;
+
+int ring_waves(int hd, int tiles) {
+    if (hd == 128) return tiles >= RING8_MIN_TILES ? 8 : 4;
+    return hd == 256 ? 4 : 0;
+}
+
+bool ring_waves_built(int hd, int waves) {
+    return (hd == 128 && (waves == 4 || waves == 8)) || (hd == 256 && waves == 4);
 }
 
 int ring_merge_splits(int hd) {
-    return hd == 128 ? Ring<128>::MS : (hd == 256 ? Ring<256>::MS : 0);
+    return hd == 128 ? Ring<128, 4>::MS : (hd == 256 ? Ring<256, 4>::MS : 0);
 }
 
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     // (RoPE on Q only at full rotary: see the Q load)
-    if ((a.rope && a.rot != a.hd) || a.hd != p.hd_tile || p.waves != ring_waves(a.hd)) return hipErrorInvalidValue;
+    if ((a.rope && a.rot != a.hd) || a.hd != p.hd_tile || !ring_waves_built(a.hd, p.waves))
+        return hipErrorInvalidValue;
     if (a.ticket && a.n_split > ring_merge_splits(a.hd)) return hipErrorInvalidValue;
-    switch (a.hd) {
-        case 128: return launch_ring_hd<128>(p, a, st);
-        case 256: return launch_ring_hd<256>(p, a, st);
-        default: return hipErrorInvalidValue;
-    }
+    if (a.hd == 128) return p.waves == 8 ? launch_ring_hd<128, 8>(p, a, st) : launch_ring_hd<128, 4>(p, a, st);
+    return launch_ring_hd<256, 4>(p, a, st);
 }
 
 }  // namespace dr

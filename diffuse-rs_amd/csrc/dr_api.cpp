@@ -1759,8 +1759,8 @@ long dr_debug_alloc_count(void) { return g_allocs.load(std::memory_order_relaxed
 
 int dr_debug_ring_tiles(size_t head_dim, size_t nk, size_t cap, long long window, long long qmin,
                         long long qmax, size_t n_split, int* min_tile, int* max_tile, int* partition_ok) {
-    const int rw = dr::ring_waves((int)head_dim);
-    if (rw == 0) return fail(DR_ERR_UNSUPPORTED, "no stream kernel at head_dim %zu", head_dim);
+    if (dr::ring_waves((int)head_dim, 1) == 0)
+        return fail(DR_ERR_UNSUPPORTED, "no stream kernel at head_dim %zu", head_dim);
     if (!min_tile || !max_tile || !partition_ok || n_split < 1 || nk > cap || cap % dr::KEY_ALIGN != 0 ||
         cap == 0 || cap >= MAX_POS)
         return fail(DR_ERR_INVALID, "dr_debug_ring_tiles: bad arguments");
@@ -1779,6 +1779,8 @@ int dr_debug_ring_tiles(size_t head_dim, size_t nk, size_t cap, long long window
         int t0, t1;
         dr::split_tile_range(kt_lo, kt_hi, (int)n_split, split, t0, t1);
         for (int rg = 0; rg < 24; ++rg) {  // (a rotated walk only reorders each wave's tiles)
+          for (int rw = 4; rw <= 8; rw += 4) {  // every wave count built
+            if (!dr::ring_waves_built((int)head_dim, rw)) continue;
             std::vector<int> seen(cap_tiles, 0);
             for (int w = 0; w < rw; ++w) {
                 const dr::RingWaveTiles wt(t0, t1 - t0, w, rw, rg, cap_tiles);
@@ -1799,8 +1801,9 @@ int dr_debug_ring_tiles(size_t head_dim, size_t nk, size_t cap, long long window
             for (int t = 0; t < cap_tiles; ++t) {
                 const bool in = t >= t0 && t < t1;
                 if (seen[t] != (in ? 1 : 0)) ok = false;
-                if (rg == 0) mult[t] += seen[t];
+                if (rg == 0 && rw == 4) mult[t] += seen[t];
             }
+          }
         }
     }
     // the splits together cover the range once

@@ -369,7 +369,10 @@ size_t scratch_bytes();
 hipError_t scratch_init(int device);
 void* scratch_ptr(int device);
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
-int ring_waves(int hd);  // waves per workgroup of attn_ring_kernel (0: head dim not built)
+// waves per workgroup of attn_ring_kernel for a workgroup streaming `tiles`
+// key tiles (0: head dim not built), and whether a wave count is built
+int ring_waves(int hd, int tiles);
+bool ring_waves_built(int hd, int waves);
 int ring_merge_splits(int hd);  // most key splits attn_ring_kernel merges in-kernel
 hipError_t launch_hilo(const LaunchPlan& p, const AttnArgs& a, hipStream_t st);
 int hilo_rows();  // query rows per workgroup of attn_hilo_kernel

@@ -534,8 +534,9 @@ long dr_debug_alloc_count(void);
 /* The key tiles the STREAMS kernel's waves request for one workgroup of a
  * head_dim 128 / 256 problem: nk keys in a cache of cap positions (a
  * multiple of 64), queries at positions qmin..qmax under a sliding window
- * (window < 0: none), n_split key splits, every row group.  Computed on the
- * host by the same code the kernel runs.  min_tile / max_tile: the extremes
+ * (window < 0: none), n_split key splits, every row group and every wave
+ * count the kernel is built with (4 and 8 waves per workgroup at head_dim
+ * 128, 4 at 256).  Computed on the host by the same code the kernel runs.  min_tile / max_tile: the extremes
  * of every tile index any wave issues a DMA for (including a wave without
  * tiles); partition_ok: 1 if each split's waves multiply each tile of its
  * range exactly once and the splits cover the workgroup's range once. */

@@ -66,6 +66,9 @@ CASES = {
     "qk_norm": (8, 8, 400, 96, 1, None, None, True, 0),
     "split2": (4, 4, 900, 64, 1, None, None, False, 2),
     "split3_window": (4, 2, 1500, 64, 1, 400, None, False, 3),
+    # 256 one-block workgroups streaming 36 key tiles each: the 8-wave build
+    # of the per-wave-stream kernel (test_planner_hd128_waves)
+    "long_stream": (8, 8, 100, 1024, 1, None, None, False, 0),
 }
 # head dim 256 (DiffusionGemma's sliding and global layers): the same kinds
 # of problem for the 4-wave build of the per-wave-stream kernel
@@ -204,6 +207,21 @@ def test_planner_picks_streams_for_one_round(dev):
         items = [(q, dev.empty(n_c * h * hd), pc) for _ in range(2 if hkv == 4 else 1)]
         cache.attention(0, items, h, scale=0.1)
         assert dev.ctx.last_launch()["kernel"] == want, (h, hkv)
+
+
+def test_planner_hd128_waves(dev):
+    """Head dim 128: the per-wave-stream kernel runs 4 waves per workgroup
+    when a workgroup streams at most 32 key tiles (after any key split) and 8
+    above, whose loads keep twice the bytes in flight; both builds against
+    the oracle at the planner's choice."""
+    for name, waves in (("mha", 4), ("split2", 4), ("long_stream", 8)):
+        got, wants, info = _run(dev, name, dr.KERNEL_AUTO)
+        say(f"{name}: launch {info}")
+        assert info["kernel"] == dr.KERNEL_STREAMS and info["waves_per_wg"] == waves, (name, info)
+        for g, w in zip(got, wants):
+            mx, mean = err_stats(g, w)
+            say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
+            assert mx <= TOL_MAX and mean <= TOL_MEAN, (name, mx, mean)
 
 
 def test_planner_hd256_key_band(dev):
