@@ -1312,7 +1312,6 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
 template <int HD>
 __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     constexpr int CHUNKS = HD / 4;
-    constexpr int SG = 8;  // splits whose loads are issued together
     const size_t plane = (size_t)a.n_batch * a.n_head_kv * a.part_rows;
     const size_t item = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (item >= plane * CHUNKS) return;
@@ -1329,8 +1328,12 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
     // one per-thread offset and the split's plane offset as a scalar, so the
     // SG loads of a group need no address registers of their own (with 64-bit
     // addresses the compiler held back loads until earlier ones returned).
-    auto groups = [&](auto buffered) __attribute__((always_inline)) {
+    // SG, the splits whose loads are issued together: 4 up to 4 splits, else
+    // 8.  (Slots past n_split reload the last split and weigh 0; at 4 splits
+    // a group of 8 doubled the loads the address unit handles.)
+    auto groups = [&](auto buffered, auto sgc) __attribute__((always_inline)) {
         constexpr bool BUF = decltype(buffered)::value;
+        constexpr int SG = decltype(sgc)::value;
         const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o, 0xffffffffu);
         const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.part_ml, 0xffffffffu);
         const int vo = (int)((prow * HD + ch * 4) * 4), vm = (int)(prow * 8);
@@ -1358,10 +1361,18 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const AttnArgs a) {
             merge_split_states<SG, 1>(Mx, Ls, acc, m, l, o);
         }
     };
-    if ((size_t)a.n_split * plane * HD * 4 <= 0x7fffffffu)  // (uniform)
-        groups(std::integral_constant<bool, true>{});
-    else
-        groups(std::integral_constant<bool, false>{});
+    const bool buffered = (size_t)a.n_split * plane * HD * 4 <= 0x7fffffffu;  // (uniform)
+    if (a.n_split <= 4) {
+        if (buffered)
+            groups(std::integral_constant<bool, true>{}, std::integral_constant<int, 4>{});
+        else
+            groups(std::integral_constant<bool, false>{}, std::integral_constant<int, 4>{});
+    } else {
+        if (buffered)
+            groups(std::integral_constant<bool, true>{}, std::integral_constant<int, 8>{});
+        else
+            groups(std::integral_constant<bool, false>{}, std::integral_constant<int, 8>{});
+    }
     const AttnSlot& S = a.slot[b];
     if (r >= a.group * S.nq) return;
     int hg, qi;
