@@ -41,6 +41,12 @@ __device__ __forceinline__ int swz(int row) {
     }
 }
 
+// The 64-byte V^T rows read by 16-row waves (16x16x32 MFMA: lane (g, n)
+// reads chunk g of row 16 k + n) take (d >> 1) & 3, which
+// SQ_LDS_BANK_CONFLICT measures conflict-free on MI355X; swz<4> above cost
+// 0.28 of the LDS-active cycles there, and five other forms as much.
+__device__ __forceinline__ int swz_v16(int d) { return (d >> 1) & 3; }
+
 // RoPE's rotation of one pair (ops.rs:447-448), without fused multiply-adds
 // as Rust evaluates it.
 __device__ __forceinline__ float rope_lo(float a, float b, float sn, float cs) {

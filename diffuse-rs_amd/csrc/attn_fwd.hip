@@ -254,7 +254,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
             return (((R & ~31) + kperm<W16>(R & 31)) * HD + ((pk ^ swz<KCH>(R)) << 3)) * 2;
         }
         const int d = idx / VCH, pv = idx % VCH;
-        return (d * BN + ((pv ^ swz<VCH>(d)) << 3)) * 2;  // within the V^T tile
+        return (d * BN + ((pv ^ (W16 ? swz_v16(d) : swz<VCH>(d))) << 3)) * 2;  // within the V^T tile
     };
     // Compute waves that also issue DMA keep the offsets in registers; DMA
     // waves recompute them per super-tile (they have the issue slots to
@@ -730,7 +730,7 @@ __launch_bounds__((RB * KQ * (W16 ? 2 : 1) * (HD > 256 ? 2 : 1) + NP) * 64) void
                 // this tile's V^T fragments: rows 16*(db0 + db) + n16, keys 8*g16 ..
                 auto vfrag = [&](int db) __attribute__((always_inline)) {
                     const int d = 16 * (db0 + db) + n16;
-                    return *reinterpret_cast<const bf16x8*>(vs + d * BN + ((g16 ^ swz<VCH>(d)) << 3));
+                    return *reinterpret_cast<const bf16x8*>(vs + d * BN + ((g16 ^ swz_v16(d)) << 3));
                 };
                 if constexpr (PIPE16) {
 #pragma unroll

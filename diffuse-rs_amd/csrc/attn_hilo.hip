@@ -75,7 +75,7 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
     __shared__ int s_red[3][NW];
     uint16_t* const lk = smem;              // K hi tile (rows in kappa order, chunks swizzled)
     uint16_t* const lkl = smem + TILE;      // K lo tile (same layout)
-    uint16_t* const lv = smem + 2 * TILE;   // V^T tile [HD][32]
+    uint16_t* const lv = smem + 2 * TILE;   // V^T tile [HD][32] (chunks swizzled by swz_v16)
     uint16_t* const lvl = smem + 3 * TILE;  // V^T lo tile (same layout)
     float* const xch = reinterpret_cast<float*>(smem + 4 * TILE);  // [NW][8][64] partial scores
 
@@ -244,12 +244,15 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
                 dma16(rkl, dst, kvo[j], soff);
         }
     };
+    // V^T hi / lo: LDS chunk (d, pv) of a tile holds chunk pv ^ swz_v16(d)
+    // of row d
     auto issue_v = [&](int t) __attribute__((always_inline)) {
         const int soff = t * BN * HD * 2;  // V^T tile t: HD x 32 contiguous
 #pragma unroll
         for (int j = 0; j < VDMA; ++j) {
             const int first = (wave * VDMA + j) * 64;  // (the two V^T tiles are contiguous)
-            const int voff = ((first + lane) % CPT) * 16;
+            const int idx = (first + lane) % CPT, d = idx / (BN / 8), pv = idx % (BN / 8);
+            const int voff = (d * (BN / 8) + (pv ^ swz_v16(d))) * 16;
             if (first < CPT)
                 dma16(rv, lv + first * 8, voff, soff);
             else
@@ -353,8 +356,8 @@ __global__ __launch_bounds__(HiloGeom<HD>::NT) void attn_hilo_kernel(const AttnA
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
             const int d = dh * HDW + 16 * db + qc;
-            const bf16x8 vf = *reinterpret_cast<const bf16x8*>(lv + d * BN + 8 * gq);
-            const bf16x8 vl = *reinterpret_cast<const bf16x8*>(lvl + d * BN + 8 * gq);
+            const bf16x8 vf = *reinterpret_cast<const bf16x8*>(lv + d * BN + ((gq ^ swz_v16(d)) << 3));
+            const bf16x8 vl = *reinterpret_cast<const bf16x8*>(lvl + d * BN + ((gq ^ swz_v16(d)) << 3));
             o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb, o[db], 0, 0, 0);
             o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, pb, o[db], 0, 0, 0);
         }
