@@ -1486,6 +1486,9 @@ hipError_t launch_shape(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) 
 
 }  // namespace
 
+// Longest key band (32-key tiles) for which head dim 256 takes 16-row waves.
+constexpr int RING16_MAX_TILES = 44;
+
 LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max_nq, int max_nk,
                           int mask, int qepi, int window, int rot, int n_cu, int force_rb, int force_kq,
                           int force_split, int force_rows, int force_kernel, bool merge_in_kernel,
@@ -1534,6 +1537,37 @@ LaunchPlan plan_attention(int hd, int n_batch, int n_head_kv, int group, int max
                                  ntiles >= 2 * rw;
     const bool ring_auto =
         ring_blocks <= cus && (hd == 128 || (window >= 0 && window <= 1024) || ring_short_band);
+    // 16-row waves at head dim 256 (attn_ring16_kernel): one 16-row block
+    // per workgroup, no key split.  Twice the workgroups of the 32-row
+    // kernel, each streaming its whole band for half the rows, so it wins
+    // where the 32-row kernel needs a key split and the band is short (16/8
+    // heads, 256 queries, auto plan against 16-row waves, µs: window 256
+    // 13.2 / 10.7, 512 15.0 / 12.9, 1024 17.4 / 16.5, 1536 20.2 / 20.6, 2048
+    // 22.7 / 24.1; no window, 512 keys 12.7 / 10.0, 1280 16.8 / 16.5, 2304
+    // 22.2 / 23.6).  Picked for bands up to RING16_MAX_TILES tiles when its
+    // workgroups fill more than half the CUs in one round.
+    const int r16_blocks = n_batch * n_head_kv * ((group * max_nq + 15) / 16);
+    const bool r16_forced = force_kernel == KERNEL_STREAMS && force_rows == 16;
+    // (the planner's choice within the stream family too: bf16 Q or output
+    // rows ask for that family)
+    const bool r16_auto = (force_kernel == KERNEL_AUTO || force_kernel == KERNEL_STREAMS) && force_rows <= 0 &&
+                          force_split <= 0 &&
+                          band_tiles <= RING16_MAX_TILES && 2 * r16_blocks > cus && r16_blocks <= cus;
+    if (ring_ok && hd == 256 && (r16_forced || r16_auto) && force_rb <= 0 && force_kq <= 0) {
+        p.kernel = KERNEL_STREAMS;
+        p.w16 = true;
+        p.rb = 1;
+        p.stages = 1;
+        p.qepi = false;
+        p.rowgroups = (group * max_nq + 15) / 16;
+        if (p.rowgroups < 1) p.rowgroups = 1;
+        p.n_split = 1;
+        p.n_workgroups = n_batch * n_head_kv * p.rowgroups;
+        p.waves = 4;
+        p.kq = 4;
+        p.rotate = false;
+        return p;
+    }
     if (ring_ok && (force_kernel == KERNEL_STREAMS || (force_kernel == KERNEL_AUTO && ring_auto)) &&
         force_rb <= 0 && force_kq <= 0 && force_rows <= 0) {
         p.kernel = KERNEL_STREAMS;

@@ -735,6 +735,552 @@ void attn_ring_kernel(const AttnArgs a) {
     store_rows(macc, Ls);
 }
 
+// ---------------------------------------------------------------------------
+// 16-row waves at head dim 256: one 16-row block per workgroup, 4 waves, each
+// a key group streaming its own tiles as attn_ring_kernel does, on
+// v_mfma_f32_16x16x32_bf16 (the lane mappings of attn_fwd_kernel's 16-row
+// waves: lane (n16, g16) = query row n16, contraction / key group g16; LDS
+// row R of a K tile holds key kappa(R), so that the S^T accumulators of the
+// two 16-key blocks give each lane the keys 8 g16 .. 8 g16 + 7 that the PV
+// product wants from it).  A wave's O^T takes 64 registers instead of the
+// 128 of a 32-row wave, and half the rows per workgroup give twice the
+// workgroups: a short key band fills the chip without a key split, so no
+// split partials go through memory and no merge tail follows the loop.  No
+// key splits, no Q epilogue beyond the QK-norm, bias and RoPE of the 32-row
+// kernel's Q load.
+template <int HD>
+struct Ring16 {
+    static constexpr int RW = 4;                  // waves (key groups) per workgroup
+    static constexpr int ROWS = 16;               // query rows per workgroup
+    static constexpr int RT = BN * HD;            // bf16 elements per K tile (and per V^T tile)
+    static constexpr int KCH = HD / 8;            // 16-byte chunks per K row
+    static constexpr int VCH = BN / 8;            // 16-byte chunks per V^T row
+    static constexpr int NDMA = RT * 2 / 1024;    // 1 KB DMA instructions per tile
+    static constexpr int NC = HD / 32;            // contraction steps of QK^T (32 dims each)
+    static constexpr int ND = HD / 16;            // 16-dim blocks of O^T
+    static constexpr int TPR = RW * 64 / ROWS;    // threads per query row (Q load, final pass)
+    static constexpr int QP = HD / 4 / TPR;       // f32x4 pieces per thread and row
+    static constexpr int RING_BYTES = RW * 2 * RT * 2;
+    static constexpr int Q_BYTES = ROWS * HD * 2;
+    static constexpr int ML_OFF = RING_BYTES + Q_BYTES;  // [RW][16] max, then [RW][16] sum
+    static constexpr int LDS = ML_OFF + 2 * RW * ROWS * 4;
+    static_assert(HD == 256, "built for head dim 256");
+    static_assert(ROWS * HD * 4 <= 2 * RT * 2, "a wave's O^T partial fits its K + V^T buffers");
+    static_assert(QP % 2 == 0, "RoPE pairs sit in one thread");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(NDMA < 32, "two tiles of DMA fit the vmcnt counter");
+};
+
+template <int HD, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_ring16_kernel(const AttnArgs a) {
+    using G = Ring16<HD>;
+    constexpr int RW = G::RW, RT = G::RT, R_KCH = G::KCH, R_VCH = G::VCH, NDMA = G::NDMA;
+    constexpr int RHD = HD, TPR = G::TPR, QP = G::QP, NC = G::NC, ND = G::ND, ROWS = G::ROWS;
+    constexpr int RING_BYTES = G::RING_BYTES, ML_OFF = G::ML_OFF;
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    __shared__ int s_red[3];
+
+    AttnSlot S = a.slot[0];
+    const float* qn_w = a.qn_w;
+    int q_bf16 = a.q_bf16;
+    const float* qb = a.qb;
+    const float* rope = a.rope;
+    asm volatile("" : "+s"(S.q), "+s"(S.out), "+s"(S.qpos), "+s"(S.qseq), "+s"(S.qprefix),
+                 "+s"(S.k), "+s"(S.vt), "+s"(S.nq), "+s"(S.nk), "+s"(S.qpos_sorted), "+s"(qn_w),
+                 "+s"(S.qpos0), "+s"(q_bf16), "+s"(qb), "+s"(rope)
+                 : "s"(a.n_batch), "s"(a.n_head_kv), "s"(a.group), "s"(a.cap),
+                   "s"(a.q_rstride), "s"(a.rowgroups), "s"(a.mg_rowgroups), "s"(a.mg_hkv), "s"(a.c),
+                   "s"(a.n_wg), "s"(a.window), "s"(a.prefix));
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15, g16 = lane >> 4;
+
+    // Workgroup -> (batch, kv head, row group); consecutive logical ids (the
+    // row groups of one kv head) share an XCD and its L2.
+    const int nwg = a.n_wg;
+    const int hw = blockIdx.x;
+    const int lid = (nwg & 7) == 0 ? (hw & 7) * (nwg >> 3) + (hw >> 3) : hw;
+    const int q2 = udiv(lid, a.rowgroups, a.mg_rowgroups);
+    const int rg = lid - q2 * a.rowgroups;
+    const int b = udiv(q2, a.n_head_kv, a.mg_hkv);
+    const int g = q2 - b * a.n_head_kv;
+    if (a.n_batch > 1) S = a.slot[b];
+
+    const int rows_total = a.group * S.nq;
+    const int wg_row0 = rg * ROWS;
+    if (wg_row0 >= rows_total) return;  // uniform over the workgroup
+    const float inv_nq = __builtin_amdgcn_rcpf((float)S.nq);
+    auto split_row = [&](int r, int& hgo, int& qio) __attribute__((always_inline)) {
+        if (a.group == 1) {
+            hgo = 0;
+            qio = r;
+        } else {
+            row_split(r, S.nq, inv_nq, a.group, hgo, qio);
+        }
+    };
+
+    // ---- Q rows (as attn_ring_kernel): thread tid holds the QP f32x4 pieces
+    // d0 + (HD / QP) p of workgroup row tid / TPR
+    constexpr int QSTR = HD / QP;
+    const int qlr = tid / TPR;
+    const int qd0 = (tid % TPR) * 4;
+    const int qr = wg_row0 + qlr;
+    const bool qok = qr < rows_total;
+    f32x4 xq[QP], wq[QP], bq4[QP];
+    u32x2 xq16[QP];
+    f32x4 tab[QP / 2][2];
+    int tab_pos = 0;
+    auto load_tab = [&](int pos) __attribute__((always_inline)) {
+        const float* trow = rope + ((size_t)pos * (RHD / 2) + qd0) * 2;
+#pragma unroll
+        for (int p = 0; p < QP / 2; ++p) {
+            tab[p][0] = gload<f32x4>(trow + 2 * QSTR * p);
+            tab[p][1] = gload<f32x4>(trow + 2 * QSTR * p + 4);
+        }
+    };
+    {
+        int qhg, qqi;
+        split_row(qok ? qr : 0, qhg, qqi);
+        const size_t qoff = (size_t)qqi * a.q_rstride + (size_t)(g * a.group + qhg) * RHD + qd0;
+        if (q_bf16) {
+            const uint16_t* qrow = static_cast<const uint16_t*>(S.q) + qoff;
+#pragma unroll
+            for (int p = 0; p < QP; ++p) xq16[p] = gload<u32x2>(qrow + QSTR * p);
+        } else {
+            const float* qrow = static_cast<const float*>(S.q) + qoff;
+#pragma unroll
+            for (int p = 0; p < QP; ++p) xq[p] = gload<f32x4>(qrow + QSTR * p);
+        }
+        if (qn_w) {
+#pragma unroll
+            for (int p = 0; p < QP; ++p) wq[p] = gload<f32x4>(qn_w + qd0 + QSTR * p);
+        }
+        if (qb) {
+            const float* bq = qb + (size_t)(g * a.group + qhg) * RHD;
+#pragma unroll
+            for (int p = 0; p < QP; ++p) bq4[p] = gload<f32x4>(bq + qd0 + QSTR * p);
+        }
+        if (rope) {
+            if (S.qpos0 >= 0)
+                load_tab(S.qpos0 + qqi);
+            else
+                tab_pos = gload<int>(S.qpos + qqi);
+        }
+    }
+
+    // ---- this lane's query row (n16), its mask state, the key-tile range
+    const int r = wg_row0 + n16;
+    const bool rvalid = r < rows_total;
+    int hg = 0, qi = 0;
+    if (rvalid) split_row(r, hg, qi);
+    int kt_lo = 0, kt_hi = (S.nk + BN - 1) / BN;
+    int my_qpos = 0, my_qseq = 0, my_pref = -1;
+    int qmin = 0, qmax = 0;
+    bool tiles_can_be_full = MODE == MASK_NONE;
+    if constexpr (MODE == MASK_POS) {
+        my_qpos = S.qpos0 >= 0 ? S.qpos0 + (rvalid ? qi : 0) : gload<int>(S.qpos + (rvalid ? qi : 0));
+        if (S.qseq) my_qseq = gload<int>(S.qseq + (rvalid ? qi : 0));
+        my_pref = S.qprefix ? (rvalid ? gload<int>(S.qprefix + qi) : -1) : a.prefix;
+        bool prefix_free;
+        if (S.qpos_sorted && S.qprefix == nullptr) {
+            const int r1 = min(wg_row0 + ROWS, rows_total) - 1;
+            const int h0 = wg_row0 / S.nq, h1 = r1 / S.nq;
+            const int lo = h0 == h1 ? wg_row0 - h0 * S.nq : 0;
+            const int hi = h0 == h1 ? r1 - h0 * S.nq : S.nq - 1;
+            if (S.qpos0 >= 0) {
+                qmin = S.qpos0 + lo;
+                qmax = S.qpos0 + hi;
+            } else {
+                qmin = *(const __attribute__((address_space(4))) int*)(S.qpos + lo);
+                qmax = *(const __attribute__((address_space(4))) int*)(S.qpos + hi);
+            }
+            prefix_free = a.prefix < 0 || qmin >= a.prefix;
+        } else {
+            int vmin = rvalid ? my_qpos : INT_MAX;
+            int vmax = rvalid ? my_qpos : INT_MIN;
+            int pref_row = (rvalid && my_pref >= 0 && my_qpos < my_pref) ? 1 : 0;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                vmin = min(vmin, __shfl_xor(vmin, off));
+                vmax = max(vmax, __shfl_xor(vmax, off));
+                pref_row |= __shfl_xor(pref_row, off);
+            }
+            if (wave == 0 && lane == 0) {
+                s_red[0] = vmin;
+                s_red[1] = vmax;
+                s_red[2] = pref_row;
+            }
+            __syncthreads();
+            qmin = s_red[0];
+            qmax = s_red[1];
+            prefix_free = s_red[2] == 0;
+        }
+        tiles_can_be_full = prefix_free && S.qseq == nullptr;
+        if (a.window >= 0) band_tile_range(S.nk, a.window, qmin, qmax, kt_lo, kt_hi);
+    }
+    const int t0 = kt_lo, nt = kt_hi - kt_lo;
+
+    // ---- K / V^T planes of kv head g and this wave's DMA offsets: LDS row R
+    // of a K tile holds key kappa(R), chunks swizzled by R; V^T row d chunks
+    // swizzled by swz_v16(d)
+    const uint32_t plane_bytes = (uint32_t)a.cap * RHD * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k + (size_t)g * a.cap * RHD, plane_bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vt + (size_t)g * RHD * a.cap, plane_bytes);
+    int kvo[NDMA], vvo[NDMA];
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) {
+        const int idx = j * 64 + lane;
+        const int R = idx / R_KCH, pk = idx % R_KCH;
+        kvo[j] = (kappa(R) * RHD + ((pk ^ swz<R_KCH>(R)) << 3)) * 2;
+        const int d = idx / R_VCH, pv = idx % R_VCH;
+        vvo[j] = (d * BN + ((pv ^ swz_v16(d)) << 3)) * 2;
+    }
+    uint16_t* const kbuf = smem + wave * 2 * RT;
+    uint16_t* const vbuf = kbuf + RT;
+    auto issue_k = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NDMA; ++j) dma16(rk, kbuf + j * 512, kvo[j], t * (BN * RHD * 2));
+    };
+    auto issue_v = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NDMA; ++j) dma16(rv, vbuf + j * 512, vvo[j], t * (BN * RHD * 2));
+    };
+    auto issue_v_to_k = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NDMA; ++j) dma16(rv, kbuf + j * 512, vvo[j], t * (BN * RHD * 2));
+    };
+    // wave w takes tiles t0 + w, t0 + w + RW, ... (a fixed assignment: the
+    // same summation order every call)
+    const RingWaveTiles wt(t0, nt, wave, RW, 0, a.cap / BN);
+    const int kw = wt.kw;
+    auto tile_at = [&](int k) __attribute__((always_inline)) { return wt.at(k); };
+    issue_k(wt.first_dma());
+
+    if (rope && S.qpos0 < 0) load_tab(tab_pos);
+    if (q_bf16) {
+#pragma unroll
+        for (int p = 0; p < QP; ++p) {
+            const u32x2 w = xq16[p];
+            xq[p] = f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                          __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+        }
+    }
+    if (qb) {
+#pragma unroll
+        for (int p = 0; p < QP; ++p) xq[p] += bq4[p];
+    }
+    if (qn_w) {
+        double ss = 0.0;
+#pragma unroll
+        for (int p = 0; p < QP; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sq = xq[p][e] * xq[p][e];
+                ss += (double)sq;
+            }
+#pragma unroll
+        for (int off = 1; off < TPR; off <<= 1) ss += __shfl_xor(ss, off);
+        const float sc = 1.0f / (float)sqrt(ss / (double)RHD + (double)a.qn_eps);
+#pragma unroll
+        for (int p = 0; p < QP; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
+                xq[p][e] = xq[p][e] * sc * wq[p][e];
+            }
+    }
+    if (rope) {
+#pragma unroll
+        for (int p = 0; p < QP / 2; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sn = tab[p][e >> 1][2 * (e & 1)], cs = tab[p][e >> 1][2 * (e & 1) + 1];
+                const float lo = xq[p][e], hi = xq[p + QP / 2][e];
+                xq[p][e] = rope_lo(lo, hi, sn, cs);
+                xq[p + QP / 2][e] = rope_hi(lo, hi, sn, cs);
+            }
+    }
+    uint16_t* const qs = smem + RING_BYTES / 2;
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+        const int d = qd0 + QSTR * p;
+        bf16x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (__bf16)(qok ? xq[p][e] * a.c : 0.0f);
+        *reinterpret_cast<bf16x4*>(qs + qlr * RHD + (((d >> 3) ^ swz<R_KCH>(qlr)) << 3) + (d & 7)) = y;
+    }
+    lds_barrier();  // (the first K tile stays in flight)
+    issue_v(wt.first_dma());
+    // Q^T fragments: lane (n16, g16) supplies row n16, dims 32 c + 8 g16 .. + 8
+    bf16x8 qf[NC];
+    {
+        const uint16_t* qrow = qs + n16 * RHD;
+        const int sw = swz<R_KCH>(n16);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qrow + (((4 * c + g16) ^ sw) << 3));
+    }
+
+    f32x4 o[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) o[db] = f32x4{};
+    float mu = 0.0f;
+    bool m_set = false;
+    float thr = -INFINITY;
+    float l_acc = 0.0f;
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    float negm = 0.0f;  // -m: the accumulator init of QK^T
+
+    // V^T fragments of a tile: lane (n16, g16) supplies row d = 16 db + n16,
+    // keys 8 g16 .. + 8 (the keys of the P^T operand it holds)
+    auto read_v = [&](const uint16_t* vsrc, bf16x8 (&vf)[ND]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+            const int d = 16 * db + n16;
+            vf[db] = *reinterpret_cast<const bf16x8*>(vsrc + d * BN + ((g16 ^ swz_v16(d)) << 3));
+        }
+    };
+    auto pv = [&](const bf16x8 (&vf)[ND], const bf16x8& pp) __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < ND; ++db) o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pp, o[db], 0, 0, 0);
+    };
+    // S^T = K Q^T - m of the tile in the K buffer: block b holds LDS rows
+    // 16 b + n16; slot i of block b is key 8 g16 + 4 b + i
+    auto qk = [&](f32x4& s0, f32x4& s1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s0[i] = s1[i] = negm;
+        const uint16_t* kr0 = kbuf + n16 * RHD;
+        const uint16_t* kr1 = kbuf + (16 + n16) * RHD;
+        const int sw0 = swz<R_KCH>(n16), sw1 = swz<R_KCH>(16 + n16);
+        constexpr int NKH = 2, NCH = NC / NKH;
+#pragma unroll
+        for (int h = 0; h < NKH; ++h) {
+            bf16x8 kf0[NCH], kf1[NCH];
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int cc = h * NCH + c;
+                kf0[c] = *reinterpret_cast<const bf16x8*>(kr0 + (((4 * cc + g16) ^ sw0) << 3));
+                kf1[c] = *reinterpret_cast<const bf16x8*>(kr1 + (((4 * cc + g16) ^ sw1) << 3));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf0[c], qf[h * NCH + c], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf1[c], qf[h * NCH + c], s1, 0, 0, 0);
+            }
+        }
+    };
+    // masking and the lazily moved max; a row's 32 scores sit in the four
+    // lanes n16 + 16 g16
+    auto mask_and_max = [&](f32x4& s0, f32x4& s1, int tt, float& alpha) __attribute__((always_inline)) {
+        const int kbase = tt * BN;
+        bool full = kbase + BN <= S.nk;
+        if constexpr (MODE == MASK_POS) {
+            const bool win_ok =
+                a.window < 0 || (qmax - kbase < a.window && kbase + BN - 1 - qmin < a.window);
+            full = full && tiles_can_be_full && win_ok;
+        }
+        if (!full) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int kidx = kbase + 8 * g16 + j;
+                bool vis = kidx < S.nk;
+                if constexpr (MODE == MASK_POS)
+                    vis = vis & visible(my_qpos, kidx, my_qseq, 0, a.window, my_pref);
+                if (j < 4)
+                    s0[j] = vis ? s0[j] : -INFINITY;
+                else
+                    s1[j - 4] = vis ? s1[j - 4] : -INFINITY;
+            }
+        }
+        float mx = max3(s0[0], s0[1], s0[2]);
+        mx = max3(mx, s0[3], s1[0]);
+        mx = max3(mx, s1[1], s1[2]);
+        mx = __builtin_fmaxf(mx, s1[3]);
+        const bool moved = __builtin_amdgcn_ballot_w64(mx > thr) != 0;
+        alpha = 1.0f;
+        if (moved) {
+            float cm = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+            cm = __builtin_fmaxf(cm, __shfl_xor(cm, 32));
+            const bool upd = cm > thr;
+            const float delta = upd ? cm : 0.0f;
+            alpha = upd ? (m_set ? __builtin_amdgcn_exp2f(-delta) : 0.0f) : 1.0f;
+            mu += delta;
+            m_set = m_set | upd;
+            thr = m_set ? RESCALE_THRESHOLD : -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s0[i] -= delta;
+                s1[i] -= delta;
+            }
+            negm = -mu;
+            l_acc *= alpha;
+        }
+        return moved;
+    };
+    // p = exp2(s) rounded to bf16 in pairs, l += the rounded p
+    auto softmax_p = [&](const f32x4& s0, const f32x4& s1, u32x4& pw) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float x0 = j < 2 ? s0[2 * j] : s1[2 * j - 4];
+            const float x1 = j < 2 ? s0[2 * j + 1] : s1[2 * j - 3];
+            const bf16x2 pr = {(__bf16)__builtin_amdgcn_exp2f(x0), (__bf16)__builtin_amdgcn_exp2f(x1)};
+            pw[j] = __builtin_bit_cast(uint32_t, pr);
+            l_acc = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l_acc, false);
+        }
+    };
+    auto pin = [&](const u32x4& pw) __attribute__((always_inline)) {
+        asm volatile("" ::"v"(pw[0]), "v"(pw[1]), "v"(pw[2]), "v"(pw[3]), "v"(l_acc));
+    };
+
+    // Software pipeline and DMA order as attn_ring_kernel: step i runs QK^T
+    // of tile i and its softmax, and the PV product of tile i - 1 under the
+    // exponentials.  K0 V0 | K1 | K2 V1 | K3 V2 | ...; the last tile's V^T
+    // goes to the K buffer once its QK^T has read that.
+    u32x4 pprev;
+    bool last_in_k = false;
+    int t = kw > 0 ? tile_at(0) : -1;
+    if (t >= 0) {
+        wait_vmcnt<NDMA>();
+        f32x4 s0, s1;
+        qk(s0, s1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const int tn = kw > 1 ? tile_at(1) : -1;
+        if (tn >= 0) issue_k(tn);
+        float alpha;
+        mask_and_max(s0, s1, t, alpha);  // (O is still zero: no rescale)
+        softmax_p(s0, s1, pprev);
+        t = tn;
+    }
+    for (int i = 1; t >= 0; ++i) {
+        if (i == 1)
+            wait_vmcnt<0>();
+        else
+            wait_vmcnt<NDMA>();
+        f32x4 s0, s1;
+        qk(s0, s1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const int tn = i + 1 < kw ? tile_at(i + 1) : -1;
+        if (tn >= 0)
+            issue_k(tn);
+        else
+            issue_v_to_k(t);
+        wait_vmcnt<NDMA>();
+        bf16x8 vf[ND];
+        read_v(vbuf, vf);
+        float alpha;
+        const bool moved = mask_and_max(s0, s1, t, alpha);
+        u32x4 pcur;
+        softmax_p(s0, s1, pcur);
+        pv(vf, __builtin_bit_cast(bf16x8, pprev));
+#pragma unroll
+        for (int k = 0; k < ND; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, 1, 0);  // VALU / transcendental
+        }
+        pin(pcur);
+        __builtin_amdgcn_sched_barrier(0);
+        if (moved) {
+#pragma unroll
+            for (int db = 0; db < ND; ++db) o[db] *= alpha;
+        }
+        pprev = pcur;
+        if (tn >= 0) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue_v(t);
+        }
+        last_in_k = true;
+        t = tn;
+    }
+    wait_vmcnt<0>();
+    if (kw > 0) {
+        bf16x8 vf[ND];
+        read_v(last_in_k ? kbuf : vbuf, vf);
+        pv(vf, __builtin_bit_cast(bf16x8, pprev));
+    }
+
+    // ---- merge the RW key groups of each row through LDS (as
+    // attn_ring_kernel): wave w's O^T (16 rows x HD f32) into its own K and
+    // V^T buffers, 16-byte chunk c of row n at chunk c ^ n, then every thread
+    // finishes its share of a row
+    float* const sm = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + ML_OFF);  // [RW][16]
+    float* const sl = sm + RW * ROWS;                                                  // [RW][16]
+    float l_tot = l_acc + __shfl_xor(l_acc, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    if (g16 == 0) {
+        sm[wave * ROWS + n16] = m_set ? mu : -INFINITY;
+        sl[wave * ROWS + n16] = l_tot;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    {
+        // o[db][i] is O^T[d = 16 db + 4 g16 + i][n16]: chunk 4 db + g16 of row n16
+        float* myrow = reinterpret_cast<float*>(kbuf) + n16 * RHD;
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+            *reinterpret_cast<f32x4*>(myrow + 4 * ((4 * db + g16) ^ n16)) = o[db];
+    }
+    lds_barrier();
+    // thread tid: row rr = tid / TPR (TPR = 16: a read's 16 lanes are one
+    // row's 16 chunk slots), chunks ch + TPR k
+    constexpr int CPT = HD / 4 / TPR;
+    const int rr = tid / TPR, ch = tid % TPR;
+    const int row = wg_row0 + rr;
+    if (row >= rows_total) return;
+    float mw[RW];
+    float M = -INFINITY, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < RW; ++w) {
+        mw[w] = sm[w * ROWS + rr];
+        M = __builtin_fmaxf(M, mw[w]);
+    }
+    f32x4 acc[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < RW; ++w) {
+        const float wt_w = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+        const float* prow = reinterpret_cast<const float*>(smem + w * 2 * RT) + rr * RHD;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k)
+            acc[k] += wt_w * *reinterpret_cast<const f32x4*>(prow + 4 * ((ch + TPR * k) ^ rr));
+        L += wt_w * sl[w * ROWS + rr];
+    }
+    int ohg, oqi;
+    split_row(row, ohg, oqi);
+    const size_t o0 = (size_t)oqi * a.o_rstride + (size_t)(g * a.group + ohg) * RHD;
+    const float il = __builtin_amdgcn_rcpf(L);
+    if (a.o_bf16) {
+        uint16_t* orow = reinterpret_cast<uint16_t*>(S.out) + o0;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const f32x4 v = acc[k] * il;
+            const bf16x4 y = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+            gstore(orow + 4 * (ch + TPR * k), y);
+        }
+    } else {
+        float* orow = S.out + o0;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) gstore(orow + 4 * (ch + TPR * k), acc[k] * il);
+    }
+}
+
+template <int HD, int MODE>
+hipError_t launch_ring16_mode(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
+    static bool attr_set = false;
+    auto fn = attn_ring16_kernel<HD, MODE>;
+    constexpr int lds = Ring16<HD>::LDS;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(fn, dim3(p.n_workgroups), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
 template <int HD, int MODE, int W>
 hipError_t launch_ring_mode(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     static bool attr_set = false;
@@ -779,6 +1325,15 @@ int ring_merge_splits(int hd) {
 
 hipError_t launch_ring(const LaunchPlan& p, const AttnArgs& a, hipStream_t st) {
     // (RoPE on Q only at full rotary: see the Q load)
+    if (p.w16) {  // 16-row waves: head dim 256, one 16-row block per workgroup, no key split
+        if ((a.rope && a.rot != a.hd) || a.hd != 256 || p.hd_tile != 256 || p.n_split != 1 || p.waves != 4)
+            return hipErrorInvalidValue;
+        switch (p.mask) {
+            case MASK_NONE: return launch_ring16_mode<256, MASK_NONE>(p, a, st);
+            case MASK_POS: return launch_ring16_mode<256, MASK_POS>(p, a, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     if ((a.rope && a.rot != a.hd) || a.hd != p.hd_tile || !ring_waves_built(a.hd, p.waves))
         return hipErrorInvalidValue;
     if (a.ticket && a.n_split > ring_merge_splits(a.hd)) return hipErrorInvalidValue;

@@ -87,7 +87,7 @@ CASES_256 = {
 }
 
 
-def _run(dev, name, kernel, hd=128):
+def _run(dev, name, kernel, hd=128, wave_rows=0):
     h, hkv, n_p, n_c, batch, window, prefix, qk_norm, n_split = (CASES if hd == 128 else CASES_256)[name]
     n_t = n_p + n_c
     kvs = hkv * hd
@@ -111,6 +111,7 @@ def _run(dev, name, kernel, hd=128):
         ins.append((Q, K, V))
     dev.ctx.set_kernel(kernel)
     dev.ctx.set_split(n_split)
+    dev.ctx.set_wave_rows(wave_rows)
     try:
         cache.attention(0, items, h, sliding_window=window, causal_prefix=prefix,
                         scale=1 / math.sqrt(hd), q_norm_w=dev.put(qn) if qk_norm else None,
@@ -119,6 +120,7 @@ def _run(dev, name, kernel, hd=128):
     finally:
         dev.ctx.set_kernel(dr.KERNEL_AUTO)
         dev.ctx.set_split(0)
+        dev.ctx.set_wave_rows(0)
     got = [dev.get(o) for o in outs]
     s = Shape(n_c, n_t, h, hkv, hd, sliding_window=window, causal_prefix=prefix, scale=1 / math.sqrt(hd))
     qr, kr = RowsSpec(list(range(n_p, n_t))), RowsSpec(list(range(n_t)))
@@ -164,6 +166,19 @@ def test_kernel_family_hd256_vs_oracle(dev, name, kernel):
         assert info["waves_per_wg"] == 4
     if CASES_256[name][8]:
         assert info["n_split"] == CASES_256[name][8]
+    for b, (g, w) in enumerate(zip(got, wants)):
+        mx, mean = err_stats(g, w)
+        say(f"  batch {b}: max-abs {mx:.3e} mean-abs {mean:.3e}")
+        assert mx <= TOL_MAX and mean <= TOL_MEAN, (name, b, mx, mean)
+
+
+@pytest.mark.parametrize("name", [n for n in CASES_256 if not CASES_256[n][8]])
+def test_streams_16_row_waves_hd256_vs_oracle(dev, name):
+    """The per-wave-stream kernel with 16-row waves at head dim 256
+    (attn_ring16_kernel: one 16-row block per workgroup, no key split)."""
+    got, wants, info = _run(dev, name, dr.KERNEL_STREAMS, hd=256, wave_rows=16)
+    say(f"hd 256 {name} 16-row waves: launch {info}")
+    assert info["kernel"] == dr.KERNEL_STREAMS and info["rows_per_wave"] == 16 and info["n_split"] == 1, info
     for b, (g, w) in enumerate(zip(got, wants)):
         mx, mean = err_stats(g, w)
         say(f"  batch {b}: max-abs {mx:.3e} mean-abs {mean:.3e}")
@@ -222,6 +237,35 @@ def test_planner_hd128_waves(dev):
             mx, mean = err_stats(g, w)
             say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
             assert mx <= TOL_MAX and mean <= TOL_MEAN, (name, mx, mean)
+
+
+def test_planner_hd256_16_row_waves(dev):
+    """Head dim 256 with a short key band: 16-row waves (one 16-row block per
+    workgroup, no key split) where their workgroups fill more than half the
+    CUs in one round; longer bands keep the 32-row kernel's two splits."""
+    hd = 256
+    # (h, hkv, n_prompt, n_canvas, window, rows per wave, n_split)
+    cases = (
+        (16, 8, 4096, 256, 1024, 16, 1),   # C5 sliding: band of 1279 keys
+        (16, 8, 4096, 256, 256, 16, 1),
+        (16, 8, 4096, 256, 1536, 32, 2),   # band of 1791 keys
+        (16, 8, 1024, 256, None, 16, 1),   # 1280 keys
+        (16, 8, 2048, 256, None, 32, 2),   # 2304 keys
+        (8, 4, 1000, 256, None, 32, 2),    # 128 16-row workgroups: half the CUs
+    )
+    for h, hkv, n_p, n_c, window, rows, n_split in cases:
+        n_t = n_p + n_c
+        cache = dr.StepCache(dev.ctx, n_t, [hkv], [hd])
+        z = dev.put(np.zeros((n_t, hkv * hd), np.float32))
+        cache.store(0, dr.Pass(dev.ctx, range(n_t)), z, z)
+        q = dev.put(np.zeros((n_c, h * hd), np.float32))
+        cache.attention(0, [(q, dev.empty(n_c * h * hd), dr.Pass(dev.ctx, range(n_p, n_t)))], h,
+                        sliding_window=window, scale=1 / math.sqrt(hd))
+        info = dev.ctx.last_launch()
+        say(f"h {h}/{hkv} keys {n_t} window {window}: launch {info}")
+        assert info["kernel"] == dr.KERNEL_STREAMS, info
+        assert info["rows_per_wave"] == rows and info["n_split"] == n_split, (h, hkv, n_t, window, info)
+        del cache
 
 
 def test_planner_hd256_key_band(dev):

@@ -141,9 +141,13 @@ def test_graph_replays_of_in_kernel_merge(dev):
 
 
 def test_planner_splits_gemma_sliding_layer_in_kernel(dev):
-    """DiffusionGemma's sliding layer (C5 sliding: 128 one-block workgroups
-    at head dim 256) runs as two key splits merged in-kernel, and unsplit when
-    the in-kernel merge is off (the separate merge kernel made the split lose)."""
+    """DiffusionGemma's sliding layer (C5 sliding: canvas rows at the end, a
+    band of 1279 keys at head dim 256) runs 16-row waves, 256 workgroups with
+    no key split, whether the in-kernel merge is on or off.  The same window
+    over canvas rows in the middle of the sequence (a band of 2302 keys)
+    keeps the 32-row kernel: two key splits merged in-kernel, and unsplit when
+    the in-kernel merge is off (the separate merge kernel made the split
+    lose)."""
     from helpers import CONFIGS
     cfg = CONFIGS["C5S"]
     h, hkv, hd, n_t, n_c = cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.n_total, cfg.n_canvas
@@ -151,10 +155,13 @@ def test_planner_splits_gemma_sliding_layer_in_kernel(dev):
     z = dev.put(np.zeros((n_t, hkv * hd), np.float32))
     cache.store(0, dr.Pass(dev.ctx, range(n_t)), z, z)
     q = dev.put(np.zeros((n_c, h * hd), np.float32))
-    item = [(q, dev.empty(n_c * h * hd), dr.Pass(dev.ctx, range(cfg.n_prompt, n_t)))]
-    cache.attention(0, item, h, sliding_window=cfg.window, scale=cfg.attn_scale)
-    info = dev.ctx.last_launch()
-    assert (info["kernel"], info["n_split"], info["split_merge"]) == (dr.KERNEL_STREAMS, 2, 2), info
-    _with(dev, False, lambda: cache.attention(0, item, h, sliding_window=cfg.window, scale=cfg.attn_scale))
-    info = dev.ctx.last_launch()
-    assert (info["kernel"], info["n_split"], info["split_merge"]) == (dr.KERNEL_STREAMS, 1, 0), info
+    for first, want_on, want_off in ((cfg.n_prompt, (16, 1, 0), (16, 1, 0)), (2048, (32, 2, 2), (32, 1, 0))):
+        item = [(q, dev.empty(n_c * h * hd), dr.Pass(dev.ctx, range(first, first + n_c)))]
+        cache.attention(0, item, h, sliding_window=cfg.window, scale=cfg.attn_scale)
+        info = dev.ctx.last_launch()
+        assert info["kernel"] == dr.KERNEL_STREAMS, info
+        assert (info["rows_per_wave"], info["n_split"], info["split_merge"]) == want_on, (first, info)
+        _with(dev, False, lambda: cache.attention(0, item, h, sliding_window=cfg.window, scale=cfg.attn_scale))
+        info = dev.ctx.last_launch()
+        assert info["kernel"] == dr.KERNEL_STREAMS, info
+        assert (info["rows_per_wave"], info["n_split"], info["split_merge"]) == want_off, (first, info)
