@@ -9,7 +9,9 @@ or by the merge kernel, bf16 Q rows where the stream kernel runs, key
 counts that fill whole 32-key tiles (the cache store's tile kernel), and
 hi/lo-precision layers (checked against the oracle on the unrounded f32
 inputs, since that kernel is f32-accurate).  The seeds are fixed, so every
-run draws the same cases.  Needs an MI355X.
+run draws the same cases.  A second set forces the stream kernel's 16-row
+waves at head dim 256 over bands of up to ~1850 keys and grids of up to
+three rounds of workgroups.  Needs an MI355X.
 """
 from __future__ import annotations
 
@@ -59,9 +61,40 @@ def _draw(seed: int) -> dict:
                 qk_norm=qk_norm, bf16_q=bf16_q, hilo=hilo, seed=seed)
 
 
+def _draw16(seed: int) -> dict:
+    """A case for the stream kernel's 16-row waves at head dim 256
+    (attn_ring16_kernel), forced so that bands longer than the planner's
+    limit and grids of several rounds run on it too."""
+    rng = np.random.default_rng(5000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 3, 7]))
+    n_p = int(rng.integers(0, 1600))
+    n_c = int(rng.integers(1, 260))
+    window = int(rng.integers(16, 1100)) if rng.random() < 0.5 else None
+    prefix = int(rng.integers(0, n_p + n_c)) if rng.random() < 0.3 else None
+    if seed % 4 == 0:
+        n_p = (n_p + n_c + 31) // 32 * 32 - n_c
+        if prefix is not None:
+            prefix = min(prefix, n_p + n_c - 1)
+    return dict(kernel=dr.KERNEL_STREAMS, hd=256, hkv=hkv, h=hkv * group, n_p=n_p, n_c=n_c,
+                batch=int(rng.choice([1, 1, 2])), window=window, prefix=prefix,
+                scattered=bool(rng.random() < 0.3), split=0, in_kernel=True,
+                qk_norm=bool(rng.random() < 0.4), bf16_q=bool(rng.random() < 0.5), hilo=False,
+                wave_rows=16, seed=seed)
+
+
 @pytest.mark.parametrize("seed", range(N_CASES))
 def test_random_shape_vs_oracle(dev, seed):
-    c = _draw(seed)
+    _check_case(dev, _draw(seed))
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_shape_16_row_waves_vs_oracle(dev, seed):
+    _check_case(dev, _draw16(seed))
+
+
+def _check_case(dev, c):
+    seed = c["seed"]
     say(f"case {seed}: {c}")
     t = dev.t
     rng = np.random.default_rng(7000 + seed)
@@ -105,6 +138,7 @@ def test_random_shape_vs_oracle(dev, seed):
     ctx.set_split(c["split"])
     ctx.set_split_merge(c["in_kernel"])
     ctx.set_q_dtype(dr.DTYPE_BF16 if c["bf16_q"] else dr.DTYPE_F32)
+    ctx.set_wave_rows(c.get("wave_rows", 0))
     try:
         cache.attention(0, items, h, sliding_window=c["window"], causal_prefix=c["prefix"], scale=scale,
                         q_norm_w=dev.put(qn) if qn is not None else None, q_norm_eps=1e-6)
@@ -114,7 +148,10 @@ def test_random_shape_vs_oracle(dev, seed):
         ctx.set_split(0)
         ctx.set_split_merge(True)
         ctx.set_q_dtype(dr.DTYPE_F32)
+        ctx.set_wave_rows(0)
     say(f"  launch {info}")
+    if c.get("wave_rows") == 16:
+        assert info["kernel"] == dr.KERNEL_STREAMS and info["rows_per_wave"] == 16 and info["n_split"] == 1, info
     if c["kernel"] != dr.KERNEL_AUTO:
         assert info["kernel"] in (c["kernel"], dr.KERNEL_STAGED)  # STREAMS falls back where it does not apply
     if c["bf16_q"]:
