@@ -460,7 +460,8 @@ typedef struct {
     int head_dim_tile;
     int row_blocks;
     int key_groups;
-    int rows_per_wave; /* query rows per compute wave: 32, or 16 (two waves per row block) */
+    int rows_per_wave; /* query rows per compute wave: 32, or 16 (STAGED: two waves per row
+                        * block; STREAMS at head dim 256: one 16-row block per workgroup) */
     int kernel; /* DR_KERNEL_STAGED, DR_KERNEL_STREAMS or DR_KERNEL_HILO: which attention kernel ran */
     int split_merge; /* key splits merged: 0 no split, 1 by a second kernel, 2 in-kernel */
 } dr_launch_info;
@@ -469,7 +470,8 @@ int dr_ctx_last_launch(const dr_ctx* ctx, dr_launch_info* info);
 /* Override the key-split heuristic for later calls on ctx (0 = automatic). */
 int dr_ctx_set_split(dr_ctx* ctx, int n_split);
 /* Query rows per compute wave for later calls on ctx: 16 or 32 where the
- * head-dim tile builds both, 0 = automatic. */
+ * head-dim tile builds both, 0 = automatic.  With DR_KERNEL_STREAMS at head
+ * dim 256, 16 selects the 16-row-wave stream kernel (no key split). */
 int dr_ctx_set_wave_rows(dr_ctx* ctx, int rows);
 /* Attention kernel families, for dr_ctx_set_kernel and dr_launch_info.kernel.
  * STAGED: the workgroup's waves share K/V super-tiles staged in LDS (every
